@@ -1,0 +1,78 @@
+"""Build ``libdrt_rocm.so`` in-tree from ``csrc/*.hip`` for gfx950.
+
+Each source compiles to an object with ``hipcc --offload-arch=gfx950`` in
+parallel, then one link produces ``diffusorrt_amd/libdrt_rocm.so``. No cmake,
+no JIT cache: the built library sits next to this file so it travels with the
+repository tree.
+"""
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIB = PKG / "libdrt_rocm.so"
+ARCH = os.environ.get("DRT_OFFLOAD_ARCH", "gfx950")
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
+    # Packed fp32 VALU forms are kept out of every kernel.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (ROCm is required to build libdrt_rocm.so)")
+
+
+def _compile(src: Path, obj: Path) -> tuple[Path, int, str]:
+    cmd = [_hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    log = "\n".join(line for line in (proc.stdout + proc.stderr).splitlines() if noise not in line)
+    return src, proc.returncode, log
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every ``csrc/*.hip`` and link the shared library. Always rebuilds."""
+    sources = sorted(CSRC.glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    BUILD.mkdir(exist_ok=True)
+    jobs = jobs or min(len(sources), max(1, min(16, os.cpu_count() or 1)))
+    objs = []
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+        futs = [pool.submit(_compile, s, BUILD / (s.stem + ".o")) for s in sources]
+        failed = []
+        for fut in futs:
+            src, rc, log = fut.result()
+            if verbose and log.strip():
+                print(f"[{src.name}]\n{log}", file=sys.stderr)
+            if rc != 0:
+                failed.append((src, log))
+            objs.append(BUILD / (src.stem + ".o"))
+    if failed:
+        msg = "\n".join(f"--- {s.name} ---\n{log}" for s, log in failed)
+        raise RuntimeError(f"hipcc failed for {len(failed)} source(s):\n{msg}")
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+           *[str(o) for o in objs]]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,390 @@
+// Block-over-prefix GQA attention for gfx950 (flash-decode over key splits).
+//
+// Queries of one KV head are flattened to query vectors qv = row * G + gi
+// (G = Hq / Hkv, head = kvh * G + gi) and processed in 32-vector tiles, one
+// tile per wave. Keys come in 32-key tiles staged through LDS (double
+// buffered) and shared by the QW waves of a work-group.
+//
+// Per 32x32 tile the wave computes S^T = K Q^T (8 MFMAs over head_dim 128), so
+// lane l owns query (l & 31) and 16 of its 32 keys; the partner lane l ^ 32
+// owns the other 16. Online softmax keeps (m, l) per lane; one xor-32 exchange
+// gives the tile max, and the partial sums are only joined at the end. P^T then
+// feeds the B operand of O^T += V^T P^T (8 MFMAs) directly from registers.
+//
+// KV cache tile layout (T = _Float16 or __bf16), per (layer, kv head, tile of 32
+// keys) a contiguous 16 KiB: K block (4096 elements) then V block (4096):
+//   K[key kk][hd]: ((t*2 + h)*32 + kk)*8 + e        t = hd/16, h = (hd/8)&1, e = hd&7
+//   V[key kk][hd]: (((hb*2 + kh)*2 + h)*32 + hl)*8 + j
+//       hb = hd/32, hl = hd&31, kh = kk/16, q = kk&15, h = (q>>2)&1, j = (q&3) + 4*(q>>3)
+// so that every MFMA operand a wave reads is one contiguous 1 KiB of LDS.
+//
+// Masks: kind 0 = none (bidirectional, or a block whose keys are all visible);
+// kind 1 = d2f_hybrid: eff(p) = p < prompt_len ? -1 : (p - prompt_len) / block,
+// key visible iff eff(key) <= eff(query position).
+#include "common.h"
+#include "launch.h"
+
+namespace {
+
+template <typename T> struct MfmaT;
+template <> struct MfmaT<_Float16> {
+  typedef f16x8 vec;
+  static DRT_DEV f32x16 mma(vec a, vec b, f32x16 c) { return mfma_f16(a, b, c); }
+  static DRT_DEV _Float16 from_float(float f) { return (_Float16)f; }
+};
+template <> struct MfmaT<__bf16> {
+  typedef bf16x8 vec;
+  static DRT_DEV f32x16 mma(vec a, vec b, f32x16 c) { return mfma_bf16(a, b, c); }
+  static DRT_DEV __bf16 from_float(float f) {
+    return __builtin_bit_cast(__bf16, float_to_bf16_bits(f));
+  }
+};
+
+DRT_DEV int eff_block(int p, int prompt_len, int block) {
+  return p < prompt_len ? -1 : (p - prompt_len) / block;
+}
+
+}  // namespace
+
+constexpr int KV_TILE_ELEMS = 8192;  // K block + V block per 32-key tile
+
+template <typename T, int QW>
+__global__ __launch_bounds__(64 * QW) void attn_split_kernel(
+    const T* __restrict__ q,       // [n_rows][Hq][128]
+    const T* __restrict__ kv,      // this layer: [Hkv][tile_cap][8192]
+    int64_t kv_head_stride,        // elements between kv heads
+    int n_rows, int Hq, int Hkv, int n_keys, int row_pos0,
+    int mask_kind, int mask_prompt_len, int mask_block, int tiles_per_split,
+    float* __restrict__ o_part,    // [splits][Hkv][n_qv][128]
+    float* __restrict__ ml_part,   // [splits][Hkv][n_qv][2]
+    float scale) {
+  typedef typename MfmaT<T>::vec vec;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int G = Hq / Hkv;
+  const int n_qv = n_rows * G;
+  const int n_splits = gridDim.x / Hkv;
+  const int split = blockIdx.x / Hkv;
+  const int kvh = blockIdx.x - split * Hkv;
+  const int qt = blockIdx.y * QW + wave;
+  const int n_tiles = (n_keys + 31) >> 5;
+  const int t_begin = split * tiles_per_split;
+  const int t_end = min(n_tiles, t_begin + tiles_per_split);
+
+  extern __shared__ __align__(16) char smem[];
+  T* lds = (T*)smem;  // [2][8192]
+
+  // This lane's query (B operand of S^T) and its absolute position.
+  const int qv = qt * 32 + (lane & 31);
+  const bool q_ok = qv < n_qv;
+  const int qrow = q_ok ? qv / G : 0;
+  const int qhead = kvh * G + (q_ok ? qv - (qv / G) * G : 0);
+  vec qf[8];
+  {
+    const T* qp = q + ((int64_t)qrow * Hq + qhead) * 128 + 8 * (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (q_ok) qf[i] = *(const vec*)(qp + 16 * i);
+      else qf[i] = vec{};
+    }
+  }
+  const int qpos = row_pos0 + qrow;
+  const int q_eff = mask_kind == 1 ? eff_block(qpos, mask_prompt_len, mask_block) : 0;
+  // Wave-uniform visibility bound: no key beyond the last visible key of the
+  // wave's rows needs loading into this wave's math.
+  int wave_key_end = n_keys;
+  if (mask_kind == 1) {
+    const int last_row = min(n_rows - 1, (qt * 32 + 31) / G);
+    const int e = eff_block(row_pos0 + last_row, mask_prompt_len, mask_block);
+    wave_key_end = min(n_keys, e < 0 ? mask_prompt_len : mask_prompt_len + (e + 1) * mask_block);
+  }
+  // WG-uniform bound (the last wave's rows are the latest).
+  int wg_key_end = n_keys;
+  if (mask_kind == 1) {
+    const int last_row = min(n_rows - 1, (blockIdx.y * QW * 32 + QW * 32 - 1) / G);
+    const int e = eff_block(row_pos0 + last_row, mask_prompt_len, mask_block);
+    wg_key_end = min(n_keys, e < 0 ? mask_prompt_len : mask_prompt_len + (e + 1) * mask_block);
+  }
+  const int t_stop = min(t_end, (wg_key_end + 31) >> 5);
+
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x16 o[4];
+#pragma unroll
+  for (int hb = 0; hb < 4; ++hb) o[hb] = f32x16{};
+
+  const T* kvh_base = kv + (int64_t)kvh * kv_head_stride;
+  constexpr int VEC_PER_TILE = KV_TILE_ELEMS / 8;  // 16-byte vectors per tile
+  constexpr int PER_THREAD = VEC_PER_TILE / (64 * QW);
+  u32x4 stage[PER_THREAD];
+  auto load_tile = [&](int t) {
+    const u32x4* src = (const u32x4*)(kvh_base + (int64_t)t * KV_TILE_ELEMS);
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) stage[i] = src[threadIdx.x + i * 64 * QW];
+  };
+  auto store_tile = [&](int buf) {
+    u32x4* dst = (u32x4*)(lds + buf * KV_TILE_ELEMS);
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) dst[threadIdx.x + i * 64 * QW] = stage[i];
+  };
+
+  if (t_begin < t_stop) {
+    load_tile(t_begin);
+    store_tile(0);
+  }
+  __syncthreads();
+  for (int t = t_begin; t < t_stop; ++t) {
+    const int buf = (t - t_begin) & 1;
+    const bool more = t + 1 < t_stop;
+    if (more) load_tile(t + 1);
+    const int key0 = t * 32;
+    if (key0 < wave_key_end) {
+      const T* kt = lds + buf * KV_TILE_ELEMS;
+      const T* vt = kt + 4096;
+      f32x16 s = f32x16{};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const vec kf = *(const vec*)(kt + (i * 64 + lane) * 8);
+        s = MfmaT<T>::mma(kf, qf[i], s);
+      }
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = key0 + mfma_row(r, lane);
+        bool vis = key < n_keys;
+        if (mask_kind == 1) vis = vis && eff_block(key, mask_prompt_len, mask_block) <= q_eff;
+        s[r] = vis ? s[r] * scale : -INFINITY;
+        tmax = fmaxf(tmax, s[r]);
+      }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float m_new = fmaxf(m_run, tmax);
+      const float base = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __expf(m_run - base);
+      float psum = 0.f;
+      float p[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        p[r] = __expf(s[r] - base);
+        psum += p[r];
+      }
+      l_run = l_run * alpha + psum;
+      m_run = m_new;
+#pragma unroll
+      for (int hb = 0; hb < 4; ++hb) o[hb] *= alpha;
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+        vec pf;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pf[j] = MfmaT<T>::from_float(p[kh * 8 + j]);
+#pragma unroll
+        for (int hb = 0; hb < 4; ++hb) {
+          const vec vf = *(const vec*)(vt + (((hb * 2 + kh) * 64) + lane) * 8);
+          o[hb] = MfmaT<T>::mma(vf, pf, o[hb]);
+        }
+      }
+    }
+    if (more) {
+      // The other buffer was last read before the previous iteration's barrier.
+      store_tile(buf ^ 1);
+      __syncthreads();
+    }
+  }
+  l_run += __shfl_xor(l_run, 32, 64);
+
+  // Transpose O^T through LDS so each query's 128 values are written contiguously.
+  __syncthreads();
+  float* ot = (float*)smem + wave * (32 * 132);
+#pragma unroll
+  for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ot[(lane & 31) * 132 + hb * 32 + mfma_row(r, lane)] = o[hb][r];
+  __syncthreads();
+  const int64_t part_base = ((int64_t)split * Hkv + kvh) * n_qv;
+  for (int i = lane; i < 32 * 32; i += 64) {
+    const int qq = i >> 5, c4 = (i & 31) * 4;
+    const int qv2 = qt * 32 + qq;
+    if (qv2 < n_qv) {
+      f32x4 v = {ot[qq * 132 + c4], ot[qq * 132 + c4 + 1], ot[qq * 132 + c4 + 2],
+                 ot[qq * 132 + c4 + 3]};
+      *(f32x4*)(o_part + (part_base + qv2) * 128 + c4) = v;
+    }
+  }
+  if (lane < 32 && q_ok) {
+    ml_part[(part_base + qv) * 2 + 0] = m_run;
+    ml_part[(part_base + qv) * 2 + 1] = l_run;
+  }
+  (void)n_splits;
+}
+
+// Combine key splits. One wave per (row, head); lane holds hd = lane, lane + 64.
+// out_fmt: 0 = ACT_F16P (+ xsum), 1 = ACT_BF16, 2 = fp32 plain, 3 = bf16 plain.
+extern "C" __global__ void attn_combine_kernel(const float* __restrict__ o_part,
+                                               const float* __restrict__ ml_part, int n_splits,
+                                               int n_rows, int Hq, int Hkv, void* __restrict__ out,
+                                               float* __restrict__ xsum, int out_fmt) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
+  if (wid >= (int64_t)n_rows * Hq) return;
+  const int row = (int)(wid / Hq), head = (int)(wid % Hq);
+  const int G = Hq / Hkv;
+  const int kvh = head / G, qv = row * G + (head - kvh * G);
+  const int n_qv = n_rows * G;
+  float mmax = -INFINITY;
+  for (int s = 0; s < n_splits; ++s)
+    mmax = fmaxf(mmax, ml_part[((((int64_t)s * Hkv + kvh) * n_qv) + qv) * 2]);
+  float lsum = 0.f, a0 = 0.f, a1 = 0.f;
+  for (int s = 0; s < n_splits; ++s) {
+    const int64_t idx = ((int64_t)s * Hkv + kvh) * n_qv + qv;
+    const float ms = ml_part[idx * 2];
+    if (ms == -INFINITY) continue;
+    const float w = __expf(ms - mmax);
+    lsum += w * ml_part[idx * 2 + 1];
+    a0 += w * o_part[idx * 128 + lane];
+    a1 += w * o_part[idx * 128 + 64 + lane];
+  }
+  const float inv = 1.f / lsum;
+  const float v0 = a0 * inv, v1 = a1 * inv;
+  const int D = Hq * 128;
+  const int c0 = head * 128 + lane, c1 = c0 + 64;
+  if (out_fmt == 0) {
+    _Float16* o = (_Float16*)out + (int64_t)row * D;
+    const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
+    o[f16p_index(c0)] = h0;
+    o[f16p_index(c1)] = h1;
+    const float s0 = wave_sum((float)h0), s1 = wave_sum((float)h1);
+    if (lane == 0) {
+      xsum[(int64_t)row * (D >> 6) + (c0 >> 6)] = s0;
+      xsum[(int64_t)row * (D >> 6) + (c0 >> 6) + 1] = s1;
+    }
+  } else if (out_fmt == 1 || out_fmt == 3) {
+    uint16_t* o = (uint16_t*)out + (int64_t)row * D;
+    o[c0] = float_to_bf16_bits(v0);
+    o[c1] = float_to_bf16_bits(v1);
+  } else {
+    float* o = (float*)out + (int64_t)row * D;
+    o[c0] = v0;
+    o[c1] = v1;
+  }
+}
+
+// Write K/V rows (logical [n][Hkv][128] fp32 or bf16) into the tiled cache of
+// one layer at absolute positions pos0 .. pos0 + n - 1. One wave per (row, kv head).
+template <typename T>
+__global__ void kv_pack_kernel(const void* __restrict__ k_src, const void* __restrict__ v_src,
+                               int src_is_bf16, int n, int Hkv, int pos0, T* __restrict__ kv,
+                               int64_t kv_head_stride) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
+  if (wid >= (int64_t)n * Hkv) return;
+  const int row = (int)(wid / Hkv), h = (int)(wid % Hkv);
+  const int pos = pos0 + row;
+  T* tile = kv + (int64_t)h * kv_head_stride + (int64_t)(pos >> 5) * KV_TILE_ELEMS;
+  const int kk = pos & 31;
+  for (int e = 0; e < 2; ++e) {
+    const int hd = lane + 64 * e;
+    float kf, vf;
+    const int64_t si = ((int64_t)row * Hkv + h) * 128 + hd;
+    if (src_is_bf16) {
+      kf = bf16_bits_to_float(((const uint16_t*)k_src)[si]);
+      vf = bf16_bits_to_float(((const uint16_t*)v_src)[si]);
+    } else {
+      kf = ((const float*)k_src)[si];
+      vf = ((const float*)v_src)[si];
+    }
+    const int ko = (((hd >> 4) * 2 + ((hd >> 3) & 1)) * 32 + kk) * 8 + (hd & 7);
+    const int q16 = kk & 15;
+    const int vo = ((((hd >> 5) * 2 + (kk >> 4)) * 2 + ((q16 >> 2) & 1)) * 32 + (hd & 31)) * 8 +
+                   (q16 & 3) + 4 * (q16 >> 3);
+    tile[ko] = MfmaT<T>::from_float(kf);
+    tile[4096 + vo] = MfmaT<T>::from_float(vf);
+  }
+}
+
+template __global__ void attn_split_kernel<_Float16, 2>(const _Float16*, const _Float16*, int64_t,
+                                                        int, int, int, int, int, int, int, int, int,
+                                                        float*, float*, float);
+template __global__ void attn_split_kernel<_Float16, 4>(const _Float16*, const _Float16*, int64_t,
+                                                        int, int, int, int, int, int, int, int, int,
+                                                        float*, float*, float);
+template __global__ void attn_split_kernel<__bf16, 2>(const __bf16*, const __bf16*, int64_t, int,
+                                                      int, int, int, int, int, int, int, int,
+                                                      float*, float*, float);
+template __global__ void attn_split_kernel<__bf16, 4>(const __bf16*, const __bf16*, int64_t, int,
+                                                      int, int, int, int, int, int, int, int,
+                                                      float*, float*, float);
+template __global__ void kv_pack_kernel<_Float16>(const void*, const void*, int, int, int, int,
+                                                  _Float16*, int64_t);
+template __global__ void kv_pack_kernel<__bf16>(const void*, const void*, int, int, int, int,
+                                                __bf16*, int64_t);
+
+namespace drt {
+
+AttnPlan plan_attention(int n_rows, int Hq, int Hkv, int n_keys, size_t part_budget_bytes) {
+  AttnPlan p;
+  const int G = Hq / Hkv;
+  const int qtiles = (n_rows * G + 31) / 32;
+  p.qw = qtiles <= 2 ? 2 : 4;
+  p.qgroups = (qtiles + p.qw - 1) / p.qw;
+  const int n_tiles = std::max(1, (n_keys + 31) / 32);
+  const int target_wgs = 512;
+  int splits = std::max(1, target_wgs / (Hkv * p.qgroups));
+  splits = std::min(splits, n_tiles);
+  // keep the fp32 partials within budget
+  const size_t per_split = (size_t)Hkv * n_rows * G * 130 * 4;
+  if (per_split > 0) splits = (int)std::max<size_t>(1, std::min<size_t>(splits, part_budget_bytes / per_split));
+  p.tiles_per_split = (n_tiles + splits - 1) / splits;
+  p.splits = (n_tiles + p.tiles_per_split - 1) / p.tiles_per_split;
+  return p;
+}
+
+size_t attention_part_bytes(const AttnPlan& p, int n_rows, int Hq, int Hkv) {
+  const size_t n_qv = (size_t)n_rows * (Hq / Hkv);
+  return (size_t)p.splits * Hkv * n_qv * 130 * 4;
+}
+
+void attention(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_stride,
+               int n_rows, int Hq, int Hkv, int n_keys, int row_pos0, int mask_kind,
+               int mask_prompt_len, int mask_block, const AttnPlan& plan, float* o_part,
+               float* ml_part, void* out, float* xsum, int out_fmt, hipStream_t s) {
+  require(Hq % Hkv == 0, "attention needs Hq % Hkv == 0");
+  require(n_keys >= 1 && n_rows >= 1, "attention needs at least one query row and key");
+  const float scale = 1.0f / sqrtf(128.0f);
+  const size_t lds_kv = (size_t)2 * 8192 * 2;
+  const size_t lds = std::max(lds_kv, (size_t)plan.qw * 32 * 132 * 4);
+  const dim3 grid(plan.splits * Hkv, plan.qgroups);
+  const dim3 block(64 * plan.qw);
+#define DRT_ATTN(T, QW)                                                                         \
+  {                                                                                             \
+    auto fn = attn_split_kernel<T, QW>;                                                         \
+    static size_t granted = 0;                                                                  \
+    grant_lds((const void*)fn, lds, granted);                                                   \
+    hipLaunchKernelGGL(fn, grid, block, lds, s, (const T*)q, (const T*)kv_layer, kv_head_stride, \
+                       n_rows, Hq, Hkv, n_keys, row_pos0, mask_kind, mask_prompt_len,           \
+                       mask_block, plan.tiles_per_split, o_part, ml_part, scale);               \
+  }
+  if (bf16) {
+    if (plan.qw == 2) DRT_ATTN(__bf16, 2) else DRT_ATTN(__bf16, 4)
+  } else {
+    if (plan.qw == 2) DRT_ATTN(_Float16, 2) else DRT_ATTN(_Float16, 4)
+  }
+#undef DRT_ATTN
+  DRT_HIP(hipGetLastError());
+  const int64_t waves = (int64_t)n_rows * Hq;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s,
+                     o_part, ml_part, plan.splits, n_rows, Hq, Hkv, out, xsum, out_fmt);
+  DRT_HIP(hipGetLastError());
+}
+
+void kv_pack(bool kv_bf16, const void* k, const void* v, bool src_bf16, int n, int Hkv, int pos0,
+             void* kv_layer, int64_t kv_head_stride, hipStream_t s) {
+  const int64_t waves = (int64_t)n * Hkv;
+  const dim3 grid((unsigned)((waves + 3) / 4));
+  if (kv_bf16)
+    hipLaunchKernelGGL(kv_pack_kernel<__bf16>, grid, dim3(256), 0, s, k, v, (int)src_bf16, n, Hkv,
+                       pos0, (__bf16*)kv_layer, kv_head_stride);
+  else
+    hipLaunchKernelGGL(kv_pack_kernel<_Float16>, grid, dim3(256), 0, s, k, v, (int)src_bf16, n,
+                       Hkv, pos0, (_Float16*)kv_layer, kv_head_stride);
+  DRT_HIP(hipGetLastError());
+}
+
+}  // namespace drt

@@ -1,0 +1,73 @@
+// Shared device-side helpers for the gfx950 (CDNA4) kernels of the denoise step.
+//
+// Conventions used by every kernel in this library:
+//  * wave64; MFMA v_mfma_f32_32x32x16_{f16,bf16}: lane l supplies A row (l & 31)
+//    and B column (l & 31), each with 8 k-slots [8*(l>>5), 8*(l>>5)+8); the
+//    32x32 fp32 result leaves lane l holding column (l & 31) of rows
+//    8*(r>>2) + 4*(l>>5) + (r & 3) for r = 0..15.
+//  * Any permutation of the k-slots is harmless as long as A and B use the same
+//    one; the q4 and attention layouts below exploit that to make every lane's
+//    loads 16-byte contiguous and every wave instruction a contiguous 1 KiB.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#define DRT_DEV __device__ __forceinline__
+
+DRT_DEV f32x16 mfma_f16(const f16x8 a, const f16x8 b, const f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+DRT_DEV f32x16 mfma_bf16(const bf16x8 a, const bf16x8 b, const f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Row of the 32x32 MFMA result held in accumulator r by this lane.
+DRT_DEV int mfma_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+
+DRT_DEV float bf16_bits_to_float(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+// float -> bf16 bits, round to nearest even (NaN kept quiet).
+DRT_DEV uint16_t float_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+DRT_DEV float round_bf16(float f) { return bf16_bits_to_float(float_to_bf16_bits(f)); }
+
+DRT_DEV uint16_t half_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
+
+// Wave-level reductions (64 lanes) via cross-lane shuffles.
+DRT_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+DRT_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+DRT_DEV double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Activation formats written by producers and read by the linear kernels.
+enum ActFmt : int {
+  ACT_F16P = 0,  // fp16, each 8-chunk stored (0,4,1,5,2,6,3,7) + fp32 group sums
+  ACT_BF16 = 1,  // bf16, natural order (bf16-weight linears)
+};
+
+// Position of element k within an ACT_F16P row: chunk order (0,4,1,5,2,6,3,7).
+DRT_DEV int f16p_index(int k) {
+  const int j = k & 7;
+  return (k & ~7) | ((j & 3) << 1) | (j >> 2);
+}

@@ -1,0 +1,1053 @@
+// Runtime, device session and C-ABI of libdrt_rocm.so (see include/drt_rocm.h).
+//
+// A Runtime owns the model in device layouts (fused [q|k|v] and [gate|up]
+// linears, q4 tile32-g64 or bf16 tiles), the rotary tables, one HIP stream and
+// the forward workspace. A Session owns one request: the token canvas (host
+// mirror + device copy) and the exact prefix K/V cache.
+//
+// Exact prefix K/V (BD3, d2f_hybrid with block origin 0): the reference
+// recomputes the whole visible prefix x[:block_end] every denoise step
+// (backends/diffusion_runtime.py:1331-1334). Under the absolute block-causal
+// mask a row's K/V depend only on tokens of blocks <= its own, and a block's
+// tokens never change once its rounds end (:1314-1322). So the K/V of every
+// block before the active one is computed once, by one "commit" forward when
+// the policy first proposes past it, and reused by every later step; each
+// denoise step forwards only the active block's rows. This is the same math,
+// re-associated.
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/drt_rocm.h"
+#include "launch.h"
+
+namespace drt {
+
+thread_local std::string g_last_error;
+
+// ------------------------------------------------------------------ handles
+
+enum class Kind : int { RUNTIME = 1, SESSION = 2 };
+
+struct Runtime;
+struct Session;
+
+struct HandleTable {
+  std::mutex mu;
+  uint64_t next = 1;  // NULL_HANDLE = 0 is never issued
+  std::map<uint64_t, std::pair<Kind, std::shared_ptr<void>>> live;
+
+  uint64_t add(Kind k, std::shared_ptr<void> obj) {
+    std::lock_guard<std::mutex> g(mu);
+    const uint64_t h = next++;
+    live.emplace(h, std::make_pair(k, std::move(obj)));
+    return h;
+  }
+  template <typename T> std::shared_ptr<T> get(uint64_t h, Kind k) {
+    std::lock_guard<std::mutex> g(mu);
+    auto it = live.find(h);
+    if (it == live.end()) fail(INVALID_ARGUMENT, "handle " + std::to_string(h) + " is not live");
+    if (it->second.first != k)
+      fail(INVALID_ARGUMENT, "handle " + std::to_string(h) + " has another kind");
+    return std::static_pointer_cast<T>(it->second.second);
+  }
+  void release(uint64_t h) {
+    std::shared_ptr<void> keep;
+    {
+      std::lock_guard<std::mutex> g(mu);
+      auto it = live.find(h);
+      if (it == live.end())
+        fail(INVALID_ARGUMENT, "handle " + std::to_string(h) + " is not live; double release");
+      keep = std::move(it->second.second);
+      live.erase(it);
+    }
+    // `keep` is destroyed here, outside the lock (may free device memory).
+  }
+};
+
+HandleTable& handles() {
+  static HandleTable t;
+  return t;
+}
+
+// ------------------------------------------------------------------ runtime
+
+struct LayerW {
+  LinearW qkv, o, gu, down;
+  DevBuf in_norm, post_norm, q_norm, k_norm;
+};
+
+struct Runtime {
+  drt_engine_config engine{};
+  drt_model_geometry geo{};
+  bool q4 = false;
+  bool kv_bf16 = false;
+  int device = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  std::vector<LayerW> layers;
+  DevBuf embed;       // bf16 [V][d]
+  DevBuf final_norm;  // bf16 [d]
+  LinearW lm_head;
+  DevBuf rope_cos, rope_sin;  // fp32 [P][64]
+  int rope_positions = 0;
+  int max_rows = 0;
+
+  // workspace (sized for max_rows)
+  DevBuf hidden, act, xsum, act_lm, xsum_lm, part, qbuf, attn_part, stats, scores, tokens_out,
+      lm_rows, lm_pos, logits;
+  size_t part_bytes = 0, attn_part_budget = 0;
+  int logits_rows_cap = 0;
+
+  ~Runtime() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    if (ev0) (void)hipEventDestroy(ev0);
+    if (ev1) (void)hipEventDestroy(ev1);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+
+  int d() const { return geo.hidden_size; }
+  int Hq() const { return geo.num_heads; }
+  int Hkv() const { return geo.num_kv_heads; }
+  int F() const { return geo.intermediate_size; }
+  int V() const { return geo.vocab_size; }
+  int fmt() const { return q4 ? F16P : BF16; }
+};
+
+namespace {
+
+struct WeightMap {
+  std::map<std::string, const drt_tensor*> by_name;
+  const drt_tensor& get(const std::string& n) const {
+    auto it = by_name.find(n);
+    if (it == by_name.end()) fail(INVALID_ARGUMENT, "missing weight tensor '" + n + "'");
+    return *it->second;
+  }
+  bool has(const std::string& n) const { return by_name.count(n) != 0; }
+};
+
+void check_tensor(const drt_tensor& t, int dtype, std::initializer_list<int64_t> shape) {
+  const std::string n = t.name ? t.name : "?";
+  if (t.dtype != dtype) fail(INVALID_ARGUMENT, "tensor '" + n + "' has dtype " +
+                                                   std::to_string(t.dtype) + ", expected " +
+                                                   std::to_string(dtype));
+  if (t.ndim != (int)shape.size()) fail(INVALID_ARGUMENT, "tensor '" + n + "' has wrong rank");
+  int i = 0;
+  for (int64_t s : shape) {
+    if (t.shape[i] != s)
+      fail(INVALID_ARGUMENT, "tensor '" + n + "' dim " + std::to_string(i) + " is " +
+                                 std::to_string(t.shape[i]) + ", expected " + std::to_string(s));
+    ++i;
+  }
+  if (!t.data) fail(INVALID_ARGUMENT, "tensor '" + n + "' has a null data pointer");
+}
+
+void copy_bf16_vec(DevBuf& dst, const WeightMap& wm, const std::string& name, int n,
+                   hipStream_t s) {
+  const drt_tensor& t = wm.get(name);
+  check_tensor(t, DRT_BF16, {n});
+  dst.alloc((size_t)n * 2);
+  DRT_HIP(hipMemcpyAsync(dst.p, t.data, (size_t)n * 2, hipMemcpyDeviceToDevice, s));
+}
+
+// Build one fused linear from parts stacked along N (each part N_i rows, same K).
+void build_linear(LinearW& w, const WeightMap& wm, const std::vector<std::string>& parts,
+                  const std::vector<int>& Ns, int K, bool q4, bool with_bias, hipStream_t s) {
+  int N = 0;
+  for (int n : Ns) N += n;
+  w.N = N;
+  w.K = K;
+  w.q4 = q4;
+  if (q4) {
+    require(K % 64 == 0, "q4 linear in-dim must be a multiple of 64");
+    w.qw.alloc((size_t)N * K / 2);
+    w.sb.alloc((size_t)N * (K / 64) * 4);
+  } else {
+    w.wb.alloc((size_t)N * K * 2);
+  }
+  int n0 = 0;
+  for (size_t i = 0; i < parts.size(); ++i) {
+    const int n = Ns[i];
+    require(n % 32 == 0, "linear out-dim must be a multiple of 32");
+    if (q4) {
+      const drt_tensor& wq = wm.get(parts[i] + ".weight");
+      const drt_tensor& sc = wm.get(parts[i] + ".scales");
+      const drt_tensor& bi = wm.get(parts[i] + ".biases");
+      check_tensor(wq, DRT_I32, {n, K / 8});
+      check_tensor(sc, DRT_BF16, {n, K / 64});
+      check_tensor(bi, DRT_BF16, {n, K / 64});
+      // tile layout is n-tile major, so part i starts at n-tile n0/32
+      q4_repack((const uint32_t*)wq.data, (const uint16_t*)sc.data, (const uint16_t*)bi.data, n,
+                K, w.qw.as<uint32_t>() + (size_t)(n0 / 32) * (K / 64) * 256,
+                w.sb.as<uint32_t>() + (size_t)(n0 / 32) * (K / 64) * 32, s);
+    } else {
+      const drt_tensor& wt = wm.get(parts[i] + ".weight");
+      check_tensor(wt, DRT_BF16, {n, K});
+      bf16_repack((const uint16_t*)wt.data, n, K, w.wb.as<uint16_t>() + (size_t)n0 * K, s);
+    }
+    n0 += n;
+  }
+  if (with_bias) {
+    w.bias.alloc((size_t)N * 2);
+    n0 = 0;
+    for (size_t i = 0; i < parts.size(); ++i) {
+      const drt_tensor& b = wm.get(parts[i] + ".bias");
+      check_tensor(b, DRT_BF16, {Ns[i]});
+      DRT_HIP(hipMemcpyAsync(w.bias.as<uint16_t>() + n0, b.data, (size_t)Ns[i] * 2,
+                             hipMemcpyDeviceToDevice, s));
+      n0 += Ns[i];
+    }
+  }
+}
+
+}  // namespace
+
+std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_model_geometry& g,
+                                        const drt_tensor* ws, int nw) {
+  require(g.head_dim == 128, "head_dim must be 128");
+  require(g.layer_count >= 1 && g.hidden_size % 256 == 0 && g.hidden_size <= 3584,
+          "hidden_size must be a multiple of 256 and <= 3584");
+  require(g.num_heads >= 1 && g.num_kv_heads >= 1 && g.num_heads % g.num_kv_heads == 0,
+          "num_heads must be a multiple of num_kv_heads");
+  require(g.intermediate_size % 64 == 0, "intermediate_size must be a multiple of 64");
+  require(g.vocab_size % 64 == 0, "vocab_size must be a multiple of 64");
+  require(e.linear_quant_bits == 4 || e.linear_quant_bits == -1,
+          "linear_quant_bits must be 4 (q4 affine) or -1 (bf16 weights)");
+  if (e.linear_quant_bits == 4)
+    require(e.linear_quant_group_size == 64, "only group size 64 is supported");
+  if (e.layer0_kv_cache_enabled || e.prefix_kv_cache || e.block_kv_cache ||
+      e.d2f_exact_kv_cache || e.cross_request_cache || e.canvas_cache)
+    fail(UNSUPPORTED, "the fixed-quota denoise step admits no approximate or D2F caches");
+  require(e.kv_dtype == DRT_F16 || e.kv_dtype == DRT_BF16, "kv_dtype must be DRT_F16 or DRT_BF16");
+  require(e.max_forward_rows >= 32, "max_forward_rows must be >= 32");
+
+  auto rt = std::make_shared<Runtime>();
+  rt->engine = e;
+  rt->geo = g;
+  rt->q4 = e.linear_quant_bits == 4;
+  rt->kv_bf16 = e.kv_dtype == DRT_BF16;
+  rt->device = e.device_ordinal;
+  rt->max_rows = (e.max_forward_rows + 31) / 32 * 32;
+  DRT_HIP(hipSetDevice(rt->device));
+  DRT_HIP(hipStreamCreateWithFlags(&rt->stream, hipStreamNonBlocking));
+  DRT_HIP(hipEventCreate(&rt->ev0));
+  DRT_HIP(hipEventCreate(&rt->ev1));
+  hipStream_t s = rt->stream;
+
+  WeightMap wm;
+  for (int i = 0; i < nw; ++i) {
+    require(ws[i].name != nullptr, "weight tensor without a name");
+    wm.by_name[ws[i].name] = &ws[i];
+  }
+  const int d = g.hidden_size, hd = 128, Hq = g.num_heads, Hkv = g.num_kv_heads,
+            F = g.intermediate_size, V = g.vocab_size;
+  {
+    const drt_tensor& t = wm.get("model.embed_tokens.weight");
+    check_tensor(t, DRT_BF16, {V, d});
+    rt->embed.alloc((size_t)V * d * 2);
+    DRT_HIP(hipMemcpyAsync(rt->embed.p, t.data, (size_t)V * d * 2, hipMemcpyDeviceToDevice, s));
+  }
+  rt->layers.resize(g.layer_count);
+  for (int l = 0; l < g.layer_count; ++l) {
+    const std::string p = "model.layers." + std::to_string(l) + ".";
+    LayerW& L = rt->layers[l];
+    build_linear(L.qkv, wm,
+                 {p + "self_attn.q_proj", p + "self_attn.k_proj", p + "self_attn.v_proj"},
+                 {Hq * hd, Hkv * hd, Hkv * hd}, d, rt->q4, g.qkv_bias != 0, s);
+    build_linear(L.o, wm, {p + "self_attn.o_proj"}, {d}, Hq * hd, rt->q4, false, s);
+    build_linear(L.gu, wm, {p + "mlp.gate_proj", p + "mlp.up_proj"}, {F, F}, d, rt->q4, false, s);
+    build_linear(L.down, wm, {p + "mlp.down_proj"}, {d}, F, rt->q4, false, s);
+    copy_bf16_vec(L.in_norm, wm, p + "input_layernorm.weight", d, s);
+    copy_bf16_vec(L.post_norm, wm, p + "post_attention_layernorm.weight", d, s);
+    if (g.qk_norm) {
+      copy_bf16_vec(L.q_norm, wm, p + "self_attn.q_norm.weight", hd, s);
+      copy_bf16_vec(L.k_norm, wm, p + "self_attn.k_norm.weight", hd, s);
+    }
+  }
+  copy_bf16_vec(rt->final_norm, wm, "model.norm.weight", d, s);
+  build_linear(rt->lm_head, wm, {"lm_head"}, {V}, d, rt->q4, false, s);
+  {
+    const drt_tensor& c = wm.get("rope.cos");
+    const drt_tensor& sn = wm.get("rope.sin");
+    require(c.ndim == 2 && c.shape[1] == 64 && c.dtype == DRT_F32, "rope.cos must be F32 [P, 64]");
+    check_tensor(sn, DRT_F32, {c.shape[0], 64});
+    rt->rope_positions = (int)c.shape[0];
+    rt->rope_cos.alloc((size_t)c.shape[0] * 64 * 4);
+    rt->rope_sin.alloc((size_t)c.shape[0] * 64 * 4);
+    DRT_HIP(hipMemcpyAsync(rt->rope_cos.p, c.data, rt->rope_cos.bytes, hipMemcpyDeviceToDevice, s));
+    DRT_HIP(hipMemcpyAsync(rt->rope_sin.p, sn.data, rt->rope_sin.bytes, hipMemcpyDeviceToDevice, s));
+  }
+
+  // Workspace for up to max_rows rows per forward.
+  const int M = rt->max_rows;
+  const int widest = std::max({d, Hq * hd, F});
+  rt->hidden.alloc((size_t)M * d * 4);
+  rt->act.alloc((size_t)M * widest * 2);
+  rt->xsum.alloc((size_t)M * (widest / 64) * 4);
+  rt->qbuf.alloc((size_t)M * Hq * hd * 2);
+  // partials: the largest of any linear's plan at M rows or at 32 rows
+  size_t pb = 0;
+  for (int rows : {32, M}) {
+    for (const LinearW* w : {&rt->layers[0].qkv, &rt->layers[0].o, &rt->layers[0].gu,
+                             &rt->layers[0].down}) {
+      const SplitPlan sp = plan_linear(*w, rows);
+      pb = std::max(pb, (size_t)sp.splits * rows * w->N * 4);
+    }
+  }
+  rt->part_bytes = pb;
+  rt->part.alloc(pb);
+  rt->attn_part_budget = std::max<size_t>((size_t)64 << 20,
+                                          (size_t)Hkv * M * (Hq / Hkv) * 130 * 4);
+  rt->attn_part.alloc(rt->attn_part_budget);
+  const int lm_cap = M;  // LM rows per forward <= rows forwarded
+  rt->act_lm.alloc((size_t)lm_cap * d * 2);
+  rt->xsum_lm.alloc((size_t)lm_cap * (d / 64) * 4);
+  rt->stats.alloc(lmhead_stats_bytes(lm_cap, V));
+  rt->scores.alloc((size_t)lm_cap * 8);
+  rt->tokens_out.alloc((size_t)lm_cap * 4);
+  rt->lm_rows.alloc((size_t)lm_cap * 4);
+  rt->lm_pos.alloc((size_t)lm_cap * 4);
+  DRT_HIP(hipStreamSynchronize(s));
+  size_t total = rt->embed.bytes + rt->final_norm.bytes + rt->lm_head.qw.bytes +
+                 rt->lm_head.sb.bytes + rt->lm_head.wb.bytes + rt->hidden.bytes + rt->act.bytes +
+                 rt->part.bytes + rt->attn_part.bytes + rt->stats.bytes;
+  for (auto& L : rt->layers)
+    for (LinearW* w : {&L.qkv, &L.o, &L.gu, &L.down}) total += w->qw.bytes + w->sb.bytes + w->wb.bytes;
+  if (e.creation_memory_budget_bytes > 0 && (int64_t)total > e.creation_memory_budget_bytes)
+    fail(INVALID_ARGUMENT, "runtime needs " + std::to_string(total) +
+                               " device bytes, above creation_memory_budget_bytes");
+  return rt;
+}
+
+// ------------------------------------------------------------------ forward
+
+// One forward over canvas rows [row0, row0 + n_rows) (absolute positions),
+// attending keys [0, n_keys) of the session's cache. Writes every layer's K/V
+// for these rows into the cache. If n_lm > 0, runs the final norm + LM head on
+// the given row indices (relative to row0) and produces scores/tokens (and
+// logits when `logits` is non-null).
+struct ForwardArgs {
+  const int32_t* tokens_dev;  // device tokens of the whole canvas
+  int row0 = 0, n_rows = 0, n_keys = 0;
+  int mask_kind = 0, mask_prompt_len = 0, mask_block = 1;
+  int n_lm = 0;
+  std::vector<int32_t> lm_rows, lm_pos;  // host
+  float* logits = nullptr;               // device [n_lm][V] or null
+  float temperature = 0.f;
+  uint64_t seed = 0;
+  int step = 0;
+};
+
+void run_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_stride,
+                 const ForwardArgs& a) {
+  hipStream_t s = rt.stream;
+  const int M = a.n_rows, d = rt.d(), Hq = rt.Hq(), Hkv = rt.Hkv(), F = rt.F();
+  const int fmt = rt.fmt();
+  const bool rnd = !rt.q4;  // bf16 weights: linear outputs are bf16-rounded
+  const float eps = rt.geo.rms_norm_eps;
+  require(M >= 1 && M <= rt.max_rows, "forward rows exceed max_forward_rows");
+  require(a.row0 + M <= rt.rope_positions, "positions exceed the rotary table");
+  require(a.n_lm <= M, "more LM rows than forwarded rows");
+  float* hidden = rt.hidden.as<float>();
+  float* part = rt.part.as<float>();
+  float* xs = rt.xsum.as<float>();
+  // both cache dtypes are 2 bytes per element
+  auto kv_layer = [&](int l) { return (void*)((char*)kv + (size_t)l * layer_stride * 2); };
+
+  embed(a.tokens_dev + a.row0, rt.embed.as<uint16_t>(), hidden, M, d, s);
+  residual_norm(hidden, nullptr, 0, M, false, nullptr, false, rt.layers[0].in_norm.as<uint16_t>(),
+                eps, d, fmt, rt.act.p, xs, M, s);
+  const AttnPlan ap = plan_attention(M, Hq, Hkv, a.n_keys, rt.attn_part_budget);
+  const size_t apb = attention_part_bytes(ap, M, Hq, Hkv);
+  require(apb <= rt.attn_part.bytes, "attention partials exceed the workspace");
+  float* o_part = rt.attn_part.as<float>();
+  float* ml_part = o_part + (size_t)ap.splits * Hkv * M * (Hq / Hkv) * 128;
+  if (a.n_lm > 0) {
+    DRT_HIP(hipMemcpyAsync(rt.lm_rows.p, a.lm_rows.data(), a.n_lm * 4, hipMemcpyHostToDevice, s));
+    DRT_HIP(hipMemcpyAsync(rt.lm_pos.p, a.lm_pos.data(), a.n_lm * 4, hipMemcpyHostToDevice, s));
+  }
+  const int L = (int)rt.layers.size();
+  for (int l = 0; l < L; ++l) {
+    LayerW& w = rt.layers[l];
+    SplitPlan sp = plan_linear(w.qkv, M);
+    linear_partials(w.qkv, rt.act.p, xs, M, part, sp, s);
+    qkv_epilogue(rt.kv_bf16, part, sp.splits, M, w.qkv.bias.as<uint16_t>(), rnd,
+                 w.q_norm.as<uint16_t>(), w.k_norm.as<uint16_t>(), eps, rt.rope_cos.as<float>(),
+                 rt.rope_sin.as<float>(), a.row0, Hq, Hkv, rt.qbuf.p, kv_layer(l), head_stride, s);
+    attention(rt.kv_bf16, rt.qbuf.p, kv_layer(l), head_stride, M, Hq, Hkv, a.n_keys, a.row0,
+              a.mask_kind, a.mask_prompt_len, a.mask_block, ap, o_part, ml_part, rt.act.p, xs,
+              fmt, s);
+    const bool last = l == L - 1;
+    if (last && a.n_lm == 0) break;  // commit-only forward: every layer's K/V is written
+    sp = plan_linear(w.o, M);
+    linear_partials(w.o, rt.act.p, xs, M, part, sp, s);
+    residual_norm(hidden, part, sp.splits, M, rnd, nullptr, true, w.post_norm.as<uint16_t>(), eps,
+                  d, fmt, rt.act.p, xs, M, s);
+    sp = plan_linear(w.gu, M);
+    linear_partials(w.gu, rt.act.p, xs, M, part, sp, s);
+    swiglu(part, sp.splits, M, F, rnd, fmt, rt.act.p, xs, s);
+    sp = plan_linear(w.down, M);
+    linear_partials(w.down, rt.act.p, xs, M, part, sp, s);
+    if (!last) {
+      residual_norm(hidden, part, sp.splits, M, rnd, nullptr, true,
+                    rt.layers[l + 1].in_norm.as<uint16_t>(), eps, d, fmt, rt.act.p, xs, M, s);
+    } else {
+      residual_norm(hidden, part, sp.splits, M, rnd, rt.lm_rows.as<int32_t>(), false,
+                    rt.final_norm.as<uint16_t>(), eps, d, fmt, rt.act_lm.p, rt.xsum_lm.as<float>(),
+                    a.n_lm, s);
+    }
+  }
+  if (a.n_lm > 0) {
+    lmhead(rt.lm_head, rt.act_lm.p, rt.xsum_lm.as<float>(), a.n_lm, a.logits, rt.stats.p,
+           a.temperature, a.seed, a.step, rt.lm_pos.as<int32_t>(), rt.scores.as<double>(),
+           rt.tokens_out.as<int32_t>(), s);
+  }
+}
+
+// ------------------------------------------------------------------ session
+
+struct Session {
+  std::shared_ptr<Runtime> rt;
+  drt_session_config cfg{};
+  bool started = false;
+  std::vector<int32_t> canvas;
+  DevBuf tokens_dev;
+  DevBuf kv;
+  int tile_cap = 0;
+  int64_t head_stride = 0, layer_stride = 0;
+  int origin = 0, block = 32, mask_id = 0, steps = 0;
+  double temperature = 0.0;
+  uint64_t seed = 0;
+  int cache_len = 0;  // rows [0, cache_len) hold exact K/V of the current canvas
+  int proposals = 0;
+  // execute_window identity of the cached prefix
+  int win_prompt_len = -1, win_block = -1;
+  std::vector<int32_t> win_tokens;
+  drt_metrics m{};
+
+  // Grow the cache to hold n_tokens rows. Existing tiles keep their contents
+  // (copied head by head), so a longer window does not lose the exact prefix.
+  void ensure_cache(int n_tokens) {
+    const int want = std::max(n_tokens, cfg.max_tokens);
+    const int tiles = (want + 31) / 32;
+    if (tiles <= tile_cap) return;
+    const Runtime& r = *rt;
+    const int64_t new_head = (int64_t)tiles * 8192;
+    const size_t rows = r.layers.size() * (size_t)r.Hkv();
+    DevBuf grown;
+    grown.alloc(rows * new_head * 2);
+    // Zero once: partially filled tiles are multiplied by exactly-zero
+    // probabilities, and 0 * NaN from stale bits would poison the sums.
+    DRT_HIP(hipMemsetAsync(grown.p, 0, grown.bytes, r.stream));
+    if (kv.p && tile_cap > 0)
+      DRT_HIP(hipMemcpy2DAsync(grown.p, new_head * 2, kv.p, head_stride * 2, head_stride * 2,
+                               rows, hipMemcpyDeviceToDevice, r.stream));
+    DRT_HIP(hipStreamSynchronize(r.stream));
+    kv = std::move(grown);
+    tile_cap = tiles;
+    head_stride = new_head;
+    layer_stride = head_stride * r.Hkv();
+    m.kv_cache_bytes = (int64_t)kv.bytes;
+  }
+
+  void upload_tokens(int lo, int hi) {
+    if (hi <= lo) return;
+    DRT_HIP(hipMemcpyAsync(tokens_dev.as<int32_t>() + lo, canvas.data() + lo, (size_t)(hi - lo) * 4,
+                           hipMemcpyHostToDevice, rt->stream));
+  }
+
+  // d2f block start of position p under geometry (prompt_len, block).
+  static int seg_start(int p, int prompt_len, int blk) {
+    if (p < prompt_len) return 0;
+    return prompt_len + ((p - prompt_len) / blk) * blk;
+  }
+
+  // Commit forwards for rows [lo, hi): chunks end on block boundaries.
+  void commit_rows(int lo, int hi, int prompt_len, int blk) {
+    const Runtime& r = *rt;
+    int row = lo;
+    while (row < hi) {
+      int end = std::min(hi, row + r.max_rows);
+      if (end < hi) {
+        const int snapped = seg_start(end, prompt_len, blk);
+        require(snapped > row, "a mask segment is longer than max_forward_rows");
+        end = snapped;
+      }
+      ForwardArgs a;
+      a.tokens_dev = tokens_dev.as<int32_t>();
+      a.row0 = row;
+      a.n_rows = end - row;
+      a.n_keys = end;
+      a.mask_kind = 1;
+      a.mask_prompt_len = prompt_len;
+      a.mask_block = blk;
+      run_forward(*rt, kv.p, head_stride, layer_stride, a);
+      m.commit_rows += end - row;
+      row = end;
+    }
+  }
+
+  double finish_timing() {
+    Runtime& r = *rt;
+    DRT_HIP(hipEventSynchronize(r.ev1));
+    float ms = 0.f;
+    DRT_HIP(hipEventElapsedTime(&ms, r.ev0, r.ev1));
+    m.last_forward_ms = ms;
+    m.total_forward_ms += ms;
+    return ms;
+  }
+
+  int raw_row(int p) const {
+    if (rt->geo.logits_convention == DRT_LOGITS_DREAM_AR_SHIFT) return p >= 1 ? p - 1 : 0;
+    return p;
+  }
+};
+
+}  // namespace drt
+
+// ====================================================================== C-ABI
+
+using namespace drt;
+
+namespace {
+
+template <typename Fn> int32_t guarded(Fn&& fn) {
+  try {
+    fn();
+    return DRT_OK;
+  } catch (const Error& e) {
+    g_last_error = e.what();
+    return e.status;
+  } catch (const std::bad_alloc&) {
+    g_last_error = "host allocation failed";
+    return DRT_INTERNAL_ERROR;
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+    return DRT_INTERNAL_ERROR;
+  }
+}
+
+hipStream_t as_stream(void* s) { return (hipStream_t)s; }
+
+}  // namespace
+
+extern "C" {
+
+void drt_abi_version(int32_t* major, int32_t* minor, int32_t* patch) {
+  if (major) *major = 0;
+  if (minor) *minor = 1;
+  if (patch) *patch = 0;
+}
+
+size_t drt_last_error(char* buf, size_t len) {
+  const std::string& e = g_last_error;
+  if (buf && len) {
+    const size_t n = std::min(len - 1, e.size());
+    std::memcpy(buf, e.data(), n);
+    buf[n] = 0;
+  }
+  return e.size();
+}
+
+int32_t drt_release_handle(uint64_t handle) {
+  return guarded([&] { handles().release(handle); });
+}
+
+int32_t drt_runtime_create(const drt_engine_config* engine, const drt_model_geometry* geometry,
+                           const drt_tensor* weights, int32_t n_weights, uint64_t* out_runtime) {
+  return guarded([&] {
+    require(engine && geometry && weights && out_runtime && n_weights > 0,
+            "drt_runtime_create needs engine, geometry, weights and an output handle");
+    auto rt = create_runtime(*engine, *geometry, weights, n_weights);
+    *out_runtime = handles().add(Kind::RUNTIME, rt);
+  });
+}
+
+int32_t drt_session_open(uint64_t runtime, const drt_session_config* config,
+                         uint64_t* out_session) {
+  return guarded([&] {
+    require(config && out_session, "drt_session_open needs a config and an output handle");
+    auto rt = handles().get<Runtime>(runtime, Kind::RUNTIME);
+    const drt_session_config& c = *config;
+    const bool bd3 = c.decode_strategy == DRT_DECODE_BD3_FIXED_QUOTA;
+    const bool fq = c.decode_strategy == DRT_DECODE_FIXED_QUOTA;
+    const bool window_only = c.decode_strategy < 0;  // forward-only window session
+    if (!bd3 && !fq && !window_only)
+      fail(UNSUPPORTED, "rocm sessions run only fixed_quota and bd3_fixed_quota");
+    if (bd3) require(c.attention_mask_kind == DRT_MASK_D2F_HYBRID,
+                     "bd3_fixed_quota runs only on a d2f_hybrid graph");
+    if (fq) require(c.attention_mask_kind == DRT_MASK_BIDIRECTIONAL,
+                    "fixed_quota runs only on a bidirectional graph");
+    if (!window_only) require(c.commit_policy == DRT_COMMIT_FIXED_QUOTA,
+                              "fixed-quota strategies need the fixed_quota commit policy");
+    auto sess = std::make_shared<Session>();
+    sess->rt = rt;
+    sess->cfg = c;
+    DRT_HIP(hipSetDevice(rt->device));
+    *out_session = handles().add(Kind::SESSION, sess);
+  });
+}
+
+int32_t drt_session_start(uint64_t session, const int32_t* tokens, int32_t n_tokens,
+                          int32_t prompt_len, int32_t block_size, int32_t mask_token_id,
+                          int32_t exact_kv, int32_t steps, int64_t memory_budget_bytes,
+                          double temperature, uint64_t seed) {
+  return guarded([&] {
+    auto s = handles().get<Session>(session, Kind::SESSION);
+    Runtime& r = *s->rt;
+    require(tokens && n_tokens > 0, "start_device needs a non-empty canvas");
+    require(n_tokens <= r.rope_positions, "canvas longer than the rotary table");
+    require(block_size >= 1 && prompt_len >= 0 && prompt_len <= n_tokens, "bad block geometry");
+    require(steps >= 1, "steps must be >= 1");
+    require(!(temperature < 0.0) && std::isfinite(temperature), "temperature must be >= 0");
+    if (exact_kv) fail(UNSUPPORTED, "D2F exact K/V is not offered by the fixed-quota path");
+    if (s->cfg.attention_mask_kind == DRT_MASK_BIDIRECTIONAL)
+      require(n_tokens <= r.max_rows, "a bidirectional canvas must fit max_forward_rows");
+    for (int i = 0; i < n_tokens; ++i)
+      require(tokens[i] >= 0 && tokens[i] < r.V(), "token id outside the vocabulary");
+    DRT_HIP(hipSetDevice(r.device));
+    s->canvas.assign(tokens, tokens + n_tokens);
+    s->tokens_dev.ensure((size_t)n_tokens * 4);
+    s->ensure_cache(n_tokens);
+    s->cache_len = 0;  // a new request: nothing in the cache belongs to it yet
+    s->origin = prompt_len;
+    s->block = block_size;
+    s->mask_id = mask_token_id;
+    s->steps = steps;
+    s->temperature = temperature;
+    s->seed = seed;
+    s->proposals = 0;
+    s->win_prompt_len = -1;
+    s->started = true;
+    if (memory_budget_bytes > 0 && s->kv.bytes > (size_t)memory_budget_bytes)
+      fail(INVALID_ARGUMENT, "prefix K/V cache needs " + std::to_string(s->kv.bytes) +
+                                 " bytes, above memory_budget_bytes");
+    s->upload_tokens(0, n_tokens);
+    DRT_HIP(hipStreamSynchronize(r.stream));
+  });
+}
+
+int32_t drt_session_propose(uint64_t session, const int32_t* frontier, int32_t n_frontier,
+                            int32_t window_end, int32_t frozen_prefix, double* out_scores,
+                            int32_t* out_tokens, int32_t* out_forwarded_rows) {
+  return guarded([&] {
+    auto s = handles().get<Session>(session, Kind::SESSION);
+    Runtime& r = *s->rt;
+    require(s->started, "propose_device before start_device");
+    require(frontier && n_frontier > 0 && out_scores && out_tokens,
+            "propose_device needs a non-empty frontier and outputs");
+    const int n = (int)s->canvas.size();
+    DRT_HIP(hipSetDevice(r.device));
+    ForwardArgs a;
+    a.tokens_dev = s->tokens_dev.as<int32_t>();
+    a.temperature = (float)s->temperature;
+    a.seed = s->seed;
+    a.step = s->proposals;
+    int forwarded = 0;
+    if (s->cfg.attention_mask_kind == DRT_MASK_D2F_HYBRID) {
+      require(window_end >= 1 && window_end <= n, "window_end outside the canvas");
+      require(frozen_prefix >= 0 && frozen_prefix < window_end, "frozen_prefix outside the window");
+      require(Session::seg_start(frozen_prefix, s->origin, s->block) == frozen_prefix,
+              "frozen_prefix must start a block of the session geometry");
+      for (int i = 0; i < n_frontier; ++i) {
+        const int p = frontier[i];
+        require(p >= frozen_prefix && p < window_end,
+                "frontier position outside [frozen_prefix, window_end)");
+        const int rr = s->raw_row(p);
+        require(rr >= frozen_prefix, "frontier reads a row before frozen_prefix");
+      }
+      // An earlier frozen prefix shrinks the exact cache; a later one commits blocks.
+      if (s->cache_len > frozen_prefix) s->cache_len = frozen_prefix;
+      DRT_HIP(hipEventRecord(r.ev0, r.stream));
+      if (s->cache_len < frozen_prefix) {
+        s->upload_tokens(s->cache_len, frozen_prefix);
+        s->commit_rows(s->cache_len, frozen_prefix, s->origin, s->block);
+        forwarded += frozen_prefix - s->cache_len;
+        s->cache_len = frozen_prefix;
+      }
+      s->upload_tokens(frozen_prefix, window_end);
+      a.row0 = frozen_prefix;
+      a.n_rows = window_end - frozen_prefix;
+      a.n_keys = window_end;
+      a.mask_kind = 1;
+      a.mask_prompt_len = s->origin;
+      a.mask_block = s->block;
+    } else {
+      // Full bidirectional canvas, no cache (Dream / MDLM fixed_quota).
+      for (int i = 0; i < n_frontier; ++i)
+        require(frontier[i] >= 0 && frontier[i] < n, "frontier position outside the canvas");
+      DRT_HIP(hipEventRecord(r.ev0, r.stream));
+      s->upload_tokens(0, n);
+      a.row0 = 0;
+      a.n_rows = n;
+      a.n_keys = n;
+      a.mask_kind = 0;
+    }
+    a.n_lm = n_frontier;
+    for (int i = 0; i < n_frontier; ++i) {
+      a.lm_rows.push_back(s->raw_row(frontier[i]) - a.row0);
+      a.lm_pos.push_back(frontier[i]);
+    }
+    run_forward(r, s->kv.p, s->head_stride, s->layer_stride, a);
+    forwarded += a.n_rows;
+    DRT_HIP(hipEventRecord(r.ev1, r.stream));
+    DRT_HIP(hipMemcpyAsync(out_scores, r.scores.p, (size_t)n_frontier * 8, hipMemcpyDeviceToHost,
+                           r.stream));
+    DRT_HIP(hipMemcpyAsync(out_tokens, r.tokens_out.p, (size_t)n_frontier * 4,
+                           hipMemcpyDeviceToHost, r.stream));
+    DRT_HIP(hipStreamSynchronize(r.stream));
+    s->finish_timing();
+    s->proposals += 1;
+    s->m.forward_count += 1;
+    s->m.active_rows += a.n_rows;
+    s->m.lm_rows += n_frontier;
+    s->m.kv_cache_len = s->cache_len;
+    if (out_forwarded_rows) *out_forwarded_rows = forwarded;
+  });
+}
+
+int32_t drt_session_commit(uint64_t session, const int32_t* positions, const int32_t* tokens,
+                           int32_t n) {
+  return guarded([&] {
+    auto s = handles().get<Session>(session, Kind::SESSION);
+    require(s->started, "commit_device before start_device");
+    require(n >= 0 && (n == 0 || (positions && tokens)), "commit_device needs positions and tokens");
+    const int len = (int)s->canvas.size();
+    for (int i = 0; i < n; ++i) {
+      require(positions[i] >= 0 && positions[i] < len, "commit position outside the canvas");
+      require(positions[i] >= s->cache_len,
+              "commit position inside the committed prefix K/V (a frozen block)");
+      require(tokens[i] >= 0 && tokens[i] < s->rt->V(), "commit token outside the vocabulary");
+    }
+    for (int i = 0; i < n; ++i) s->canvas[positions[i]] = tokens[i];
+  });
+}
+
+int32_t drt_session_execute_window(uint64_t session, const int32_t* token_ids, int32_t n_tokens,
+                                   const int32_t* scope, int32_t n_scope,
+                                   int32_t mask_prompt_len, int32_t mask_block_size,
+                                   float* out_logits, int64_t out_capacity,
+                                   int32_t* out_n_vocab, int32_t* out_forwarded_rows) {
+  return guarded([&] {
+    auto s = handles().get<Session>(session, Kind::SESSION);
+    Runtime& r = *s->rt;
+    require(token_ids && n_tokens > 0 && scope && n_scope > 0 && out_logits,
+            "execute_window needs tokens, a non-empty scope and an output buffer");
+    require((int64_t)n_scope * r.V() <= out_capacity, "execute_window output buffer too small");
+    require(n_tokens <= r.rope_positions, "window longer than the rotary table");
+    for (int i = 0; i < n_tokens; ++i)
+      require(token_ids[i] >= 0 && token_ids[i] < r.V(), "token id outside the vocabulary");
+    for (int i = 0; i < n_scope; ++i)
+      require(scope[i] >= 0 && scope[i] < n_tokens, "scope position outside the window");
+    const bool d2f = mask_block_size > 0;
+    if (s->cfg.attention_mask_kind == DRT_MASK_D2F_HYBRID)
+      require(d2f, "a d2f_hybrid session needs the window's mask geometry");
+    else
+      require(!d2f, "mask geometry is only consumed by the d2f_hybrid kind");
+    DRT_HIP(hipSetDevice(r.device));
+    // The window replaces the session canvas.
+    const int old_n = (int)s->canvas.size();
+    s->canvas.assign(token_ids, token_ids + n_tokens);
+    if ((size_t)n_tokens * 4 > s->tokens_dev.bytes) {
+      DevBuf t;
+      t.alloc((size_t)std::max(n_tokens, s->cfg.max_tokens) * 4);
+      s->tokens_dev = std::move(t);  // rows below the reuse point are never re-read
+    }
+    s->ensure_cache(n_tokens);
+    (void)old_n;
+    ForwardArgs a;
+    a.tokens_dev = s->tokens_dev.as<int32_t>();
+    int forwarded = 0;
+    int min_raw = n_tokens;
+    for (int i = 0; i < n_scope; ++i) min_raw = std::min(min_raw, s->raw_row(scope[i]));
+    DRT_HIP(hipEventRecord(r.ev0, r.stream));
+    if (d2f) {
+      require(mask_prompt_len >= 0 && mask_prompt_len <= n_tokens, "bad mask geometry");
+      const int frozen = Session::seg_start(min_raw, mask_prompt_len, mask_block_size);
+      // Reuse the cached exact prefix only for the same geometry and tokens.
+      int valid = 0;
+      if (s->win_prompt_len == mask_prompt_len && s->win_block == mask_block_size) {
+        const int lim = std::min({s->cache_len, frozen, (int)s->win_tokens.size()});
+        while (valid < lim && s->win_tokens[valid] == token_ids[valid]) ++valid;
+        valid = valid < mask_prompt_len ? 0 : Session::seg_start(valid, mask_prompt_len, mask_block_size);
+        if (valid > lim) valid = 0;
+      }
+      s->cache_len = valid;
+      if (valid < frozen) {
+        s->upload_tokens(valid, frozen);
+        s->commit_rows(valid, frozen, mask_prompt_len, mask_block_size);
+        forwarded += frozen - valid;
+      }
+      s->cache_len = frozen;
+      s->win_prompt_len = mask_prompt_len;
+      s->win_block = mask_block_size;
+      s->win_tokens.assign(token_ids, token_ids + frozen);
+      s->upload_tokens(frozen, n_tokens);
+      a.row0 = frozen;
+      a.n_rows = n_tokens - frozen;
+      a.n_keys = n_tokens;
+      a.mask_kind = 1;
+      a.mask_prompt_len = mask_prompt_len;
+      a.mask_block = mask_block_size;
+    } else {
+      require(n_tokens <= r.max_rows, "a bidirectional window must fit max_forward_rows");
+      s->upload_tokens(0, n_tokens);
+      a.row0 = 0;
+      a.n_rows = n_tokens;
+      a.n_keys = n_tokens;
+      a.mask_kind = 0;
+      s->cache_len = 0;
+    }
+    a.n_lm = n_scope;
+    for (int i = 0; i < n_scope; ++i) {
+      a.lm_rows.push_back(s->raw_row(scope[i]) - a.row0);
+      a.lm_pos.push_back(scope[i]);
+    }
+    require(a.n_rows <= r.max_rows, "the active window exceeds max_forward_rows");
+    s->rt->logits.ensure((size_t)n_scope * r.V() * 4);
+    a.logits = r.logits.as<float>();
+    run_forward(r, s->kv.p, s->head_stride, s->layer_stride, a);
+    forwarded += a.n_rows;
+    DRT_HIP(hipEventRecord(r.ev1, r.stream));
+    DRT_HIP(hipMemcpyAsync(out_logits, r.logits.p, (size_t)n_scope * r.V() * 4,
+                           hipMemcpyDeviceToHost, r.stream));
+    DRT_HIP(hipStreamSynchronize(r.stream));
+    s->finish_timing();
+    s->m.forward_count += 1;
+    s->m.active_rows += a.n_rows;
+    s->m.lm_rows += n_scope;
+    s->m.kv_cache_len = s->cache_len;
+    if (out_n_vocab) *out_n_vocab = r.V();
+    if (out_forwarded_rows) *out_forwarded_rows = forwarded;
+  });
+}
+
+int32_t drt_session_metrics(uint64_t session, drt_metrics* out) {
+  return guarded([&] {
+    require(out != nullptr, "drt_session_metrics needs an output struct");
+    auto s = handles().get<Session>(session, Kind::SESSION);
+    *out = s->m;
+  });
+}
+
+// ------------------------------------------------------------------ per-op
+
+size_t drt_op_q4_linear_workspace_bytes(int32_t m, int32_t n, int32_t k) {
+  LinearW w;
+  w.N = n;
+  w.K = k;
+  w.q4 = true;
+  const SplitPlan p = plan_linear(w, m);
+  return (size_t)m * k * 2 + (size_t)m * (k / 64) * 4 + (size_t)p.splits * m * n * 4 + 256;
+}
+
+int32_t drt_op_q4_repack(const void* w_q, const void* scales, const void* biases, int32_t n,
+                         int32_t k, void* qw, void* sb, void* stream) {
+  return guarded([&] {
+    require(w_q && scales && biases && qw && sb && n > 0 && k > 0, "bad q4_repack arguments");
+    q4_repack((const uint32_t*)w_q, (const uint16_t*)scales, (const uint16_t*)biases, n, k,
+              (uint32_t*)qw, (uint32_t*)sb, as_stream(stream));
+  });
+}
+
+int32_t drt_op_q4_linear(const void* qw, const void* sb, const void* x, int32_t x_dtype,
+                         int32_t m, int32_t n, int32_t k, const void* bias, float* y,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  return guarded([&] {
+    require(qw && sb && x && y && m > 0 && n > 0 && k > 0, "bad q4_linear arguments");
+    require(n % 32 == 0 && k % 64 == 0, "q4_linear needs n % 32 == 0 and k % 64 == 0");
+    require(x_dtype == DRT_F32 || x_dtype == DRT_BF16, "q4_linear x must be F32 or BF16");
+    require(workspace && workspace_bytes >= drt_op_q4_linear_workspace_bytes(m, n, k),
+            "q4_linear workspace too small");
+    LinearW w;
+    w.N = n;
+    w.K = k;
+    w.q4 = true;
+    w.qw.p = const_cast<void*>(qw);
+    w.sb.p = const_cast<void*>(sb);
+    const SplitPlan p = plan_linear(w, m);
+    char* ws = (char*)workspace;
+    _Float16* xp = (_Float16*)ws;
+    float* xs = (float*)(ws + (size_t)m * k * 2);
+    float* part = (float*)(ws + (size_t)m * k * 2 + (size_t)m * (k / 64) * 4);
+    hipStream_t st = as_stream(stream);
+    try {
+      q4_act_prep(x, x_dtype == DRT_BF16, m, k, xp, xs, st);
+      linear_partials(w, xp, xs, m, part, p, st);
+      splitk_reduce(part, p.splits, (const uint16_t*)bias, y, m, n, st);
+    } catch (...) {
+      w.qw.p = nullptr;
+      w.sb.p = nullptr;
+      throw;
+    }
+    w.qw.p = nullptr;  // borrowed
+    w.sb.p = nullptr;
+  });
+}
+
+int32_t drt_op_bf16_repack(const void* w, int32_t n, int32_t k, void* wb, void* stream) {
+  return guarded([&] {
+    require(w && wb && n > 0 && k > 0, "bad bf16_repack arguments");
+    bf16_repack((const uint16_t*)w, n, k, (uint16_t*)wb, as_stream(stream));
+  });
+}
+
+size_t drt_op_bf16_linear_workspace_bytes(int32_t m, int32_t n, int32_t k) {
+  LinearW w;
+  w.N = n;
+  w.K = k;
+  w.q4 = false;
+  const SplitPlan p = plan_linear(w, m);
+  return (size_t)p.splits * m * n * 4 + 256;
+}
+
+int32_t drt_op_bf16_linear(const void* wb, const void* x, int32_t m, int32_t n, int32_t k,
+                           const void* bias, float* y, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  return guarded([&] {
+    require(wb && x && y && m > 0 && n > 0 && k > 0, "bad bf16_linear arguments");
+    require(n % 32 == 0 && k % 16 == 0, "bf16_linear needs n % 32 == 0 and k % 16 == 0");
+    require(workspace && workspace_bytes >= drt_op_bf16_linear_workspace_bytes(m, n, k),
+            "bf16_linear workspace too small");
+    LinearW w;
+    w.N = n;
+    w.K = k;
+    w.q4 = false;
+    const SplitPlan p = plan_linear(w, m);
+    hipStream_t st = as_stream(stream);
+    bf16_linear_partials((const uint16_t*)wb, (const uint16_t*)x, m, n, k, (float*)workspace,
+                         p.splits, p.per_split, st);
+    // reduce, then round to bf16 as the bf16 matmul output is (bias added after)
+    const int64_t total = (int64_t)m * n;
+    splitk_reduce((const float*)workspace, p.splits, nullptr, y, m, n, st);
+    round_bf16_inplace(y, total, (const uint16_t*)bias, n, st);
+  });
+}
+
+int32_t drt_op_kv_pack(const void* k, const void* v, int32_t src_dtype, int32_t n, int32_t hkv,
+                       int32_t pos0, void* cache, int64_t head_stride, int32_t kv_dtype,
+                       void* stream) {
+  return guarded([&] {
+    require(k && v && cache && n > 0 && hkv > 0 && pos0 >= 0, "bad kv_pack arguments");
+    require(src_dtype == DRT_F32 || src_dtype == DRT_BF16, "kv_pack source must be F32 or BF16");
+    require(kv_dtype == DRT_F16 || kv_dtype == DRT_BF16, "kv_pack cache must be F16 or BF16");
+    require(head_stride >= (int64_t)((pos0 + n + 31) / 32) * 8192,
+            "kv_pack positions exceed the cache head stride");
+    kv_pack(kv_dtype == DRT_BF16, k, v, src_dtype == DRT_BF16, n, hkv, pos0, cache, head_stride,
+            as_stream(stream));
+  });
+}
+
+size_t drt_op_attention_workspace_bytes(int32_t rows, int32_t hq, int32_t hkv, int32_t n_keys) {
+  if (rows <= 0 || hq <= 0 || hkv <= 0 || hq % hkv || n_keys <= 0) return 0;
+  const AttnPlan p = plan_attention(rows, hq, hkv, n_keys, (size_t)256 << 20);
+  return attention_part_bytes(p, rows, hq, hkv) + (size_t)rows * hq * 128 * 2 + 256;
+}
+
+int32_t drt_op_attention(const void* q, const void* cache, int64_t head_stride, int32_t kv_dtype,
+                         int32_t rows, int32_t hq, int32_t hkv, int32_t n_keys, int32_t row_pos0,
+                         int32_t mask_kind, int32_t mask_prompt_len, int32_t mask_block_size,
+                         void* out, int32_t out_dtype, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+  return guarded([&] {
+    require(q && cache && out && rows > 0 && hq > 0 && hkv > 0 && hq % hkv == 0 && n_keys > 0,
+            "bad attention arguments");
+    require(kv_dtype == DRT_F16 || kv_dtype == DRT_BF16, "attention cache must be F16 or BF16");
+    require(out_dtype == DRT_F32 || out_dtype == DRT_BF16, "attention out must be F32 or BF16");
+    require(mask_kind == DRT_MASK_BIDIRECTIONAL || mask_kind == DRT_MASK_D2F_HYBRID,
+            "attention mask kind must be bidirectional or d2f_hybrid");
+    if (mask_kind == DRT_MASK_D2F_HYBRID)
+      require(mask_block_size >= 1 && mask_prompt_len >= 0, "d2f_hybrid needs a mask geometry");
+    require(head_stride >= (int64_t)((n_keys + 31) / 32) * 8192, "n_keys exceed the cache");
+    require(workspace && workspace_bytes >= drt_op_attention_workspace_bytes(rows, hq, hkv, n_keys),
+            "attention workspace too small");
+    const AttnPlan p = plan_attention(rows, hq, hkv, n_keys, (size_t)256 << 20);
+    float* o_part = (float*)workspace;
+    float* ml_part = o_part + (size_t)p.splits * hkv * rows * (hq / hkv) * 128;
+    attention(kv_dtype == DRT_BF16, q, cache, head_stride, rows, hq, hkv, n_keys, row_pos0,
+              mask_kind == DRT_MASK_D2F_HYBRID ? 1 : 0, mask_prompt_len,
+              std::max(1, mask_block_size), p, o_part, ml_part, out, nullptr,
+              out_dtype == DRT_F32 ? 2 : 3, as_stream(stream));
+  });
+}
+
+int32_t drt_op_rms_norm(const float* x, const void* weight, float eps, float* y, int32_t rows,
+                        int32_t d, void* stream) {
+  return guarded([&] {
+    require(x && weight && y && rows > 0 && d > 0, "bad rms_norm arguments");
+    rms_norm_rows(x, (const uint16_t*)weight, eps, y, rows, d, as_stream(stream));
+  });
+}
+
+int32_t drt_op_rope(const float* x, const float* cos_t, const float* sin_t, float* y,
+                    int32_t rows, int32_t h, int32_t hd, void* stream) {
+  return guarded([&] {
+    require(x && cos_t && sin_t && y && rows > 0 && h > 0 && hd > 0 && hd % 2 == 0,
+            "bad rope arguments");
+    rope_rows(x, cos_t, sin_t, y, rows, h, hd, as_stream(stream));
+  });
+}
+
+int32_t drt_op_swiglu(const float* gate, const float* up, float* y, int64_t n, void* stream) {
+  return guarded([&] {
+    require(gate && up && y && n > 0, "bad swiglu arguments");
+    swiglu_rows(gate, up, y, n, as_stream(stream));
+  });
+}
+
+size_t drt_op_lm_head_workspace_bytes(int32_t rows, int32_t n, int32_t k) {
+  if (rows <= 0 || n <= 0 || k <= 0) return 0;
+  return (size_t)rows * k * 2 + (size_t)rows * (k / 64) * 4 + lmhead_stats_bytes(rows, n) + 512;
+}
+
+int32_t drt_op_lm_head_score(const void* qw, const void* sb, const void* wb, int32_t rows,
+                             int32_t n, int32_t k, const float* x, float temperature,
+                             uint64_t seed, int32_t step, const int32_t* positions,
+                             double* scores, int32_t* tokens, float* logits, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  return guarded([&] {
+    const bool q4 = qw && sb;
+    require(q4 || wb, "lm_head needs q4 (qw, sb) or bf16 (wb) weights");
+    require(x && scores && tokens && rows > 0 && n > 0 && k > 0, "bad lm_head arguments");
+    require(n % 64 == 0 && k % 64 == 0, "lm_head needs n % 64 == 0 and k % 64 == 0");
+    require(!(temperature > 0.f) || positions, "sampling needs positions");
+    require(workspace && workspace_bytes >= drt_op_lm_head_workspace_bytes(rows, n, k),
+            "lm_head workspace too small");
+    LinearW w;
+    w.N = n;
+    w.K = k;
+    w.q4 = q4;
+    if (q4) {
+      w.qw.p = const_cast<void*>(qw);
+      w.sb.p = const_cast<void*>(sb);
+    } else {
+      w.wb.p = const_cast<void*>(wb);
+    }
+    char* ws = (char*)workspace;
+    void* act = ws;
+    float* xs = (float*)(ws + (size_t)rows * k * 2);
+    void* stats = ws + (size_t)rows * k * 2 + (size_t)rows * (k / 64) * 4;
+    stats = (void*)(((uintptr_t)stats + 255) & ~(uintptr_t)255);
+    hipStream_t st = as_stream(stream);
+    auto release = [&] { w.qw.p = nullptr; w.sb.p = nullptr; w.wb.p = nullptr; };
+    try {
+      if (q4) q4_act_prep(x, false, rows, k, (_Float16*)act, xs, st);
+      else to_bf16(x, (uint16_t*)act, (int64_t)rows * k, st);
+      lmhead(w, act, xs, rows, logits, stats, temperature, seed, step, positions, scores, tokens,
+             st);
+    } catch (...) {
+      release();
+      throw;
+    }
+    release();
+  });
+}
+
+}  // extern "C"

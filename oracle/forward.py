@@ -1,0 +1,106 @@
+"""Full-context transformer forward, restated on the CPU (oracle; test-only).
+
+Restates the full-context branch of ``_forward_full_logits_from_weights``
+(``backends/mlx_forward.py:235-636``) with ``_transformer_layer_forward``
+(``:1164-1309``), ``_project_kv_rows`` (``:1312-1361``), ``_embedding_rows``
+(``:1538-1557``) and ``_rope_tables`` (``:1566-1595``). Every visible row is
+recomputed every call, as the reference does each denoise step; the LM head runs
+only on ``output_rows`` (``:578-601``).
+
+``weights`` is a dict keyed by the reference's package weight names
+(``model.layers.{i}.self_attn.q_proj.weight`` ...). A linear weight is either a
+float32 array holding bf16 values (``weight_kind="bf16"``) or an
+:class:`oracle.ops.Q4Weight` (``weight_kind="q4"``).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import ops
+
+
+def _lin(weights, key, x, kind):
+    w = weights[key + ".weight"]
+    b = weights.get(key + ".bias")
+    return ops.linear(x, w, b, weight_kind=kind)
+
+
+def layer_forward(weights, cfg, i, hidden, cos, sin, visible, kv_hook=None):
+    """One decoder layer over all rows of ``hidden`` (fp32 ``[S, d]``).
+
+    ``h += o(attn(rope(qnorm(q(n))), rope(knorm(k(n))), v(n)))`` with
+    ``n = rmsnorm(h)``, then ``h += down(swiglu(gate(n2), up(n2)))`` with
+    ``n2 = rmsnorm(h)`` (``mlx_forward.py:1164-1309``; op order fixed by
+    ``graph/ir.py:106``).
+    """
+    kind = cfg["weight_kind"]
+    eps = cfg["eps"]
+    hq, hkv, hd = cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"]
+    p = f"model.layers.{i}."
+    s = hidden.shape[0]
+    n = ops.rms_norm(hidden, weights[p + "input_layernorm.weight"], eps)
+    q = _lin(weights, p + "self_attn.q_proj", n, kind).reshape(s, hq, hd)
+    if cfg["qk_norm"]:
+        q = ops.rms_norm(q, weights[p + "self_attn.q_norm.weight"], eps)
+    q = ops.apply_split_half_rope(q, cos, sin)
+    k = _lin(weights, p + "self_attn.k_proj", n, kind).reshape(s, hkv, hd)
+    v = _lin(weights, p + "self_attn.v_proj", n, kind).reshape(s, hkv, hd)
+    if cfg["qk_norm"]:
+        k = ops.rms_norm(k, weights[p + "self_attn.k_norm.weight"], eps)
+    k = ops.apply_split_half_rope(k, cos, sin)
+    if kv_hook is not None:
+        kv_hook(i, k, v)
+    attn = ops.attention(q, k, v, visible=visible, dtype=np.float32).astype(np.float32)
+    hidden = (hidden + _lin(weights, p + "self_attn.o_proj", attn, kind)).astype(np.float32)
+    n2 = ops.rms_norm(hidden, weights[p + "post_attention_layernorm.weight"], eps)
+    gate = _lin(weights, p + "mlp.gate_proj", n2, kind)
+    up = _lin(weights, p + "mlp.up_proj", n2, kind)
+    mlp = _lin(weights, p + "mlp.down_proj", ops.swiglu(gate, up), kind)
+    return (hidden + mlp).astype(np.float32)
+
+
+def forward_full(weights, cfg, token_ids, *, mask_kind, mask_geometry=None,
+                 output_rows=None, n_layers=None, kv_hook=None):
+    """Raw fp32 logits for ``output_rows`` (default: every row) of ``token_ids``.
+
+    ``mask_kind`` is ``"d2f_hybrid"`` (``mask_geometry = (prompt_len,
+    block_size)``; BD3 uses origin 0) or ``"bidirectional"`` (Dream, no mask).
+    ``n_layers`` limits the layer count (the CPU baseline's bounded sample).
+    """
+    ids = np.asarray(token_ids, dtype=np.int64)
+    s = ids.shape[0]
+    emb = weights["model.embed_tokens.weight"]
+    hidden = np.asarray(emb[ids], dtype=np.float32)
+    cos, sin = ops.rope_tables(np.arange(s), cfg["head_dim"], cfg["rope_theta"])
+    if mask_kind == "d2f_hybrid":
+        prompt_len, block_size = mask_geometry
+        visible = ops.d2f_visible(np.arange(s), s, prompt_len=prompt_len,
+                                  block_size=block_size)
+    elif mask_kind == "bidirectional":
+        visible = None
+    else:
+        raise ValueError(f"unsupported mask kind {mask_kind!r}")
+    layers = cfg["n_layers"] if n_layers is None else n_layers
+    for i in range(layers):
+        hidden = layer_forward(weights, cfg, i, hidden, cos, sin, visible, kv_hook)
+    rows = list(range(s)) if output_rows is None else [int(r) for r in output_rows]
+    h = hidden[rows]
+    h = ops.rms_norm(h, weights["model.norm.weight"], cfg["eps"])
+    logits = ops.linear(h, weights["lm_head.weight"], None, weight_kind=cfg["weight_kind"])
+    return logits.astype(np.float32)
+
+
+def window_logits(weights, cfg, token_ids, scope, *, mask_kind, mask_geometry,
+                  logits_convention):
+    """Convention-applied logits for ``scope`` positions (``execute_window``).
+
+    Raw row selection per ``_required_raw_row`` (``mlx_d2f_forward.py:74-93``);
+    rows are returned in ``scope`` order (``backend_runner.py:385-390``).
+    """
+    raw_rows = [ops.required_raw_row(int(p), logits_convention=logits_convention)
+                for p in scope]
+    uniq = sorted(set(raw_rows))
+    logits = forward_full(weights, cfg, token_ids, mask_kind=mask_kind,
+                          mask_geometry=mask_geometry, output_rows=uniq)
+    index = {r: j for j, r in enumerate(uniq)}
+    return logits[[index[r] for r in raw_rows]]

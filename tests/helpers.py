@@ -1,0 +1,90 @@
+"""Shared test helpers: oracle views of synthetic models, tolerances, tie reports."""
+from __future__ import annotations
+
+import numpy as np
+
+from diffusorrt_amd import synthetic as syn
+from oracle import ops as O
+
+# Tolerances stated once (see DESIGN.md "Parity bars").
+LOGITS_REL_TOL = 2e-2      # north-star bar for logits (relative to the row's max |logit|)
+NEAR_TIE_REL = 1e-3        # confidences within this relative gap are reported ties
+
+
+def oracle_weights(model: syn.SyntheticModel) -> dict:
+    out = {}
+    for key, value in syn.to_oracle_weights(model).items():
+        out[key] = O.Q4Weight(*value) if isinstance(value, tuple) else value
+    return out
+
+
+def tiny_geometry(**kw) -> syn.ModelGeometry:
+    """A small model with the BD3 layout (qk-norm, GQA 2:1, head_dim 128)."""
+    base = dict(name="tiny-bd3", layer_count=2, hidden_size=256, num_heads=4, num_kv_heads=2,
+                head_dim=128, intermediate_size=512, vocab_size=1024, rms_norm_eps=1e-6,
+                rope_theta=1e6, qk_norm=True, qkv_bias=False, logits_convention="raw",
+                mask_token_id=1000, eos_token_id=1001, tie_word_embeddings=True,
+                max_position_embeddings=4096)
+    base.update(kw)
+    return syn.ModelGeometry(**base)
+
+
+def tiny_dream_geometry(**kw) -> syn.ModelGeometry:
+    base = dict(name="tiny-dream", layer_count=2, hidden_size=256, num_heads=4,
+                num_kv_heads=1, head_dim=128, intermediate_size=512, vocab_size=1024,
+                rms_norm_eps=1e-6, rope_theta=1e6, qk_norm=False, qkv_bias=True,
+                logits_convention="dream_ar_shift", mask_token_id=1000, eos_token_id=1001,
+                tie_word_embeddings=False, max_position_embeddings=4096)
+    base.update(kw)
+    return syn.ModelGeometry(**base)
+
+
+def rel_err_rows(got, ref) -> np.ndarray:
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    return np.abs(got - ref).max(axis=-1) / np.maximum(np.abs(ref).max(axis=-1), 1e-30)
+
+
+def bf16_ulp(v) -> np.ndarray:
+    """Spacing of bf16 values at magnitude |v| (8 significant bits)."""
+    a = np.maximum(np.abs(np.asarray(v, dtype=np.float64)), 1e-30)
+    return 2.0 ** (np.floor(np.log2(a)) - 7)
+
+
+def compare_proposals(gpu_scores, gpu_tokens, ref_logits, *, quota=None, gpu_chosen=None,
+                      bf16_logits=False):
+    """Token / score / chosen-row parity of one step against oracle logits.
+
+    Returns (report, problems). A disagreement is a reported near-tie when the
+    oracle's own margin is within the tie band, else a problem:
+      * fp32 logits (q4 weights): relative probability gap <= NEAR_TIE_REL (1e-3);
+      * bf16 logits (bf16 weights; the reference rounds its logits to bf16):
+        margins within 2 bf16 ulps of the row's max logit, the resolution at
+        which the reference's own logits exist."""
+    ref_logits = np.asarray(ref_logits, dtype=np.float64)
+    ref_scores, ref_tokens = O.raw_max_prob(ref_logits)
+    report, problems = [], []
+    srt = np.sort(ref_logits, axis=-1)
+    top = srt[:, -1]
+    for r, (gt, rt) in enumerate(zip(gpu_tokens, ref_tokens)):
+        if gt != rt:
+            margin = srt[r, -1] - srt[r, -2]
+            if bf16_logits:
+                tie = margin <= 2 * bf16_ulp(top[r])
+            else:
+                tie = 1.0 - np.exp(-margin) <= NEAR_TIE_REL  # relative probability gap
+            (report if tie else problems).append(("token", r, int(gt), int(rt), float(margin)))
+    rel = np.abs(np.asarray(gpu_scores) - ref_scores) / ref_scores
+    if quota is not None and gpu_chosen is not None:
+        ref_chosen = O.topk_count_choices(ref_scores, quota)
+        if sorted(ref_chosen) != sorted(gpu_chosen):
+            idx = np.argsort(-ref_scores)
+            if quota < len(idx):
+                a, b = idx[quota - 1], idx[quota]
+                gap = (ref_scores[a] - ref_scores[b]) / ref_scores[a]
+                band = 2 * float(bf16_ulp(max(top[a], top[b]))) if bf16_logits else NEAR_TIE_REL
+            else:
+                gap, band = 1.0, 0.0
+            (report if gap <= band else problems).append(
+                ("chosen", tuple(sorted(gpu_chosen)), tuple(sorted(ref_chosen)), float(gap)))
+    return {"score_rel_max": float(rel.max()), "report": report}, problems

@@ -1,0 +1,260 @@
+"""GPU parity of the per-op kernels against the oracle (configs 2 and 3 shapes).
+
+Each test prints the case it runs before touching the GPU.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import ops as O
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print("[case]", *a, flush=True)
+
+
+def _q4_case(n, k, seed, centred=False):
+    from diffusorrt_amd import synthetic as syn
+
+    gen = torch.Generator().manual_seed(seed)
+    q = syn.random_q4(gen, n, k, scale_lo=0.005, scale_hi=0.02, centred=centred)
+    return gen, q
+
+
+# ---------------------------------------------------------------- q4 linear (config 3)
+
+Q4_SHAPES = [(1024, 1024), (3072, 1024), (1024, 3072), (18944, 3584), (3584, 18944)]
+
+
+@pytest.mark.parametrize("m", [32, 128])
+@pytest.mark.parametrize("n,k", Q4_SHAPES)
+def test_q4_linear_config3(m, n, k):
+    from diffusorrt_amd import kernels
+
+    _say("q4_linear", m, n, k)
+    gen, q = _q4_case(n, k, seed=2)
+    x = torch.randn((m, k), generator=gen).to(torch.bfloat16)
+    w = kernels.DeviceQ4Weight(q.w_q.cuda(), q.scales.cuda(), q.biases.cuda())
+    y = kernels.linear(x.cuda(), w).cpu().numpy().astype(np.float64)
+    W = O.Q4Weight(q.w_q.numpy().view(np.uint32), q.scales.float().numpy(),
+                   q.biases.float().numpy())
+    xf = x.float().numpy()
+    # what the kernel multiplies: fp16 activations, exact integer nibbles
+    ref16 = O.q4_linear64(xf.astype(np.float16).astype(np.float64), W)
+    scale = np.abs(ref16).max()
+    err16 = np.abs(y - ref16).max() / scale
+    # the reference's semantics: fp32 activation into mx.quantized_matmul
+    ref = O.q4_linear64(xf, W)
+    err = np.abs(y - ref).max() / np.abs(ref).max()
+    _say(f"  err_vs_fp16_input={err16:.2e} err_vs_reference={err:.2e}")
+    assert err16 < 2e-5  # fp32 accumulation only
+    assert err < 2e-3    # bf16 inputs are exact in fp16, so this is accumulation too
+
+
+def test_q4_linear_fp32_input_and_bias():
+    from diffusorrt_amd import kernels
+
+    m, n, k = 5, 96, 192  # ragged rows, 3 n-tiles, 3 groups
+    _say("q4_linear fp32 ragged", m, n, k)
+    gen, q = _q4_case(n, k, seed=7, centred=True)
+    x = torch.randn((m, k), generator=gen)
+    bias = (torch.randn(n, generator=gen) * 0.1).to(torch.bfloat16)
+    w = kernels.DeviceQ4Weight(q.w_q.cuda(), q.scales.cuda(), q.biases.cuda())
+    y = kernels.linear(x.cuda(), w, bias.cuda()).cpu().numpy().astype(np.float64)
+    W = O.Q4Weight(q.w_q.numpy().view(np.uint32), q.scales.float().numpy(),
+                   q.biases.float().numpy())
+    ref = O.q4_linear64(x.numpy().astype(np.float16).astype(np.float64), W) + bias.float().numpy()
+    assert np.abs(y - ref).max() / np.abs(ref).max() < 2e-5
+
+
+@pytest.mark.parametrize("m,n,k", [(32, 1024, 1024), (128, 3072, 1024), (3, 64, 2048)])
+def test_bf16_linear(m, n, k):
+    from diffusorrt_amd import kernels
+
+    _say("bf16_linear", m, n, k)
+    gen = torch.Generator().manual_seed(11)
+    wt = (torch.randn((n, k), generator=gen) * 0.02).to(torch.bfloat16)
+    x = torch.randn((m, k), generator=gen)
+    y = kernels.linear(x.cuda(), kernels.DeviceBF16Weight(wt.cuda())).cpu().numpy()
+    ref = O.linear(x.numpy(), wt.float().numpy(), None, weight_kind="bf16")
+    # both round the same fp32 sum to bf16: equal except at rounding boundaries
+    exact = np.mean(y == ref)
+    rel = np.abs(y.astype(np.float64) - ref).max() / np.abs(ref).max()
+    _say(f"  exact_frac={exact:.4f} rel={rel:.2e}")
+    assert exact > 0.97
+    assert rel < 1e-2
+
+
+# ---------------------------------------------------------------- attention (config 2)
+
+def _attention_inputs(L, seed=1, rows=32, hq=16, hkv=8):
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn((rows, hq, 128), generator=gen).to(torch.bfloat16)
+    k = torch.randn((L + rows, hkv, 128), generator=gen).to(torch.bfloat16)
+    v = torch.randn((L + rows, hkv, 128), generator=gen).to(torch.bfloat16)
+    return q, k, v
+
+
+@pytest.mark.parametrize("L", [512, 2048, 8192])
+def test_block_attention_config2_bf16(L):
+    from diffusorrt_amd.kernels import PrefixKVCache
+
+    _say("attention bf16 config2 L=", L)
+    q, k, v = _attention_inputs(L)
+    cache = PrefixKVCache(1, 8, L + 32, dtype="bf16")
+    cache.store(0, k.cuda(), v.cuda(), 0)
+    out = cache.attention(0, q.cuda(), n_keys=L + 32, row_pos0=L, kind="bidirectional",
+                          out_dtype=torch.bfloat16)
+    got = out.float().cpu().numpy().astype(np.float64)
+    ref = O.attention(q.float().numpy(), k.float().numpy(), v.float().numpy())
+    err = np.abs(got - ref).max() / np.abs(ref).max()
+    mean_rel = np.mean(np.abs(got - ref)) / np.mean(np.abs(ref))
+    _say(f"  max_err={err:.2e} mean_rel={mean_rel:.2e}")
+    assert err < 2e-2
+    assert mean_rel < 6e-3
+
+
+@pytest.mark.parametrize("kind,rows,pos0,L", [("d2f_hybrid", 96, 64, 160),
+                                              ("d2f_hybrid", 32, 8192, 8224),
+                                              ("bidirectional", 100, 0, 100)])
+def test_attention_masks_f16(kind, rows, pos0, L):
+    from diffusorrt_amd.kernels import PrefixKVCache
+
+    _say("attention f16", kind, rows, pos0, L)
+    gen = torch.Generator().manual_seed(5)
+    q = torch.randn((rows, 16, 128), generator=gen)
+    k = torch.randn((L, 8, 128), generator=gen)
+    v = torch.randn((L, 8, 128), generator=gen)
+    cache = PrefixKVCache(1, 8, L, dtype="f16")
+    cache.store(0, k.cuda(), v.cuda(), 0)
+    geom = (0, 32) if kind == "d2f_hybrid" else None
+    out = cache.attention(0, q.to(torch.float16).cuda(), n_keys=pos0 + rows, row_pos0=pos0,
+                          kind=kind, mask_geometry=geom)
+    got = out.cpu().numpy().astype(np.float64)
+    q16 = q.numpy().astype(np.float16).astype(np.float64)
+    k16 = k.numpy().astype(np.float16).astype(np.float64)
+    v16 = v.numpy().astype(np.float16).astype(np.float64)
+    vis = None
+    if kind == "d2f_hybrid":
+        vis = O.d2f_visible(np.arange(pos0, pos0 + rows), pos0 + rows, prompt_len=0, block_size=32)
+    ref = O.attention(q16, k16[:pos0 + rows], v16[:pos0 + rows], visible=vis)
+    err = np.abs(got - ref).max() / np.abs(ref).max()
+    _say(f"  max_err={err:.2e}")
+    assert err < 3e-3
+
+
+# ---------------------------------------------------------------- small ops
+
+def test_rms_norm_rope_swiglu():
+    from diffusorrt_amd import kernels
+
+    _say("rms_norm/rope/swiglu")
+    gen = torch.Generator().manual_seed(3)
+    x = torch.randn((37, 1024), generator=gen) * 3
+    w = (1 + 0.1 * torch.randn(1024, generator=gen)).to(torch.bfloat16)
+    y = kernels.rms_norm(x.cuda(), w.cuda(), 1e-6).cpu().numpy()
+    ref = O.rms_norm64(x.numpy(), w.float().numpy(), 1e-6)
+    assert np.abs(y - ref).max() < 1e-5 * np.abs(ref).max() * 10
+
+    xr = torch.randn((9, 4, 128), generator=gen)
+    pos = np.arange(100, 109)
+    cos, sin = O.rope_tables(pos, 128, 1e6)
+    yr = kernels.rope(xr.cuda(), torch.from_numpy(cos), torch.from_numpy(sin)).cpu().numpy()
+    refr = O.apply_split_half_rope(xr.numpy(), cos, sin)
+    assert np.abs(yr - refr).max() < 1e-5
+
+    g = torch.randn(5000, generator=gen) * 4
+    u = torch.randn(5000, generator=gen)
+    ys = kernels.swiglu(g.cuda(), u.cuda()).cpu().numpy()
+    refs = O.swiglu(g.numpy(), u.numpy())
+    assert np.abs(ys - refs).max() < 1e-5 * max(1.0, np.abs(refs).max())
+
+
+# ---------------------------------------------------------------- LM head + scoring
+
+@pytest.mark.parametrize("kind", ["q4", "bf16"])
+def test_lm_head_scores_tokens(kind):
+    from diffusorrt_amd import _lib, kernels
+    from diffusorrt_amd import synthetic as syn
+    import ctypes as C
+
+    rows, n, k = 32, 151936, 1024
+    _say("lm_head", kind, rows, n, k)
+    gen = torch.Generator().manual_seed(9)
+    x = torch.randn((rows, k), generator=gen)
+    lib = _lib.load()
+    scores = torch.empty(rows, dtype=torch.float64, device="cuda")
+    tokens = torch.empty(rows, dtype=torch.int32, device="cuda")
+    logits = torch.empty((rows, n), dtype=torch.float32, device="cuda")
+    ws_b = lib.drt_op_lm_head_workspace_bytes(rows, n, k)
+    ws = torch.empty(ws_b, dtype=torch.uint8, device="cuda")
+    xc = x.cuda()
+    if kind == "q4":
+        q = syn.random_q4(gen, n, k)
+        w = kernels.DeviceQ4Weight(q.w_q.cuda(), q.scales.cuda(), q.biases.cuda())
+        args = (C.c_void_p(w.qw.data_ptr()), C.c_void_p(w.sb.data_ptr()), None)
+        W = O.Q4Weight(q.w_q.numpy().view(np.uint32), q.scales.float().numpy(),
+                       q.biases.float().numpy())
+        ref_logits = O.q4_linear64(x.numpy().astype(np.float16).astype(np.float64), W)
+    else:
+        wt = (torch.randn((n, k), generator=gen) * 0.02).to(torch.bfloat16)
+        w = kernels.DeviceBF16Weight(wt.cuda())
+        args = (None, None, C.c_void_p(w.wb.data_ptr()))
+        ref_logits = O.linear(x.numpy(), wt.float().numpy(), None, weight_kind="bf16")
+    _lib.check(lib.drt_op_lm_head_score(*args, rows, n, k, C.c_void_p(xc.data_ptr()), 0.0, 0, 0,
+                                        None, C.c_void_p(scores.data_ptr()),
+                                        C.c_void_p(tokens.data_ptr()),
+                                        C.c_void_p(logits.data_ptr()), C.c_void_p(ws.data_ptr()),
+                                        ws_b, None))
+    torch.cuda.synchronize()
+    got_logits = logits.cpu().numpy()
+    err = np.abs(got_logits - ref_logits).max() / np.abs(ref_logits).max()
+    _say(f"  logits err={err:.2e}")
+    # q4: fp32 accumulation with the exact-nibble offset trick (~1e-5 of the row max);
+    # bf16: the reference rounds logits to bf16, so compare at that resolution
+    assert err < (5e-5 if kind == "q4" else 1e-2)
+    # scores/tokens must be exactly the float64 scoring of the kernel's own logits
+    s_own, t_own = O.raw_max_prob(got_logits)
+    assert tokens.cpu().tolist() == t_own
+    np.testing.assert_allclose(scores.cpu().numpy(), s_own, rtol=1e-6)
+
+
+def test_lm_head_sampling_matches_oracle_rule():
+    from diffusorrt_amd import _lib, kernels
+    import ctypes as C
+
+    rows, n, k = 4, 2048, 256
+    _say("lm_head sampling", rows, n, k)
+    gen = torch.Generator().manual_seed(21)
+    x = torch.randn((rows, k), generator=gen)
+    wt = (torch.randn((n, k), generator=gen) * 0.05).to(torch.bfloat16)
+    w = kernels.DeviceBF16Weight(wt.cuda())
+    lib = _lib.load()
+    positions = torch.tensor([5, 6, 9, 40], dtype=torch.int32, device="cuda")
+    scores = torch.empty(rows, dtype=torch.float64, device="cuda")
+    tokens = torch.empty(rows, dtype=torch.int32, device="cuda")
+    logits = torch.empty((rows, n), dtype=torch.float32, device="cuda")
+    ws_b = lib.drt_op_lm_head_workspace_bytes(rows, n, k)
+    ws = torch.empty(ws_b, dtype=torch.uint8, device="cuda")
+    xc = x.cuda()
+    T, seed, step = 0.7, 1234, 3
+    _lib.check(lib.drt_op_lm_head_score(None, None, C.c_void_p(w.wb.data_ptr()), rows, n, k,
+                                        C.c_void_p(xc.data_ptr()), T, seed, step,
+                                        C.c_void_p(positions.data_ptr()),
+                                        C.c_void_p(scores.data_ptr()),
+                                        C.c_void_p(tokens.data_ptr()),
+                                        C.c_void_p(logits.data_ptr()), C.c_void_p(ws.data_ptr()),
+                                        ws_b, None))
+    torch.cuda.synchronize()
+    got_logits = logits.cpu().numpy()
+    s_ref, t_ref = O.sampled_max_prob(got_logits, temperature=T, seed=seed, step=step,
+                                      positions=positions.cpu().tolist())
+    assert tokens.cpu().tolist() == t_ref
+    np.testing.assert_allclose(scores.cpu().numpy(), s_ref, rtol=1e-6)

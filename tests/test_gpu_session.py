@@ -1,0 +1,208 @@
+"""Device-session parity on small models (full recompute oracle vs prefix K/V path)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import forward as F
+from oracle import ops as O
+from oracle import policy as P
+
+from helpers import (LOGITS_REL_TOL, compare_proposals, oracle_weights, rel_err_rows,
+                      tiny_dream_geometry, tiny_geometry)
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print("[case]", *a, flush=True)
+
+
+def _build(geom, kind, seed):
+    from diffusorrt_amd import synthetic as syn
+    from diffusorrt_amd.runtime import Runtime
+
+    model = syn.build_model(geom, kind, seed)
+    rt = Runtime(model, max_forward_rows=512, max_positions=1024)
+    return model, rt
+
+
+def _oracle(model):
+    from diffusorrt_amd import synthetic as syn
+
+    return oracle_weights(model), syn.oracle_config(model.geometry, model.weight_kind)
+
+
+@pytest.mark.parametrize("kind", ["q4", "bf16"])
+def test_bd3_execute_window_and_propose(kind):
+    from diffusorrt_amd.runtime import bd3_session_config
+
+    _say("bd3 window/propose", kind)
+    geom = tiny_geometry()
+    model, rt = _build(geom, kind, seed=10)
+    W, cfg = _oracle(model)
+    rng = np.random.default_rng(0)
+    prompt = rng.integers(0, 900, 64).tolist()
+    x = prompt + [geom.mask_token_id] * 64
+    with rt.session(bd3_session_config(32, 16, len(x))) as s:
+        # block 2 (positions 64..95) active, prompt blocks 0-1 committed by the window
+        scope = list(range(64, 96))
+        win = s.execute_window(x[:96], scope, mask_geometry=(0, 32))
+        got = win.array()
+        ref = F.forward_full(W, cfg, x[:96], mask_kind="d2f_hybrid", mask_geometry=(0, 32),
+                             output_rows=scope)
+        err = rel_err_rows(got, ref)
+        _say(f"  window logits rel err max={err.max():.2e}")
+        assert err.max() < LOGITS_REL_TOL
+        assert win.forwarded_rows == 96
+        # fill some rows of block 2, advance to block 3: prefix reuse + commit forward
+        x2 = list(x)
+        for p in range(64, 96):
+            x2[p] = int(rng.integers(0, 900))
+        scope3 = list(range(96, 128))
+        win3 = s.execute_window(x2, scope3, mask_geometry=(0, 32))
+        ref3 = F.forward_full(W, cfg, x2, mask_kind="d2f_hybrid", mask_geometry=(0, 32),
+                              output_rows=scope3)
+        err3 = rel_err_rows(win3.array(), ref3)
+        _say(f"  window(block 3) rel err max={err3.max():.2e} forwarded={win3.forwarded_rows}")
+        assert err3.max() < LOGITS_REL_TOL
+        assert win3.forwarded_rows == 64  # block 2 committed once + block 3 active
+
+    with rt.session(bd3_session_config(32, 16, len(x))) as s:
+        s.start_device(x, prompt_len=0, block_size=32, mask_token_id=geom.mask_token_id,
+                       exact_kv=False, steps=16)
+        frontier = list(range(64, 96))
+        scores, tokens, fwd = s.propose_device(frontier, window_end=96, frozen_prefix=64)
+        assert fwd == 96
+        ref = F.forward_full(W, cfg, x[:96], mask_kind="d2f_hybrid", mask_geometry=(0, 32),
+                             output_rows=frontier)
+        rep, problems = compare_proposals(scores, tokens, ref, bf16_logits=kind == "bf16")
+        _say(f"  propose {rep}")
+        assert not problems, problems
+        # second propose in the same block: no commit forward, only the active rows
+        s.commit_device([64, 70], [tokens[0], tokens[6]])
+        scores2, tokens2, fwd2 = s.propose_device([p for p in frontier if p not in (64, 70)],
+                                                  window_end=96, frozen_prefix=64)
+        assert fwd2 == 32
+        m = s.device_metrics()
+        assert m["rocm_kv_cache_len"] == 64 and m["rocm_commit_rows"] == 64
+    rt.close()
+
+
+@pytest.mark.parametrize("kind", ["q4", "bf16"])
+def test_bd3_full_decode_teacher_forced(kind):
+    from diffusorrt_amd import decode
+    from diffusorrt_amd.runtime import bd3_session_config
+
+    _say("bd3 decode", kind)
+    geom = tiny_geometry()
+    model, rt = _build(geom, kind, seed=11)
+    W, cfg = _oracle(model)
+    rng = np.random.default_rng(1)
+    prompt = rng.integers(0, 900, 64).tolist()
+    trace = []
+    with rt.session(bd3_session_config(32, 16, 64 + 64)) as s:
+        res = decode.generate_device_tokens(s, prompt, max_tokens=64,
+                                            mask_token_id=geom.mask_token_id,
+                                            eos_token_id=geom.eos_token_id, steps=16,
+                                            block_size=32, trace=trace)
+    assert res.forward_count == 16 and res.committed_token_count == 64
+    # teacher forcing: the oracle scores each step's canvas as the GPU saw it
+    x = prompt + [geom.mask_token_id] * 64
+    problems, ties = [], []
+    for t in trace:
+        ref = F.forward_full(W, cfg, x[:t["window_end"]], mask_kind="d2f_hybrid",
+                             mask_geometry=(0, 32), output_rows=t["frontier"])
+        quota = len(t["chosen"])
+        rep, bad = compare_proposals(t["scores"], t["tokens"], ref, quota=quota,
+                                     gpu_chosen=t["chosen"], bf16_logits=kind == "bf16")
+        ties += rep["report"]
+        problems += [(t["step"],) + tuple(b) for b in bad]
+        for r in t["chosen"]:
+            x[t["frontier"][r]] = t["tokens"][r]
+    _say(f"  near-ties reported: {ties}")
+    assert not problems, problems
+    # free-running oracle decode reproduces the same tokens unless a tie was hit
+    if not ties:
+        def logits_fn(xx, frontier, wend):
+            return F.forward_full(W, cfg, xx[:wend], mask_kind="d2f_hybrid",
+                                  mask_geometry=(0, 32), output_rows=frontier)
+
+        ref_run = P.run_fixed_quota_decode(prompt, max_tokens=64, mask_id=geom.mask_token_id,
+                                           eos_id=geom.eos_token_id, block_size=32, steps=16,
+                                           strategy="bd3_fixed_quota",
+                                           frontier_logits_fn=logits_fn)
+        assert ref_run["x"] == res.full_token_ids
+    rt.close()
+
+
+def test_dream_fixed_quota_window_and_decode():
+    from diffusorrt_amd import decode
+    from diffusorrt_amd.runtime import fixed_quota_session_config
+
+    _say("dream tiny fixed_quota")
+    geom = tiny_dream_geometry()
+    model, rt = _build(geom, "q4", seed=12)
+    W, cfg = _oracle(model)
+    rng = np.random.default_rng(2)
+    prompt = rng.integers(0, 900, 48).tolist()
+    x = prompt + [geom.mask_token_id] * 48
+    scope = list(range(48, 96))
+    with rt.session(fixed_quota_session_config(256, 12, len(x))) as s:
+        win = s.execute_window(x, scope)
+        ref = F.window_logits(W, cfg, x, scope, mask_kind="bidirectional", mask_geometry=None,
+                              logits_convention="dream_ar_shift")
+        err = rel_err_rows(win.array(), ref)
+        _say(f"  dream window rel err max={err.max():.2e}")
+        assert err.max() < LOGITS_REL_TOL
+    trace = []
+    with rt.session(fixed_quota_session_config(256, 12, len(x))) as s:
+        res = decode.generate_device_tokens(s, prompt, max_tokens=48,
+                                            mask_token_id=geom.mask_token_id,
+                                            eos_token_id=geom.eos_token_id, steps=12,
+                                            block_size=256, decode_strategy="fixed_quota",
+                                            trace=trace)
+    assert res.forward_count == 12 and res.committed_token_count == 48
+    xx = prompt + [geom.mask_token_id] * 48
+    problems = []
+    for t in trace:
+        ref = F.window_logits(W, cfg, xx, t["frontier"], mask_kind="bidirectional",
+                              mask_geometry=None, logits_convention="dream_ar_shift")
+        _, bad = compare_proposals(t["scores"], t["tokens"], ref, quota=len(t["chosen"]),
+                                   gpu_chosen=t["chosen"])
+        problems += bad
+        for r in t["chosen"]:
+            xx[t["frontier"][r]] = t["tokens"][r]
+    assert not problems, problems
+    rt.close()
+
+
+def test_session_errors_fail_closed():
+    from diffusorrt_amd import _lib
+    from diffusorrt_amd.runtime import bd3_session_config
+
+    _say("session error paths")
+    geom = tiny_geometry()
+    _, rt = _build(geom, "bf16", seed=13)
+    x = list(range(64)) + [geom.mask_token_id] * 32
+    s = rt.session(bd3_session_config(32, 8, len(x)))
+    with pytest.raises(ValueError):
+        s.propose_device([64], window_end=96, frozen_prefix=64)  # before start_device
+    s.start_device(x, prompt_len=0, block_size=32, mask_token_id=geom.mask_token_id,
+                   exact_kv=False, steps=8)
+    with pytest.raises(ValueError):
+        s.propose_device([10], window_end=96, frozen_prefix=64)  # outside the window
+    with pytest.raises(ValueError):
+        s.propose_device([64], window_end=96, frozen_prefix=60)  # not a block start
+    s.propose_device([64, 65], window_end=96, frozen_prefix=64)
+    with pytest.raises(ValueError):
+        s.commit_device([3], [5])  # inside the committed prefix K/V
+    with pytest.raises(NotImplementedError):
+        s.start_device(x, prompt_len=0, block_size=32, mask_token_id=geom.mask_token_id,
+                       exact_kv=True, steps=8)
+    h = s.handle
+    s.close()
+    lib = _lib.load()
+    assert lib.drt_release_handle(h) == _lib.INVALID_ARGUMENT  # double release
+    rt.close()
