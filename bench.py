@@ -1,0 +1,231 @@
+#!/usr/bin/env python3
+"""Benchmark of the BD3LM denoise step on one MI355X.
+
+Workload (one GPU): BD3LM on the Qwen3-0.6B architecture with q4 affine g64
+weights (seed 4), an 8192-token random prefix already committed to the K/V
+cache, then blocks of 32 masked tokens, 8 denoise steps per block, 4 tokens
+unmasked per step (greedy max-probability). A *step* is one denoise step:
+propose on the device (forward of the active block over the cached prefix,
+fused LM head + float64 softmax scoring of the frontier) -> host top-k select
+-> commit. The once-per-block forward that writes a finished block's K/V is
+counted in the step that triggers it.
+
+Prints one JSON line. ``value`` is generated tokens/s over the timed steps;
+``roofline`` is the dominant kernel (block-over-prefix attention) timed per
+dispatch over the timed region; ``cpu_baseline`` times the oracle's
+reference-semantics CPU path (full prefix recompute) on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "generated tokens/sec + ms/denoise step on 1 MI355X; % HBM roofline"
+HBM_PEAK_GBS = 8000.0
+PREFIX = 8192
+BLOCK = 32
+STEPS_PER_BLOCK = 8
+SEED = 4
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64, help="timed denoise steps")
+    ap.add_argument("--warmup", type=int, default=8, help="untimed denoise steps")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-layers", type=int, default=1)
+    ap.add_argument("--no-profile", action="store_true",
+                    help="time steps without per-dispatch timestamps (no roofline)")
+    return ap.parse_args()
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(model, prefix_ids, mask_id, layers_sampled: int):
+    """Reference-semantics CPU step (oracle), bounded sample.
+
+    The reference recomputes the whole visible prefix every denoise step
+    (S = prefix + block rows through all layers). The sample times the
+    embedding, ``layers_sampled`` decoder layers and the final norm + LM head on
+    the 32 frontier rows at S = 8224, and scales the layer time to all layers."""
+    import numpy as np
+
+    from diffusorrt_amd import synthetic as syn
+    from oracle import forward as F
+    from oracle import ops as O
+
+    g = model.geometry
+    W = {}
+    for k, v in syn.to_oracle_weights(model).items():
+        W[k] = O.Q4Weight(*v) if isinstance(v, tuple) else v
+    cfg = syn.oracle_config(g, "q4")
+    ids = np.asarray(list(prefix_ids) + [mask_id] * BLOCK)
+    s = len(ids)
+    # weight dequantization is load-time work: do it before the clock starts
+    for i in range(layers_sampled):
+        for suf in syn.LINEAR_SUFFIXES:
+            W[f"model.layers.{i}.{suf}.weight"].dense()
+    W["lm_head.weight"].dense()
+    t0 = time.perf_counter()
+    hidden = np.asarray(W["model.embed_tokens.weight"][ids], dtype=np.float32)
+    cos, sin = O.rope_tables(np.arange(s), g.head_dim, g.rope_theta)
+    visible = O.d2f_visible(np.arange(s), s, prompt_len=0, block_size=BLOCK)
+    t1 = time.perf_counter()
+    for i in range(layers_sampled):
+        hidden = F.layer_forward(W, cfg, i, hidden, cos, sin, visible)
+    t2 = time.perf_counter()
+    rows = list(range(PREFIX, PREFIX + BLOCK))
+    h = O.rms_norm(hidden[rows], W["model.norm.weight"], g.rms_norm_eps)
+    logits = O.linear(h, W["lm_head.weight"], None, weight_kind="q4")
+    O.raw_max_prob(logits)
+    t3 = time.perf_counter()
+    per_layer = (t2 - t1) / layers_sampled
+    step_s = (t1 - t0) + per_layer * g.layer_count + (t3 - t2)
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.environ.get("OPENBLAS_NUM_THREADS",
+                                                                      os.cpu_count() or 1)))
+    return {
+        "value": round(4.0 / step_s, 4),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "ms_per_step": round(step_s * 1e3, 1),
+        "sample": (f"oracle (numpy fp32, reference semantics: full recompute of S={s} rows) "
+                   f"timed for embedding + {layers_sampled} of {g.layer_count} decoder layers + "
+                   f"final norm/LM head/float64 scoring of 32 rows; layer time scaled x"
+                   f"{g.layer_count / layers_sampled:g}; 4 tokens per step"),
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build has no "
+              "multi-GPU path; see DESIGN.md for how the step would shard.", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from diffusorrt_amd import decode
+    from diffusorrt_amd import synthetic as syn
+    from diffusorrt_amd.runtime import Runtime, bd3_session_config
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    g = syn.BD3_QWEN3_06B
+    total = args.warmup + args.steps
+    n_blocks = max(1, math.ceil(total / STEPS_PER_BLOCK))
+    max_tokens = n_blocks * BLOCK
+    steps_budget = n_blocks * STEPS_PER_BLOCK
+    t = time.perf_counter()
+    model = syn.build_model(g, "q4", seed=SEED)
+    prefix = syn.prompt_ids(SEED, PREFIX)
+    log(f"model generated in {time.perf_counter() - t:.1f}s; {n_blocks} blocks")
+    rt = Runtime(model, max_forward_rows=2048, max_positions=PREFIX + max_tokens + 64)
+    sess = rt.session(bd3_session_config(BLOCK, steps_budget, PREFIX + max_tokens))
+    state = decode.MaskState(x=list(prefix) + [g.mask_token_id] * max_tokens, prompt_len=PREFIX,
+                             mask_token_id=g.mask_token_id, eos_token_id=g.eos_token_id)
+    layout = decode.BlockLayout(start=PREFIX, length=max_tokens, block_size=BLOCK, origin=0)
+    policy = decode.BD3FixedQuotaCommit(block_size=BLOCK, requested_steps=steps_budget,
+                                        generated_token_count=max_tokens, block_layout=layout)
+    sess.start_device(state.x, prompt_len=0, block_size=BLOCK, mask_token_id=g.mask_token_id,
+                      exact_kv=False, steps=steps_budget)
+    step_iter = iter(range(policy.iteration_limit))
+
+    def one_step() -> int:
+        for step in step_iter:
+            plan = policy.plan(state=state, step=step)
+            if plan.stop:
+                raise RuntimeError("decode stopped early (EOS at a block boundary)")
+            if plan.skip:
+                continue
+            frozen = (min(plan.frontier) // BLOCK) * BLOCK
+            scores, toks, _ = sess.propose_device(plan.frontier, window_end=plan.window_end,
+                                                  frozen_prefix=frozen)
+            chosen = policy.select(scores=scores, step=step)
+            pos = [plan.frontier[r] for r in chosen]
+            tk = [toks[r] for r in chosen]
+            sess.commit_device(pos, tk)
+            for p, tok in zip(pos, tk):
+                state.commit(position=p, token_id=tok)
+            return len(chosen)
+        raise RuntimeError("ran out of scheduled steps")
+
+    t = time.perf_counter()
+    for _ in range(args.warmup):
+        one_step()
+    torch.cuda.synchronize()
+    log(f"warmup ({args.warmup} steps, incl. the {PREFIX}-row prefix commit) "
+        f"{time.perf_counter() - t:.2f}s")
+    if not args.no_profile:
+        sess.set_profiling(True)
+    m0 = sess.device_metrics()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    committed = 0
+    for _ in range(args.steps):
+        committed += one_step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    m1 = sess.device_metrics()
+    sess.set_profiling(False)
+    sess.close()
+    rt.close()
+
+    ms_step = elapsed / args.steps * 1e3
+    tok_s = committed / elapsed
+    dev_ms = (m1["rocm_total_forward_ms"] - m0["rocm_total_forward_ms"]) / args.steps
+    out = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "bd3lm-qwen3-0.6b-q4g64 denoise step, 8192-token committed "
+                               "prefix, block 32, 8 steps/block, 4 tokens/step",
+                   "prefix_len": PREFIX, "block_size": BLOCK, "steps_per_block": STEPS_PER_BLOCK,
+                   "tokens_per_step": 4, "weights": "q4 affine g64 (MLX packing), seed 4",
+                   "kv_cache": "fp16", "mfma_operands": "fp16, fp32 accumulate",
+                   "parallelism": "single GPU"},
+        "ms_per_denoise_step": round(ms_step, 4),
+        "device_forward_ms_per_step": round(dev_ms, 4),
+        "committed_tokens": committed,
+    }
+    if not args.no_profile:
+        names = ("attention", "linear", "lm_head")
+        comp = {}
+        for n in names:
+            ms = m1[f"rocm_prof_ms_{n}"]
+            launches = m1[f"rocm_prof_launches_{n}"]
+            byts = m1[f"rocm_prof_bytes_{n}"]
+            comp[n] = {"ms_per_step": round(ms / args.steps, 4), "launches": int(launches),
+                       "avg_launch_us": round(ms / max(1, launches) * 1e3, 3),
+                       "algorithmic_GBps": round(byts / max(ms, 1e-9) / 1e6, 1)}
+        out["components"] = comp
+        a = comp["attention"]
+        achieved = m1["rocm_prof_bytes_attention"] / max(m1["rocm_prof_ms_attention"], 1e-9) / 1e6
+        per_launch = m1["rocm_prof_bytes_attention"] / max(1, m1["rocm_prof_launches_attention"])
+        out["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                           "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                           "traffic": None, "kernel": "attn_split_kernel",
+                           "algorithmic_bytes_per_launch": round(per_launch),
+                           "avg_launch_us": a["avg_launch_us"]}
+    if not args.no_cpu_baseline:
+        t = time.perf_counter()
+        out["cpu_baseline"] = cpu_baseline(model, prefix, g.mask_token_id, args.cpu_sample_layers)
+        log(f"cpu baseline sample took {time.perf_counter() - t:.1f}s")
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

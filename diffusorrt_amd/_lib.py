@@ -78,7 +78,9 @@ class Metrics(C.Structure):
     _fields_ = [("forward_count", C.c_int64), ("active_rows", C.c_int64),
                 ("commit_rows", C.c_int64), ("lm_rows", C.c_int64),
                 ("kv_cache_len", C.c_int64), ("kv_cache_bytes", C.c_int64),
-                ("last_forward_ms", C.c_double), ("total_forward_ms", C.c_double)]
+                ("last_forward_ms", C.c_double), ("total_forward_ms", C.c_double),
+                ("prof_ms", C.c_double * 3), ("prof_bytes", C.c_double * 3),
+                ("prof_launches", C.c_int64 * 3)]
 
 
 _VP, _I32, _I64, _U64, _SZ = C.c_void_p, C.c_int32, C.c_int64, C.c_uint64, C.c_size_t
@@ -99,6 +101,7 @@ SIGNATURES = {
     "drt_session_execute_window": (_I32, [_U64, _PI32, _I32, _PI32, _I32, _I32, _I32, _PF32,
                                           _I64, _PI32, _PI32]),
     "drt_session_metrics": (_I32, [_U64, C.POINTER(Metrics)]),
+    "drt_session_set_profiling": (_I32, [_U64, _I32]),
     "drt_op_q4_repack": (_I32, [_VP, _VP, _VP, _I32, _I32, _VP, _VP, _VP]),
     "drt_op_q4_linear_workspace_bytes": (_SZ, [_I32, _I32, _I32]),
     "drt_op_q4_linear": (_I32, [_VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _VP, _VP, _SZ,

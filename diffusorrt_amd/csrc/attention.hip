@@ -215,7 +215,203 @@ __global__ __launch_bounds__(64 * QW) void attn_split_kernel(
   (void)n_splits;
 }
 
+// Decode attention: rows of one mask segment (every key in [0, n_keys) is
+// visible to every row) with at most 32*QT query vectors per KV head. Grid
+// (R ranges, Hkv), 4 waves per work-group; wave w of range r takes tiles
+// t0 + w, t0 + w + 4, ... K/V fragments go straight from the cache into
+// registers (the tile layout makes each wave load a contiguous 1 KiB),
+// double-buffered; each wave serves all QT query tiles with one K/V load. The
+// four waves' (m, l, O) are merged through LDS, so each range writes one partial.
+// n_keys comes from `desc` when it is set (graph replays), else from the argument.
+template <typename T, int QT>
+__global__ __launch_bounds__(256) void attn_decode_kernel(
+    const T* __restrict__ q, const T* __restrict__ kv, int64_t kv_head_stride, int n_rows,
+    int Hq, int Hkv, int n_keys_arg, const StepDesc* __restrict__ desc,
+    float* __restrict__ o_part, float* __restrict__ ml_part, float scale) {
+  typedef typename MfmaT<T>::vec vec;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int G = Hq / Hkv;
+  const int n_qv = n_rows * G;
+  const int R = gridDim.x, rg = blockIdx.x, kvh = blockIdx.y;
+  const int n_keys = desc ? desc->n_keys : n_keys_arg;
+  const int n_tiles = (n_keys + 31) >> 5;
+  const int tpr = (n_tiles + R - 1) / R;
+  const int t_begin = rg * tpr;
+  const int t_end = min(n_tiles, t_begin + tpr);
+  extern __shared__ __align__(16) char smem[];
+
+  vec qf[QT][8];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int qv = qt * 32 + (lane & 31);
+    if (qv < n_qv) {
+      const int row = qv / G, head = kvh * G + (qv - (qv / G) * G);
+      const T* qp = q + ((int64_t)row * Hq + head) * 128 + 8 * (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qf[qt][i] = *(const vec*)(qp + 16 * i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qf[qt][i] = vec{};
+    }
+  }
+  float m_run[QT], l_run[QT];
+  f32x16 o[QT][4];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    m_run[qt] = -INFINITY;
+    l_run[qt] = 0.f;
+#pragma unroll
+    for (int hb = 0; hb < 4; ++hb) o[qt][hb] = f32x16{};
+  }
+  const T* base = kv + (int64_t)kvh * kv_head_stride;
+  vec kc[8], vc[8];
+  int t = t_begin + wave;
+  if (t < t_end) {
+    const T* tp = base + (int64_t)t * KV_TILE_ELEMS;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      kc[i] = *(const vec*)(tp + (i * 64 + lane) * 8);
+      vc[i] = *(const vec*)(tp + 4096 + (i * 64 + lane) * 8);
+    }
+  }
+  for (; t < t_end; t += 4) {
+    vec kn[8], vn[8];
+    const bool more = t + 4 < t_end;
+    if (more) {
+      const T* tp = base + (int64_t)(t + 4) * KV_TILE_ELEMS;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        kn[i] = *(const vec*)(tp + (i * 64 + lane) * 8);
+        vn[i] = *(const vec*)(tp + 4096 + (i * 64 + lane) * 8);
+      }
+    }
+    const int key0 = t * 32;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      if (qt * 32 >= n_qv) break;  // uniform
+      f32x16 s = f32x16{};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s = MfmaT<T>::mma(kc[i], qf[qt][i], s);
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const bool vis = key0 + mfma_row(r, lane) < n_keys;
+        s[r] = vis ? s[r] * scale : -INFINITY;
+        tmax = fmaxf(tmax, s[r]);
+      }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float m_new = fmaxf(m_run[qt], tmax);
+      const float basev = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __expf(m_run[qt] - basev);
+      float p[16];
+      float psum = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        p[r] = __expf(s[r] - basev);
+        psum += p[r];
+      }
+      l_run[qt] = l_run[qt] * alpha + psum;
+      m_run[qt] = m_new;
+#pragma unroll
+      for (int hb = 0; hb < 4; ++hb) o[qt][hb] *= alpha;
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+        vec pf;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pf[j] = MfmaT<T>::from_float(p[kh * 8 + j]);
+#pragma unroll
+        for (int hb = 0; hb < 4; ++hb) o[qt][hb] = MfmaT<T>::mma(vc[hb * 2 + kh], pf, o[qt][hb]);
+      }
+    }
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        kc[i] = kn[i];
+        vc[i] = vn[i];
+      }
+    }
+  }
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) l_run[qt] += __shfl_xor(l_run[qt], 32, 64);
+
+  // Merge the four waves: 3,2 -> 1,0 -> 0 through LDS (same register layout in all waves).
+  float* lds = (float*)smem;
+  constexpr int SLOT = QT * 64 * 64 + QT * 64 * 2;
+  auto put = [&](int slot) {
+    float* b = lds + slot * SLOT;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+      for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) b[(qt * 64 + hb * 16 + r) * 64 + lane] = o[qt][hb][r];
+      b[QT * 4096 + (qt * 64 + lane) * 2] = m_run[qt];
+      b[QT * 4096 + (qt * 64 + lane) * 2 + 1] = l_run[qt];
+    }
+  };
+  auto merge = [&](int slot) {
+    const float* b = lds + slot * SLOT;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const float m2 = b[QT * 4096 + (qt * 64 + lane) * 2];
+      const float l2 = b[QT * 4096 + (qt * 64 + lane) * 2 + 1];
+      const float mm = fmaxf(m_run[qt], m2);
+      const float a1 = mm == -INFINITY ? 0.f : __expf(m_run[qt] - mm);
+      const float a2 = mm == -INFINITY ? 0.f : __expf(m2 - mm);
+      l_run[qt] = a1 * l_run[qt] + a2 * l2;
+      m_run[qt] = mm;
+#pragma unroll
+      for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          o[qt][hb][r] = a1 * o[qt][hb][r] + a2 * b[(qt * 64 + hb * 16 + r) * 64 + lane];
+    }
+  };
+  __syncthreads();
+  if (wave >= 2) put(wave - 2);
+  __syncthreads();
+  if (wave < 2) merge(wave);
+  __syncthreads();
+  if (wave == 1) put(0);
+  __syncthreads();
+  if (wave == 0) merge(0);
+  __syncthreads();
+  if (wave != 0) return;
+  // wave 0: transpose O^T through LDS and write this range's partial.
+  const int64_t part_base = ((int64_t)rg * Hkv + kvh) * n_qv;
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    if (qt * 32 >= n_qv) break;
+    float* ot = lds;
+#pragma unroll
+    for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ot[(lane & 31) * 132 + hb * 32 + mfma_row(r, lane)] = o[qt][hb][r];
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    for (int i = lane; i < 32 * 32; i += 64) {
+      const int qq = i >> 5, c4 = (i & 31) * 4;
+      const int qv2 = qt * 32 + qq;
+      if (qv2 < n_qv) {
+        f32x4 v = {ot[qq * 132 + c4], ot[qq * 132 + c4 + 1], ot[qq * 132 + c4 + 2],
+                   ot[qq * 132 + c4 + 3]};
+        *(f32x4*)(o_part + (part_base + qv2) * 128 + c4) = v;
+      }
+    }
+    const int qv = qt * 32 + (lane & 31);
+    if (lane < 32 && qv < n_qv) {
+      ml_part[(part_base + qv) * 2] = m_run[qt];
+      ml_part[(part_base + qv) * 2 + 1] = l_run[qt];
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
 // Combine key splits. One wave per (row, head); lane holds hd = lane, lane + 64.
+// The split statistics are loaded across lanes (split s by lane s), the weights
+// broadcast by shuffles, and every partial-O load is independent, so the
+// combine costs one memory latency, not one per split. n_splits <= 64.
 // out_fmt: 0 = ACT_F16P (+ xsum), 1 = ACT_BF16, 2 = fp32 plain, 3 = bf16 plain.
 extern "C" __global__ void attn_combine_kernel(const float* __restrict__ o_part,
                                                const float* __restrict__ ml_part, int n_splits,
@@ -228,18 +424,34 @@ extern "C" __global__ void attn_combine_kernel(const float* __restrict__ o_part,
   const int G = Hq / Hkv;
   const int kvh = head / G, qv = row * G + (head - kvh * G);
   const int n_qv = n_rows * G;
-  float mmax = -INFINITY;
-  for (int s = 0; s < n_splits; ++s)
-    mmax = fmaxf(mmax, ml_part[((((int64_t)s * Hkv + kvh) * n_qv) + qv) * 2]);
-  float lsum = 0.f, a0 = 0.f, a1 = 0.f;
-  for (int s = 0; s < n_splits; ++s) {
-    const int64_t idx = ((int64_t)s * Hkv + kvh) * n_qv + qv;
-    const float ms = ml_part[idx * 2];
-    if (ms == -INFINITY) continue;
-    const float w = __expf(ms - mmax);
-    lsum += w * ml_part[idx * 2 + 1];
-    a0 += w * o_part[idx * 128 + lane];
-    a1 += w * o_part[idx * 128 + 64 + lane];
+  const int64_t stride = (int64_t)Hkv * n_qv;  // between splits
+  const int64_t idx0 = (int64_t)kvh * n_qv + qv;
+  float ms = -INFINITY, ls = 0.f;
+  if (lane < n_splits) {
+    ms = ml_part[(idx0 + lane * stride) * 2];
+    ls = ml_part[(idx0 + lane * stride) * 2 + 1];
+  }
+  const float mmax = wave_max(ms);
+  const float w = (ms == -INFINITY) ? 0.f : __expf(ms - mmax);
+  const float lsum = wave_sum(w * ls);
+  float a0 = 0.f, a1 = 0.f;
+  for (int s0 = 0; s0 < n_splits; s0 += 16) {
+    float p0[16], p1[16], ws[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int sp = s0 + j;
+      ws[j] = __shfl(w, sp & 63, 64);
+      const int64_t base = (idx0 + (int64_t)min(sp, n_splits - 1) * stride) * 128;
+      p0[j] = o_part[base + lane];
+      p1[j] = o_part[base + 64 + lane];
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      if (s0 + j < n_splits) {
+        a0 += ws[j] * p0[j];
+        a1 += ws[j] * p1[j];
+      }
+    }
   }
   const float inv = 1.f / lsum;
   const float v0 = a0 * inv, v1 = a1 * inv;
@@ -311,6 +523,18 @@ template __global__ void attn_split_kernel<__bf16, 2>(const __bf16*, const __bf1
 template __global__ void attn_split_kernel<__bf16, 4>(const __bf16*, const __bf16*, int64_t, int,
                                                       int, int, int, int, int, int, int, int,
                                                       float*, float*, float);
+template __global__ void attn_decode_kernel<_Float16, 1>(const _Float16*, const _Float16*,
+                                                         int64_t, int, int, int, int,
+                                                         const StepDesc*, float*, float*, float);
+template __global__ void attn_decode_kernel<_Float16, 2>(const _Float16*, const _Float16*,
+                                                         int64_t, int, int, int, int,
+                                                         const StepDesc*, float*, float*, float);
+template __global__ void attn_decode_kernel<__bf16, 1>(const __bf16*, const __bf16*, int64_t, int,
+                                                       int, int, int, const StepDesc*, float*,
+                                                       float*, float);
+template __global__ void attn_decode_kernel<__bf16, 2>(const __bf16*, const __bf16*, int64_t, int,
+                                                       int, int, int, const StepDesc*, float*,
+                                                       float*, float);
 template __global__ void kv_pack_kernel<_Float16>(const void*, const void*, int, int, int, int,
                                                   _Float16*, int64_t);
 template __global__ void kv_pack_kernel<__bf16>(const void*, const void*, int, int, int, int,
@@ -327,7 +551,7 @@ AttnPlan plan_attention(int n_rows, int Hq, int Hkv, int n_keys, size_t part_bud
   const int n_tiles = std::max(1, (n_keys + 31) / 32);
   const int target_wgs = 512;
   int splits = std::max(1, target_wgs / (Hkv * p.qgroups));
-  splits = std::min(splits, n_tiles);
+  splits = std::min({splits, n_tiles, 64});  // the combine reads <= 64 splits
   // keep the fp32 partials within budget
   const size_t per_split = (size_t)Hkv * n_rows * G * 130 * 4;
   if (per_split > 0) splits = (int)std::max<size_t>(1, std::min<size_t>(splits, part_budget_bytes / per_split));
@@ -352,14 +576,16 @@ void attention(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_s
   const size_t lds = std::max(lds_kv, (size_t)plan.qw * 32 * 132 * 4);
   const dim3 grid(plan.splits * Hkv, plan.qgroups);
   const dim3 block(64 * plan.qw);
+  // algorithmic bytes of this launch: Q read + the K/V of n_keys keys
+  const double bytes = 2.0 * n_rows * Hq * 128 + 4.0 * n_keys * Hkv * 128;
 #define DRT_ATTN(T, QW)                                                                         \
   {                                                                                             \
     auto fn = attn_split_kernel<T, QW>;                                                         \
     static size_t granted = 0;                                                                  \
     grant_lds((const void*)fn, lds, granted);                                                   \
-    hipLaunchKernelGGL(fn, grid, block, lds, s, (const T*)q, (const T*)kv_layer, kv_head_stride, \
-                       n_rows, Hq, Hkv, n_keys, row_pos0, mask_kind, mask_prompt_len,           \
-                       mask_block, plan.tiles_per_split, o_part, ml_part, scale);               \
+    DRT_LAUNCH(Profiler::ATTN, bytes, fn, grid, block, lds, s, (const T*)q, (const T*)kv_layer,  \
+               kv_head_stride, n_rows, Hq, Hkv, n_keys, row_pos0, mask_kind, mask_prompt_len,   \
+               mask_block, plan.tiles_per_split, o_part, ml_part, scale);                       \
   }
   if (bf16) {
     if (plan.qw == 2) DRT_ATTN(__bf16, 2) else DRT_ATTN(__bf16, 4)
@@ -371,6 +597,40 @@ void attention(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_s
   const int64_t waves = (int64_t)n_rows * Hq;
   hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s,
                      o_part, ml_part, plan.splits, n_rows, Hq, Hkv, out, xsum, out_fmt);
+  DRT_HIP(hipGetLastError());
+}
+
+// Decode attention (one mask segment, <= 64 query vectors per KV head) + combine.
+void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_stride,
+                      int n_rows, int Hq, int Hkv, int n_keys, const StepDesc* desc, int ranges,
+                      float* o_part, float* ml_part, void* out, float* xsum, int out_fmt,
+                      hipStream_t s) {
+  const int G = Hq / Hkv;
+  require(Hq % Hkv == 0 && n_rows * G <= 64, "decode attention needs <= 64 query vectors per head");
+  const int qt = (n_rows * G + 31) / 32;
+  const float scale = 1.0f / sqrtf(128.0f);
+  const size_t lds = (size_t)2 * (qt * 64 * 64 + qt * 64 * 2) * 4;
+  const dim3 grid(ranges, Hkv);
+  const double bytes = 2.0 * n_rows * Hq * 128 + 4.0 * n_keys * Hkv * 128;
+#define DRT_DEC(T, QT)                                                                      \
+  {                                                                                         \
+    auto fn = attn_decode_kernel<T, QT>;                                                    \
+    static size_t granted = 0;                                                              \
+    grant_lds((const void*)fn, lds, granted);                                               \
+    DRT_LAUNCH(Profiler::ATTN, bytes, fn, grid, dim3(256), lds, s, (const T*)q,             \
+               (const T*)kv_layer, kv_head_stride, n_rows, Hq, Hkv, n_keys, desc, o_part,   \
+               ml_part, scale);                                                             \
+  }
+  if (bf16) {
+    if (qt == 1) DRT_DEC(__bf16, 1) else DRT_DEC(__bf16, 2)
+  } else {
+    if (qt == 1) DRT_DEC(_Float16, 1) else DRT_DEC(_Float16, 2)
+  }
+#undef DRT_DEC
+  DRT_HIP(hipGetLastError());
+  const int64_t waves = (int64_t)n_rows * Hq;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s,
+                     o_part, ml_part, ranges, n_rows, Hq, Hkv, out, xsum, out_fmt);
   DRT_HIP(hipGetLastError());
 }
 

@@ -71,3 +71,20 @@ DRT_DEV int f16p_index(int k) {
   const int j = k & 7;
   return (k & ~7) | ((j & 3) << 1) | (j >> 2);
 }
+
+// Per-forward parameters read by the kernels from device memory, so that one
+// captured HIP graph can serve every decode step (the host rewrites this small
+// struct before each replay; shapes stay fixed).
+struct StepDesc {
+  int32_t row0;             // absolute position of row 0 of this forward
+  int32_t n_rows;           // rows forwarded
+  int32_t n_keys;           // keys [0, n_keys) are attended
+  int32_t n_lm;             // LM-head rows (<= 32 per tile)
+  int32_t mask_kind;        // 0 none, 1 d2f_hybrid
+  int32_t mask_prompt_len;
+  int32_t mask_block;
+  int32_t step;             // sampling forward index
+  uint64_t seed;
+  float temperature;
+  int32_t pad;
+};

@@ -1,13 +1,11 @@
 // Elementwise and epilogue kernels of the decoder layer (gfx950).
 //
-// Every split-K linear writes fp32 partials [splits][M][N]; the kernels here
-// reduce them in a fixed order (deterministic) and fuse the op that follows:
-//   * residual_norm_kernel: h += sum(partials) [bf16-rounded for bf16 weights,
-//     as the reference's bf16 matmul output is], then RMSNorm(h) * w written
-//     in the activation format the next linear reads.
-//   * qkv_epilogue_kernel:  q/k/v reduce (+ bias), per-head q/k RMSNorm,
-//     split-half RoPE, Q out for attention, K/V into the tiled KV cache.
-//   * swiglu_kernel:        gate/up reduce, silu(g) * u, activation for down.
+//   * embed_kernel:         token rows of the bf16 table -> fp32 residual stream.
+//   * residual_norm_kernel: (optional split partials added to) the residual
+//     stream, then RMSNorm(h) * w of selected rows in an activation format;
+//     the runtime uses it for the final norm of the LM-head rows.
+//   * per-op fp32 kernels of the kernel-table seam: rms_norm, rope, swiglu.
+// The decoder layer's other epilogues are fused into fused_linear.hip.
 // Reference math: backends/mlx_ops.py:21-35 (rms_norm), :97-130 (linear
 // dtypes), :133-144 (rope), :147-154 (swiglu); backends/mlx_forward.py:1164-1361.
 #include "common.h"
@@ -111,109 +109,6 @@ extern "C" __global__ void residual_norm_kernel(
   }
 }
 
-// QKV epilogue. One WG (4 waves) per row; each wave takes whole heads, lane l
-// holding head elements l and l + 64 (the RoPE pair). Heads 0..Hq-1 are q,
-// then Hkv k heads, then Hkv v heads, matching the fused [q | k | v] linear.
-template <typename T>
-__global__ void qkv_epilogue_kernel(const float* __restrict__ part, int splits, int M,
-                                    const uint16_t* __restrict__ bias, int rnd_bf16,
-                                    const uint16_t* __restrict__ q_norm,
-                                    const uint16_t* __restrict__ k_norm, float eps,
-                                    const float* __restrict__ rope_cos,
-                                    const float* __restrict__ rope_sin, int row_pos0, int Hq,
-                                    int Hkv, T* __restrict__ q_out, T* __restrict__ kv_layer,
-                                    int64_t kv_head_stride) {
-  const int m = blockIdx.x;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int N = (Hq + 2 * Hkv) * 128;
-  const int pos = row_pos0 + m;
-  const float c = rope_cos[(int64_t)pos * 64 + lane];
-  const float s = rope_sin[(int64_t)pos * 64 + lane];
-  for (int h = wave; h < Hq + 2 * Hkv; h += blockDim.x >> 6) {
-    const int col0 = h * 128 + lane, col1 = col0 + 64;
-    float x0 = 0.f, x1 = 0.f;
-    for (int p = 0; p < splits; ++p) {
-      const float* pr = part + ((int64_t)p * M + m) * N;
-      x0 += pr[col0];
-      x1 += pr[col1];
-    }
-    if (rnd_bf16) {
-      x0 = round_bf16(x0);
-      x1 = round_bf16(x1);
-    }
-    if (bias) {
-      x0 += bf16_bits_to_float(bias[col0]);
-      x1 += bf16_bits_to_float(bias[col1]);
-    }
-    const bool is_q = h < Hq, is_k = !is_q && h < Hq + Hkv;
-    if (is_q || is_k) {
-      const uint16_t* nw = is_q ? q_norm : k_norm;
-      if (nw) {
-        const float ms = wave_sum(x0 * x0 + x1 * x1) / 128.f;
-        const float inv = 1.f / sqrtf(ms + eps);
-        x0 = (x0 * inv) * bf16_bits_to_float(nw[lane]);
-        x1 = (x1 * inv) * bf16_bits_to_float(nw[lane + 64]);
-      }
-      // split-half RoPE: out = x*cos + rotate_half(x)*sin, rotate_half = [-x2, x1]
-      const float r0 = x0 * c - x1 * s;
-      const float r1 = x1 * c + x0 * s;
-      x0 = r0;
-      x1 = r1;
-    }
-    if (is_q) {
-      T* qo = q_out + ((int64_t)m * Hq + h) * 128;
-      qo[lane] = cvt<T>(x0);
-      qo[lane + 64] = cvt<T>(x1);
-    } else {
-      const int kvh = is_k ? h - Hq : h - Hq - Hkv;
-      T* tile = kv_layer + (int64_t)kvh * kv_head_stride + (int64_t)(pos >> 5) * KV_TILE;
-      const int kk = pos & 31;
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int hd = lane + 64 * e;
-        const float val = e ? x1 : x0;
-        if (is_k) {
-          const int ko = (((hd >> 4) * 2 + ((hd >> 3) & 1)) * 32 + kk) * 8 + (hd & 7);
-          tile[ko] = cvt<T>(val);
-        } else {
-          const int q16 = kk & 15;
-          const int vo =
-              ((((hd >> 5) * 2 + (kk >> 4)) * 2 + ((q16 >> 2) & 1)) * 32 + (hd & 31)) * 8 +
-              (q16 & 3) + 4 * (q16 >> 3);
-          tile[4096 + vo] = cvt<T>(val);
-        }
-      }
-    }
-  }
-}
-
-// SwiGLU epilogue: part [splits][M][2F] of the fused [gate | up] linear.
-// One wave per (row, 64-column group) of the F outputs.
-extern "C" __global__ void swiglu_kernel(const float* __restrict__ part, int splits, int M, int F,
-                                         int rnd_bf16, int fmt, void* __restrict__ act,
-                                         float* __restrict__ xsum) {
-  const int lane = threadIdx.x & 63;
-  const int64_t wid = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
-  const int groups = F >> 6;
-  if (wid >= (int64_t)M * groups) return;
-  const int m = (int)(wid / groups), g = (int)(wid % groups);
-  const int f = g * 64 + lane;
-  float gv = 0.f, uv = 0.f;
-  for (int p = 0; p < splits; ++p) {
-    const float* pr = part + ((int64_t)p * M + m) * (2 * F);
-    gv += pr[f];
-    uv += pr[F + f];
-  }
-  if (rnd_bf16) {
-    gv = round_bf16(gv);
-    uv = round_bf16(uv);
-  }
-  const float sig = 1.f / (1.f + expf(-gv));
-  const float y = gv * sig * uv;
-  char* arow = (char*)act + (size_t)m * act_row_bytes(fmt, F);
-  write_act(fmt, arow, f, y, xsum ? xsum + (int64_t)m * groups : nullptr, lane);
-}
-
 // ---- per-op kernels for the KernelTable seam (fp32 tensors) ----
 
 // RMSNorm over the last axis of x [rows][d] (d <= 4096), bf16 weight.
@@ -261,15 +156,6 @@ extern "C" __global__ void swiglu_rows_kernel(const float* __restrict__ g,
   }
 }
 
-template __global__ void qkv_epilogue_kernel<_Float16>(const float*, int, int, const uint16_t*,
-                                                       int, const uint16_t*, const uint16_t*,
-                                                       float, const float*, const float*, int,
-                                                       int, int, _Float16*, _Float16*, int64_t);
-template __global__ void qkv_epilogue_kernel<__bf16>(const float*, int, int, const uint16_t*, int,
-                                                     const uint16_t*, const uint16_t*, float,
-                                                     const float*, const float*, int, int, int,
-                                                     __bf16*, __bf16*, int64_t);
-
 namespace drt {
 
 void embed(const int32_t* tokens, const uint16_t* table, float* hidden, int M, int d,
@@ -286,30 +172,6 @@ void residual_norm(float* hidden, const float* part, int splits, int M_part, boo
   hipLaunchKernelGGL(residual_norm_kernel, dim3(n_out_rows), dim3(256), 0, s, hidden, part, splits,
                      M_part, (int)rnd_bf16, src_rows, (int)write_hidden, norm_w, eps, d, fmt, act,
                      xsum);
-  DRT_HIP(hipGetLastError());
-}
-
-void qkv_epilogue(bool kv_bf16, const float* part, int splits, int M, const uint16_t* bias,
-                  bool rnd_bf16, const uint16_t* q_norm, const uint16_t* k_norm, float eps,
-                  const float* rope_cos, const float* rope_sin, int row_pos0, int Hq, int Hkv,
-                  void* q_out, void* kv_layer, int64_t kv_head_stride, hipStream_t s) {
-  if (kv_bf16)
-    hipLaunchKernelGGL(qkv_epilogue_kernel<__bf16>, dim3(M), dim3(256), 0, s, part, splits, M,
-                       bias, (int)rnd_bf16, q_norm, k_norm, eps, rope_cos, rope_sin, row_pos0, Hq,
-                       Hkv, (__bf16*)q_out, (__bf16*)kv_layer, kv_head_stride);
-  else
-    hipLaunchKernelGGL(qkv_epilogue_kernel<_Float16>, dim3(M), dim3(256), 0, s, part, splits, M,
-                       bias, (int)rnd_bf16, q_norm, k_norm, eps, rope_cos, rope_sin, row_pos0, Hq,
-                       Hkv, (_Float16*)q_out, (_Float16*)kv_layer, kv_head_stride);
-  DRT_HIP(hipGetLastError());
-}
-
-void swiglu(const float* part, int splits, int M, int F, bool rnd_bf16, int fmt, void* act,
-            float* xsum, hipStream_t s) {
-  require(F % 64 == 0, "swiglu needs F % 64 == 0");
-  const int64_t waves = (int64_t)M * (F / 64);
-  hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, part,
-                     splits, M, F, (int)rnd_bf16, fmt, act, xsum);
   DRT_HIP(hipGetLastError());
 }
 

@@ -1,0 +1,48 @@
+// Arguments and modes of the fused linear kernel (fused_linear.hip).
+#pragma once
+#include "common.h"
+
+enum { W_Q4 = 0, W_BF16 = 1 };
+enum { PRO_ACT = 0, PRO_NORM = 1 };
+enum { EPI_STORE = 0, EPI_QKV = 1, EPI_RESID = 2, EPI_SWIGLU = 3 };
+// launch kinds (prologue + epilogue pairs used by the runtime)
+enum { FL_QKV = 0, FL_RESID = 1, FL_SWIGLU = 2, FL_STORE = 3 };
+
+struct FusedArgs {
+  // weights: q4 tile32-g64 (qw, sb) or bf16 tiles (wb); optional bf16 bias [N]
+  const uint32_t* qw = nullptr;
+  const uint32_t* sb = nullptr;
+  const uint16_t* wb = nullptr;
+  const uint16_t* bias = nullptr;
+  int M = 0, N = 0, K = 0;
+  // PRO_ACT: activation [M][K] (ACT_F16P + xsum[M][K/64], or ACT_BF16)
+  const void* act = nullptr;
+  const float* act_xsum = nullptr;
+  // PRO_NORM: fp32 residual stream [M][K] and bf16 norm weight [K]
+  const float* hidden = nullptr;
+  const uint16_t* norm_w = nullptr;
+  float eps = 1e-6f;
+  int rnd_bf16 = 0;  // bf16 weights: round the linear output to bf16
+  // EPI_STORE
+  float* y = nullptr;
+  // EPI_RESID
+  float* hidden_out = nullptr;
+  // EPI_SWIGLU: activation of the down projection [M][N/2]
+  void* act_out = nullptr;
+  float* xsum_out = nullptr;
+  int act_fmt = 0;
+  // EPI_QKV
+  const uint16_t* q_norm = nullptr;
+  const uint16_t* k_norm = nullptr;
+  const float* rope_cos = nullptr;
+  const float* rope_sin = nullptr;
+  void* q_out = nullptr;
+  void* kv_layer = nullptr;
+  int64_t kv_head_stride = 0;
+  int Hq = 0, Hkv = 0, kv_bf16 = 0;
+  const StepDesc* desc = nullptr;  // row0: absolute position of row 0
+};
+
+namespace drt {
+void fused_linear(const FusedArgs& a, int kind, hipStream_t s);
+}

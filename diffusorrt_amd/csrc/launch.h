@@ -1,11 +1,15 @@
 // Host-side launch helpers shared by the runtime and the per-op C-ABI.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "common.h"
 
 #include <algorithm>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 namespace drt {
 
@@ -67,6 +71,67 @@ inline void grant_lds(const void* fn, size_t bytes, size_t& granted) {
   granted = bytes;
 }
 
+// Per-dispatch device timing for the hot kernel classes. When a profiler is
+// installed on the calling thread and switched on, DRT_LAUNCH dispatches with
+// hipExtLaunchKernelGGL, whose start/stop events are the dispatch packet's own
+// timestamps (no extra packets in the stream); collect() reads them after the
+// stream has drained.
+struct Profiler {
+  enum Class : int { ATTN = 0, GEMM = 1, LMHEAD = 2, NCLASS = 3 };
+  bool on = false;
+  std::vector<hipEvent_t> pool;
+  struct Rec { int cls; double bytes; };
+  std::vector<Rec> recs;
+  double ms[NCLASS] = {};
+  double bytes[NCLASS] = {};
+  int64_t launches[NCLASS] = {};
+
+  void pair(hipEvent_t* a, hipEvent_t* b, int cls, double nbytes) {
+    const size_t i = recs.size();
+    while (pool.size() < 2 * (i + 1)) {
+      hipEvent_t e;
+      DRT_HIP(hipEventCreate(&e));
+      pool.push_back(e);
+    }
+    *a = pool[2 * i];
+    *b = pool[2 * i + 1];
+    recs.push_back({cls, nbytes});
+  }
+  void collect() {
+    for (size_t i = 0; i < recs.size(); ++i) {
+      float t = 0.f;
+      DRT_HIP(hipEventElapsedTime(&t, pool[2 * i], pool[2 * i + 1]));
+      ms[recs[i].cls] += t;
+      bytes[recs[i].cls] += recs[i].bytes;
+      launches[recs[i].cls] += 1;
+    }
+    recs.clear();
+  }
+  void reset() {
+    recs.clear();
+    for (int c = 0; c < NCLASS; ++c) { ms[c] = 0; bytes[c] = 0; launches[c] = 0; }
+  }
+  ~Profiler() {
+    for (hipEvent_t e : pool) (void)hipEventDestroy(e);
+  }
+};
+
+// The profiler of the session running on this thread (null when none).
+extern thread_local Profiler* g_prof;
+
+// Launch `fn` (a kernel function pointer variable), timed when profiling.
+#define DRT_LAUNCH(CLS, BYTES, FN, GRID, BLOCK, SHMEM, STREAM, ...)                        \
+  do {                                                                                     \
+    ::drt::Profiler* p_ = ::drt::g_prof;                                                   \
+    if (p_ && p_->on) {                                                                    \
+      hipEvent_t a_, b_;                                                                   \
+      p_->pair(&a_, &b_, (CLS), (BYTES));                                                  \
+      hipExtLaunchKernelGGL(FN, GRID, BLOCK, SHMEM, STREAM, a_, b_, 0, __VA_ARGS__);       \
+    } else {                                                                               \
+      hipLaunchKernelGGL(FN, GRID, BLOCK, SHMEM, STREAM, __VA_ARGS__);                     \
+    }                                                                                      \
+  } while (0)
+
 // Activation formats (match ActFmt in common.h; 2 = fp32 plain).
 enum Fmt : int { F16P = 0, BF16 = 1, F32 = 2 };
 
@@ -86,20 +151,6 @@ void bf16_repack(const uint16_t* w, int N, int K, uint16_t* wb, hipStream_t s);
 void q4_act_prep(const void* x, bool x_bf16, int M, int K, _Float16* xp, float* xsum,
                  hipStream_t s);
 
-// Split-K plan for a linear on M rows.
-struct SplitPlan {
-  int splits = 1;
-  int per_split = 1;  // q4: groups; bf16: 16-k chunks
-};
-SplitPlan plan_linear(const LinearW& w, int M);
-// Writes partials [plan.splits][M][N] fp32 into part. act: F16P (+xsum) for q4, BF16 for bf16.
-void linear_partials(const LinearW& w, const void* act, const float* xsum, int M, float* part,
-                     const SplitPlan& plan, hipStream_t s);
-void bf16_linear_partials(const uint16_t* wb, const uint16_t* x, int M, int N, int K, float* part,
-                          int splits, int chunks_per_split, hipStream_t s);
-void splitk_reduce(const float* part, int splits, const uint16_t* bias, float* y, int M, int N,
-                   hipStream_t s);
-
 // Attention over the tiled cache of one layer.
 struct AttnPlan {
   int qw = 2, qgroups = 1, splits = 1, tiles_per_split = 1;
@@ -110,6 +161,10 @@ void attention(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_s
                int n_rows, int Hq, int Hkv, int n_keys, int row_pos0, int mask_kind,
                int mask_prompt_len, int mask_block, const AttnPlan& plan, float* o_part,
                float* ml_part, void* out, float* xsum, int out_fmt, hipStream_t s);
+void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_stride,
+                      int n_rows, int Hq, int Hkv, int n_keys, const StepDesc* desc, int ranges,
+                      float* o_part, float* ml_part, void* out, float* xsum, int out_fmt,
+                      hipStream_t s);
 void kv_pack(bool kv_bf16, const void* k, const void* v, bool src_bf16, int n, int Hkv, int pos0,
              void* kv_layer, int64_t kv_head_stride, hipStream_t s);
 
@@ -119,13 +174,6 @@ void embed(const int32_t* tokens, const uint16_t* table, float* hidden, int M, i
 void residual_norm(float* hidden, const float* part, int splits, int M_part, bool rnd_bf16,
                    const int32_t* src_rows, bool write_hidden, const uint16_t* norm_w, float eps,
                    int d, int fmt, void* act, float* xsum, int n_out_rows, hipStream_t s);
-void qkv_epilogue(bool kv_bf16, const float* part, int splits, int M, const uint16_t* bias,
-                  bool rnd_bf16, const uint16_t* q_norm, const uint16_t* k_norm, float eps,
-                  const float* rope_cos, const float* rope_sin, int row_pos0, int Hq, int Hkv,
-                  void* q_out, void* kv_layer, int64_t kv_head_stride, hipStream_t s);
-void swiglu(const float* part, int splits, int M, int F, bool rnd_bf16, int fmt, void* act,
-            float* xsum, hipStream_t s);
-
 // LM head: per-row scores (f64) and tokens, optional raw logits.
 size_t lmhead_stats_bytes(int M, int N);
 void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* logits_out,

@@ -319,16 +319,19 @@ void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* 
     auto fn = lmhead_kernel<0, WAVES, 4>;
     static size_t granted = 0;
     grant_lds((const void*)fn, lds, granted);
-    hipLaunchKernelGGL(fn, grid, dim3(64 * WAVES), lds, s, w.qw.as<uint32_t>(),
-                       w.sb.as<uint32_t>(), (const uint16_t*)nullptr, act, xsum, M, w.N, w.K,
-                       chunk_k, logits_out, (LmStat*)stats, temperature, seed, step, positions);
+    const double bytes = (double)w.N * w.K / 2 + (double)w.N * w.K / 16 + 2.0 * M * w.K;
+    DRT_LAUNCH(Profiler::LMHEAD, bytes, fn, grid, dim3(64 * WAVES), lds, s, w.qw.as<uint32_t>(),
+               w.sb.as<uint32_t>(), (const uint16_t*)nullptr, act, xsum, M, w.N, w.K, chunk_k,
+               logits_out, (LmStat*)stats, temperature, seed, step, positions);
   } else {
     auto fn = lmhead_kernel<1, WAVES, 8>;
     static size_t granted = 0;
     grant_lds((const void*)fn, lds, granted);
-    hipLaunchKernelGGL(fn, grid, dim3(64 * WAVES), lds, s, (const uint32_t*)nullptr,
-                       (const uint32_t*)nullptr, w.wb.as<uint16_t>(), act, xsum, M, w.N, w.K,
-                       chunk_k, logits_out, (LmStat*)stats, temperature, seed, step, positions);
+    const double bytes = 2.0 * w.N * w.K + 2.0 * M * w.K;
+    DRT_LAUNCH(Profiler::LMHEAD, bytes, fn, grid, dim3(64 * WAVES), lds, s,
+               (const uint32_t*)nullptr, (const uint32_t*)nullptr, w.wb.as<uint16_t>(), act, xsum,
+               M, w.N, w.K, chunk_k, logits_out, (LmStat*)stats, temperature, seed, step,
+               positions);
   }
   DRT_HIP(hipGetLastError());
   if (scores && tokens) {

@@ -26,11 +26,19 @@
 #include <vector>
 
 #include "../../include/drt_rocm.h"
+#include "fused.h"
 #include "launch.h"
 
 namespace drt {
 
 thread_local std::string g_last_error;
+thread_local Profiler* g_prof = nullptr;
+
+// Installs a session's profiler on this thread for the duration of a call.
+struct ProfScope {
+  explicit ProfScope(Profiler* p) { g_prof = p; }
+  ~ProfScope() { g_prof = nullptr; }
+};
 
 // ------------------------------------------------------------------ handles
 
@@ -101,9 +109,9 @@ struct Runtime {
   int max_rows = 0;
 
   // workspace (sized for max_rows)
-  DevBuf hidden, act, xsum, act_lm, xsum_lm, part, qbuf, attn_part, stats, scores, tokens_out,
-      lm_rows, lm_pos, logits;
-  size_t part_bytes = 0, attn_part_budget = 0;
+  DevBuf hidden, act, xsum, act_lm, xsum_lm, qbuf, attn_part, stats, scores, tokens_out, lm_rows,
+      lm_pos, logits, desc;
+  size_t attn_part_budget = 0;
   int logits_rows_cap = 0;
 
   ~Runtime() {
@@ -157,9 +165,31 @@ void copy_bf16_vec(DevBuf& dst, const WeightMap& wm, const std::string& name, in
   DRT_HIP(hipMemcpyAsync(dst.p, t.data, (size_t)n * 2, hipMemcpyDeviceToDevice, s));
 }
 
+// Device n-tile offsets of a part's 64-row block b when parts are interleaved in
+// 64-column blocks ([gate 64 | up 64] per 128 columns, for the SwiGLU epilogue).
+void repack_rows(LinearW& w, const WeightMap& wm, const std::string& part, int row0, int rows,
+                 int dst_tile, int K, bool q4, hipStream_t s) {
+  if (q4) {
+    const drt_tensor& wq = wm.get(part + ".weight");
+    const drt_tensor& sc = wm.get(part + ".scales");
+    const drt_tensor& bi = wm.get(part + ".biases");
+    const int G = K / 64;
+    q4_repack((const uint32_t*)wq.data + (size_t)row0 * (K / 8),
+              (const uint16_t*)sc.data + (size_t)row0 * G, (const uint16_t*)bi.data + (size_t)row0 * G,
+              rows, K, w.qw.as<uint32_t>() + (size_t)dst_tile * G * 256,
+              w.sb.as<uint32_t>() + (size_t)dst_tile * G * 32, s);
+  } else {
+    const drt_tensor& wt = wm.get(part + ".weight");
+    bf16_repack((const uint16_t*)wt.data + (size_t)row0 * K, rows, K,
+                w.wb.as<uint16_t>() + (size_t)dst_tile * 32 * K, s);
+  }
+}
+
 // Build one fused linear from parts stacked along N (each part N_i rows, same K).
+// interleave64: two parts of equal N laid out as [p0 64 | p1 64] per 128 columns.
 void build_linear(LinearW& w, const WeightMap& wm, const std::vector<std::string>& parts,
-                  const std::vector<int>& Ns, int K, bool q4, bool with_bias, hipStream_t s) {
+                  const std::vector<int>& Ns, int K, bool q4, bool with_bias, hipStream_t s,
+                  bool interleave64 = false) {
   int N = 0;
   for (int n : Ns) N += n;
   w.N = N;
@@ -172,31 +202,32 @@ void build_linear(LinearW& w, const WeightMap& wm, const std::vector<std::string
   } else {
     w.wb.alloc((size_t)N * K * 2);
   }
-  int n0 = 0;
   for (size_t i = 0; i < parts.size(); ++i) {
     const int n = Ns[i];
-    require(n % 32 == 0, "linear out-dim must be a multiple of 32");
+    require(n % (interleave64 ? 64 : 32) == 0, "linear out-dim must be a multiple of 32");
     if (q4) {
-      const drt_tensor& wq = wm.get(parts[i] + ".weight");
-      const drt_tensor& sc = wm.get(parts[i] + ".scales");
-      const drt_tensor& bi = wm.get(parts[i] + ".biases");
-      check_tensor(wq, DRT_I32, {n, K / 8});
-      check_tensor(sc, DRT_BF16, {n, K / 64});
-      check_tensor(bi, DRT_BF16, {n, K / 64});
-      // tile layout is n-tile major, so part i starts at n-tile n0/32
-      q4_repack((const uint32_t*)wq.data, (const uint16_t*)sc.data, (const uint16_t*)bi.data, n,
-                K, w.qw.as<uint32_t>() + (size_t)(n0 / 32) * (K / 64) * 256,
-                w.sb.as<uint32_t>() + (size_t)(n0 / 32) * (K / 64) * 32, s);
+      check_tensor(wm.get(parts[i] + ".weight"), DRT_I32, {n, K / 8});
+      check_tensor(wm.get(parts[i] + ".scales"), DRT_BF16, {n, K / 64});
+      check_tensor(wm.get(parts[i] + ".biases"), DRT_BF16, {n, K / 64});
     } else {
-      const drt_tensor& wt = wm.get(parts[i] + ".weight");
-      check_tensor(wt, DRT_BF16, {n, K});
-      bf16_repack((const uint16_t*)wt.data, n, K, w.wb.as<uint16_t>() + (size_t)n0 * K, s);
+      check_tensor(wm.get(parts[i] + ".weight"), DRT_BF16, {n, K});
     }
-    n0 += n;
+  }
+  if (interleave64) {
+    require(parts.size() == 2 && Ns[0] == Ns[1], "interleaving needs two equal parts");
+    for (int b = 0; b < Ns[0] / 64; ++b)
+      for (int i = 0; i < 2; ++i) repack_rows(w, wm, parts[i], 64 * b, 64, 4 * b + 2 * i, K, q4, s);
+  } else {
+    int n0 = 0;
+    for (size_t i = 0; i < parts.size(); ++i) {
+      repack_rows(w, wm, parts[i], 0, Ns[i], n0 / 32, K, q4, s);
+      n0 += Ns[i];
+    }
   }
   if (with_bias) {
+    require(!interleave64, "biases are not interleaved");
     w.bias.alloc((size_t)N * 2);
-    n0 = 0;
+    int n0 = 0;
     for (size_t i = 0; i < parts.size(); ++i) {
       const drt_tensor& b = wm.get(parts[i] + ".bias");
       check_tensor(b, DRT_BF16, {Ns[i]});
@@ -262,7 +293,8 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
                  {p + "self_attn.q_proj", p + "self_attn.k_proj", p + "self_attn.v_proj"},
                  {Hq * hd, Hkv * hd, Hkv * hd}, d, rt->q4, g.qkv_bias != 0, s);
     build_linear(L.o, wm, {p + "self_attn.o_proj"}, {d}, Hq * hd, rt->q4, false, s);
-    build_linear(L.gu, wm, {p + "mlp.gate_proj", p + "mlp.up_proj"}, {F, F}, d, rt->q4, false, s);
+    build_linear(L.gu, wm, {p + "mlp.gate_proj", p + "mlp.up_proj"}, {F, F}, d, rt->q4, false, s,
+                 /*interleave64=*/true);
     build_linear(L.down, wm, {p + "mlp.down_proj"}, {d}, F, rt->q4, false, s);
     copy_bf16_vec(L.in_norm, wm, p + "input_layernorm.weight", d, s);
     copy_bf16_vec(L.post_norm, wm, p + "post_attention_layernorm.weight", d, s);
@@ -292,17 +324,7 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
   rt->act.alloc((size_t)M * widest * 2);
   rt->xsum.alloc((size_t)M * (widest / 64) * 4);
   rt->qbuf.alloc((size_t)M * Hq * hd * 2);
-  // partials: the largest of any linear's plan at M rows or at 32 rows
-  size_t pb = 0;
-  for (int rows : {32, M}) {
-    for (const LinearW* w : {&rt->layers[0].qkv, &rt->layers[0].o, &rt->layers[0].gu,
-                             &rt->layers[0].down}) {
-      const SplitPlan sp = plan_linear(*w, rows);
-      pb = std::max(pb, (size_t)sp.splits * rows * w->N * 4);
-    }
-  }
-  rt->part_bytes = pb;
-  rt->part.alloc(pb);
+  rt->desc.alloc(sizeof(StepDesc));
   rt->attn_part_budget = std::max<size_t>((size_t)64 << 20,
                                           (size_t)Hkv * M * (Hq / Hkv) * 130 * 4);
   rt->attn_part.alloc(rt->attn_part_budget);
@@ -317,7 +339,7 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
   DRT_HIP(hipStreamSynchronize(s));
   size_t total = rt->embed.bytes + rt->final_norm.bytes + rt->lm_head.qw.bytes +
                  rt->lm_head.sb.bytes + rt->lm_head.wb.bytes + rt->hidden.bytes + rt->act.bytes +
-                 rt->part.bytes + rt->attn_part.bytes + rt->stats.bytes;
+                 rt->attn_part.bytes + rt->stats.bytes;
   for (auto& L : rt->layers)
     for (LinearW* w : {&L.qkv, &L.o, &L.gu, &L.down}) total += w->qw.bytes + w->sb.bytes + w->wb.bytes;
   if (e.creation_memory_budget_bytes > 0 && (int64_t)total > e.creation_memory_budget_bytes)
@@ -345,70 +367,147 @@ struct ForwardArgs {
   int step = 0;
 };
 
+// Rows [row0, row0 + n_rows) sit in one mask segment and see every key in
+// [0, n_keys): the decode attention kernel applies.
+bool one_segment(const ForwardArgs& a) {
+  if (a.mask_kind == 0) return true;
+  auto seg = [&](int p) { return p < a.mask_prompt_len ? -1 : (p - a.mask_prompt_len) / a.mask_block; };
+  const int s0 = seg(a.row0), s1 = seg(a.row0 + a.n_rows - 1);
+  if (s0 != s1) return false;
+  const int seg_end = s0 < 0 ? a.mask_prompt_len : a.mask_prompt_len + (s0 + 1) * a.mask_block;
+  return a.n_keys <= seg_end;
+}
+
+int decode_ranges(int n_keys) {
+  const int tiles = (n_keys + 31) / 32;
+  return std::max(1, std::min(32, (tiles + 7) / 8));
+}
+
 void run_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_stride,
                  const ForwardArgs& a) {
   hipStream_t s = rt.stream;
   const int M = a.n_rows, d = rt.d(), Hq = rt.Hq(), Hkv = rt.Hkv(), F = rt.F();
   const int fmt = rt.fmt();
-  const bool rnd = !rt.q4;  // bf16 weights: linear outputs are bf16-rounded
+  const int G = Hq / Hkv;
   const float eps = rt.geo.rms_norm_eps;
   require(M >= 1 && M <= rt.max_rows, "forward rows exceed max_forward_rows");
   require(a.row0 + M <= rt.rope_positions, "positions exceed the rotary table");
   require(a.n_lm <= M, "more LM rows than forwarded rows");
   float* hidden = rt.hidden.as<float>();
-  float* part = rt.part.as<float>();
   float* xs = rt.xsum.as<float>();
   // both cache dtypes are 2 bytes per element
   auto kv_layer = [&](int l) { return (void*)((char*)kv + (size_t)l * layer_stride * 2); };
 
-  embed(a.tokens_dev + a.row0, rt.embed.as<uint16_t>(), hidden, M, d, s);
-  residual_norm(hidden, nullptr, 0, M, false, nullptr, false, rt.layers[0].in_norm.as<uint16_t>(),
-                eps, d, fmt, rt.act.p, xs, M, s);
-  const AttnPlan ap = plan_attention(M, Hq, Hkv, a.n_keys, rt.attn_part_budget);
-  const size_t apb = attention_part_bytes(ap, M, Hq, Hkv);
+  StepDesc hd{};
+  hd.row0 = a.row0;
+  hd.n_rows = M;
+  hd.n_keys = a.n_keys;
+  hd.n_lm = a.n_lm;
+  hd.mask_kind = a.mask_kind;
+  hd.mask_prompt_len = a.mask_prompt_len;
+  hd.mask_block = a.mask_block;
+  hd.step = a.step;
+  hd.seed = a.seed;
+  hd.temperature = a.temperature;
+  DRT_HIP(hipMemcpyAsync(rt.desc.p, &hd, sizeof(hd), hipMemcpyHostToDevice, s));
+  const StepDesc* desc = rt.desc.as<StepDesc>();
+
+  const bool decode_attn = M * G <= 64 && one_segment(a);
+  AttnPlan ap;
+  int ranges = 1;
+  size_t apb;
+  if (decode_attn) {
+    ranges = decode_ranges(a.n_keys);
+    apb = (size_t)ranges * Hkv * M * G * 130 * 4;
+  } else {
+    ap = plan_attention(M, Hq, Hkv, a.n_keys, rt.attn_part_budget);
+    apb = attention_part_bytes(ap, M, Hq, Hkv);
+  }
   require(apb <= rt.attn_part.bytes, "attention partials exceed the workspace");
+  const int splits = decode_attn ? ranges : ap.splits;
   float* o_part = rt.attn_part.as<float>();
-  float* ml_part = o_part + (size_t)ap.splits * Hkv * M * (Hq / Hkv) * 128;
+  float* ml_part = o_part + (size_t)splits * Hkv * M * G * 128;
   if (a.n_lm > 0) {
     DRT_HIP(hipMemcpyAsync(rt.lm_rows.p, a.lm_rows.data(), a.n_lm * 4, hipMemcpyHostToDevice, s));
     DRT_HIP(hipMemcpyAsync(rt.lm_pos.p, a.lm_pos.data(), a.n_lm * 4, hipMemcpyHostToDevice, s));
   }
+
+  embed(a.tokens_dev + a.row0, rt.embed.as<uint16_t>(), hidden, M, d, s);
   const int L = (int)rt.layers.size();
   for (int l = 0; l < L; ++l) {
     LayerW& w = rt.layers[l];
-    SplitPlan sp = plan_linear(w.qkv, M);
-    linear_partials(w.qkv, rt.act.p, xs, M, part, sp, s);
-    qkv_epilogue(rt.kv_bf16, part, sp.splits, M, w.qkv.bias.as<uint16_t>(), rnd,
-                 w.q_norm.as<uint16_t>(), w.k_norm.as<uint16_t>(), eps, rt.rope_cos.as<float>(),
-                 rt.rope_sin.as<float>(), a.row0, Hq, Hkv, rt.qbuf.p, kv_layer(l), head_stride, s);
-    attention(rt.kv_bf16, rt.qbuf.p, kv_layer(l), head_stride, M, Hq, Hkv, a.n_keys, a.row0,
-              a.mask_kind, a.mask_prompt_len, a.mask_block, ap, o_part, ml_part, rt.act.p, xs,
-              fmt, s);
+    auto base = [&](const LinearW& lw) {
+      FusedArgs f;
+      f.qw = lw.q4 ? lw.qw.as<uint32_t>() : nullptr;
+      f.sb = lw.q4 ? lw.sb.as<uint32_t>() : nullptr;
+      f.wb = lw.q4 ? nullptr : lw.wb.as<uint16_t>();
+      f.bias = lw.bias.as<uint16_t>();
+      f.M = M;
+      f.N = lw.N;
+      f.K = lw.K;
+      f.eps = eps;
+      f.rnd_bf16 = !rt.q4;
+      f.desc = desc;
+      return f;
+    };
+    {  // input RMSNorm -> fused q|k|v -> q/k norm + RoPE -> Q, K/V cache
+      FusedArgs f = base(w.qkv);
+      f.hidden = hidden;
+      f.norm_w = w.in_norm.as<uint16_t>();
+      f.q_norm = w.q_norm.as<uint16_t>();
+      f.k_norm = w.k_norm.as<uint16_t>();
+      f.rope_cos = rt.rope_cos.as<float>();
+      f.rope_sin = rt.rope_sin.as<float>();
+      f.q_out = rt.qbuf.p;
+      f.kv_layer = kv_layer(l);
+      f.kv_head_stride = head_stride;
+      f.Hq = Hq;
+      f.Hkv = Hkv;
+      f.kv_bf16 = rt.kv_bf16;
+      fused_linear(f, FL_QKV, s);
+    }
+    if (decode_attn)
+      attention_decode(rt.kv_bf16, rt.qbuf.p, kv_layer(l), head_stride, M, Hq, Hkv, a.n_keys, desc,
+                       ranges, o_part, ml_part, rt.act.p, xs, fmt, s);
+    else
+      attention(rt.kv_bf16, rt.qbuf.p, kv_layer(l), head_stride, M, Hq, Hkv, a.n_keys, a.row0,
+                a.mask_kind, a.mask_prompt_len, a.mask_block, ap, o_part, ml_part, rt.act.p, xs,
+                fmt, s);
     const bool last = l == L - 1;
     if (last && a.n_lm == 0) break;  // commit-only forward: every layer's K/V is written
-    sp = plan_linear(w.o, M);
-    linear_partials(w.o, rt.act.p, xs, M, part, sp, s);
-    residual_norm(hidden, part, sp.splits, M, rnd, nullptr, true, w.post_norm.as<uint16_t>(), eps,
-                  d, fmt, rt.act.p, xs, M, s);
-    sp = plan_linear(w.gu, M);
-    linear_partials(w.gu, rt.act.p, xs, M, part, sp, s);
-    swiglu(part, sp.splits, M, F, rnd, fmt, rt.act.p, xs, s);
-    sp = plan_linear(w.down, M);
-    linear_partials(w.down, rt.act.p, xs, M, part, sp, s);
-    if (!last) {
-      residual_norm(hidden, part, sp.splits, M, rnd, nullptr, true,
-                    rt.layers[l + 1].in_norm.as<uint16_t>(), eps, d, fmt, rt.act.p, xs, M, s);
-    } else {
-      residual_norm(hidden, part, sp.splits, M, rnd, rt.lm_rows.as<int32_t>(), false,
-                    rt.final_norm.as<uint16_t>(), eps, d, fmt, rt.act_lm.p, rt.xsum_lm.as<float>(),
-                    a.n_lm, s);
+    {  // o_proj + residual
+      FusedArgs f = base(w.o);
+      f.act = rt.act.p;
+      f.act_xsum = xs;
+      f.hidden_out = hidden;
+      fused_linear(f, FL_RESID, s);
+    }
+    {  // post-attention RMSNorm -> [gate | up] -> SwiGLU -> down activation
+      FusedArgs f = base(w.gu);
+      f.hidden = hidden;
+      f.norm_w = w.post_norm.as<uint16_t>();
+      f.act_out = rt.act.p;
+      f.xsum_out = xs;
+      f.act_fmt = fmt;
+      fused_linear(f, FL_SWIGLU, s);
+    }
+    {  // down_proj + residual
+      FusedArgs f = base(w.down);
+      f.act = rt.act.p;
+      f.act_xsum = xs;
+      f.hidden_out = hidden;
+      fused_linear(f, FL_RESID, s);
     }
   }
   if (a.n_lm > 0) {
+    residual_norm(hidden, nullptr, 0, M, false, rt.lm_rows.as<int32_t>(), false,
+                  rt.final_norm.as<uint16_t>(), eps, d, fmt, rt.act_lm.p, rt.xsum_lm.as<float>(),
+                  a.n_lm, s);
     lmhead(rt.lm_head, rt.act_lm.p, rt.xsum_lm.as<float>(), a.n_lm, a.logits, rt.stats.p,
            a.temperature, a.seed, a.step, rt.lm_pos.as<int32_t>(), rt.scores.as<double>(),
            rt.tokens_out.as<int32_t>(), s);
   }
+  (void)F;
 }
 
 // ------------------------------------------------------------------ session
@@ -431,6 +530,16 @@ struct Session {
   int win_prompt_len = -1, win_block = -1;
   std::vector<int32_t> win_tokens;
   drt_metrics m{};
+  Profiler prof;
+
+  void publish_profile() {
+    prof.collect();
+    for (int c = 0; c < Profiler::NCLASS; ++c) {
+      m.prof_ms[c] = prof.ms[c];
+      m.prof_bytes[c] = prof.bytes[c];
+      m.prof_launches[c] = prof.launches[c];
+    }
+  }
 
   // Grow the cache to hold n_tokens rows. Existing tiles keep their contents
   // (copied head by head), so a longer window does not lose the exact prefix.
@@ -643,6 +752,7 @@ int32_t drt_session_propose(uint64_t session, const int32_t* frontier, int32_t n
     require(s->started, "propose_device before start_device");
     require(frontier && n_frontier > 0 && out_scores && out_tokens,
             "propose_device needs a non-empty frontier and outputs");
+    ProfScope ps(&s->prof);
     const int n = (int)s->canvas.size();
     DRT_HIP(hipSetDevice(r.device));
     ForwardArgs a;
@@ -704,6 +814,7 @@ int32_t drt_session_propose(uint64_t session, const int32_t* frontier, int32_t n
                            hipMemcpyDeviceToHost, r.stream));
     DRT_HIP(hipStreamSynchronize(r.stream));
     s->finish_timing();
+    s->publish_profile();
     s->proposals += 1;
     s->m.forward_count += 1;
     s->m.active_rows += a.n_rows;
@@ -747,6 +858,7 @@ int32_t drt_session_execute_window(uint64_t session, const int32_t* token_ids, i
     for (int i = 0; i < n_scope; ++i)
       require(scope[i] >= 0 && scope[i] < n_tokens, "scope position outside the window");
     const bool d2f = mask_block_size > 0;
+    ProfScope ps(&s->prof);
     if (s->cfg.attention_mask_kind == DRT_MASK_D2F_HYBRID)
       require(d2f, "a d2f_hybrid session needs the window's mask geometry");
     else
@@ -820,6 +932,7 @@ int32_t drt_session_execute_window(uint64_t session, const int32_t* token_ids, i
                            hipMemcpyDeviceToHost, r.stream));
     DRT_HIP(hipStreamSynchronize(r.stream));
     s->finish_timing();
+    s->publish_profile();
     s->m.forward_count += 1;
     s->m.active_rows += a.n_rows;
     s->m.lm_rows += n_scope;
@@ -837,15 +950,26 @@ int32_t drt_session_metrics(uint64_t session, drt_metrics* out) {
   });
 }
 
+int32_t drt_session_set_profiling(uint64_t session, int32_t enable) {
+  return guarded([&] {
+    auto s = handles().get<Session>(session, Kind::SESSION);
+    if (enable && !s->prof.on) {
+      s->prof.reset();
+      for (int c = 0; c < Profiler::NCLASS; ++c) {
+        s->m.prof_ms[c] = 0;
+        s->m.prof_bytes[c] = 0;
+        s->m.prof_launches[c] = 0;
+      }
+    }
+    s->prof.on = enable != 0;
+  });
+}
+
 // ------------------------------------------------------------------ per-op
 
 size_t drt_op_q4_linear_workspace_bytes(int32_t m, int32_t n, int32_t k) {
-  LinearW w;
-  w.N = n;
-  w.K = k;
-  w.q4 = true;
-  const SplitPlan p = plan_linear(w, m);
-  return (size_t)m * k * 2 + (size_t)m * (k / 64) * 4 + (size_t)p.splits * m * n * 4 + 256;
+  if (m <= 0 || k <= 0) return 0;
+  return (size_t)m * k * 2 + (size_t)m * (k / 64) * 4 + 256;
 }
 
 int32_t drt_op_q4_repack(const void* w_q, const void* scales, const void* biases, int32_t n,
@@ -866,29 +990,22 @@ int32_t drt_op_q4_linear(const void* qw, const void* sb, const void* x, int32_t 
     require(x_dtype == DRT_F32 || x_dtype == DRT_BF16, "q4_linear x must be F32 or BF16");
     require(workspace && workspace_bytes >= drt_op_q4_linear_workspace_bytes(m, n, k),
             "q4_linear workspace too small");
-    LinearW w;
-    w.N = n;
-    w.K = k;
-    w.q4 = true;
-    w.qw.p = const_cast<void*>(qw);
-    w.sb.p = const_cast<void*>(sb);
-    const SplitPlan p = plan_linear(w, m);
     char* ws = (char*)workspace;
     _Float16* xp = (_Float16*)ws;
     float* xs = (float*)(ws + (size_t)m * k * 2);
-    float* part = (float*)(ws + (size_t)m * k * 2 + (size_t)m * (k / 64) * 4);
     hipStream_t st = as_stream(stream);
-    try {
-      q4_act_prep(x, x_dtype == DRT_BF16, m, k, xp, xs, st);
-      linear_partials(w, xp, xs, m, part, p, st);
-      splitk_reduce(part, p.splits, (const uint16_t*)bias, y, m, n, st);
-    } catch (...) {
-      w.qw.p = nullptr;
-      w.sb.p = nullptr;
-      throw;
-    }
-    w.qw.p = nullptr;  // borrowed
-    w.sb.p = nullptr;
+    q4_act_prep(x, x_dtype == DRT_BF16, m, k, xp, xs, st);
+    FusedArgs f;
+    f.qw = (const uint32_t*)qw;
+    f.sb = (const uint32_t*)sb;
+    f.bias = (const uint16_t*)bias;
+    f.M = m;
+    f.N = n;
+    f.K = k;
+    f.act = xp;
+    f.act_xsum = xs;
+    f.y = y;
+    fused_linear(f, FL_STORE, st);
   });
 }
 
@@ -900,12 +1017,8 @@ int32_t drt_op_bf16_repack(const void* w, int32_t n, int32_t k, void* wb, void* 
 }
 
 size_t drt_op_bf16_linear_workspace_bytes(int32_t m, int32_t n, int32_t k) {
-  LinearW w;
-  w.N = n;
-  w.K = k;
-  w.q4 = false;
-  const SplitPlan p = plan_linear(w, m);
-  return (size_t)p.splits * m * n * 4 + 256;
+  (void)m; (void)n; (void)k;
+  return 256;
 }
 
 int32_t drt_op_bf16_linear(const void* wb, const void* x, int32_t m, int32_t n, int32_t k,
@@ -914,20 +1027,18 @@ int32_t drt_op_bf16_linear(const void* wb, const void* x, int32_t m, int32_t n, 
   return guarded([&] {
     require(wb && x && y && m > 0 && n > 0 && k > 0, "bad bf16_linear arguments");
     require(n % 32 == 0 && k % 16 == 0, "bf16_linear needs n % 32 == 0 and k % 16 == 0");
-    require(workspace && workspace_bytes >= drt_op_bf16_linear_workspace_bytes(m, n, k),
-            "bf16_linear workspace too small");
-    LinearW w;
-    w.N = n;
-    w.K = k;
-    w.q4 = false;
-    const SplitPlan p = plan_linear(w, m);
-    hipStream_t st = as_stream(stream);
-    bf16_linear_partials((const uint16_t*)wb, (const uint16_t*)x, m, n, k, (float*)workspace,
-                         p.splits, p.per_split, st);
-    // reduce, then round to bf16 as the bf16 matmul output is (bias added after)
-    const int64_t total = (int64_t)m * n;
-    splitk_reduce((const float*)workspace, p.splits, nullptr, y, m, n, st);
-    round_bf16_inplace(y, total, (const uint16_t*)bias, n, st);
+    (void)workspace;
+    (void)workspace_bytes;
+    FusedArgs f;
+    f.wb = (const uint16_t*)wb;
+    f.bias = (const uint16_t*)bias;
+    f.M = m;
+    f.N = n;
+    f.K = k;
+    f.act = x;
+    f.rnd_bf16 = 1;  // the bf16 matmul output is bf16; the bias is added after
+    f.y = y;
+    fused_linear(f, FL_STORE, as_stream(stream));
   });
 }
 
@@ -948,7 +1059,9 @@ int32_t drt_op_kv_pack(const void* k, const void* v, int32_t src_dtype, int32_t 
 size_t drt_op_attention_workspace_bytes(int32_t rows, int32_t hq, int32_t hkv, int32_t n_keys) {
   if (rows <= 0 || hq <= 0 || hkv <= 0 || hq % hkv || n_keys <= 0) return 0;
   const AttnPlan p = plan_attention(rows, hq, hkv, n_keys, (size_t)256 << 20);
-  return attention_part_bytes(p, rows, hq, hkv) + (size_t)rows * hq * 128 * 2 + 256;
+  const size_t general = attention_part_bytes(p, rows, hq, hkv);
+  const size_t decode = (size_t)decode_ranges(n_keys) * hkv * rows * (hq / hkv) * 130 * 4;
+  return std::max(general, decode) + 256;
 }
 
 int32_t drt_op_attention(const void* q, const void* cache, int64_t head_stride, int32_t kv_dtype,
@@ -968,13 +1081,27 @@ int32_t drt_op_attention(const void* q, const void* cache, int64_t head_stride, 
     require(head_stride >= (int64_t)((n_keys + 31) / 32) * 8192, "n_keys exceed the cache");
     require(workspace && workspace_bytes >= drt_op_attention_workspace_bytes(rows, hq, hkv, n_keys),
             "attention workspace too small");
-    const AttnPlan p = plan_attention(rows, hq, hkv, n_keys, (size_t)256 << 20);
+    ForwardArgs fa;
+    fa.row0 = row_pos0;
+    fa.n_rows = rows;
+    fa.n_keys = n_keys;
+    fa.mask_kind = mask_kind == DRT_MASK_D2F_HYBRID ? 1 : 0;
+    fa.mask_prompt_len = mask_prompt_len;
+    fa.mask_block = std::max(1, mask_block_size);
     float* o_part = (float*)workspace;
-    float* ml_part = o_part + (size_t)p.splits * hkv * rows * (hq / hkv) * 128;
-    attention(kv_dtype == DRT_BF16, q, cache, head_stride, rows, hq, hkv, n_keys, row_pos0,
-              mask_kind == DRT_MASK_D2F_HYBRID ? 1 : 0, mask_prompt_len,
-              std::max(1, mask_block_size), p, o_part, ml_part, out, nullptr,
-              out_dtype == DRT_F32 ? 2 : 3, as_stream(stream));
+    const int ofmt = out_dtype == DRT_F32 ? 2 : 3;
+    if (rows * (hq / hkv) <= 64 && one_segment(fa)) {
+      const int ranges = decode_ranges(n_keys);
+      float* ml_part = o_part + (size_t)ranges * hkv * rows * (hq / hkv) * 128;
+      attention_decode(kv_dtype == DRT_BF16, q, cache, head_stride, rows, hq, hkv, n_keys,
+                       nullptr, ranges, o_part, ml_part, out, nullptr, ofmt, as_stream(stream));
+    } else {
+      const AttnPlan p = plan_attention(rows, hq, hkv, n_keys, (size_t)256 << 20);
+      float* ml_part = o_part + (size_t)p.splits * hkv * rows * (hq / hkv) * 128;
+      attention(kv_dtype == DRT_BF16, q, cache, head_stride, rows, hq, hkv, n_keys, row_pos0,
+                fa.mask_kind, mask_prompt_len, fa.mask_block, p, o_part, ml_part, out, nullptr,
+                ofmt, as_stream(stream));
+    }
   });
 }
 

@@ -247,7 +247,19 @@ class DeviceSession:
     def device_metrics(self) -> dict:
         m = _lib.Metrics()
         _lib.check(self._lib.drt_session_metrics(self.handle, C.byref(m)))
-        return {"rocm_" + name: getattr(m, name) for name, _ in _lib.Metrics._fields_}
+        out = {}
+        for name, _ in _lib.Metrics._fields_:
+            v = getattr(m, name)
+            if name.startswith("prof_"):
+                for i, cls in enumerate(("attention", "linear", "lm_head")):
+                    out[f"rocm_{name}_{cls}"] = v[i]
+            else:
+                out["rocm_" + name] = v
+        return out
+
+    def set_profiling(self, enable: bool) -> None:
+        """Time each attention / linear / LM-head dispatch (dispatch timestamps)."""
+        _lib.check(self._lib.drt_session_set_profiling(self.handle, int(bool(enable))))
 
     def close(self) -> None:
         if self._handle:

@@ -122,6 +122,12 @@ typedef struct drt_metrics {
   int64_t kv_cache_bytes;         /* device bytes held by the prefix K/V cache */
   double last_forward_ms;         /* device time of the last forward (HIP events) */
   double total_forward_ms;
+  /* per-dispatch device time while profiling is on (drt_session_set_profiling), by
+   * kernel class 0 = attention split, 1 = linear GEMMs, 2 = LM head: summed ms,
+   * summed algorithmic bytes, launch counts */
+  double prof_ms[3];
+  double prof_bytes[3];
+  int64_t prof_launches[3];
 } drt_metrics;
 
 /* ---- library / handles ---- */
@@ -166,6 +172,11 @@ int32_t drt_session_execute_window(uint64_t session, const int32_t* token_ids,
                                    int32_t* out_n_vocab, int32_t* out_forwarded_rows);
 /* session.device_metrics(). */
 int32_t drt_session_metrics(uint64_t session, drt_metrics* out);
+/* Time every attention / linear / LM-head dispatch of this session with its own
+ * dispatch timestamps (1 = on, 0 = off; switching on clears the counters). No
+ * counterpart in the reference: the stage timers of backends/mlx_forward.py:1447-1459
+ * are host wall clock. */
+int32_t drt_session_set_profiling(uint64_t session, int32_t enable);
 
 /* ---- per-op kernels: the KernelTable seam (backends/kernel_table.py:118-126) ---- */
 
