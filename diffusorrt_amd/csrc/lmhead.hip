@@ -59,8 +59,13 @@ __global__ __launch_bounds__(64 * WAVES) void lmhead_kernel(
     const uint32_t* __restrict__ qw, const uint32_t* __restrict__ sb,
     const uint16_t* __restrict__ wb, const void* __restrict__ x,
     const float* __restrict__ xsum, int M, int N, int K, int chunk_k,
-    float* __restrict__ logits_out, LmStat* __restrict__ stats, float temperature,
-    uint64_t seed, int step, const int32_t* __restrict__ positions) {
+    float* __restrict__ logits_out, LmStat* __restrict__ stats, float temperature_arg,
+    uint64_t seed_arg, int step_arg, const int32_t* __restrict__ positions,
+    const StepDesc* __restrict__ desc) {
+  // sampling controls come from the step descriptor when one is given (graph replays)
+  const float temperature = desc ? desc->temperature : temperature_arg;
+  const uint64_t seed = desc ? desc->seed : seed_arg;
+  const int step = desc ? desc->step : step_arg;
   constexpr int NT = 2;
   const int G = K >> 6, KC = K >> 4;
   const int NTILES = N >> 5, NB = N >> 6;
@@ -226,8 +231,11 @@ __global__ __launch_bounds__(64 * WAVES) void lmhead_kernel(
 
 // One 256-thread WG per row: join the N/64 block statistics in float64.
 extern "C" __global__ void lmhead_finalize_kernel(const LmStat* __restrict__ stats, int NB,
-                                                  int sampling, double* __restrict__ scores,
+                                                  int sampling_arg,
+                                                  const StepDesc* __restrict__ desc,
+                                                  double* __restrict__ scores,
                                                   int32_t* __restrict__ tokens) {
+  const int sampling = desc ? (desc->temperature > 0.f) : sampling_arg;
   __shared__ float red_f[4];
   __shared__ int red_i[4];
   __shared__ double red_d[4];
@@ -293,11 +301,11 @@ extern "C" __global__ void lmhead_finalize_kernel(const LmStat* __restrict__ sta
 template __global__ void lmhead_kernel<0, 4, 4>(const uint32_t*, const uint32_t*, const uint16_t*,
                                                 const void*, const float*, int, int, int, int,
                                                 float*, LmStat*, float, uint64_t, int,
-                                                const int32_t*);
+                                                const int32_t*, const StepDesc*);
 template __global__ void lmhead_kernel<1, 4, 8>(const uint32_t*, const uint32_t*, const uint16_t*,
                                                 const void*, const float*, int, int, int, int,
                                                 float*, LmStat*, float, uint64_t, int,
-                                                const int32_t*);
+                                                const int32_t*, const StepDesc*);
 
 namespace drt {
 
@@ -305,7 +313,7 @@ size_t lmhead_stats_bytes(int M, int N) { return (size_t)M * (N / 64) * sizeof(L
 
 void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* logits_out,
             void* stats, float temperature, uint64_t seed, int step, const int32_t* positions,
-            double* scores, int32_t* tokens, hipStream_t s) {
+            double* scores, int32_t* tokens, hipStream_t s, const StepDesc* desc) {
   require(w.N % 64 == 0, "lm head needs vocab % 64 == 0");
   require(M >= 1, "lm head needs at least one row");
   const int chunk_k = std::min(512, w.K);
@@ -322,7 +330,7 @@ void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* 
     const double bytes = (double)w.N * w.K / 2 + (double)w.N * w.K / 16 + 2.0 * M * w.K;
     DRT_LAUNCH(Profiler::LMHEAD, bytes, fn, grid, dim3(64 * WAVES), lds, s, w.qw.as<uint32_t>(),
                w.sb.as<uint32_t>(), (const uint16_t*)nullptr, act, xsum, M, w.N, w.K, chunk_k,
-               logits_out, (LmStat*)stats, temperature, seed, step, positions);
+               logits_out, (LmStat*)stats, temperature, seed, step, positions, desc);
   } else {
     auto fn = lmhead_kernel<1, WAVES, 8>;
     static size_t granted = 0;
@@ -331,12 +339,12 @@ void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* 
     DRT_LAUNCH(Profiler::LMHEAD, bytes, fn, grid, dim3(64 * WAVES), lds, s,
                (const uint32_t*)nullptr, (const uint32_t*)nullptr, w.wb.as<uint16_t>(), act, xsum,
                M, w.N, w.K, chunk_k, logits_out, (LmStat*)stats, temperature, seed, step,
-               positions);
+               positions, desc);
   }
   DRT_HIP(hipGetLastError());
   if (scores && tokens) {
     hipLaunchKernelGGL(lmhead_finalize_kernel, dim3(M), dim3(256), 0, s, (const LmStat*)stats, NB,
-                       (int)(temperature > 0.f), scores, tokens);
+                       (int)(temperature > 0.f), desc, scores, tokens);
     DRT_HIP(hipGetLastError());
   }
 }

@@ -18,6 +18,7 @@
 
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -110,12 +111,26 @@ struct Runtime {
 
   // workspace (sized for max_rows)
   DevBuf hidden, act, xsum, act_lm, xsum_lm, qbuf, attn_part, stats, scores, tokens_out, lm_rows,
-      lm_pos, logits, desc;
+      lm_pos, logits;
+  // Per-forward inputs: one pinned host slot + its device copy per forward, moved
+  // by a single async copy. Slot 0 belongs to the commit graph, slot 1 to the
+  // step graph; eager forwards rotate through the rest.
+  struct StepUpload {
+    StepDesc desc;
+    int32_t lm_rows[32];
+    int32_t lm_pos[32];
+    int32_t tokens[32];
+  };
+  static constexpr int UPLOAD_SLOTS = 64;
+  StepUpload* up_host = nullptr;
+  DevBuf up_dev;
+  int up_next = 2;
   size_t attn_part_budget = 0;
   int logits_rows_cap = 0;
 
   ~Runtime() {
     if (stream) (void)hipStreamSynchronize(stream);
+    if (up_host) (void)hipHostFree(up_host);
     if (ev0) (void)hipEventDestroy(ev0);
     if (ev1) (void)hipEventDestroy(ev1);
     if (stream) (void)hipStreamDestroy(stream);
@@ -324,7 +339,9 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
   rt->act.alloc((size_t)M * widest * 2);
   rt->xsum.alloc((size_t)M * (widest / 64) * 4);
   rt->qbuf.alloc((size_t)M * Hq * hd * 2);
-  rt->desc.alloc(sizeof(StepDesc));
+  DRT_HIP(hipHostMalloc((void**)&rt->up_host, sizeof(Runtime::StepUpload) * Runtime::UPLOAD_SLOTS,
+                        hipHostMallocDefault));
+  rt->up_dev.alloc(sizeof(Runtime::StepUpload) * Runtime::UPLOAD_SLOTS);
   rt->attn_part_budget = std::max<size_t>((size_t)64 << 20,
                                           (size_t)Hkv * M * (Hq / Hkv) * 130 * 4);
   rt->attn_part.alloc(rt->attn_part_budget);
@@ -356,7 +373,7 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
 // the given row indices (relative to row0) and produces scores/tokens (and
 // logits when `logits` is non-null).
 struct ForwardArgs {
-  const int32_t* tokens_dev;  // device tokens of the whole canvas
+  const int32_t* tokens_dev = nullptr;  // device tokens of the whole canvas
   int row0 = 0, n_rows = 0, n_keys = 0;
   int mask_kind = 0, mask_prompt_len = 0, mask_block = 1;
   int n_lm = 0;
@@ -383,10 +400,79 @@ int decode_ranges(int n_keys) {
   return std::max(1, std::min(32, (tiles + 7) / 8));
 }
 
-void run_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_stride,
-                 const ForwardArgs& a) {
+// Device addresses of one forward's inputs.
+struct ForwardPtrs {
+  const StepDesc* desc = nullptr;
+  const int32_t* tokens_rel = nullptr;  // tokens of rows 0 .. n_rows-1 of this forward
+  const int32_t* lm_rows = nullptr;
+  const int32_t* lm_pos = nullptr;
+  int n_lm_launch = 0;  // LM rows launched (graph mode pads to 32)
+  int ranges = 0;       // decode-attention ranges (0: from n_keys)
+};
+
+// Upload the forward's descriptor, LM rows and (graph mode) tokens with one
+// async copy from a pinned slot. slot < 0 takes the next eager slot.
+ForwardPtrs stage_forward(Runtime& rt, const ForwardArgs& a, int slot, bool graph_mode,
+                          const int32_t* tokens_host) {
   hipStream_t s = rt.stream;
-  const int M = a.n_rows, d = rt.d(), Hq = rt.Hq(), Hkv = rt.Hkv(), F = rt.F();
+  if (slot < 0) {
+    if (rt.up_next >= Runtime::UPLOAD_SLOTS) {  // every slot in flight: drain first
+      DRT_HIP(hipStreamSynchronize(s));
+      rt.up_next = 2;
+    }
+    slot = rt.up_next++;
+  }
+  Runtime::StepUpload* u = rt.up_host + slot;
+  Runtime::StepUpload* d = rt.up_dev.as<Runtime::StepUpload>() + slot;
+  StepDesc& hd = u->desc;
+  hd = StepDesc{};
+  hd.row0 = a.row0;
+  hd.n_rows = a.n_rows;
+  hd.n_keys = a.n_keys;
+  hd.n_lm = a.n_lm;
+  hd.mask_kind = a.mask_kind;
+  hd.mask_prompt_len = a.mask_prompt_len;
+  hd.mask_block = a.mask_block;
+  hd.step = a.step;
+  hd.seed = a.seed;
+  hd.temperature = a.temperature;
+  ForwardPtrs p;
+  p.desc = &d->desc;
+  if (a.n_lm <= 32) {
+    const int n = graph_mode && a.n_lm > 0 ? 32 : a.n_lm;
+    for (int i = 0; i < n; ++i) {
+      // pad by repeating the last row (independent rows; padded results are unread)
+      const int j = std::min(i, a.n_lm - 1);
+      u->lm_rows[i] = a.lm_rows[j];
+      u->lm_pos[i] = a.lm_pos[j];
+    }
+    p.lm_rows = d->lm_rows;
+    p.lm_pos = d->lm_pos;
+    p.n_lm_launch = n;
+  } else {
+    DRT_HIP(hipMemcpyAsync(rt.lm_rows.p, a.lm_rows.data(), a.n_lm * 4, hipMemcpyHostToDevice, s));
+    DRT_HIP(hipMemcpyAsync(rt.lm_pos.p, a.lm_pos.data(), a.n_lm * 4, hipMemcpyHostToDevice, s));
+    p.lm_rows = rt.lm_rows.as<int32_t>();
+    p.lm_pos = rt.lm_pos.as<int32_t>();
+    p.n_lm_launch = a.n_lm;
+  }
+  if (graph_mode) {
+    require(a.n_rows <= 32 && tokens_host, "graph forwards take at most 32 rows");
+    for (int i = 0; i < a.n_rows; ++i) u->tokens[i] = tokens_host[a.row0 + i];
+    p.tokens_rel = d->tokens;
+  } else {
+    p.tokens_rel = a.tokens_dev + a.row0;
+  }
+  DRT_HIP(hipMemcpyAsync(d, u, sizeof(Runtime::StepUpload), hipMemcpyHostToDevice, s));
+  return p;
+}
+
+// The kernels of one forward (no host copies: capturable into a HIP graph when
+// the shapes and pointers are fixed and every per-step value is in p.desc).
+void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_stride,
+                    const ForwardArgs& a, const ForwardPtrs& p) {
+  hipStream_t s = rt.stream;
+  const int M = a.n_rows, d = rt.d(), Hq = rt.Hq(), Hkv = rt.Hkv();
   const int fmt = rt.fmt();
   const int G = Hq / Hkv;
   const float eps = rt.geo.rms_norm_eps;
@@ -397,27 +483,14 @@ void run_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_strid
   float* xs = rt.xsum.as<float>();
   // both cache dtypes are 2 bytes per element
   auto kv_layer = [&](int l) { return (void*)((char*)kv + (size_t)l * layer_stride * 2); };
-
-  StepDesc hd{};
-  hd.row0 = a.row0;
-  hd.n_rows = M;
-  hd.n_keys = a.n_keys;
-  hd.n_lm = a.n_lm;
-  hd.mask_kind = a.mask_kind;
-  hd.mask_prompt_len = a.mask_prompt_len;
-  hd.mask_block = a.mask_block;
-  hd.step = a.step;
-  hd.seed = a.seed;
-  hd.temperature = a.temperature;
-  DRT_HIP(hipMemcpyAsync(rt.desc.p, &hd, sizeof(hd), hipMemcpyHostToDevice, s));
-  const StepDesc* desc = rt.desc.as<StepDesc>();
+  const StepDesc* desc = p.desc;
 
   const bool decode_attn = M * G <= 64 && one_segment(a);
   AttnPlan ap;
   int ranges = 1;
   size_t apb;
   if (decode_attn) {
-    ranges = decode_ranges(a.n_keys);
+    ranges = p.ranges > 0 ? p.ranges : decode_ranges(a.n_keys);
     apb = (size_t)ranges * Hkv * M * G * 130 * 4;
   } else {
     ap = plan_attention(M, Hq, Hkv, a.n_keys, rt.attn_part_budget);
@@ -427,12 +500,8 @@ void run_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_strid
   const int splits = decode_attn ? ranges : ap.splits;
   float* o_part = rt.attn_part.as<float>();
   float* ml_part = o_part + (size_t)splits * Hkv * M * G * 128;
-  if (a.n_lm > 0) {
-    DRT_HIP(hipMemcpyAsync(rt.lm_rows.p, a.lm_rows.data(), a.n_lm * 4, hipMemcpyHostToDevice, s));
-    DRT_HIP(hipMemcpyAsync(rt.lm_pos.p, a.lm_pos.data(), a.n_lm * 4, hipMemcpyHostToDevice, s));
-  }
 
-  embed(a.tokens_dev + a.row0, rt.embed.as<uint16_t>(), hidden, M, d, s);
+  embed(p.tokens_rel, rt.embed.as<uint16_t>(), hidden, M, d, s);
   const int L = (int)rt.layers.size();
   for (int l = 0; l < L; ++l) {
     LayerW& w = rt.layers[l];
@@ -500,14 +569,18 @@ void run_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_strid
     }
   }
   if (a.n_lm > 0) {
-    residual_norm(hidden, nullptr, 0, M, false, rt.lm_rows.as<int32_t>(), false,
-                  rt.final_norm.as<uint16_t>(), eps, d, fmt, rt.act_lm.p, rt.xsum_lm.as<float>(),
-                  a.n_lm, s);
-    lmhead(rt.lm_head, rt.act_lm.p, rt.xsum_lm.as<float>(), a.n_lm, a.logits, rt.stats.p,
-           a.temperature, a.seed, a.step, rt.lm_pos.as<int32_t>(), rt.scores.as<double>(),
-           rt.tokens_out.as<int32_t>(), s);
+    residual_norm(hidden, nullptr, 0, M, false, p.lm_rows, false, rt.final_norm.as<uint16_t>(),
+                  eps, d, fmt, rt.act_lm.p, rt.xsum_lm.as<float>(), p.n_lm_launch, s);
+    lmhead(rt.lm_head, rt.act_lm.p, rt.xsum_lm.as<float>(), p.n_lm_launch, a.logits, rt.stats.p,
+           a.temperature, a.seed, a.step, p.lm_pos, rt.scores.as<double>(),
+           rt.tokens_out.as<int32_t>(), s, desc);
   }
-  (void)F;
+}
+
+void run_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_stride,
+                 const ForwardArgs& a) {
+  const ForwardPtrs p = stage_forward(rt, a, -1, false, nullptr);
+  launch_forward(rt, kv, head_stride, layer_stride, a, p);
 }
 
 // ------------------------------------------------------------------ session
@@ -531,6 +604,63 @@ struct Session {
   std::vector<int32_t> win_tokens;
   drt_metrics m{};
   Profiler prof;
+  // HIP graphs of the two fixed-shape forwards of a block-diffusion decode: the
+  // commit of one finished block and the denoise step of the active block.
+  hipGraphExec_t g_commit = nullptr, g_step = nullptr;
+  bool g_commit_warm = false, g_step_warm = false;
+  int g_ranges = 0;
+  bool use_graphs = getenv("DRT_DISABLE_GRAPHS") == nullptr;
+
+  void drop_graphs() {
+    if (g_commit) (void)hipGraphExecDestroy(g_commit);
+    if (g_step) (void)hipGraphExecDestroy(g_step);
+    g_commit = g_step = nullptr;
+    g_commit_warm = g_step_warm = false;
+  }
+  ~Session() {
+    if (rt && rt->stream) (void)hipStreamSynchronize(rt->stream);
+    drop_graphs();
+  }
+
+  // Run a <= 32-row forward whose inputs live in a fixed upload slot: eager the
+  // first time (grants kernel attributes), captured into a graph the second
+  // time, replayed afterwards.
+  void graph_forward(bool commit, const ForwardArgs& a) {
+    Runtime& r = *rt;
+    hipGraphExec_t& exec = commit ? g_commit : g_step;
+    bool& warm = commit ? g_commit_warm : g_step_warm;
+    ForwardPtrs p = stage_forward(r, a, commit ? 0 : 1, true, canvas.data());
+    p.ranges = g_ranges;
+    if (!warm) {
+      launch_forward(r, kv.p, head_stride, layer_stride, a, p);
+      warm = true;
+      return;
+    }
+    if (!exec) {
+      hipGraph_t g = nullptr;
+      DRT_HIP(hipStreamBeginCapture(r.stream, hipStreamCaptureModeThreadLocal));
+      try {
+        launch_forward(r, kv.p, head_stride, layer_stride, a, p);
+      } catch (...) {
+        (void)hipStreamEndCapture(r.stream, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+      }
+      DRT_HIP(hipStreamEndCapture(r.stream, &g));
+      const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(g);
+      DRT_HIP(e);
+    }
+    DRT_HIP(hipGraphLaunch(exec, r.stream));
+  }
+
+  // Graph forwards apply to block-sized rows of a session whose decode
+  // attention covers the whole block (block rows x GQA group <= 64 vectors).
+  bool graphable(int rows) const {
+    const Runtime& r = *rt;
+    return use_graphs && !prof.on && rows == block && rows <= 32 &&
+           rows * (r.Hq() / r.Hkv()) <= 64;
+  }
 
   void publish_profile() {
     prof.collect();
@@ -559,8 +689,10 @@ struct Session {
       DRT_HIP(hipMemcpy2DAsync(grown.p, new_head * 2, kv.p, head_stride * 2, head_stride * 2,
                                rows, hipMemcpyDeviceToDevice, r.stream));
     DRT_HIP(hipStreamSynchronize(r.stream));
+    drop_graphs();  // captured forwards point at the old cache
     kv = std::move(grown);
     tile_cap = tiles;
+    g_ranges = decode_ranges(tile_cap * 32);
     head_stride = new_head;
     layer_stride = head_stride * r.Hkv();
     m.kv_cache_bytes = (int64_t)kv.bytes;
@@ -777,18 +909,38 @@ int32_t drt_session_propose(uint64_t session, const int32_t* frontier, int32_t n
       if (s->cache_len > frozen_prefix) s->cache_len = frozen_prefix;
       DRT_HIP(hipEventRecord(r.ev0, r.stream));
       if (s->cache_len < frozen_prefix) {
-        s->upload_tokens(s->cache_len, frozen_prefix);
-        s->commit_rows(s->cache_len, frozen_prefix, s->origin, s->block);
-        forwarded += frozen_prefix - s->cache_len;
+        const int todo = frozen_prefix - s->cache_len;
+        const bool by_block = s->graphable(s->block) && s->origin == 0 &&
+                              s->cache_len % s->block == 0 && todo % s->block == 0 &&
+                              todo <= 4 * s->block;
+        if (by_block) {
+          for (int b = s->cache_len; b < frozen_prefix; b += s->block) {
+            ForwardArgs c;
+            c.tokens_dev = s->tokens_dev.as<int32_t>();
+            c.row0 = b;
+            c.n_rows = s->block;
+            c.n_keys = b + s->block;
+            c.mask_kind = 1;
+            c.mask_prompt_len = s->origin;
+            c.mask_block = s->block;
+            s->graph_forward(true, c);
+            if (b + s->block < frozen_prefix) DRT_HIP(hipStreamSynchronize(r.stream));  // slot reuse
+            s->m.commit_rows += s->block;
+          }
+        } else {
+          s->upload_tokens(s->cache_len, frozen_prefix);
+          s->commit_rows(s->cache_len, frozen_prefix, s->origin, s->block);
+        }
+        forwarded += todo;
         s->cache_len = frozen_prefix;
       }
-      s->upload_tokens(frozen_prefix, window_end);
       a.row0 = frozen_prefix;
       a.n_rows = window_end - frozen_prefix;
       a.n_keys = window_end;
       a.mask_kind = 1;
       a.mask_prompt_len = s->origin;
       a.mask_block = s->block;
+      if (!(s->graphable(a.n_rows) && n_frontier <= 32)) s->upload_tokens(frozen_prefix, window_end);
     } else {
       // Full bidirectional canvas, no cache (Dream / MDLM fixed_quota).
       for (int i = 0; i < n_frontier; ++i)
@@ -805,7 +957,11 @@ int32_t drt_session_propose(uint64_t session, const int32_t* frontier, int32_t n
       a.lm_rows.push_back(s->raw_row(frontier[i]) - a.row0);
       a.lm_pos.push_back(frontier[i]);
     }
-    run_forward(r, s->kv.p, s->head_stride, s->layer_stride, a);
+    if (a.mask_kind == 1 && s->graphable(a.n_rows) && n_frontier <= 32)
+      s->graph_forward(false, a);
+    else
+      run_forward(r, s->kv.p, s->head_stride, s->layer_stride, a);
+    r.up_next = 2;  // the stream is drained below before any slot is reused
     forwarded += a.n_rows;
     DRT_HIP(hipEventRecord(r.ev1, r.stream));
     DRT_HIP(hipMemcpyAsync(out_scores, r.scores.p, (size_t)n_frontier * 8, hipMemcpyDeviceToHost,
