@@ -10,10 +10,17 @@ fused LM head + float64 softmax scoring of the frontier) -> host top-k select
 -> commit. The once-per-block forward that writes a finished block's K/V is
 counted in the step that triggers it.
 
-Prints one JSON line. ``value`` is generated tokens/s over the timed steps;
-``roofline`` is the dominant kernel (block-over-prefix attention) timed per
-dispatch over the timed region; ``cpu_baseline`` times the oracle's
+Prints one JSON line. ``value`` is generated tokens/s over the timed steps,
+which replay the captured HIP graphs of the step and block-commit forwards.
+``roofline`` is the dominant kernel (the block-over-prefix decode attention,
+``attn_decode_kernel``): its dispatches are timed one by one with HIP events
+(hipExtLaunchKernelGGL start/stop events on the launch stream) over a second
+timed region of the same number of steps run eagerly, since a graph replay
+cannot carry per-dispatch events. ``cpu_baseline`` times the oracle's
 reference-semantics CPU path (full prefix recompute) on a bounded sample.
+
+``--calibrate-copy`` instead times a plain device copy of a known size (the
+scale for rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and prints its line.
 """
 from __future__ import annotations
 
@@ -43,8 +50,10 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=8, help="untimed denoise steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-layers", type=int, default=1)
-    ap.add_argument("--no-profile", action="store_true",
-                    help="time steps without per-dispatch timestamps (no roofline)")
+    ap.add_argument("--profile-steps", type=int, default=None,
+                    help="eager steps timed per dispatch for the roofline (default: --steps; 0 = none)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="time a 256 MiB device-to-device copy and exit")
     return ap.parse_args()
 
 
@@ -107,8 +116,47 @@ def cpu_baseline(model, prefix_ids, mask_id, layers_sampled: int):
     }
 
 
+def calibrate_copy(steps: int) -> None:
+    """A plain copy kernel of known size: 256 MiB read + 256 MiB written."""
+    import torch
+
+    n = 256 << 20
+    src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": steps,
+                      "ms_per_copy": round(dt * 1e3, 4),
+                      "GBps_read_plus_write": round(2 * n / dt / 1e9, 1)}), flush=True)
+
+
+def read_traffic():
+    """HBM bytes per decode-attention dispatch measured with rocprofv3 counters
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter's reading for the
+    plain copy), recorded as ``traffic_bytes_per_launch = N`` in the profile
+    summary; None when that file is absent."""
+    path = os.path.join(ROOT, "profiles", "attn_decode_kernel_bd3_q4_8k_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch ="):
+                    return float(line.split("=", 1)[1].strip().split()[0])
+    except OSError:
+        return None
+    return None
+
+
 def main():
     args = parse_args()
+    if args.calibrate_copy:
+        calibrate_copy(max(1, args.steps))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build has no "
               "multi-GPU path; see DESIGN.md for how the step would shard.", file=sys.stderr)
@@ -124,7 +172,8 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     g = syn.BD3_QWEN3_06B
-    total = args.warmup + args.steps
+    prof_steps = args.steps if args.profile_steps is None else args.profile_steps
+    total = args.warmup + args.steps + prof_steps
     n_blocks = max(1, math.ceil(total / STEPS_PER_BLOCK))
     max_tokens = n_blocks * BLOCK
     steps_budget = n_blocks * STEPS_PER_BLOCK
@@ -168,8 +217,6 @@ def main():
     torch.cuda.synchronize()
     log(f"warmup ({args.warmup} steps, incl. the {PREFIX}-row prefix commit) "
         f"{time.perf_counter() - t:.2f}s")
-    if not args.no_profile:
-        sess.set_profiling(True)
     m0 = sess.device_metrics()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -179,7 +226,19 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     m1 = sess.device_metrics()
-    sess.set_profiling(False)
+    log(f"timed {args.steps} steps (graph replay) {elapsed * 1e3:.1f} ms")
+    if prof_steps > 0:
+        # per-dispatch events force eager launches (no graph replay)
+        sess.set_profiling(True)
+        torch.cuda.synchronize()
+        tp = time.perf_counter()
+        for _ in range(prof_steps):
+            one_step()
+        torch.cuda.synchronize()
+        prof_elapsed = time.perf_counter() - tp
+        mp = sess.device_metrics()
+        sess.set_profiling(False)
+        log(f"profiled {prof_steps} eager steps {prof_elapsed * 1e3:.1f} ms")
     sess.close()
     rt.close()
 
@@ -201,25 +260,27 @@ def main():
         "device_forward_ms_per_step": round(dev_ms, 4),
         "committed_tokens": committed,
     }
-    if not args.no_profile:
+    if prof_steps > 0:
         names = ("attention", "linear", "lm_head")
         comp = {}
         for n in names:
-            ms = m1[f"rocm_prof_ms_{n}"]
-            launches = m1[f"rocm_prof_launches_{n}"]
-            byts = m1[f"rocm_prof_bytes_{n}"]
-            comp[n] = {"ms_per_step": round(ms / args.steps, 4), "launches": int(launches),
+            ms = mp[f"rocm_prof_ms_{n}"]
+            launches = mp[f"rocm_prof_launches_{n}"]
+            byts = mp[f"rocm_prof_bytes_{n}"]
+            comp[n] = {"ms_per_step": round(ms / prof_steps, 4), "launches": int(launches),
                        "avg_launch_us": round(ms / max(1, launches) * 1e3, 3),
                        "algorithmic_GBps": round(byts / max(ms, 1e-9) / 1e6, 1)}
         out["components"] = comp
+        out["profiled_eager_ms_per_step"] = round(prof_elapsed / prof_steps * 1e3, 4)
         a = comp["attention"]
-        achieved = m1["rocm_prof_bytes_attention"] / max(m1["rocm_prof_ms_attention"], 1e-9) / 1e6
-        per_launch = m1["rocm_prof_bytes_attention"] / max(1, m1["rocm_prof_launches_attention"])
+        achieved = mp["rocm_prof_bytes_attention"] / max(mp["rocm_prof_ms_attention"], 1e-9) / 1e6
+        per_launch = mp["rocm_prof_bytes_attention"] / max(1, mp["rocm_prof_launches_attention"])
         out["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                           "traffic": None, "kernel": "attn_split_kernel",
+                           "traffic": read_traffic(), "kernel": "attn_decode_kernel",
                            "algorithmic_bytes_per_launch": round(per_launch),
-                           "avg_launch_us": a["avg_launch_us"]}
+                           "avg_launch_us": a["avg_launch_us"], "launches": a["launches"],
+                           "timed_over": f"{prof_steps} eager steps after the graph-timed region"}
     if not args.no_cpu_baseline:
         t = time.perf_counter()
         out["cpu_baseline"] = cpu_baseline(model, prefix, g.mask_token_id, args.cpu_sample_layers)

@@ -206,3 +206,51 @@ def test_session_errors_fail_closed():
     lib = _lib.load()
     assert lib.drt_release_handle(h) == _lib.INVALID_ARGUMENT  # double release
     rt.close()
+
+
+@pytest.mark.parametrize("kind", ["q4", "bf16"])
+def test_reference_mask_cases_against_golden(kind):
+    """The reference's three BD3 cases (tests/golden/bd3_mask_cases.json) at the
+    real vocabulary: device window logits of the selected rows against the
+    oracle's golden summaries (tests/golden/bd3_real_vocab_logits.json)."""
+    import json
+    import os
+    import sys
+
+    from diffusorrt_amd import synthetic as syn
+    from diffusorrt_amd.runtime import Runtime, bd3_session_config
+
+    golden = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    sys.path.insert(0, golden)
+    import make_golden
+
+    with open(os.path.join(golden, "bd3_mask_cases.json")) as f:
+        cases = json.load(f)["cases"]
+    with open(os.path.join(golden, "bd3_real_vocab_logits.json")) as f:
+        gold = json.load(f)
+    probe = gold["probe_ids"]
+    model = syn.build_model(make_golden.real_vocab_geometry(), kind, seed=gold["seed"])
+    rt = Runtime(model, max_forward_rows=256, max_positions=512)
+    try:
+        for c in cases:
+            _say("golden case", kind, c["name"])
+            ids, rows = c["input_ids"], c["selected_rows"]
+            with rt.session(bd3_session_config(32, 8, len(ids))) as s:
+                got = s.execute_window(ids, rows, mask_geometry=(0, 32)).array()
+            want = gold["kinds"][kind][c["name"]]
+            scores, tokens = O.raw_max_prob(got)
+            for r, w in enumerate(want):
+                scale = max(abs(w["max"]), 1e-30)
+                err = max(abs(float(got[r, i]) - v) for i, v in zip(probe, w["probe"])) / scale
+                err = max(err, abs(float(got[r].max()) - w["max"]) / scale)
+                assert err < LOGITS_REL_TOL, (c["name"], r, err)
+                if tokens[r] != w["argmax"]:
+                    margin = w["max"] - w["second"]
+                    band = (2 * 2.0 ** (np.floor(np.log2(scale)) - 7) if kind == "bf16"
+                            else -np.log1p(-1e-3))
+                    assert margin <= band, (c["name"], r, tokens[r], w["argmax"], margin)
+                    _say(f"  near-tie row {r}: {tokens[r]} vs {w['argmax']} margin {margin:.3g}")
+                else:
+                    assert abs(scores[r] - w["score"]) / w["score"] < 1e-2
+    finally:
+        rt.close()

@@ -1,0 +1,170 @@
+"""Pins the oracle's full-context forward (CPU only).
+
+Checks: a second implementation of the decoder written with torch's CPU
+kernels (rms_norm, scaled_dot_product_attention with a boolean mask, silu) and
+its own q4 dequantisation; the BD3 staircase invariants (rows never see later
+blocks, so a longer canvas leaves earlier rows unchanged); the Dream logits
+shift; the bf16 choreography against torch's bf16 matmul.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from diffusorrt_amd import synthetic as syn
+from oracle import forward as F
+from oracle import ops as O
+from helpers import oracle_weights, tiny_dream_geometry, tiny_geometry
+
+
+def _torch_q4_dense(w_q, scales, biases):
+    words = torch.from_numpy(np.asarray(w_q, dtype=np.uint32).astype(np.int64))
+    shifts = torch.arange(8, dtype=torch.int64) * 4
+    q = ((words[:, :, None] >> shifts) & 15).reshape(words.shape[0], -1).to(torch.float64)
+    s = torch.from_numpy(np.asarray(scales, np.float32)).to(torch.float64)
+    b = torch.from_numpy(np.asarray(biases, np.float32)).to(torch.float64)
+    s = s.repeat_interleave(64, dim=1)
+    b = b.repeat_interleave(64, dim=1)
+    return (s * q + b).to(torch.float32)
+
+
+def _torch_forward(model, g, ids, visible, kind):
+    """Independent decoder forward with torch CPU ops (fp32; bf16 matmuls for bf16)."""
+    raw = syn.to_oracle_weights(model)
+
+    def W(key):
+        v = raw[key]
+        return _torch_q4_dense(*v) if isinstance(v, tuple) else torch.from_numpy(np.asarray(v))
+
+    def lin(x, key, bias_key=None):
+        w = W(key)
+        if kind == "bf16":
+            y = (x.bfloat16() @ w.bfloat16().T).float()
+        else:
+            y = x @ w.T
+        if bias_key is not None and bias_key in raw:
+            y = y + torch.from_numpy(np.asarray(raw[bias_key], np.float32))
+        return y
+
+    s = len(ids)
+    hd, hq, hkv = g.head_dim, g.num_heads, g.num_kv_heads
+    h = torch.from_numpy(np.asarray(raw["model.embed_tokens.weight"], np.float32))[ids]
+    pos = torch.arange(s, dtype=torch.float64)
+    inv = 1.0 / (g.rope_theta ** (torch.arange(0, hd // 2, dtype=torch.float64) / (hd // 2)))
+    ang = pos[:, None] * inv[None, :]
+    cos = torch.cat([ang.cos(), ang.cos()], -1).float()[:, None, :]
+    sin = torch.cat([ang.sin(), ang.sin()], -1).float()[:, None, :]
+
+    def rope(x):
+        x1, x2 = x[..., : hd // 2], x[..., hd // 2:]
+        return x * cos + torch.cat([-x2, x1], -1) * sin
+
+    mask = None if visible is None else torch.from_numpy(visible)
+    for i in range(g.layer_count):
+        p = f"model.layers.{i}."
+        n = torch.nn.functional.rms_norm(h, (g.hidden_size,), W(p + "input_layernorm.weight"),
+                                         eps=g.rms_norm_eps)
+        q = lin(n, p + "self_attn.q_proj.weight", p + "self_attn.q_proj.bias").view(s, hq, hd)
+        k = lin(n, p + "self_attn.k_proj.weight", p + "self_attn.k_proj.bias").view(s, hkv, hd)
+        v = lin(n, p + "self_attn.v_proj.weight", p + "self_attn.v_proj.bias").view(s, hkv, hd)
+        if g.qk_norm:
+            q = torch.nn.functional.rms_norm(q, (hd,), W(p + "self_attn.q_norm.weight"),
+                                             eps=g.rms_norm_eps)
+            k = torch.nn.functional.rms_norm(k, (hd,), W(p + "self_attn.k_norm.weight"),
+                                             eps=g.rms_norm_eps)
+        q, k = rope(q), rope(k)
+        rep = hq // hkv
+        kk = k.repeat_interleave(rep, dim=1).transpose(0, 1)
+        vv = v.repeat_interleave(rep, dim=1).transpose(0, 1)
+        a = torch.nn.functional.scaled_dot_product_attention(q.transpose(0, 1), kk, vv,
+                                                             attn_mask=mask)
+        h = h + lin(a.transpose(0, 1).reshape(s, hq * hd), p + "self_attn.o_proj.weight")
+        n2 = torch.nn.functional.rms_norm(h, (g.hidden_size,),
+                                          W(p + "post_attention_layernorm.weight"),
+                                          eps=g.rms_norm_eps)
+        act = torch.nn.functional.silu(lin(n2, p + "mlp.gate_proj.weight")) * \
+            lin(n2, p + "mlp.up_proj.weight")
+        h = h + lin(act, p + "mlp.down_proj.weight")
+    hn = torch.nn.functional.rms_norm(h, (g.hidden_size,), W("model.norm.weight"),
+                                      eps=g.rms_norm_eps)
+    return lin(hn, "lm_head.weight").numpy()
+
+
+@pytest.mark.parametrize("kind,tol", [("q4", 2e-4), ("bf16", 3e-2)])
+def test_forward_matches_independent_torch_decoder(kind, tol):
+    g = tiny_geometry()
+    model = syn.build_model(g, kind, seed=11)
+    ids = syn.prompt_ids(11, 70, high=1000)
+    cfg = syn.oracle_config(g, kind)
+    got = F.forward_full(oracle_weights(model), cfg, ids, mask_kind="d2f_hybrid",
+                         mask_geometry=(0, 32))
+    vis = O.d2f_visible(np.arange(70), 70, prompt_len=0, block_size=32)
+    ref = _torch_forward(model, g, ids, vis, kind)
+    err = np.abs(got - ref).max(axis=-1) / np.abs(ref).max(axis=-1)
+    assert err.max() < tol, err.max()
+
+
+def test_dream_forward_matches_independent_torch_decoder():
+    g = tiny_dream_geometry()
+    model = syn.build_model(g, "q4", seed=12)
+    ids = syn.prompt_ids(12, 48, high=1000)
+    got = F.forward_full(oracle_weights(model), syn.oracle_config(g, "q4"), ids,
+                         mask_kind="bidirectional")
+    ref = _torch_forward(model, g, ids, None, "q4")
+    err = np.abs(got - ref).max(axis=-1) / np.abs(ref).max(axis=-1)
+    assert err.max() < 2e-4, err.max()
+
+
+def test_staircase_rows_never_see_later_blocks():
+    g = tiny_geometry()
+    model = syn.build_model(g, "q4", seed=13)
+    W = oracle_weights(model)
+    cfg = syn.oracle_config(g, "q4")
+    ids = syn.prompt_ids(13, 96, high=1000)
+    base = F.forward_full(W, cfg, ids, mask_kind="d2f_hybrid", mask_geometry=(0, 32))
+    # change every token of the last block: rows of blocks 0 and 1 are untouched
+    ids2 = list(ids[:64]) + [g.mask_token_id] * 32
+    alt = F.forward_full(W, cfg, ids2, mask_kind="d2f_hybrid", mask_geometry=(0, 32))
+    np.testing.assert_array_equal(base[:64], alt[:64])
+    assert not np.allclose(base[64:], alt[64:])
+    # a shorter canvas ending at a block boundary gives the same rows
+    short = F.forward_full(W, cfg, ids[:64], mask_kind="d2f_hybrid", mask_geometry=(0, 32))
+    np.testing.assert_allclose(short, base[:64], rtol=1e-5, atol=1e-5)
+    # inside a block attention is bidirectional: a later in-block token matters
+    ids3 = list(ids)
+    ids3[70] = (ids3[70] + 1) % 1000
+    alt3 = F.forward_full(W, cfg, ids3, mask_kind="d2f_hybrid", mask_geometry=(0, 32))
+    assert not np.allclose(base[64], alt3[64])
+
+
+def test_window_logits_dream_shift_reads_previous_row():
+    g = tiny_dream_geometry()
+    model = syn.build_model(g, "q4", seed=14)
+    W = oracle_weights(model)
+    cfg = syn.oracle_config(g, "q4")
+    ids = syn.prompt_ids(14, 40, high=1000)
+    full = F.forward_full(W, cfg, ids, mask_kind="bidirectional")
+    scope = [0, 1, 5, 39]
+    win = F.window_logits(W, cfg, ids, scope, mask_kind="bidirectional", mask_geometry=None,
+                          logits_convention="dream_ar_shift")
+    np.testing.assert_allclose(win, full[[0, 0, 4, 38]], rtol=1e-6, atol=1e-6)
+    raw = F.window_logits(W, cfg, ids, scope, mask_kind="bidirectional", mask_geometry=None,
+                          logits_convention="raw")
+    np.testing.assert_allclose(raw, full[scope], rtol=1e-6, atol=1e-6)
+
+
+def test_kv_hook_sees_roped_keys():
+    """The K/V a cache would store are post-norm, post-RoPE keys and raw values."""
+    g = tiny_geometry(layer_count=1)
+    model = syn.build_model(g, "q4", seed=15)
+    W = oracle_weights(model)
+    cfg = syn.oracle_config(g, "q4")
+    ids = syn.prompt_ids(15, 8, high=1000)
+    seen = {}
+    F.forward_full(W, cfg, ids, mask_kind="d2f_hybrid", mask_geometry=(0, 32),
+                   kv_hook=lambda i, k, v: seen.update(k=k, v=v))
+    # position 0 has an identity rotation; the per-head key norm gives unit RMS
+    k0 = seen["k"][0].astype(np.float64)
+    np.testing.assert_allclose(np.sqrt((k0 ** 2).mean(axis=-1)), 1.0, rtol=1e-4)
+    assert seen["v"].shape == (8, g.num_kv_heads, g.head_dim)

@@ -1,0 +1,202 @@
+"""Decode control plane (CPU only): the oracle's literal loops against closed
+forms, and the product's host policies (``diffusorrt_amd.decode``) against the
+oracle on random canvases."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from diffusorrt_amd import decode as D
+from oracle import ops as O
+from oracle import policy as P
+
+MASK, EOS = 99, 98
+
+
+def _bd3_plans(prompt_len, gen, steps, bs=32):
+    x = [1] * prompt_len + [MASK] * gen
+    state, out = {}, []
+    sched = math.ceil(gen / bs)
+    spb = math.ceil(steps / sched)
+    for step in range(P.block_count(prompt_len, gen, bs, 0) * spb):
+        kind, frontier, wend, quota = P.bd3_schedule_step(x, prompt_len, MASK, EOS, bs, steps,
+                                                          step, state)
+        if kind == "stop":
+            break
+        out.append((step, kind, frontier, wend, quota))
+        if kind == "go":
+            for p in frontier[:quota]:
+                x[p] = 7
+    return out, x
+
+
+def test_bd3_schedule_config1_closed_form():
+    """Prompt 64, 128 tokens, steps 32: 4 blocks x 8 rounds x 4 tokens, window = block end."""
+    plans, x = _bd3_plans(64, 128, 32)
+    assert len(plans) == 32
+    for step, kind, frontier, wend, quota in plans:
+        b = step // 8
+        assert kind == "go" and quota == 4
+        assert wend == 96 + 32 * b
+        assert all(64 + 32 * b <= p < 96 + 32 * b for p in frontier)
+        assert len(frontier) == 32 - 4 * (step % 8)
+    assert MASK not in x
+
+
+def test_bd3_schedule_uneven_quota_and_absolute_blocks():
+    """divmod(masked, steps_per_block): remainder rounds get one more token; blocks
+    are absolute (origin 0), so a prompt of 40 leaves a first block of 24."""
+    plans, _ = _bd3_plans(64, 64, 5)   # 2 blocks, spb = 3: quotas 11, 11, 10
+    assert [q for *_, q in plans[:3]] == [11, 11, 10]
+    with pytest.raises(ValueError):
+        _bd3_plans(40, 64, 4)
+    assert P.block_span(40, 64, 32, 0, 0) == (40, 64)
+    assert P.block_span(40, 64, 32, 0, 2) == (96, 104)
+    assert P.block_count(40, 64, 32, 0) == 3
+
+
+def test_bd3_eos_stops_only_at_block_boundary():
+    x = [1] * 32 + [MASK] * 64
+    state = {}
+    k, *_ = P.bd3_schedule_step(x, 32, MASK, EOS, 32, 8, 0, state)
+    assert k == "go"
+    x[40] = EOS  # EOS committed inside block 0
+    for step in (1, 2, 3):
+        k, *_ = P.bd3_schedule_step(x, 32, MASK, EOS, 32, 8, step, state)
+        assert k == "go"
+    k, *_ = P.bd3_schedule_step(x, 32, MASK, EOS, 32, 8, 4, state)  # next block boundary
+    assert k == "stop"
+
+
+def test_fixed_quota_dream_config():
+    """256 prompt + 256 masks, block >= 256, steps 64: one block, 64 rounds x 4, no window."""
+    x = [1] * 256 + [MASK] * 256
+    state = {}
+    n = 0
+    for step in range(64):
+        kind, frontier, wend, quota = P.fixed_quota_schedule_step(x, 256, MASK, 256, 64, step,
+                                                                  state)
+        assert kind == "go" and quota == 4 and wend is None
+        assert len(frontier) == 256 - 4 * step
+        for p in frontier[:4]:
+            x[p] = 5
+        n += 4
+    assert n == 256
+    assert P.fixed_quota_schedule_step(x, 256, MASK, 256, 64, 64, state)[0] == "stop"
+
+
+def test_finalize_cases():
+    assert P.finalize([1, 2, 3, EOS, 4], 1, MASK, EOS) == {
+        "visible_token_ids": [2, 3], "hit_eos": True, "remaining_mask_count": 0,
+        "finish_reason": "stop"}
+    assert P.finalize([1, 2, MASK, 3], 1, MASK, EOS) == {
+        "visible_token_ids": [2], "hit_eos": False, "remaining_mask_count": 1,
+        "finish_reason": "length"}
+    assert P.finalize([1, 2, 3], 1, MASK, EOS)["finish_reason"] == "length"
+
+
+def _fake_logits(vocab):
+    """Deterministic frontier logits from the canvas (a stand-in model)."""
+    def fn(x, frontier, _wend):
+        rows = []
+        for p in frontier:
+            rng = np.random.default_rng(hash((tuple(x), p)) & 0xFFFFFFFF)
+            rows.append(rng.standard_normal(vocab).astype(np.float32) * 3)
+        return np.stack(rows)
+    return fn
+
+
+@pytest.mark.parametrize("strategy,prompt_len,gen,bs,steps", [
+    ("bd3_fixed_quota", 32, 96, 32, 12),
+    ("bd3_fixed_quota", 64, 70, 32, 7),
+    ("fixed_quota", 20, 48, 16, 9),
+    ("fixed_quota", 16, 40, 64, 10),
+])
+def test_product_loop_matches_oracle_loop(strategy, prompt_len, gen, bs, steps):
+    vocab = 120
+    fn = _fake_logits(vocab)
+    prompt = list(np.random.default_rng(prompt_len).integers(0, 90, prompt_len))
+    trace_o = []
+    ref = P.run_fixed_quota_decode(prompt, max_tokens=gen, mask_id=MASK, eos_id=EOS,
+                                   block_size=bs, steps=steps, strategy=strategy,
+                                   frontier_logits_fn=fn, trace=trace_o)
+    state = D.MaskState(x=[*prompt, *([MASK] * gen)], prompt_len=prompt_len,
+                        mask_token_id=MASK, eos_token_id=EOS)
+    if strategy == "bd3_fixed_quota":
+        layout = D.BlockLayout(start=prompt_len, length=gen, block_size=bs, origin=0)
+        pol = D.BD3FixedQuotaCommit(block_size=bs, requested_steps=steps,
+                                    generated_token_count=gen, block_layout=layout)
+    else:
+        pol = D.FixedQuotaCommit(block_size=bs, requested_steps=steps, generated_token_count=gen)
+
+    def propose(plan):
+        scores, toks = O.raw_max_prob(fn(list(state.x), plan.frontier, plan.window_end))
+        return scores, toks, len(plan.frontier)
+
+    trace_p = []
+    fwd, committed, _ = D.run_decode_loop(state, commit_policy=pol,
+                                          iteration_limit=pol.iteration_limit,
+                                          propose_fn=propose, commit_device_fn=lambda p, t: None,
+                                          trace=trace_p)
+    assert state.x == ref["x"]
+    assert fwd == ref["forward_count"] and committed == ref["committed_token_count"]
+    assert [t["chosen"] for t in trace_p] == [t["chosen"] for t in trace_o]
+    assert [t["window_end"] for t in trace_p] == [t["window_end"] for t in trace_o]
+    assert state.finalize() == {k: ref[k] for k in
+                                ("visible_token_ids", "hit_eos", "remaining_mask_count",
+                                 "finish_reason")}
+
+
+def test_product_bd3_eos_boundary_matches_oracle():
+    """A stand-in model that emits EOS early: both loops stop at the same boundary."""
+    vocab = 120
+
+    def fn(x, frontier, _wend):
+        out = np.zeros((len(frontier), vocab), np.float32)
+        for r, p in enumerate(frontier):
+            out[r, EOS if p == 40 else (p % 50)] = 5.0 + (p % 7) * 0.1
+        return out
+
+    ref = P.run_fixed_quota_decode([3] * 32, max_tokens=96, mask_id=MASK, eos_id=EOS,
+                                   block_size=32, steps=24, strategy="bd3_fixed_quota",
+                                   frontier_logits_fn=fn)
+    state = D.MaskState(x=[3] * 32 + [MASK] * 96, prompt_len=32, mask_token_id=MASK,
+                        eos_token_id=EOS)
+    layout = D.BlockLayout(start=32, length=96, block_size=32, origin=0)
+    pol = D.BD3FixedQuotaCommit(block_size=32, requested_steps=24, generated_token_count=96,
+                                block_layout=layout)
+
+    def propose(plan):
+        s, t = O.raw_max_prob(fn(list(state.x), plan.frontier, plan.window_end))
+        return s, t, 32
+
+    D.run_decode_loop(state, commit_policy=pol, iteration_limit=pol.iteration_limit,
+                      propose_fn=propose, commit_device_fn=lambda p, t: None)
+    assert state.x == ref["x"]
+    assert ref["hit_eos"] and MASK in ref["x"]   # stopped with later blocks still masked
+
+
+def test_product_policy_validation():
+    with pytest.raises(ValueError):
+        D.BlockLayout(start=-1, length=4, block_size=2)
+    with pytest.raises(ValueError):
+        D.BlockLayout(start=4, length=4, block_size=2, origin=5)
+    with pytest.raises(ValueError):
+        D.BD3FixedQuotaCommit(block_size=0, requested_steps=1, generated_token_count=1,
+                              block_layout=D.BlockLayout(start=0, length=1, block_size=1))
+    with pytest.raises(D.GenerationCancelled):
+        state = D.MaskState(x=[1, MASK], prompt_len=1, mask_token_id=MASK, eos_token_id=EOS)
+        pol = D.FixedQuotaCommit(block_size=1, requested_steps=1, generated_token_count=1)
+        D.run_decode_loop(state, commit_policy=pol, iteration_limit=1,
+                          propose_fn=lambda p: ([1.0], [5], 1),
+                          commit_device_fn=lambda p, t: None, cancelled=lambda: True)
+
+
+def test_topk_matches_oracle_and_numpy_quicksort():
+    rng = np.random.default_rng(3)
+    for _ in range(50):
+        s = rng.random(rng.integers(1, 40))
+        k = int(rng.integers(0, len(s) + 1))
+        assert D.topk_count_choices(s, k) == O.topk_count_choices(s, k)
