@@ -216,44 +216,152 @@ __global__ __launch_bounds__(64 * QW) void attn_split_kernel(
 }
 
 // Decode attention: rows of one mask segment (every key in [0, n_keys) is
-// visible to every row) with at most 32*QT query vectors per KV head. Grid
-// (R ranges, Hkv), 4 waves per work-group; wave w of range r takes tiles
-// t0 + w, t0 + w + 4, ... K/V fragments go straight from the cache into
-// registers (the tile layout makes each wave load a contiguous 1 KiB),
-// double-buffered; each wave serves all QT query tiles with one K/V load. The
-// four waves' (m, l, O) are merged through LDS, so each range writes one partial.
+// visible to every row) with at most 32*QT query vectors per KV head.
+//
+// Grid (R ranges, Hkv), 4 waves per work-group, one work-group per CU (the
+// host keeps R * Hkv <= 256). Range r owns the tiles [n_tiles*r/R,
+// n_tiles*(r+1)/R) of its KV head; wave w takes tiles t0 + w, t0 + w + 4 and
+// t0 + w + 8 and issues all three tiles' K/V loads (nontemporal: the cache is
+// streamed once per layer) before anything else, so one memory latency covers
+// a range of up to 12 tiles (longer ranges continue with a load-then-use loop).
+// The head's Q vectors are loaded once per work-group into LDS (fragments are
+// read from LDS at each MFMA). After the tiles all four waves store (m, l, O)
+// to LDS and all 256 threads combine them slot by slot, so every range writes
+// one partial in the MFMA register order ("slot" order, see
+// attn_decode_combine_kernel) with coalesced stores. Empty ranges write only
+// m = -inf, l = 0; the combine then skips their O.
 // n_keys comes from `desc` when it is set (graph replays), else from the argument.
+constexpr int DEC_QROW = 136;  // 16-bit elements per Q row in LDS (+16 B pad)
+constexpr int DEC_TILES_UP_FRONT = 3;
+
+// K/V fragments of tile t. With real == false every lane reads the first 16
+// bytes of the tile (one cache line per wave: a placeholder that keeps the load
+// count static; the caller gives such a tile no visible key).
+template <typename T>
+DRT_DEV void load_tile_nt(const T* __restrict__ base, int t, int lane, bool real,
+                          typename MfmaT<T>::vec (&k)[8], typename MfmaT<T>::vec (&v)[8]) {
+  typedef typename MfmaT<T>::vec vec;
+  const vec* tp = (const vec*)(base + (int64_t)t * KV_TILE_ELEMS);
+  const int l = real ? lane : 0, step = real ? 64 : 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    k[i] = __builtin_nontemporal_load(tp + i * step + l);
+    v[i] = __builtin_nontemporal_load(tp + (real ? 512 : 0) + i * step + l);
+  }
+}
+
+// One 32-key tile for all query tiles: S^T = K Q^T, online softmax, O^T += V^T P^T.
+// Keys at or beyond n_keys get zero weight (n_keys = 0 makes the tile a no-op).
+template <typename T, int QT>
+DRT_DEV void attend_tile(const typename MfmaT<T>::vec (&kc)[8],
+                         const typename MfmaT<T>::vec (&vc)[8], const T* __restrict__ qs,
+                         int key0, int n_keys, int n_qv, float scale, int lane,
+                         float (&m_run)[QT], float (&l_run)[QT], f32x16 (&o)[QT][4]) {
+  typedef typename MfmaT<T>::vec vec;
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    // uniform; query tile 0 always runs (n_qv >= 1), so the tile's loads are used
+    // unconditionally and stay where they were issued
+    if (qt > 0 && qt * 32 >= n_qv) break;
+    const T* qrow = qs + (qt * 32 + (lane & 31)) * DEC_QROW + 8 * (lane >> 5);
+    f32x16 sc = f32x16{};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sc = MfmaT<T>::mma(kc[i], *(const vec*)(qrow + 16 * i), sc);
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const bool vis = key0 + mfma_row(r, lane) < n_keys;
+      sc[r] = vis ? sc[r] * scale : -INFINITY;
+      tmax = fmaxf(tmax, sc[r]);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run[qt], tmax);
+    const float basev = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = __expf(m_run[qt] - basev);
+    float pr[16];
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      pr[r] = __expf(sc[r] - basev);
+      psum += pr[r];
+    }
+    l_run[qt] = l_run[qt] * alpha + psum;
+    m_run[qt] = m_new;
+#pragma unroll
+    for (int hb = 0; hb < 4; ++hb) o[qt][hb] *= alpha;
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      vec pf;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pf[j] = MfmaT<T>::from_float(pr[kh * 8 + j]);
+#pragma unroll
+      for (int hb = 0; hb < 4; ++hb) o[qt][hb] = MfmaT<T>::mma(vc[hb * 2 + kh], pf, o[qt][hb]);
+    }
+  }
+}
+
 template <typename T, int QT>
 __global__ __launch_bounds__(256) void attn_decode_kernel(
     const T* __restrict__ q, const T* __restrict__ kv, int64_t kv_head_stride, int n_rows,
     int Hq, int Hkv, int n_keys_arg, const StepDesc* __restrict__ desc,
     float* __restrict__ o_part, float* __restrict__ ml_part, float scale) {
   typedef typename MfmaT<T>::vec vec;
+  constexpr int SLOTS = QT * 4096;              // O slots of one partial
+  constexpr int SLOT = SLOTS + QT * 64 * 2;     // + (m, l) per lane, one wave's LDS share
+  constexpr int UP = DEC_TILES_UP_FRONT;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int G = Hq / Hkv;
   const int n_qv = n_rows * G;
   const int R = gridDim.x, rg = blockIdx.x, kvh = blockIdx.y;
   const int n_keys = desc ? desc->n_keys : n_keys_arg;
   const int n_tiles = (n_keys + 31) >> 5;
-  const int tpr = (n_tiles + R - 1) / R;
-  const int t_begin = rg * tpr;
-  const int t_end = min(n_tiles, t_begin + tpr);
+  const int t_begin = (int)((int64_t)n_tiles * rg / R);
+  const int t_end = (int)((int64_t)n_tiles * (rg + 1) / R);
+  const int64_t part = (int64_t)rg * Hkv + kvh;
   extern __shared__ __align__(16) char smem[];
+  T* qs = (T*)smem;                                       // [QT*32][DEC_QROW]
+  float* mrg = (float*)(smem + QT * 32 * DEC_QROW * 2);   // [4][SLOT]
 
-  vec qf[QT][8];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    const int qv = qt * 32 + (lane & 31);
-    if (qv < n_qv) {
-      const int row = qv / G, head = kvh * G + (qv - (qv / G) * G);
-      const T* qp = q + ((int64_t)row * Hq + head) * 128 + 8 * (lane >> 5);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) qf[qt][i] = *(const vec*)(qp + 16 * i);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) qf[qt][i] = vec{};
+  if (t_begin >= t_end) {  // no keys in this range
+    if (threadIdx.x < QT * 32) {
+      ml_part[(part * (QT * 32) + threadIdx.x) * 2] = -INFINITY;
+      ml_part[(part * (QT * 32) + threadIdx.x) * 2 + 1] = 0.f;
     }
+    return;
   }
+  // Q of the head's query vectors (qv = row*G + g) as 16-byte chunks; loads are
+  // unconditional (clamped rows) so the wait for Q below does not also wait for
+  // the K/V loads issued after it.
+  constexpr int QCH = QT * 2;  // QT*32 rows x 16 chunks / 256 threads
+  u32x4 qraw[QCH];
+#pragma unroll
+  for (int i = 0; i < QCH; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    const int qvc = min(c >> 4, n_qv - 1);
+    const int row = qvc / G, head = kvh * G + (qvc - row * G);
+    qraw[i] = *(const u32x4*)(q + ((int64_t)row * Hq + head) * 128 + (c & 15) * 8);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const T* base = kv + (int64_t)kvh * kv_head_stride;
+  const int t0 = t_begin + wave;
+  vec kt[UP][8], vt[UP][8];
+  // a wave short of tiles loads a placeholder (one line of the range's last
+  // tile) and processes it with no visible key, which changes nothing
+#pragma unroll
+  for (int u = 0; u < UP; ++u)
+    load_tile_nt<T>(base, min(t0 + 4 * u, t_end - 1), lane, t0 + 4 * u < t_end, kt[u], vt[u]);
+  // every load is issued before any wait: a compiler-level memory barrier keeps
+  // the loads from being moved past the work-group barrier below
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < QCH; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    *(u32x4*)(qs + (c >> 4) * DEC_QROW + (c & 15) * 8) =
+        (c >> 4) < n_qv ? qraw[i] : u32x4{0u, 0u, 0u, 0u};
+  }
+  __syncthreads();
+
   float m_run[QT], l_run[QT];
   f32x16 o[QT][4];
 #pragma unroll
@@ -263,148 +371,162 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 #pragma unroll
     for (int hb = 0; hb < 4; ++hb) o[qt][hb] = f32x16{};
   }
-  const T* base = kv + (int64_t)kvh * kv_head_stride;
-  vec kc[8], vc[8];
-  int t = t_begin + wave;
-  if (t < t_end) {
-    const T* tp = base + (int64_t)t * KV_TILE_ELEMS;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      kc[i] = *(const vec*)(tp + (i * 64 + lane) * 8);
-      vc[i] = *(const vec*)(tp + 4096 + (i * 64 + lane) * 8);
-    }
+  for (int u = 0; u < UP; ++u) {
+    const int t = t0 + 4 * u;
+    attend_tile<T, QT>(kt[u], vt[u], qs, t * 32, t < t_end ? n_keys : 0, n_qv, scale, lane,
+                       m_run, l_run, o);
   }
-  for (; t < t_end; t += 4) {
-    vec kn[8], vn[8];
-    const bool more = t + 4 < t_end;
-    if (more) {
-      const T* tp = base + (int64_t)(t + 4) * KV_TILE_ELEMS;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        kn[i] = *(const vec*)(tp + (i * 64 + lane) * 8);
-        vn[i] = *(const vec*)(tp + 4096 + (i * 64 + lane) * 8);
-      }
-    }
-    const int key0 = t * 32;
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      if (qt * 32 >= n_qv) break;  // uniform
-      f32x16 s = f32x16{};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) s = MfmaT<T>::mma(kc[i], qf[qt][i], s);
-      float tmax = -INFINITY;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const bool vis = key0 + mfma_row(r, lane) < n_keys;
-        s[r] = vis ? s[r] * scale : -INFINITY;
-        tmax = fmaxf(tmax, s[r]);
-      }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const float m_new = fmaxf(m_run[qt], tmax);
-      const float basev = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __expf(m_run[qt] - basev);
-      float p[16];
-      float psum = 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        p[r] = __expf(s[r] - basev);
-        psum += p[r];
-      }
-      l_run[qt] = l_run[qt] * alpha + psum;
-      m_run[qt] = m_new;
-#pragma unroll
-      for (int hb = 0; hb < 4; ++hb) o[qt][hb] *= alpha;
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
-        vec pf;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) pf[j] = MfmaT<T>::from_float(p[kh * 8 + j]);
-#pragma unroll
-        for (int hb = 0; hb < 4; ++hb) o[qt][hb] = MfmaT<T>::mma(vc[hb * 2 + kh], pf, o[qt][hb]);
-      }
-    }
-    if (more) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        kc[i] = kn[i];
-        vc[i] = vn[i];
-      }
-    }
+  for (int t = t0 + 4 * UP; t < t_end; t += 4) {  // ranges longer than 4*UP tiles
+    load_tile_nt<T>(base, t, lane, true, kt[0], vt[0]);
+    attend_tile<T, QT>(kt[0], vt[0], qs, t * 32, n_keys, n_qv, scale, lane, m_run, l_run, o);
   }
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) l_run[qt] += __shfl_xor(l_run[qt], 32, 64);
 
-  // Merge the four waves: 3,2 -> 1,0 -> 0 through LDS (same register layout in all waves).
-  float* lds = (float*)smem;
-  constexpr int SLOT = QT * 64 * 64 + QT * 64 * 2;
-  auto put = [&](int slot) {
-    float* b = lds + slot * SLOT;
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-#pragma unroll
-      for (int hb = 0; hb < 4; ++hb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) b[(qt * 64 + hb * 16 + r) * 64 + lane] = o[qt][hb][r];
-      b[QT * 4096 + (qt * 64 + lane) * 2] = m_run[qt];
-      b[QT * 4096 + (qt * 64 + lane) * 2 + 1] = l_run[qt];
-    }
-  };
-  auto merge = [&](int slot) {
-    const float* b = lds + slot * SLOT;
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      const float m2 = b[QT * 4096 + (qt * 64 + lane) * 2];
-      const float l2 = b[QT * 4096 + (qt * 64 + lane) * 2 + 1];
-      const float mm = fmaxf(m_run[qt], m2);
-      const float a1 = mm == -INFINITY ? 0.f : __expf(m_run[qt] - mm);
-      const float a2 = mm == -INFINITY ? 0.f : __expf(m2 - mm);
-      l_run[qt] = a1 * l_run[qt] + a2 * l2;
-      m_run[qt] = mm;
-#pragma unroll
-      for (int hb = 0; hb < 4; ++hb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          o[qt][hb][r] = a1 * o[qt][hb][r] + a2 * b[(qt * 64 + hb * 16 + r) * 64 + lane];
-    }
-  };
-  __syncthreads();
-  if (wave >= 2) put(wave - 2);
-  __syncthreads();
-  if (wave < 2) merge(wave);
-  __syncthreads();
-  if (wave == 1) put(0);
-  __syncthreads();
-  if (wave == 0) merge(0);
-  __syncthreads();
-  if (wave != 0) return;
-  // wave 0: transpose O^T through LDS and write this range's partial.
-  const int64_t part_base = ((int64_t)rg * Hkv + kvh) * n_qv;
+  // every wave stores its (O, m, l); slot (qt*64 + hb*16 + r)*64 + lane
+  float* mine = mrg + wave * SLOT;
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    if (qt * 32 >= n_qv) break;
-    float* ot = lds;
 #pragma unroll
     for (int hb = 0; hb < 4; ++hb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) ot[(lane & 31) * 132 + hb * 32 + mfma_row(r, lane)] = o[qt][hb][r];
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-    for (int i = lane; i < 32 * 32; i += 64) {
-      const int qq = i >> 5, c4 = (i & 31) * 4;
-      const int qv2 = qt * 32 + qq;
-      if (qv2 < n_qv) {
-        f32x4 v = {ot[qq * 132 + c4], ot[qq * 132 + c4 + 1], ot[qq * 132 + c4 + 2],
-                   ot[qq * 132 + c4 + 3]};
-        *(f32x4*)(o_part + (part_base + qv2) * 128 + c4) = v;
-      }
+      for (int r = 0; r < 16; ++r) mine[(qt * 64 + hb * 16 + r) * 64 + lane] = o[qt][hb][r];
+    mine[SLOTS + (qt * 64 + lane) * 2] = m_run[qt];
+    mine[SLOTS + (qt * 64 + lane) * 2 + 1] = l_run[qt];
+  }
+  __syncthreads();
+  // combine the four waves; slot s = threadIdx.x + 256*i has lane (s & 63) = lane.
+  // A wave without keys holds O = 0 and weight 0 (its O is finite: the cache
+  // tiles are zero-initialised and invisible keys get probability 0).
+  float wgt[QT][4];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    float mw[4], lw[4];
+    float mm = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      mw[w] = mrg[w * SLOT + SLOTS + (qt * 64 + lane) * 2];
+      lw[w] = mrg[w * SLOT + SLOTS + (qt * 64 + lane) * 2 + 1];
+      mm = fmaxf(mm, mw[w]);
     }
-    const int qv = qt * 32 + (lane & 31);
-    if (lane < 32 && qv < n_qv) {
-      ml_part[(part_base + qv) * 2] = m_run[qt];
-      ml_part[(part_base + qv) * 2 + 1] = l_run[qt];
+    float ll = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      wgt[qt][w] = mw[w] == -INFINITY ? 0.f : __expf(mw[w] - mm);
+      ll += wgt[qt][w] * lw[w];
     }
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
+    if (wave == 0 && lane < 32) {
+      ml_part[(part * (QT * 32) + qt * 32 + lane) * 2] = mm;
+      ml_part[(part * (QT * 32) + qt * 32 + lane) * 2 + 1] = ll;
+    }
+  }
+  float* op = o_part + part * SLOTS;
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int sl = qt * 4096 + threadIdx.x + 256 * i;
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) v = fmaf(wgt[qt][w], mrg[w * SLOT + sl], v);
+      op[sl] = v;
+    }
+  }
+}
+
+// Combine the ranges of the decode attention. Slot (qt*64 + hb*16 + r)*64 + l of a
+// partial holds query vector qt*32 + (l & 31) and head dim hb*32 + 8*(r >> 2) +
+// 4*(l >> 5) + (r & 3) (the MFMA result layout). Work-group (kvh, qt, hb*4 + rq)
+// owns the 256 slots with r in [4rq, 4rq + 4): 32 query vectors x the 8
+// consecutive head dims hb*32 + 8rq .. +8, one thread per slot, so 256
+// work-groups share the reads. Each query vector's 8 dims are one 8-element
+// chunk of the output row. Empty ranges (m = -inf) are skipped.
+// out_fmt: 0 = ACT_F16P (no group sums: its consumer sums the fp16 values
+// itself), 1 = ACT_BF16, 2 = fp32 plain, 3 = bf16 plain.
+template <int QT>
+__global__ __launch_bounds__(256) void attn_decode_combine_kernel(
+    const float* __restrict__ o_part, const float* __restrict__ ml_part, int R, int n_rows,
+    int Hq, int Hkv, void* __restrict__ out, int out_fmt) {
+  constexpr int SLOTS = QT * 4096;
+  const int kvh = blockIdx.x, qt = blockIdx.y, hb = blockIdx.z >> 2, rq = blockIdx.z & 3;
+  const int j = threadIdx.x;
+  const int G = Hq / Hkv;
+  const int n_qv = n_rows * G;
+  __shared__ float mx[8][32];
+  __shared__ float ls[8][32];
+  __shared__ float tile[32][9];
+  extern __shared__ float wts[];  // [R][32] unnormalised weights
+  // 1. per query vector c: max over ranges, weights, normaliser (8 range groups)
+  {
+    const int c = j & 31, pg = j >> 5;
+    float m_loc = -INFINITY;
+    for (int r = pg; r < R; r += 8)
+      m_loc = fmaxf(m_loc, ml_part[(((int64_t)r * Hkv + kvh) * (QT * 32) + qt * 32 + c) * 2]);
+    mx[pg][c] = m_loc;
+    __syncthreads();
+    float mm = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) mm = fmaxf(mm, mx[g][c]);
+    float l_loc = 0.f;
+    for (int r = pg; r < R; r += 8) {
+      const int64_t mi = (((int64_t)r * Hkv + kvh) * (QT * 32) + qt * 32 + c) * 2;
+      const float m_r = ml_part[mi];
+      const float w = m_r == -INFINITY ? 0.f : __expf(m_r - mm);
+      wts[r * 32 + c] = w;
+      l_loc += w * ml_part[mi + 1];
+    }
+    ls[pg][c] = l_loc;
+    __syncthreads();
+  }
+  // 2. this thread's slot: r = 4rq + (j >> 6), lane l = j & 63
+  const int l = j & 63, r = 4 * rq + (j >> 6), c = l & 31;
+  float lsum = 0.f;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) lsum += ls[g][c];
+  const int64_t sl = (int64_t)qt * 4096 + (hb * 16 + r) * 64 + l;
+  float acc = 0.f;
+  int rr = 0;
+  for (; rr + 8 <= R; rr += 8) {
+    float v[8], w[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      w[e] = wts[(rr + e) * 32 + c];
+      v[e] = w[e] == 0.f ? 0.f : o_part[((int64_t)(rr + e) * Hkv + kvh) * SLOTS + sl];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = fmaf(w[e], v[e], acc);
+  }
+  for (; rr < R; ++rr) {
+    const float w = wts[rr * 32 + c];
+    if (w != 0.f) acc = fmaf(w, o_part[((int64_t)rr * Hkv + kvh) * SLOTS + sl], acc);
+  }
+  // 3. gather each query vector's 8 dims: dim offset 4*(l >> 5) + (r & 3)
+  tile[c][4 * (l >> 5) + (r & 3)] = acc / lsum;
+  __syncthreads();
+  if (j >= 32) return;
+  const int qv = qt * 32 + j;
+  if (qv >= n_qv) return;
+  const int row = qv / G, head = kvh * G + (qv - row * G);
+  const int D = Hq * 128;
+  const int col0 = head * 128 + hb * 32 + 8 * rq;
+  float vals[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) vals[e] = tile[j][e];
+  if (out_fmt == 0) {
+    _Float16 pk[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pk[f16p_index(e)] = (_Float16)vals[e];
+    *(u32x4*)((_Float16*)out + (int64_t)row * D + col0) = __builtin_bit_cast(u32x4, pk);
+  } else if (out_fmt == 1 || out_fmt == 3) {
+    uint16_t pk[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pk[e] = float_to_bf16_bits(vals[e]);
+    *(u32x4*)((uint16_t*)out + (int64_t)row * D + col0) = __builtin_bit_cast(u32x4, pk);
+  } else {
+    float* o = (float*)out + (int64_t)row * D + col0;
+    *(f32x4*)o = f32x4{vals[0], vals[1], vals[2], vals[3]};
+    *(f32x4*)(o + 4) = f32x4{vals[4], vals[5], vals[6], vals[7]};
   }
 }
 
@@ -600,18 +722,35 @@ void attention(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_s
   DRT_HIP(hipGetLastError());
 }
 
+size_t attention_decode_part_bytes(int ranges, int Hkv, int n_qv) {
+  const int qt = (n_qv + 31) / 32;
+  return (size_t)ranges * Hkv * ((size_t)qt * 4096 + (size_t)qt * 32 * 2) * 4;
+}
+
+// Key ranges per KV head: as many as spread the tiles one per wave, at most one
+// work-group per CU of the 256 (beyond that a second round of work-groups would
+// double the time), so a range holds <= 12 tiles up to 32 * 12 * 256 / Hkv keys.
+int attention_decode_ranges(int n_keys, int Hkv) {
+  const int tiles = (n_keys + 31) / 32;
+  const int per_cu = std::max(1, 256 / std::max(1, Hkv));
+  return std::max(1, std::min(std::min(per_cu, 128), (tiles + 3) / 4));
+}
+
 // Decode attention (one mask segment, <= 64 query vectors per KV head) + combine.
+// `part` holds attention_decode_part_bytes(ranges, Hkv, n_rows * Hq / Hkv).
 void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_stride,
                       int n_rows, int Hq, int Hkv, int n_keys, const StepDesc* desc, int ranges,
-                      float* o_part, float* ml_part, void* out, float* xsum, int out_fmt,
-                      hipStream_t s) {
+                      float* part, void* out, float* xsum, int out_fmt, hipStream_t s) {
   const int G = Hq / Hkv;
   require(Hq % Hkv == 0 && n_rows * G <= 64, "decode attention needs <= 64 query vectors per head");
+  require(ranges >= 1 && ranges <= 128, "decode attention takes 1..128 key ranges");
   const int qt = (n_rows * G + 31) / 32;
   const float scale = 1.0f / sqrtf(128.0f);
-  const size_t lds = (size_t)2 * (qt * 64 * 64 + qt * 64 * 2) * 4;
+  const size_t lds = (size_t)qt * 32 * DEC_QROW * 2 + (size_t)4 * (qt * 4096 + qt * 128) * 4;
   const dim3 grid(ranges, Hkv);
   const double bytes = 2.0 * n_rows * Hq * 128 + 4.0 * n_keys * Hkv * 128;
+  float* o_part = part;
+  float* ml_part = part + (size_t)ranges * Hkv * qt * 4096;
 #define DRT_DEC(T, QT)                                                                      \
   {                                                                                         \
     auto fn = attn_decode_kernel<T, QT>;                                                    \
@@ -628,9 +767,15 @@ void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv
   }
 #undef DRT_DEC
   DRT_HIP(hipGetLastError());
-  const int64_t waves = (int64_t)n_rows * Hq;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s,
-                     o_part, ml_part, ranges, n_rows, Hq, Hkv, out, xsum, out_fmt);
+  (void)xsum;  // the F16P output's consumer computes its own group sums
+  const dim3 cgrid(Hkv, qt, 16);
+  const size_t clds = (size_t)ranges * 32 * 4;
+  if (qt == 1)
+    hipLaunchKernelGGL(attn_decode_combine_kernel<1>, cgrid, dim3(256), clds, s, o_part, ml_part,
+                       ranges, n_rows, Hq, Hkv, out, out_fmt);
+  else
+    hipLaunchKernelGGL(attn_decode_combine_kernel<2>, cgrid, dim3(256), clds, s, o_part, ml_part,
+                       ranges, n_rows, Hq, Hkv, out, out_fmt);
   DRT_HIP(hipGetLastError());
 }
 

@@ -54,14 +54,32 @@ DRT_DEV size_t act_row_bytes(int fmt, int d) { return fmt == 2 ? (size_t)d * 4 :
 
 // tokens[M] -> hidden fp32 [M][d] (bf16 embedding rows cast to fp32,
 // backends/mlx_forward.py:1538-1557).
+// Also writes, when ss_out is set, the rows' partial sums of squares per 32
+// columns (ss_out[c*32 + m], c = column / 32) for the next RMSNorm; grid rows
+// M .. 31 (when launched) write zero partials.
 extern "C" __global__ void embed_kernel(const int32_t* __restrict__ tokens,
                                         const uint16_t* __restrict__ table,
-                                        float* __restrict__ hidden, int M, int d) {
+                                        float* __restrict__ hidden, int M, int d,
+                                        float* __restrict__ ss_out) {
   const int m = blockIdx.x;
-  if (m >= M) return;
+  if (m >= M) {
+    if (ss_out)
+      for (int c = threadIdx.x; c < d / 32; c += blockDim.x) ss_out[c * 32 + m] = 0.f;
+    return;
+  }
   const int64_t tok = tokens[m];
   for (int k = threadIdx.x; k < d; k += blockDim.x)
     hidden[(int64_t)m * d + k] = bf16_bits_to_float(table[tok * d + k]);
+  if (ss_out) {
+    for (int c = threadIdx.x; c < d / 32; c += blockDim.x) {
+      float q = 0.f;
+      for (int k = 0; k < 32; ++k) {
+        const float v = bf16_bits_to_float(table[tok * d + c * 32 + k]);
+        q += v * v;
+      }
+      ss_out[c * 32 + m] = q;
+    }
+  }
 }
 
 // One 256-thread WG per output row. Requires d % 256 == 0 (true for every
@@ -159,8 +177,11 @@ extern "C" __global__ void swiglu_rows_kernel(const float* __restrict__ g,
 namespace drt {
 
 void embed(const int32_t* tokens, const uint16_t* table, float* hidden, int M, int d,
-           hipStream_t s) {
-  hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, s, tokens, table, hidden, M, d);
+           float* ss_out, hipStream_t s) {
+  // with ss_out, rows up to 32 are launched so unused rows get zero partials
+  const int grid = ss_out ? std::max(M, 32) : M;
+  hipLaunchKernelGGL(embed_kernel, dim3(grid), dim3(256), 0, s, tokens, table, hidden, M, d,
+                     ss_out);
   DRT_HIP(hipGetLastError());
 }
 

@@ -41,8 +41,27 @@ struct FusedArgs {
   int64_t kv_head_stride = 0;
   int Hq = 0, Hkv = 0, kv_bf16 = 0;
   const StepDesc* desc = nullptr;  // row0: absolute position of row 0
+  // Skinny (M <= 32, q4) path: split-K partial tiles, arrival counters (zero on
+  // entry, left zero on exit) and the RMSNorm row statistics carried between
+  // kernels as per-32-column partial sums of squares ([K/32][32] floats).
+  float* part = nullptr;
+  size_t part_floats = 0;
+  int* counters = nullptr;
+  int n_counters = 0;
+  const float* ss_in = nullptr;  // PRO_NORM: partial sums of squares of `hidden` rows
+  float* ss_out = nullptr;       // EPI_RESID: partial sums of squares of the new rows
+  // XCDs of the device (work-group i runs on XCD i % n_xcc) and the flag a
+  // work-group sets if it finds itself on another XCD
+  int n_xcc = 1;
+  int* placement_err = nullptr;
 };
 
 namespace drt {
 void fused_linear(const FusedArgs& a, int kind, hipStream_t s);
+// The split-K skinny kernels for q4 weights and M <= 32 rows; returns false
+// (launching nothing) when the arguments do not fit them.
+bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s);
+// Workspace the skinny kernels need for a linear of N outputs and K inputs.
+size_t skinny_part_floats(int N, int K);
+int skinny_counters(int N);
 }

@@ -38,12 +38,23 @@ inline void require(bool ok, const std::string& m) {
 struct DevBuf {
   void* p = nullptr;
   size_t bytes = 0;
+  bool owned = true;  // false: a view into memory owned elsewhere (an arena)
   DevBuf() = default;
   DevBuf(const DevBuf&) = delete;
   DevBuf& operator=(const DevBuf&) = delete;
-  DevBuf(DevBuf&& o) noexcept : p(o.p), bytes(o.bytes) { o.p = nullptr; o.bytes = 0; }
+  DevBuf(DevBuf&& o) noexcept : p(o.p), bytes(o.bytes), owned(o.owned) {
+    o.p = nullptr;
+    o.bytes = 0;
+  }
   DevBuf& operator=(DevBuf&& o) noexcept {
-    if (this != &o) { release(); p = o.p; bytes = o.bytes; o.p = nullptr; o.bytes = 0; }
+    if (this != &o) {
+      release();
+      p = o.p;
+      bytes = o.bytes;
+      owned = o.owned;
+      o.p = nullptr;
+      o.bytes = 0;
+    }
     return *this;
   }
   ~DevBuf() { release(); }
@@ -51,12 +62,19 @@ struct DevBuf {
     release();
     if (n) DRT_HIP(hipMalloc(&p, n));
     bytes = n;
+    owned = true;
+  }
+  void view(void* q, size_t n) {
+    release();
+    p = q;
+    bytes = n;
+    owned = false;
   }
   void ensure(size_t n) {
     if (n > bytes) alloc(n);
   }
   void release() {
-    if (p) (void)hipFree(p);
+    if (p && owned) (void)hipFree(p);
     p = nullptr;
     bytes = 0;
   }
@@ -161,16 +179,22 @@ void attention(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_s
                int n_rows, int Hq, int Hkv, int n_keys, int row_pos0, int mask_kind,
                int mask_prompt_len, int mask_block, const AttnPlan& plan, float* o_part,
                float* ml_part, void* out, float* xsum, int out_fmt, hipStream_t s);
+// Decode attention over `ranges` key ranges (attention_decode_ranges(n_keys, Hkv) when
+// the key count is known at launch) + the range combine; `part` is a workspace of
+// attention_decode_part_bytes(ranges, Hkv, n_rows * Hq / Hkv) bytes.
+size_t attention_decode_part_bytes(int ranges, int Hkv, int n_qv);
+int attention_decode_ranges(int n_keys, int Hkv);
 void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_stride,
                       int n_rows, int Hq, int Hkv, int n_keys, const StepDesc* desc, int ranges,
-                      float* o_part, float* ml_part, void* out, float* xsum, int out_fmt,
-                      hipStream_t s);
+                      float* part, void* out, float* xsum, int out_fmt, hipStream_t s);
 void kv_pack(bool kv_bf16, const void* k, const void* v, bool src_bf16, int n, int Hkv, int pos0,
              void* kv_layer, int64_t kv_head_stride, hipStream_t s);
 
 // Epilogues.
+// ss_out (optional, M <= 32): per-32-column partial sums of squares of the rows,
+// [d/32][32], the row statistics of the first decoder layer's RMSNorm.
 void embed(const int32_t* tokens, const uint16_t* table, float* hidden, int M, int d,
-           hipStream_t s);
+           float* ss_out, hipStream_t s);
 void residual_norm(float* hidden, const float* part, int splits, int M_part, bool rnd_bf16,
                    const int32_t* src_rows, bool write_hidden, const uint16_t* norm_w, float eps,
                    int d, int fmt, void* act, float* xsum, int n_out_rows, hipStream_t s);

@@ -93,6 +93,19 @@ struct LayerW {
   DevBuf in_norm, post_norm, q_norm, k_norm;
 };
 
+// All weights of a runtime live in one allocation: one mapping, large pages, and
+// TLB reach for the whole model instead of a few hundred small buffers.
+struct Arena {
+  DevBuf mem;
+  size_t off = 0;
+  static size_t round(size_t n) { return (n + 255) & ~(size_t)255; }
+  void place(DevBuf& b, size_t n) {
+    require(off + round(n) <= mem.bytes, "weight arena overflow");
+    b.view((char*)mem.p + off, n);
+    off += round(n);
+  }
+};
+
 struct Runtime {
   drt_engine_config engine{};
   drt_model_geometry geo{};
@@ -105,6 +118,7 @@ struct Runtime {
   DevBuf embed;       // bf16 [V][d]
   DevBuf final_norm;  // bf16 [d]
   LinearW lm_head;
+  Arena warena;               // every weight below is a view into it
   DevBuf rope_cos, rope_sin;  // fp32 [P][64]
   int rope_positions = 0;
   int max_rows = 0;
@@ -112,6 +126,15 @@ struct Runtime {
   // workspace (sized for max_rows)
   DevBuf hidden, act, xsum, act_lm, xsum_lm, qbuf, attn_part, stats, scores, tokens_out, lm_rows,
       lm_pos, logits;
+  // split-K linears of <= 32-row forwards: partial tiles, arrival counters
+  // (zeroed once; every kernel leaves them zero) and the residual stream's
+  // per-32-column partial sums of squares
+  DevBuf sk_part, sk_counters, sk_ss;
+  size_t sk_part_floats = 0;
+  int sk_n_counters = 0;
+  int n_xcc = 1;
+  DevBuf placement_err;          // int, set by a kernel that finds itself on an unexpected XCD
+  int* placement_host = nullptr; // pinned copy, read after each synchronized forward
   // Per-forward inputs: one pinned host slot + its device copy per forward, moved
   // by a single async copy. Slot 0 belongs to the commit graph, slot 1 to the
   // step graph; eager forwards rotate through the rest.
@@ -131,6 +154,7 @@ struct Runtime {
   ~Runtime() {
     if (stream) (void)hipStreamSynchronize(stream);
     if (up_host) (void)hipHostFree(up_host);
+    if (placement_host) (void)hipHostFree(placement_host);
     if (ev0) (void)hipEventDestroy(ev0);
     if (ev1) (void)hipEventDestroy(ev1);
     if (stream) (void)hipStreamDestroy(stream);
@@ -172,11 +196,11 @@ void check_tensor(const drt_tensor& t, int dtype, std::initializer_list<int64_t>
   if (!t.data) fail(INVALID_ARGUMENT, "tensor '" + n + "' has a null data pointer");
 }
 
-void copy_bf16_vec(DevBuf& dst, const WeightMap& wm, const std::string& name, int n,
+void copy_bf16_vec(Arena& ar, DevBuf& dst, const WeightMap& wm, const std::string& name, int n,
                    hipStream_t s) {
   const drt_tensor& t = wm.get(name);
   check_tensor(t, DRT_BF16, {n});
-  dst.alloc((size_t)n * 2);
+  ar.place(dst, (size_t)n * 2);
   DRT_HIP(hipMemcpyAsync(dst.p, t.data, (size_t)n * 2, hipMemcpyDeviceToDevice, s));
 }
 
@@ -202,9 +226,16 @@ void repack_rows(LinearW& w, const WeightMap& wm, const std::string& part, int r
 
 // Build one fused linear from parts stacked along N (each part N_i rows, same K).
 // interleave64: two parts of equal N laid out as [p0 64 | p1 64] per 128 columns.
-void build_linear(LinearW& w, const WeightMap& wm, const std::vector<std::string>& parts,
-                  const std::vector<int>& Ns, int K, bool q4, bool with_bias, hipStream_t s,
-                  bool interleave64 = false) {
+size_t linear_arena_bytes(int N, int K, bool q4, bool with_bias) {
+  size_t b = q4 ? Arena::round((size_t)N * K / 2) + Arena::round((size_t)N * (K / 64) * 4)
+                : Arena::round((size_t)N * K * 2);
+  if (with_bias) b += Arena::round((size_t)N * 2);
+  return b;
+}
+
+void build_linear(Arena& ar, LinearW& w, const WeightMap& wm,
+                  const std::vector<std::string>& parts, const std::vector<int>& Ns, int K,
+                  bool q4, bool with_bias, hipStream_t s, bool interleave64 = false) {
   int N = 0;
   for (int n : Ns) N += n;
   w.N = N;
@@ -212,10 +243,10 @@ void build_linear(LinearW& w, const WeightMap& wm, const std::vector<std::string
   w.q4 = q4;
   if (q4) {
     require(K % 64 == 0, "q4 linear in-dim must be a multiple of 64");
-    w.qw.alloc((size_t)N * K / 2);
-    w.sb.alloc((size_t)N * (K / 64) * 4);
+    ar.place(w.qw, (size_t)N * K / 2);
+    ar.place(w.sb, (size_t)N * (K / 64) * 4);
   } else {
-    w.wb.alloc((size_t)N * K * 2);
+    ar.place(w.wb, (size_t)N * K * 2);
   }
   for (size_t i = 0; i < parts.size(); ++i) {
     const int n = Ns[i];
@@ -241,7 +272,7 @@ void build_linear(LinearW& w, const WeightMap& wm, const std::vector<std::string
   }
   if (with_bias) {
     require(!interleave64, "biases are not interleaved");
-    w.bias.alloc((size_t)N * 2);
+    ar.place(w.bias, (size_t)N * 2);
     int n0 = 0;
     for (size_t i = 0; i < parts.size(); ++i) {
       const drt_tensor& b = wm.get(parts[i] + ".bias");
@@ -295,31 +326,43 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
   const int d = g.hidden_size, hd = 128, Hq = g.num_heads, Hkv = g.num_kv_heads,
             F = g.intermediate_size, V = g.vocab_size;
   {
+    size_t total = Arena::round((size_t)V * d * 2) + Arena::round((size_t)d * 2) +
+                   linear_arena_bytes(V, d, rt->q4, false);
+    const size_t per_layer =
+        linear_arena_bytes((Hq + 2 * Hkv) * hd, d, rt->q4, g.qkv_bias != 0) +
+        linear_arena_bytes(d, Hq * hd, rt->q4, false) + linear_arena_bytes(2 * F, d, rt->q4, false) +
+        linear_arena_bytes(d, F, rt->q4, false) + 2 * Arena::round((size_t)d * 2) +
+        2 * Arena::round((size_t)hd * 2);
+    total += per_layer * g.layer_count;
+    rt->warena.mem.alloc(total);
+  }
+  Arena& ar = rt->warena;
+  {
     const drt_tensor& t = wm.get("model.embed_tokens.weight");
     check_tensor(t, DRT_BF16, {V, d});
-    rt->embed.alloc((size_t)V * d * 2);
+    ar.place(rt->embed, (size_t)V * d * 2);
     DRT_HIP(hipMemcpyAsync(rt->embed.p, t.data, (size_t)V * d * 2, hipMemcpyDeviceToDevice, s));
   }
   rt->layers.resize(g.layer_count);
   for (int l = 0; l < g.layer_count; ++l) {
     const std::string p = "model.layers." + std::to_string(l) + ".";
     LayerW& L = rt->layers[l];
-    build_linear(L.qkv, wm,
+    build_linear(ar, L.qkv, wm,
                  {p + "self_attn.q_proj", p + "self_attn.k_proj", p + "self_attn.v_proj"},
                  {Hq * hd, Hkv * hd, Hkv * hd}, d, rt->q4, g.qkv_bias != 0, s);
-    build_linear(L.o, wm, {p + "self_attn.o_proj"}, {d}, Hq * hd, rt->q4, false, s);
-    build_linear(L.gu, wm, {p + "mlp.gate_proj", p + "mlp.up_proj"}, {F, F}, d, rt->q4, false, s,
+    build_linear(ar, L.o, wm, {p + "self_attn.o_proj"}, {d}, Hq * hd, rt->q4, false, s);
+    build_linear(ar, L.gu, wm, {p + "mlp.gate_proj", p + "mlp.up_proj"}, {F, F}, d, rt->q4, false, s,
                  /*interleave64=*/true);
-    build_linear(L.down, wm, {p + "mlp.down_proj"}, {d}, F, rt->q4, false, s);
-    copy_bf16_vec(L.in_norm, wm, p + "input_layernorm.weight", d, s);
-    copy_bf16_vec(L.post_norm, wm, p + "post_attention_layernorm.weight", d, s);
+    build_linear(ar, L.down, wm, {p + "mlp.down_proj"}, {d}, F, rt->q4, false, s);
+    copy_bf16_vec(ar, L.in_norm, wm, p + "input_layernorm.weight", d, s);
+    copy_bf16_vec(ar, L.post_norm, wm, p + "post_attention_layernorm.weight", d, s);
     if (g.qk_norm) {
-      copy_bf16_vec(L.q_norm, wm, p + "self_attn.q_norm.weight", hd, s);
-      copy_bf16_vec(L.k_norm, wm, p + "self_attn.k_norm.weight", hd, s);
+      copy_bf16_vec(ar, L.q_norm, wm, p + "self_attn.q_norm.weight", hd, s);
+      copy_bf16_vec(ar, L.k_norm, wm, p + "self_attn.k_norm.weight", hd, s);
     }
   }
-  copy_bf16_vec(rt->final_norm, wm, "model.norm.weight", d, s);
-  build_linear(rt->lm_head, wm, {"lm_head"}, {V}, d, rt->q4, false, s);
+  copy_bf16_vec(ar, rt->final_norm, wm, "model.norm.weight", d, s);
+  build_linear(ar, rt->lm_head, wm, {"lm_head"}, {V}, d, rt->q4, false, s);
   {
     const drt_tensor& c = wm.get("rope.cos");
     const drt_tensor& sn = wm.get("rope.sin");
@@ -353,6 +396,30 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
   rt->tokens_out.alloc((size_t)lm_cap * 4);
   rt->lm_rows.alloc((size_t)lm_cap * 4);
   rt->lm_pos.alloc((size_t)lm_cap * 4);
+  {
+    const int n_qkv = (Hq + 2 * Hkv) * hd;
+    size_t pf = 0;
+    int nc = 0;
+    for (auto nk : {std::make_pair(n_qkv, d), std::make_pair(d, Hq * hd), std::make_pair(2 * F, d),
+                    std::make_pair(d, F)}) {
+      pf = std::max(pf, skinny_part_floats(nk.first, nk.second));
+      nc = std::max(nc, skinny_counters(nk.first));
+    }
+    rt->sk_part_floats = pf;
+    rt->sk_n_counters = nc;
+    rt->sk_part.alloc(std::max<size_t>(pf, 1) * 4);
+    rt->sk_counters.alloc((size_t)std::max(nc, 1) * 4);
+    DRT_HIP(hipMemsetAsync(rt->sk_counters.p, 0, rt->sk_counters.bytes, s));
+    rt->sk_ss.alloc((size_t)d * 4);  // [d/32][32]
+    int nx = 1;
+    if (hipDeviceGetAttribute(&nx, hipDeviceAttributeNumberOfXccs, rt->device) != hipSuccess)
+      nx = 1;
+    rt->n_xcc = std::max(1, nx);
+    rt->placement_err.alloc(4);
+    DRT_HIP(hipMemsetAsync(rt->placement_err.p, 0, 4, s));
+    DRT_HIP(hipHostMalloc((void**)&rt->placement_host, 4, hipHostMallocDefault));
+    *rt->placement_host = 0;
+  }
   DRT_HIP(hipStreamSynchronize(s));
   size_t total = rt->embed.bytes + rt->final_norm.bytes + rt->lm_head.qw.bytes +
                  rt->lm_head.sb.bytes + rt->lm_head.wb.bytes + rt->hidden.bytes + rt->act.bytes +
@@ -395,10 +462,7 @@ bool one_segment(const ForwardArgs& a) {
   return a.n_keys <= seg_end;
 }
 
-int decode_ranges(int n_keys) {
-  const int tiles = (n_keys + 31) / 32;
-  return std::max(1, std::min(32, (tiles + 7) / 8));
-}
+
 
 // Device addresses of one forward's inputs.
 struct ForwardPtrs {
@@ -490,8 +554,8 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
   int ranges = 1;
   size_t apb;
   if (decode_attn) {
-    ranges = p.ranges > 0 ? p.ranges : decode_ranges(a.n_keys);
-    apb = (size_t)ranges * Hkv * M * G * 130 * 4;
+    ranges = p.ranges > 0 ? p.ranges : attention_decode_ranges(a.n_keys, Hkv);
+    apb = attention_decode_part_bytes(ranges, Hkv, M * G);
   } else {
     ap = plan_attention(M, Hq, Hkv, a.n_keys, rt.attn_part_budget);
     apb = attention_part_bytes(ap, M, Hq, Hkv);
@@ -501,7 +565,10 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
   float* o_part = rt.attn_part.as<float>();
   float* ml_part = o_part + (size_t)splits * Hkv * M * G * 128;
 
-  embed(p.tokens_rel, rt.embed.as<uint16_t>(), hidden, M, d, s);
+  // <= 32-row forwards use the split-K linears, which carry the RMSNorm row
+  // statistics from each residual update to the next norm
+  float* ss = M <= 32 ? rt.sk_ss.as<float>() : nullptr;
+  embed(p.tokens_rel, rt.embed.as<uint16_t>(), hidden, M, d, ss, s);
   const int L = (int)rt.layers.size();
   for (int l = 0; l < L; ++l) {
     LayerW& w = rt.layers[l];
@@ -517,6 +584,12 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
       f.eps = eps;
       f.rnd_bf16 = !rt.q4;
       f.desc = desc;
+      f.part = rt.sk_part.as<float>();
+      f.part_floats = rt.sk_part_floats;
+      f.counters = rt.sk_counters.as<int>();
+      f.n_counters = rt.sk_n_counters;
+      f.n_xcc = rt.n_xcc;
+      f.placement_err = rt.placement_err.as<int>();
       return f;
     };
     {  // input RMSNorm -> fused q|k|v -> q/k norm + RoPE -> Q, K/V cache
@@ -533,11 +606,12 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
       f.Hq = Hq;
       f.Hkv = Hkv;
       f.kv_bf16 = rt.kv_bf16;
+      f.ss_in = ss;
       fused_linear(f, FL_QKV, s);
     }
     if (decode_attn)
       attention_decode(rt.kv_bf16, rt.qbuf.p, kv_layer(l), head_stride, M, Hq, Hkv, a.n_keys, desc,
-                       ranges, o_part, ml_part, rt.act.p, xs, fmt, s);
+                       ranges, o_part, rt.act.p, xs, fmt, s);
     else
       attention(rt.kv_bf16, rt.qbuf.p, kv_layer(l), head_stride, M, Hq, Hkv, a.n_keys, a.row0,
                 a.mask_kind, a.mask_prompt_len, a.mask_block, ap, o_part, ml_part, rt.act.p, xs,
@@ -549,6 +623,7 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
       f.act = rt.act.p;
       f.act_xsum = xs;
       f.hidden_out = hidden;
+      f.ss_out = ss;
       fused_linear(f, FL_RESID, s);
     }
     {  // post-attention RMSNorm -> [gate | up] -> SwiGLU -> down activation
@@ -558,6 +633,7 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
       f.act_out = rt.act.p;
       f.xsum_out = xs;
       f.act_fmt = fmt;
+      f.ss_in = ss;
       fused_linear(f, FL_SWIGLU, s);
     }
     {  // down_proj + residual
@@ -565,6 +641,7 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
       f.act = rt.act.p;
       f.act_xsum = xs;
       f.hidden_out = hidden;
+      f.ss_out = ss;
       fused_linear(f, FL_RESID, s);
     }
   }
@@ -575,6 +652,15 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
            a.temperature, a.seed, a.step, p.lm_pos, rt.scores.as<double>(),
            rt.tokens_out.as<int32_t>(), s, desc);
   }
+}
+
+// The split-K linears rely on work-group i running on XCD i % n_xcc; a kernel
+// that observed otherwise left a flag (read back with the forward's results).
+void check_placement(const Runtime& rt) {
+  if (*rt.placement_host != 0)
+    fail(INTERNAL_ERROR,
+         "a split-K linear ran on an unexpected XCD (work-group placement is not the "
+         "round-robin the kernels assume); results of this runtime are not valid");
 }
 
 void run_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_stride,
@@ -692,7 +778,7 @@ struct Session {
     drop_graphs();  // captured forwards point at the old cache
     kv = std::move(grown);
     tile_cap = tiles;
-    g_ranges = decode_ranges(tile_cap * 32);
+    g_ranges = attention_decode_ranges(tile_cap * 32, r.Hkv());
     head_stride = new_head;
     layer_stride = head_stride * r.Hkv();
     m.kv_cache_bytes = (int64_t)kv.bytes;
@@ -968,7 +1054,10 @@ int32_t drt_session_propose(uint64_t session, const int32_t* frontier, int32_t n
                            r.stream));
     DRT_HIP(hipMemcpyAsync(out_tokens, r.tokens_out.p, (size_t)n_frontier * 4,
                            hipMemcpyDeviceToHost, r.stream));
+    DRT_HIP(hipMemcpyAsync(r.placement_host, r.placement_err.p, 4, hipMemcpyDeviceToHost,
+                           r.stream));
     DRT_HIP(hipStreamSynchronize(r.stream));
+    check_placement(r);
     s->finish_timing();
     s->publish_profile();
     s->proposals += 1;
@@ -1086,7 +1175,10 @@ int32_t drt_session_execute_window(uint64_t session, const int32_t* token_ids, i
     DRT_HIP(hipEventRecord(r.ev1, r.stream));
     DRT_HIP(hipMemcpyAsync(out_logits, r.logits.p, (size_t)n_scope * r.V() * 4,
                            hipMemcpyDeviceToHost, r.stream));
+    DRT_HIP(hipMemcpyAsync(r.placement_host, r.placement_err.p, 4, hipMemcpyDeviceToHost,
+                           r.stream));
     DRT_HIP(hipStreamSynchronize(r.stream));
+    check_placement(r);
     s->finish_timing();
     s->publish_profile();
     s->m.forward_count += 1;
@@ -1216,7 +1308,7 @@ size_t drt_op_attention_workspace_bytes(int32_t rows, int32_t hq, int32_t hkv, i
   if (rows <= 0 || hq <= 0 || hkv <= 0 || hq % hkv || n_keys <= 0) return 0;
   const AttnPlan p = plan_attention(rows, hq, hkv, n_keys, (size_t)256 << 20);
   const size_t general = attention_part_bytes(p, rows, hq, hkv);
-  const size_t decode = (size_t)decode_ranges(n_keys) * hkv * rows * (hq / hkv) * 130 * 4;
+  const size_t decode = attention_decode_part_bytes(attention_decode_ranges(n_keys, hkv), hkv, rows * (hq / hkv));
   return std::max(general, decode) + 256;
 }
 
@@ -1247,10 +1339,9 @@ int32_t drt_op_attention(const void* q, const void* cache, int64_t head_stride, 
     float* o_part = (float*)workspace;
     const int ofmt = out_dtype == DRT_F32 ? 2 : 3;
     if (rows * (hq / hkv) <= 64 && one_segment(fa)) {
-      const int ranges = decode_ranges(n_keys);
-      float* ml_part = o_part + (size_t)ranges * hkv * rows * (hq / hkv) * 128;
+      const int ranges = attention_decode_ranges(n_keys, hkv);
       attention_decode(kv_dtype == DRT_BF16, q, cache, head_stride, rows, hq, hkv, n_keys,
-                       nullptr, ranges, o_part, ml_part, out, nullptr, ofmt, as_stream(stream));
+                       nullptr, ranges, o_part, out, nullptr, ofmt, as_stream(stream));
     } else {
       const AttnPlan p = plan_attention(rows, hq, hkv, n_keys, (size_t)256 << 20);
       float* ml_part = o_part + (size_t)p.splits * hkv * rows * (hq / hkv) * 128;

@@ -1,0 +1,595 @@
+// Split-K linears for decode-sized activations (M <= 32 rows) and q4 weights.
+//
+// A decode step's linears read only 1-4 MB of weights; what bounds them is how
+// much each CU must pull (about 64 GB/s per CU) and how many dependent memory
+// round trips a work-group makes. So these kernels spread every linear over
+// 128-448 work-groups of 4 waves, each reading a K slice of its columns' weights
+// and only that slice of the activation, with every load issued up front. The
+// K slices of one output block meet in a global workspace: each work-group
+// writes its partial tile, bumps the block's arrival counter, and the last to
+// arrive adds the partials in slice order (deterministic) and runs the
+// epilogue. Nothing waits on another work-group, so no launch order is assumed.
+//
+// The exchange stays inside one XCD's L2: work-group i runs on XCD i % n_xcc
+// (the dispatcher's round-robin), so the grid is laid out to give every slice
+// of block b the XCD b % n_xcc. Plain stores, the L2 atomic and plain loads are
+// then coherent with each other, with no device-wide fence (an L2 writeback and
+// invalidate per work-group costs tens of microseconds). Each work-group checks
+// the XCD it runs on and raises `placement_err` if the layout assumption fails,
+// which the host turns into an error.
+//
+//   skinny_wide_kernel  : 128 columns (4 n-tiles, one per wave), RMSNorm
+//                         prologue (row statistics from the producer's
+//                         per-32-column partial sums of squares), epilogue on a
+//                         whole head (q/k norm, RoPE, Q out, K/V into the cache)
+//                         or a [gate 64 | up 64] block (SwiGLU -> down activation).
+//   skinny_narrow_kernel: 32 columns, 4 waves split the slice, the activation
+//                         (ACT_F16P) read straight from global; epilogue
+//                         hidden += tile (+ the new rows' partial sums of
+//                         squares for the next RMSNorm) or y = tile (+ bias).
+// Reference math: backends/mlx_ops.py:21-35 (rms_norm), :97-130 (q4 linear),
+// :133-154 (rope, swiglu); backends/mlx_forward.py:1164-1361 (layer).
+#include "fused.h"
+#include "gemm_core.h"
+#include "launch.h"
+#include "linear_dev.h"
+
+#include <cstdlib>
+
+namespace {
+
+constexpr int SK_RED = 4 * 32 * 33;  // floats of the [4][32][33] reduction tile
+constexpr int SK_KS_MAX = 8;         // K slices per output tile (host-enforced)
+constexpr int SK_SS_PER_THREAD = 14; // K / 32 <= 8 * 14 = 112 partial sums (d <= 3584)
+
+// LDS of the wide kernel: xs [32][64U + 8] halves, xss [U][32], rinv [32],
+// red [4][32][33], flag (16 B), then the V tile half [4096] halves.
+#define SK_WIDE_V_OFF(U) (((32 * ((U) * 64 + 8) * 2 + (U) * 32 * 4 + 32 * 4 + SK_RED * 4 + 16) + 15) / 16 * 16)
+#define SK_WIDE_LDS(U) (SK_WIDE_V_OFF(U) + 4096 * 2)
+
+// Block and K slice of this work-group: with x = i % n_xcc and j = i / n_xcc,
+// block x + n_xcc * (j / KS) and slice j % KS, so a block's slices share an XCD.
+// Returns false for the padding work-groups past the last block.
+DRT_DEV bool sk_place(const FusedArgs& a, int n_blocks, int KS, int& blk, int& ks) {
+  const int i = blockIdx.x, x = i % a.n_xcc, j = i / a.n_xcc;
+  blk = x + a.n_xcc * (j / KS);
+  ks = j - (j / KS) * KS;
+  if (a.n_xcc > 1 && threadIdx.x == 0 && a.placement_err) {
+    const int xcc = (int)(__builtin_amdgcn_s_getreg((31 << 11) | 20) & 0xf);  // HW_REG_XCC_ID
+    if (xcc != x) __hip_atomic_fetch_or(a.placement_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return blk < n_blocks;
+}
+
+// Called after this work-group stored its partial: returns true in the last
+// work-group of the block to arrive (which then adds the partials up), false
+// elsewhere. The stores complete (in this XCD's L2) before the barrier, and the
+// counter is bumped by an L2 atomic after it.
+DRT_DEV bool last_to_arrive(int* counter, int arrivals, int* flag) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    *flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) ==
+            arrivals - 1;
+  __syncthreads();
+  return *flag != 0;
+}
+
+}  // namespace
+
+// Epilogue of one q/k/v head over the block's rows (backends/mlx_forward.py:
+// 1164-1361): (+ bias), per-head RMSNorm of q/k (mlx_ops.py:21-35), split-half
+// RoPE at the row's absolute position (mlx_ops.py:133-144), then Q out or K/V
+// into the tiled cache. Thread t owns row t >> 3 and the head dims 8c .. 8c+7
+// and 64+8c .. 64+8c+7 (c = t & 7): the RoPE pairs of its dims are its own, the
+// norm is a sum over 8 lanes, and every store is 16 bytes - except V, whose
+// tile layout spreads a key over the tile: a whole 32-key tile (M == 32,
+// aligned) is assembled in LDS first, otherwise V is written element-wise.
+template <typename T>
+DRT_DEV void qkv_epilogue(const FusedArgs& a, int head, int row0, const float* red,
+                          uint16_t* lds_v) {
+  const int M = a.M, Hq = a.Hq, Hkv = a.Hkv;
+  const int m = threadIdx.x >> 3, c = threadIdx.x & 7;
+  const bool is_q = head < Hq, is_k = !is_q && head < Hq + Hkv, is_v = !is_q && !is_k;
+  const int pos = row0 + m;
+  const int pos_t = m < M ? pos : row0;  // rows past M read a valid table row
+  float x[8], y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int d0 = 8 * c + e, d1 = 64 + 8 * c + e;
+    x[e] = red[((d0 >> 5) * 32 + m) * 33 + (d0 & 31)];
+    y[e] = red[((d1 >> 5) * 32 + m) * 33 + (d1 & 31)];
+  }
+  if (a.bias) {
+    const u32x4 b0 = *(const u32x4*)(a.bias + head * 128 + 8 * c);
+    const u32x4 b1 = *(const u32x4*)(a.bias + head * 128 + 64 + 8 * c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] += bf16_bits_to_float(b0[e] & 0xffffu);
+      x[2 * e + 1] += bf16_bits_to_float(b0[e] >> 16);
+      y[2 * e] += bf16_bits_to_float(b1[e] & 0xffffu);
+      y[2 * e + 1] += bf16_bits_to_float(b1[e] >> 16);
+    }
+  }
+  if (!is_v) {
+    const uint16_t* nw = is_q ? a.q_norm : a.k_norm;
+    // rotary tables: cos/sin [pos][64] fp32, angle i shared by dims i and i + 64
+    const f32x4* cp = (const f32x4*)(a.rope_cos + (int64_t)pos_t * 64 + 8 * c);
+    const f32x4* sp = (const f32x4*)(a.rope_sin + (int64_t)pos_t * 64 + 8 * c);
+    const f32x4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+    if (nw) {
+      const u32x4 w0 = *(const u32x4*)(nw + 8 * c), w1 = *(const u32x4*)(nw + 64 + 8 * c);
+      float q = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) q += x[e] * x[e] + y[e] * y[e];
+      q += __shfl_xor(q, 1, 64);
+      q += __shfl_xor(q, 2, 64);
+      q += __shfl_xor(q, 4, 64);
+      const float inv = 1.f / sqrtf(q / 128.f + a.eps);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[2 * e] = (x[2 * e] * inv) * bf16_bits_to_float(w0[e] & 0xffffu);
+        x[2 * e + 1] = (x[2 * e + 1] * inv) * bf16_bits_to_float(w0[e] >> 16);
+        y[2 * e] = (y[2 * e] * inv) * bf16_bits_to_float(w1[e] & 0xffffu);
+        y[2 * e + 1] = (y[2 * e + 1] * inv) * bf16_bits_to_float(w1[e] >> 16);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float cs = e < 4 ? c0[e] : c1[e - 4], sn = e < 4 ? s0[e] : s1[e - 4];
+      const float r0 = x[e] * cs - y[e] * sn;
+      const float r1 = y[e] * cs + x[e] * sn;
+      x[e] = r0;
+      y[e] = r1;
+    }
+  }
+  T hx[8], hy[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    hx[e] = cvt_to<T>(x[e]);
+    hy[e] = cvt_to<T>(y[e]);
+  }
+  if (is_q) {
+    if (m < M) {
+      T* qo = (T*)a.q_out + ((int64_t)m * Hq + head) * 128 + 8 * c;
+      *(u32x4*)qo = __builtin_bit_cast(u32x4, hx);
+      *(u32x4*)(qo + 64) = __builtin_bit_cast(u32x4, hy);
+    }
+    return;
+  }
+  const int kvh = is_k ? head - Hq : head - Hq - Hkv;
+  if (is_k) {
+    if (m < M) {
+      // K[kk][hd] at ((hd/16*2 + (hd/8)&1)*32 + kk)*8 + hd%8: dims 8c.. are chunk c
+      T* tile = (T*)a.kv_layer + (int64_t)kvh * a.kv_head_stride + (int64_t)(pos >> 5) * 8192;
+      const int kk = pos & 31;
+      *(u32x4*)(tile + (c * 32 + kk) * 8) = __builtin_bit_cast(u32x4, hx);
+      *(u32x4*)(tile + ((8 + c) * 32 + kk) * 8) = __builtin_bit_cast(u32x4, hy);
+    }
+    return;
+  }
+  // V[kk][hd] at 4096 + ((((hd/32)*2 + kk/16)*2 + h)*32 + hd%32)*8 + j with
+  // q = kk%16, h = (q/4)&1, j = q%4 + 4*(q/8)
+  auto v_off = [](int hd, int kk) {
+    const int q16 = kk & 15;
+    return 4096 + ((((hd >> 5) * 2 + (kk >> 4)) * 2 + ((q16 >> 2) & 1)) * 32 + (hd & 31)) * 8 +
+           (q16 & 3) + 4 * (q16 >> 3);
+  };
+  T* tile = (T*)a.kv_layer + (int64_t)kvh * a.kv_head_stride + (int64_t)(row0 >> 5) * 8192;
+  if (M == 32 && (row0 & 31) == 0) {
+    T* vs = (T*)lds_v;  // the V half of the tile, [4096]
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      vs[v_off(8 * c + e, m) - 4096] = hx[e];
+      vs[v_off(64 + 8 * c + e, m) - 4096] = hy[e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int ch = threadIdx.x + 256 * i;  // 16-byte chunk of the 8 KiB half
+      *(u32x4*)(tile + 4096 + ch * 8) = *(const u32x4*)(vs + ch * 8);
+    }
+  } else if (m < M) {
+    T* vt = (T*)a.kv_layer + (int64_t)kvh * a.kv_head_stride + (int64_t)(pos >> 5) * 8192;
+    const int kk = pos & 31;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      vt[v_off(8 * c + e, kk)] = hx[e];
+      vt[v_off(64 + 8 * c + e, kk)] = hy[e];
+    }
+  }
+  (void)tile;
+}
+
+template <int EPI, int U>
+__global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int KS) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int M = a.M, N = a.N, K = a.K;
+  const int G = K >> 6;
+  int grp, ks;
+  if (!sk_place(a, N / 128, KS, grp, ks)) return;
+  const int nt = grp * 4 + wave;
+  const int u0 = ks * U, kc0 = u0 * 64;
+  constexpr int KCN = U * 64;
+  constexpr int ROW_H = KCN + 8;  // 16-bit elements per LDS row (+16 B pad)
+  extern __shared__ __align__(16) char smem[];
+  uint16_t* xs = (uint16_t*)smem;                       // [32][ROW_H] ACT_F16P
+  float* xss = (float*)(smem + 32 * ROW_H * 2);         // [U][32] group sums
+  float* rinv = xss + U * 32;                           // [32]
+  float* red = rinv + 32;                               // [4][32][33]
+  int* flag = (int*)(red + SK_RED);
+  uint16_t* vbuf = (uint16_t*)(smem + SK_WIDE_V_OFF(U));  // [4096] V tile half (QKV)
+
+  // 1. this wave's weights for the U units, issued first
+  u32x4 wq[U];
+  uint32_t wsb[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    wq[u] = *q4_tile_words(a.qw, nt, G, u0 + u, lane);
+    wsb[u] = q4_tile_sb(a.sb, nt, G, u0 + u, lane);
+  }
+  // 2. the hidden slice (8-wide items: U per thread) and the matching norm weights
+  f32x4 hv[U][2];
+  u32x4 nw[U];
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const int it = threadIdx.x + 256 * j;
+    const int r = it / (8 * U), c8 = it - r * (8 * U);
+    const int k = kc0 + c8 * 8;
+    if (r < M) {
+      const f32x4* src = (const f32x4*)(a.hidden + (int64_t)r * K + k);
+      hv[j][0] = src[0];
+      hv[j][1] = src[1];
+    } else {
+      hv[j][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+      hv[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    nw[j] = *(const u32x4*)(a.norm_w + k);
+  }
+  // 3. row statistics from the producer's partial sums of squares: thread
+  // (group g = tid / 32, row r = tid % 32) loads partials g, g + 8, ... all at
+  // once (one memory round trip); the 8 group sums are added in order.
+  {
+    const int np = K >> 5;  // <= 8 * SK_SS_PER_THREAD
+    const int r = threadIdx.x & 31, g8 = threadIdx.x >> 5;
+    float sv[SK_SS_PER_THREAD];
+#pragma unroll
+    for (int e = 0; e < SK_SS_PER_THREAD; ++e) {
+      const int p = g8 + 8 * e;
+      sv[e] = 0.f;
+      if (8 * e < np)  // wave-uniform: only the rounds that exist are issued
+        sv[e] = p < np ? a.ss_in[p * 32 + r] : 0.f;
+    }
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < SK_SS_PER_THREAD; ++e) q += sv[e];
+    red[g8 * 32 + r] = q;
+  }
+  __syncthreads();
+  if (threadIdx.x < 32) {
+    float ssum = 0.f;
+#pragma unroll
+    for (int g8 = 0; g8 < 8; ++g8) ssum += red[g8 * 32 + threadIdx.x];
+    rinv[threadIdx.x] = 1.f / sqrtf(ssum / (float)K + a.eps);
+  }
+  __syncthreads();
+  // 4. RMSNorm(h) * w -> ACT_F16P (chunk order 0,4,1,5,2,6,3,7) + group sums
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const int it = threadIdx.x + 256 * j;
+    const int r = it / (8 * U), c8 = it - r * (8 * U);
+    const float inv = rinv[r];
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = (hv[j][e >> 1][(2 * e) & 3] * inv) * bf16_bits_to_float(nw[j][e] & 0xffffu);
+      x[2 * e + 1] = (hv[j][e >> 1][(2 * e + 1) & 3] * inv) * bf16_bits_to_float(nw[j][e] >> 16);
+    }
+    _Float16 h[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = (_Float16)x[e];
+    u32x4 pk;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      pk[e] = (uint32_t)half_bits(h[e]) | ((uint32_t)half_bits(h[e + 4]) << 16);
+    *(u32x4*)(xs + r * ROW_H + c8 * 8) = pk;
+    float gs = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) gs += (float)h[e];
+    // a 64-k group is 8 consecutive items of one row = 8 consecutive lanes
+    gs += __shfl_xor(gs, 1, 64);
+    gs += __shfl_xor(gs, 2, 64);
+    gs += __shfl_xor(gs, 4, 64);
+    if ((c8 & 7) == 0) xss[(c8 >> 3) * 32 + r] = gs;
+  }
+  __syncthreads();
+  // 5. this wave's n-tile over the U units
+  f32x16 acc = f32x16{};
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const _Float16* arow = (const _Float16*)xs + (lane & 31) * ROW_H + u * 64 + 32 * (lane >> 5);
+    f16x8 af[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) af[t] = *(const f16x8*)(arow + 8 * t);
+    float xsr[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) xsr[r] = xss[u * 32 + mfma_row(r, lane)];
+    q4_group_mma1(acc, af, xsr, wq[u], wsb[u]);
+  }
+  // 6. K slices meet: the last work-group of the column block adds the partials
+  if (KS > 1) {
+    // partial tile of this wave, column-major (index col*32 + row): each lane's
+    // accumulator holds 4 consecutive rows of its column, one 16-byte store each
+    float* pw = a.part + ((size_t)(grp * KS + ks) * 4 + wave) * 1024 + (lane & 31) * 32 +
+                4 * (lane >> 5);
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+      *(f32x4*)(pw + 8 * jj) = f32x4{acc[4 * jj], acc[4 * jj + 1], acc[4 * jj + 2], acc[4 * jj + 3]};
+    if (!last_to_arrive(&a.counters[grp], KS, flag)) return;
+    // 1024 16-byte chunks of the 4 tiles, 4 per thread; every slice's chunks are
+    // loaded before any is added (then added in slice order)
+    const float* pbase = a.part + (size_t)grp * KS * 4096;
+    f32x4 pv[SK_KS_MAX][4];
+#pragma unroll
+    for (int k2 = 0; k2 < SK_KS_MAX; ++k2)
+      if (k2 < KS)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          pv[k2][i] = *(const f32x4*)(pbase + (size_t)k2 * 4096 + 4 * (threadIdx.x + 256 * i));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k2 = 0; k2 < SK_KS_MAX; ++k2)
+        if (k2 < KS) sum += pv[k2][i];
+      const int q = threadIdx.x + 256 * i, tn = q >> 8, c4 = q & 255;
+      const int col = c4 >> 3, row0 = (c4 & 7) * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) red[(tn * 32 + row0 + e) * 33 + col] = sum[e];
+    }
+    if (threadIdx.x == 0) a.counters[grp] = 0;
+  } else {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[(wave * 32 + mfma_row(r, lane)) * 33 + (lane & 31)] = acc[r];
+  }
+  __syncthreads();
+#define TT(r, c) red[(((c) >> 5) * 32 + (r)) * 33 + ((c) & 31)]
+  if (EPI == EPI_SWIGLU) {
+    const int F = N >> 1;
+    const int f0 = grp * 64;
+    for (int r = wave; r < M; r += 4) {
+      const float g = TT(r, lane), u = TT(r, 64 + lane);
+      const float y = g * (1.f / (1.f + expf(-g))) * u;
+      if (a.act_fmt == ACT_F16P) {
+        const _Float16 h = (_Float16)y;
+        ((_Float16*)a.act_out)[(int64_t)r * F + f16p_index(f0 + lane)] = h;
+        if (a.xsum_out) {
+          const float s = wave_sum((float)h);
+          if (lane == 0) a.xsum_out[(int64_t)r * (F >> 6) + (f0 >> 6)] = s;
+        }
+      } else {
+        ((uint16_t*)a.act_out)[(int64_t)r * F + f0 + lane] = float_to_bf16_bits(y);
+      }
+    }
+  } else if (EPI == EPI_QKV) {
+    const int row0 = a.desc ? a.desc->row0 : 0;
+    if (a.kv_bf16) qkv_epilogue<__bf16>(a, grp, row0, red, vbuf);
+    else qkv_epilogue<_Float16>(a, grp, row0, red, vbuf);
+  }
+#undef TT
+}
+
+// UW: units per wave held in registers at once (the wave's units are processed
+// in chunks of UW, each chunk's loads issued together).
+template <int EPI, int UW>
+__global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, int KS) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int M = a.M, N = a.N, K = a.K;
+  const int G = K >> 6;
+  const int U = G / KS;
+  int nt, ks;
+  if (!sk_place(a, N / 32, KS, nt, ks)) return;
+  const int u_lo = ks * U + (U * wave) / 4, u_hi = ks * U + (U * (wave + 1)) / 4;
+  const int mr = lane & 31;
+  const bool row_ok = mr < M;
+  extern __shared__ __align__(16) char smem[];
+  float* red = (float*)smem;  // [4][32][33]
+  int* flag = (int*)(red + SK_RED);
+
+  f32x16 acc = f32x16{};
+  for (int ub = u_lo; ub < u_hi || ub == u_lo; ub += UW) {
+    u32x4 wq[UW], af[UW][4];
+    uint32_t wsb[UW];
+#pragma unroll
+    for (int i = 0; i < UW; ++i) {
+      // clamped to a valid unit; a unit beyond the wave's range gets scale and
+      // bias 0, an exact no-op, so every load is used unconditionally
+      const int u = min(ub + i, max(u_hi, u_lo + 1) - 1);
+      wq[i] = *q4_tile_words(a.qw, nt, G, u, lane);
+      wsb[i] = ub + i < u_hi ? q4_tile_sb(a.sb, nt, G, u, lane) : 0u;
+      const u32x4* ap = (const u32x4*)((const uint16_t*)a.act + (int64_t)(row_ok ? mr : 0) * K +
+                                       u * 64 + 32 * (lane >> 5));
+#pragma unroll
+      for (int t = 0; t < 4; ++t) af[i][t] = row_ok ? ap[t] : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < UW; ++i) q4_group_mma1_lane(acc, af[i], wq[i], wsb[i], lane);
+    if (ub + UW >= u_hi) break;
+  }
+  // the four waves' K ranges, in order; thread t owns row t >> 3, columns
+  // 4*(t & 7) .. +3 of the tile (one 16-byte chunk everywhere below)
+#pragma unroll
+  for (int r = 0; r < 16; ++r) red[(wave * 32 + mfma_row(r, lane)) * 33 + (lane & 31)] = acc[r];
+  __syncthreads();
+  const int m = threadIdx.x >> 3, c0 = 4 * (threadIdx.x & 7);
+  f32x4 v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    v[e] = red[m * 33 + c0 + e] + red[(32 + m) * 33 + c0 + e] + red[(64 + m) * 33 + c0 + e] +
+           red[(96 + m) * 33 + c0 + e];
+  if (KS > 1) {
+    *(f32x4*)(a.part + (size_t)(nt * KS + ks) * 1024 + m * 32 + c0) = v;
+    if (!last_to_arrive(&a.counters[nt], KS, flag)) return;
+    const float* pp = a.part + (size_t)nt * KS * 1024 + m * 32 + c0;
+    f32x4 pv[SK_KS_MAX];
+#pragma unroll
+    for (int k2 = 0; k2 < SK_KS_MAX; ++k2)
+      if (k2 < KS) pv[k2] = *(const f32x4*)(pp + (size_t)k2 * 1024);
+    v = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k2 = 0; k2 < SK_KS_MAX; ++k2)
+      if (k2 < KS) v += pv[k2];
+    if (threadIdx.x == 0) a.counters[nt] = 0;
+  }
+  const int n = nt * 32 + c0;
+  if (a.bias) {
+    const uint2 bb = *(const uint2*)(a.bias + n);
+    v[0] += bf16_bits_to_float(bb.x & 0xffffu);
+    v[1] += bf16_bits_to_float(bb.x >> 16);
+    v[2] += bf16_bits_to_float(bb.y & 0xffffu);
+    v[3] += bf16_bits_to_float(bb.y >> 16);
+  }
+  if (EPI == EPI_RESID) {
+    f32x4 h = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (m < M) {
+      f32x4* hp = (f32x4*)(a.hidden_out + (int64_t)m * N + n);
+      h = *hp + v;
+      *hp = h;
+    }
+    if (a.ss_out) {
+      float q = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];
+      q += __shfl_xor(q, 1, 64);
+      q += __shfl_xor(q, 2, 64);
+      q += __shfl_xor(q, 4, 64);
+      if ((threadIdx.x & 7) == 0) a.ss_out[nt * 32 + m] = q;
+    }
+  } else if (m < M) {
+    *(f32x4*)(a.y + (int64_t)m * N + n) = v;
+  }
+}
+
+#define DRT_WIDE(E, U) template __global__ void skinny_wide_kernel<E, U>(const FusedArgs, int);
+DRT_WIDE(EPI_QKV, 1) DRT_WIDE(EPI_QKV, 2) DRT_WIDE(EPI_QKV, 4) DRT_WIDE(EPI_QKV, 8)
+DRT_WIDE(EPI_QKV, 14) DRT_WIDE(EPI_QKV, 16)
+DRT_WIDE(EPI_SWIGLU, 1) DRT_WIDE(EPI_SWIGLU, 2) DRT_WIDE(EPI_SWIGLU, 4) DRT_WIDE(EPI_SWIGLU, 8)
+DRT_WIDE(EPI_SWIGLU, 14) DRT_WIDE(EPI_SWIGLU, 16)
+#undef DRT_WIDE
+#define DRT_NARROW(E, UW) template __global__ void skinny_narrow_kernel<E, UW>(const FusedArgs, int);
+DRT_NARROW(EPI_RESID, 1) DRT_NARROW(EPI_RESID, 2) DRT_NARROW(EPI_RESID, 4)
+DRT_NARROW(EPI_STORE, 1) DRT_NARROW(EPI_STORE, 2) DRT_NARROW(EPI_STORE, 4)
+#undef DRT_NARROW
+
+namespace drt {
+namespace {
+
+constexpr int WIDE_U[] = {4, 8, 2, 14, 16, 1};  // preference order
+
+// Wide: units per work-group U (instantiated values) with G % U == 0, the largest
+// U whose split still gives >= 128 work-groups; else the smallest U available.
+int wide_units(int N, int K) {
+  const int G = K / 64, NG = N / 128;
+  int best = 0;
+  for (int u : {16, 14, 8, 4, 2, 1}) {
+    if (G % u) continue;
+    if (best == 0) best = u;
+    if (NG * (G / u) >= 128) return u;
+    best = u;
+  }
+  return best;
+}
+
+// Narrow: K slices KS (a divisor of G) - the fewest giving >= 256 work-groups.
+int narrow_slices(int N, int K) {
+  const int G = K / 64, NT = N / 32;
+  int ks = 1;
+  for (int d = 1; d <= G; ++d) {
+    if (G % d) continue;
+    ks = d;
+    if (NT * d >= 256) break;
+  }
+  return ks;
+}
+
+}  // namespace
+
+size_t skinny_part_floats(int N, int K) {
+  if (K % 64 || N % 32) return 0;
+  size_t wide = 0;
+  if (N % 128 == 0) {
+    const int u = wide_units(N, K);
+    wide = u ? (size_t)(N / 128) * (K / 64 / u) * 4096 : 0;
+  }
+  const size_t narrow = (size_t)(N / 32) * narrow_slices(N, K) * 1024;
+  return std::max(wide, narrow);
+}
+
+int skinny_counters(int N) { return N / 32; }
+
+bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
+  // DRT_DISABLE_SKINNY=1 keeps every linear on the single-pass fused kernels
+  // (an A/B switch for parity and timing comparisons)
+  static const bool disabled = getenv("DRT_DISABLE_SKINNY") != nullptr;
+  if (disabled || !a.qw || a.M < 1 || a.M > 32 || !a.part || !a.counters || a.K % 64 ||
+      a.N % 32 || a.n_xcc < 1)
+    return false;
+  const int G = a.K / 64;
+  const double bytes = (double)a.N * a.K / 2 + (double)a.N * a.K / 16 + 2.0 * a.M * a.K +
+                       2.0 * a.M * a.N;
+  if (kind == FL_QKV || kind == FL_SWIGLU) {
+    if (!a.ss_in || a.N % 128 || a.K / 32 > 8 * SK_SS_PER_THREAD) return false;
+    const int U = wide_units(a.N, a.K);
+    if (!U) return false;
+    const int KS = G / U, NG = a.N / 128;
+    if (KS > SK_KS_MAX || (size_t)NG * KS * 4096 > a.part_floats || NG > a.n_counters)
+      return false;  // (padding work-groups past the last block exit before any access)
+    const size_t lds = SK_WIDE_LDS(U);
+    const dim3 grid((unsigned)((NG + a.n_xcc - 1) / a.n_xcc * a.n_xcc * KS));
+#define DRT_SW(E, UU)                                                             \
+  {                                                                               \
+    auto fn = skinny_wide_kernel<E, UU>;                                          \
+    static size_t granted = 0;                                                    \
+    grant_lds((const void*)fn, lds, granted);                                     \
+    DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(256), lds, s, a, KS);        \
+  }
+#define DRT_SW_U(E)                                  \
+  switch (U) {                                       \
+    case 1: DRT_SW(E, 1) break;                      \
+    case 2: DRT_SW(E, 2) break;                      \
+    case 4: DRT_SW(E, 4) break;                      \
+    case 8: DRT_SW(E, 8) break;                      \
+    case 14: DRT_SW(E, 14) break;                    \
+    default: DRT_SW(E, 16) break;                    \
+  }
+    if (kind == FL_QKV) {
+      DRT_SW_U(EPI_QKV)
+    } else {
+      DRT_SW_U(EPI_SWIGLU)
+    }
+#undef DRT_SW_U
+#undef DRT_SW
+  } else if (kind == FL_RESID || kind == FL_STORE) {
+    const int KS = narrow_slices(a.N, a.K), NT = a.N / 32;
+    if (KS > SK_KS_MAX || (size_t)NT * KS * 1024 > a.part_floats || NT > a.n_counters)
+      return false;
+    const int per_wave = (G / KS + 3) / 4;
+    const size_t lds = SK_RED * 4 + 16;
+    const dim3 grid((unsigned)((NT + a.n_xcc - 1) / a.n_xcc * a.n_xcc * KS));
+#define DRT_SN(E, UW)                                                              \
+  {                                                                                \
+    auto fn = skinny_narrow_kernel<E, UW>;                                         \
+    DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(256), lds, s, a, KS);         \
+  }
+    if (kind == FL_RESID) {
+      if (per_wave <= 1) DRT_SN(EPI_RESID, 1) else if (per_wave <= 2) DRT_SN(EPI_RESID, 2) else DRT_SN(EPI_RESID, 4)
+    } else {
+      if (per_wave <= 1) DRT_SN(EPI_STORE, 1) else if (per_wave <= 2) DRT_SN(EPI_STORE, 2) else DRT_SN(EPI_STORE, 4)
+    }
+#undef DRT_SN
+  } else {
+    return false;
+  }
+  DRT_HIP(hipGetLastError());
+  return true;
+}
+
+}  // namespace drt
