@@ -355,21 +355,33 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
   __syncthreads();
 #define TT(r, c) red[(((c) >> 5) * 32 + (r)) * 33 + ((c) & 31)]
   if (EPI == EPI_SWIGLU) {
+    // thread t: row t >> 3, outputs f0 + 8c .. +7 (c = t & 7) from gate columns
+    // 8c.. and up columns 64 + 8c.. of the [gate 64 | up 64] block; one 16-byte
+    // store per thread (ACT_F16P chunk order 0,4,1,5,2,6,3,7). No group sums:
+    // the down projection computes them from the fp16 values it reads.
     const int F = N >> 1;
     const int f0 = grp * 64;
-    for (int r = wave; r < M; r += 4) {
-      const float g = TT(r, lane), u = TT(r, 64 + lane);
-      const float y = g * (1.f / (1.f + expf(-g))) * u;
-      if (a.act_fmt == ACT_F16P) {
-        const _Float16 h = (_Float16)y;
-        ((_Float16*)a.act_out)[(int64_t)r * F + f16p_index(f0 + lane)] = h;
-        if (a.xsum_out) {
-          const float s = wave_sum((float)h);
-          if (lane == 0) a.xsum_out[(int64_t)r * (F >> 6) + (f0 >> 6)] = s;
-        }
-      } else {
-        ((uint16_t*)a.act_out)[(int64_t)r * F + f0 + lane] = float_to_bf16_bits(y);
+    const int m = threadIdx.x >> 3, c = threadIdx.x & 7;
+    if (m < M) {
+      float y[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float g = TT(m, 8 * c + e), u = TT(m, 64 + 8 * c + e);
+        y[e] = g * (1.f / (1.f + expf(-g))) * u;
       }
+      uint16_t* dst = (uint16_t*)a.act_out + (int64_t)m * F + f0 + 8 * c;
+      u32x4 pk;
+      if (a.act_fmt == ACT_F16P) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          pk[e] = (uint32_t)half_bits((_Float16)y[e]) | ((uint32_t)half_bits((_Float16)y[e + 4]) << 16);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          pk[e] = (uint32_t)float_to_bf16_bits(y[2 * e]) |
+                  ((uint32_t)float_to_bf16_bits(y[2 * e + 1]) << 16);
+      }
+      *(u32x4*)dst = pk;
     }
   } else if (EPI == EPI_QKV) {
     const int row0 = a.desc ? a.desc->row0 : 0;
@@ -422,6 +434,10 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
   for (int r = 0; r < 16; ++r) red[(wave * 32 + mfma_row(r, lane)) * 33 + (lane & 31)] = acc[r];
   __syncthreads();
   const int m = threadIdx.x >> 3, c0 = 4 * (threadIdx.x & 7);
+  const int n = nt * 32 + c0;
+  // the epilogue's input, loaded before the exchange so its latency overlaps it
+  f32x4 h_old = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (EPI == EPI_RESID && m < M) h_old = *(const f32x4*)(a.hidden_out + (int64_t)m * N + n);
   f32x4 v;
 #pragma unroll
   for (int e = 0; e < 4; ++e)
@@ -441,7 +457,6 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
       if (k2 < KS) v += pv[k2];
     if (threadIdx.x == 0) a.counters[nt] = 0;
   }
-  const int n = nt * 32 + c0;
   if (a.bias) {
     const uint2 bb = *(const uint2*)(a.bias + n);
     v[0] += bf16_bits_to_float(bb.x & 0xffffu);
@@ -452,9 +467,8 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
   if (EPI == EPI_RESID) {
     f32x4 h = f32x4{0.f, 0.f, 0.f, 0.f};
     if (m < M) {
-      f32x4* hp = (f32x4*)(a.hidden_out + (int64_t)m * N + n);
-      h = *hp + v;
-      *hp = h;
+      h = h_old + v;
+      *(f32x4*)(a.hidden_out + (int64_t)m * N + n) = h;
     }
     if (a.ss_out) {
       float q = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];

@@ -254,3 +254,73 @@ def test_reference_mask_cases_against_golden(kind):
                     assert abs(scores[r] - w["score"]) / w["score"] < 1e-2
     finally:
         rt.close()
+
+
+def _real_shape_geometry(kind):
+    """The BD3 (Qwen3-0.6B) or Dream (Qwen2.5-7B) layer shapes with two layers and
+    a 4096-token vocabulary: every linear, attention and split-K path of the real
+    model runs at its real size, while the oracle stays quick."""
+    from diffusorrt_amd import synthetic as syn
+
+    base = syn.BD3_QWEN3_06B if kind == "bd3" else syn.DREAM_QWEN25_7B
+    import dataclasses
+    return dataclasses.replace(base, layer_count=2, vocab_size=4096, mask_token_id=4000,
+                               eos_token_id=4001)
+
+
+@pytest.mark.parametrize("kind", ["q4", "bf16"])
+def test_bd3_real_shapes_decode_teacher_forced(kind):
+    """BD3 decode at the real layer shapes: 32-row steps use the split-K linears
+    (4 and 8 K slices) and the range-split decode attention."""
+    from diffusorrt_amd import decode
+    from diffusorrt_amd.runtime import bd3_session_config
+
+    _say("bd3 real shapes decode", kind)
+    geom = _real_shape_geometry("bd3")
+    model, rt = _build(geom, kind, seed=21)
+    W, cfg = _oracle(model)
+    prompt = np.random.default_rng(5).integers(0, 3900, 96).tolist()
+    trace = []
+    with rt.session(bd3_session_config(32, 16, 96 + 64)) as s:
+        res = decode.generate_device_tokens(s, prompt, max_tokens=64,
+                                            mask_token_id=geom.mask_token_id,
+                                            eos_token_id=geom.eos_token_id, steps=16,
+                                            block_size=32, trace=trace)
+    assert res.committed_token_count == 64
+    x = prompt + [geom.mask_token_id] * 64
+    problems, ties, worst = [], [], 0.0
+    for t in trace:
+        ref = F.forward_full(W, cfg, x[:t["window_end"]], mask_kind="d2f_hybrid",
+                             mask_geometry=(0, 32), output_rows=t["frontier"])
+        rep, bad = compare_proposals(t["scores"], t["tokens"], ref, quota=len(t["chosen"]),
+                                     gpu_chosen=t["chosen"], bf16_logits=kind == "bf16")
+        worst = max(worst, rep["score_rel_max"])
+        ties += rep["report"]
+        problems += [(t["step"],) + tuple(b) for b in bad]
+        for r in t["chosen"]:
+            x[t["frontier"][r]] = t["tokens"][r]
+    _say(f"  score rel max {worst:.2e}; near-ties reported: {ties}")
+    assert not problems, problems
+    rt.close()
+
+
+def test_dream_real_shapes_window():
+    """Dream's layer shapes (28/4 heads, d 3584, FFN 18944, qkv bias, shifted
+    logits) on a 64-row bidirectional canvas."""
+    from diffusorrt_amd.runtime import fixed_quota_session_config
+
+    _say("dream real shapes window")
+    geom = _real_shape_geometry("dream")
+    model, rt = _build(geom, "q4", seed=22)
+    W, cfg = _oracle(model)
+    prompt = np.random.default_rng(6).integers(0, 3900, 32).tolist()
+    x = prompt + [geom.mask_token_id] * 32
+    scope = list(range(32, 64))
+    with rt.session(fixed_quota_session_config(256, 8, len(x))) as s:
+        win = s.execute_window(x, scope)
+    ref = F.window_logits(W, cfg, x, scope, mask_kind="bidirectional", mask_geometry=None,
+                          logits_convention="dream_ar_shift")
+    err = rel_err_rows(win.array(), ref)
+    _say(f"  dream window rel err max={err.max():.2e}")
+    assert err.max() < LOGITS_REL_TOL
+    rt.close()
