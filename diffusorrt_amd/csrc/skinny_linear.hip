@@ -318,13 +318,13 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
   }
   // 6. K slices meet: the last work-group of the column block adds the partials
   if (KS > 1) {
-    // partial tile of this wave, column-major (index col*32 + row): each lane's
-    // accumulator holds 4 consecutive rows of its column, one 16-byte store each
-    float* pw = a.part + ((size_t)(grp * KS + ks) * 4 + wave) * 1024 + (lane & 31) * 32 +
-                4 * (lane >> 5);
+    // partial tile of this wave in accumulator order: chunk jj*64 + lane holds
+    // rows 8jj + 4(lane >> 5) .. +3 of column lane & 31, so each store
+    // instruction writes 1 KiB of whole cache lines
+    float* pw = a.part + ((size_t)(grp * KS + ks) * 4 + wave) * 1024 + 4 * lane;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj)
-      *(f32x4*)(pw + 8 * jj) = f32x4{acc[4 * jj], acc[4 * jj + 1], acc[4 * jj + 2], acc[4 * jj + 3]};
+      *(f32x4*)(pw + 256 * jj) = f32x4{acc[4 * jj], acc[4 * jj + 1], acc[4 * jj + 2], acc[4 * jj + 3]};
     if (!last_to_arrive(&a.counters[grp], KS, flag)) return;
     // 1024 16-byte chunks of the 4 tiles, 4 per thread; every slice's chunks are
     // loaded before any is added (then added in slice order)
@@ -343,7 +343,7 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
       for (int k2 = 0; k2 < SK_KS_MAX; ++k2)
         if (k2 < KS) sum += pv[k2][i];
       const int q = threadIdx.x + 256 * i, tn = q >> 8, c4 = q & 255;
-      const int col = c4 >> 3, row0 = (c4 & 7) * 4;
+      const int ln = c4 & 63, col = ln & 31, row0 = 8 * (c4 >> 6) + 4 * (ln >> 5);
 #pragma unroll
       for (int e = 0; e < 4; ++e) red[(tn * 32 + row0 + e) * 33 + col] = sum[e];
     }
