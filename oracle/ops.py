@@ -330,7 +330,13 @@ def sampling_uniform_bits(seed: int, step: int, position: int, token: int) -> in
     """The 64-bit counter hash keyed by (seed, forward, position, token).
 
     ``key = mix(seed + G)``; ``key = mix(key + (step+1) G)``;
-    ``key = mix(key + (position+1) G)``; ``bits = mix(key + (token+1) G)``.
+    ``key = mix(key + (position+1) G)``; ``bits = mix(key + (token+1) G)``
+    (``backends/diffusion_runtime.py:203-253``).
+
+    Parity unpinned for the chaining order: ``mix64`` is pinned by the published
+    splitmix64 sequence and the noise by its Gumbel statistics, but no reference
+    fixture holds sampled tokens, so the key order itself is checked only by
+    reading the cited lines.
     """
     g = SAMPLING_STEP
     key = mix64((seed & MASK64) + g)
