@@ -54,6 +54,10 @@ def parse_args():
                     help="eager steps timed per dispatch for the roofline (default: --steps; 0 = none)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="time a 256 MiB device-to-device copy and exit")
+    ap.add_argument("--workload", default="bd3_q4_8k",
+                    choices=["bd3_q4_8k", "bd3_bf16", "dream_q4", "attention", "q4_linear"],
+                    help="bd3_q4_8k is the headline line; the others print one JSON line per "
+                         "case of the remaining configurations")
     return ap.parse_args()
 
 
@@ -152,10 +156,155 @@ def read_traffic():
     return None
 
 
+def _event_time_us(fn, reps: int) -> float:
+    import torch
+
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps * 1e3
+
+
+def bench_attention() -> None:
+    """Isolated block-over-prefix attention: 32 query rows x 16 heads x 128, bf16,
+    K/V of L prefix + 32 block keys x 8 heads, N(0, 1) from seed 1, prefix fully
+    visible and the block bidirectional; fp32 accumulate, bf16 output. Timed per
+    call (decode attention + range combine) on the torch stream."""
+    import ctypes as C
+
+    import torch
+
+    from diffusorrt_amd import _lib, kernels
+
+    lib = _lib.load()
+    rows, hq, hkv = 32, 16, 8
+    gen = torch.Generator().manual_seed(1)
+    for L in (512, 2048, 8192):
+        n = L + 32
+        cache = kernels.PrefixKVCache(1, hkv, n, dtype="bf16")
+        k = torch.randn((n, hkv, 128), generator=gen).bfloat16().cuda()
+        v = torch.randn((n, hkv, 128), generator=gen).bfloat16().cuda()
+        cache.store(0, k, v, 0)
+        q = torch.randn((rows, hq, 128), generator=gen).bfloat16().cuda()
+        out = torch.empty((rows, hq * 128), dtype=torch.bfloat16, device="cuda")
+        ws_b = lib.drt_op_attention_workspace_bytes(rows, hq, hkv, n)
+        ws = torch.empty(ws_b, dtype=torch.uint8, device="cuda")
+        st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+        def run():
+            _lib.check(lib.drt_op_attention(
+                C.c_void_p(q.data_ptr()), C.c_void_p(cache.data.data_ptr()), cache.head_stride,
+                _lib.BF16, rows, hq, hkv, n, L, 0, 0, 1, C.c_void_p(out.data_ptr()), _lib.BF16,
+                C.c_void_p(ws.data_ptr()), ws_b, st))
+
+        us = _event_time_us(run, 50)
+        byts = 4.0 * rows * hq * 128 + 4096.0 * n
+        print(json.dumps({"workload": "attention", "prefix": L, "rows": rows, "heads": [hq, hkv],
+                          "dtype": "bf16", "us_per_call": round(us, 2),
+                          "algorithmic_bytes": byts,
+                          "achieved_GBps": round(byts / us / 1e3, 1),
+                          "hbm_frac": round(byts / us / 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
+
+
+def bench_q4_linear() -> None:
+    """Isolated q4 g64 linear (MLX packing): nibbles U{0..15}, scales U(0.005, 0.02),
+    biases U(-0.1, 0.1) (bf16), x bf16 N(0, 1), seed 2. Timed per call on the
+    per-op entry point (activation preparation + the linear)."""
+    import ctypes as C
+
+    import torch
+
+    from diffusorrt_amd import _lib, kernels
+    from diffusorrt_amd import synthetic as syn
+
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(2)
+    for (N, K) in ((1024, 1024), (3072, 1024), (1024, 3072), (18944, 3584), (3584, 18944)):
+        qt = syn.random_q4(gen, N, K, scale_lo=0.005, scale_hi=0.02, centred=False,
+                           bias_lo=-0.1, bias_hi=0.1)
+        w = kernels.DeviceQ4Weight(qt.w_q.cuda(), qt.scales.cuda(), qt.biases.cuda())
+        for M in (32, 128):
+            x = torch.randn((M, K), generator=gen).bfloat16().cuda()
+            us = _event_time_us(lambda: kernels.linear(x, w), 30)
+            byts = N * K / 2 + N * K / 16 + 2.0 * M * K + 4.0 * M * N
+            flops = 2.0 * M * N * K
+            print(json.dumps({"workload": "q4_linear", "M": M, "N": N, "K": K,
+                              "us_per_call": round(us, 2), "algorithmic_bytes": byts,
+                              "achieved_GBps": round(byts / us / 1e3, 1),
+                              "hbm_frac": round(byts / us / 1e3 / HBM_PEAK_GBS, 4),
+                              "achieved_TFLOPs": round(flops / us / 1e6, 2),
+                              "mfma_frac_fp16": round(flops / us / 1e6 / 2500.0, 4)}), flush=True)
+
+
+def bench_decode_config(args, which: str) -> None:
+    """Whole-decode configurations: `bd3_bf16` (Qwen3-0.6B BD3, bf16 N(0, 0.02) seed 0,
+    64-token prompt, 4 blocks x 32 masks, 32 steps = 8 rounds of 4 per block) and
+    `dream_q4` (Qwen2.5-7B Dream, q4 seed 3, 256-token prompt + 256 masks, 64
+    steps of 4, bidirectional full canvas). One untimed decode, then one timed."""
+    import torch
+
+    from diffusorrt_amd import decode
+    from diffusorrt_amd import synthetic as syn
+    from diffusorrt_amd.runtime import Runtime, bd3_session_config, fixed_quota_session_config
+
+    if which == "bd3_bf16":
+        g, kind, seed, prompt_len, gen_len, steps, block = syn.BD3_QWEN3_06B, "bf16", 0, 64, 128, 32, 32
+    else:
+        g, kind, seed, prompt_len, gen_len, steps, block = syn.DREAM_QWEN25_7B, "q4", 3, 256, 256, 64, 256
+    t = time.perf_counter()
+    model = syn.build_model(g, kind, seed=seed)
+    prompt = syn.prompt_ids(seed, prompt_len)
+    log(f"{which}: model generated in {time.perf_counter() - t:.1f}s")
+    rt = Runtime(model, max_forward_rows=max(512, prompt_len + gen_len),
+                 max_positions=prompt_len + gen_len + 64)
+    strategy = "bd3_fixed_quota" if which == "bd3_bf16" else "fixed_quota"
+    cfg = (bd3_session_config(block, steps, prompt_len + gen_len) if which == "bd3_bf16"
+           else fixed_quota_session_config(block, steps, prompt_len + gen_len))
+
+    def run():
+        with rt.session(cfg) as s:
+            return decode.generate_device_tokens(
+                s, prompt, max_tokens=gen_len, mask_token_id=g.mask_token_id,
+                eos_token_id=g.eos_token_id, steps=steps, block_size=block,
+                decode_strategy=strategy)
+
+    run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    res = run()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    out = {"workload": which, "tokens_per_s": round(res.committed_token_count / dt, 2),
+           "ms_per_step": round(dt / max(1, res.forward_count) * 1e3, 4),
+           "forwards": res.forward_count, "committed_tokens": res.committed_token_count,
+           "hit_eos": res.hit_eos, "weights": kind}
+    if which == "dream_q4":
+        params = g.layer_count * sum(n * k for n, k in syn.linear_shapes(g).values())
+        flops = 2.0 * (prompt_len + gen_len) * params
+        out["mfma_frac_fp16_linears"] = round(flops / (dt / res.forward_count) / 2.5e15, 4)
+    print(json.dumps(out), flush=True)
+    rt.close()
+
+
 def main():
     args = parse_args()
     if args.calibrate_copy:
         calibrate_copy(max(1, args.steps))
+        return
+    if args.workload != "bd3_q4_8k":
+        if args.workload == "attention":
+            bench_attention()
+        elif args.workload == "q4_linear":
+            bench_q4_linear()
+        else:
+            bench_decode_config(args, args.workload)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build has no "
