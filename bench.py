@@ -308,7 +308,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build has no "
-              "multi-GPU path; see DESIGN.md for how the step would shard.", file=sys.stderr)
+              "multi-GPU path (the step is measured on one GPU's share of the work).",
+              file=sys.stderr)
         sys.exit(2)
     import numpy as np
     import torch

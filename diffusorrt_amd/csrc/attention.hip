@@ -250,45 +250,60 @@ DRT_DEV void load_tile_nt(const T* __restrict__ base, int t, int lane, bool real
   }
 }
 
-// One 32-key tile for all query tiles: S^T = K Q^T, online softmax, O^T += V^T P^T.
-// Keys at or beyond n_keys get zero weight (n_keys = 0 makes the tile a no-op).
+// Softmax bookkeeping of the decode attention runs in base 2 on scaled scores:
+// u = s * scale * log2(e), p = 2^(u - base). The base of a query vector is only
+// raised when a tile's max exceeds it by more than DEC_RESCALE_LOG2 (or on its
+// first visible keys), so p <= 2^DEC_RESCALE_LOG2 (exact in the MFMA operand
+// types' range) and the rescale of O, which moves the accumulators through
+// VGPRs, is rare instead of once per tile. Any base gives the same o / l.
+constexpr float DEC_RESCALE_LOG2 = 8.f;
+
+// One 32-key tile for all query tiles: S^T = K Q^T, softmax weights against the
+// running base, O^T += V^T P^T. Keys at or beyond n_keys get zero weight
+// (n_keys <= key0 makes the tile a no-op). Every query tile runs (the kernel is
+// instantiated with QT = ceil(n_qv / 32)); rows beyond n_qv hold Q = 0.
+// c = scale * log2(e); m_run is the base in scaled units (-inf before any key).
 template <typename T, int QT>
 DRT_DEV void attend_tile(const typename MfmaT<T>::vec (&kc)[8],
                          const typename MfmaT<T>::vec (&vc)[8], const T* __restrict__ qs,
-                         int key0, int n_keys, int n_qv, float scale, int lane,
-                         float (&m_run)[QT], float (&l_run)[QT], f32x16 (&o)[QT][4]) {
+                         int key0, int n_keys, float c, int lane, float (&m_run)[QT],
+                         float (&l_run)[QT], f32x16 (&o)[QT][4]) {
   typedef typename MfmaT<T>::vec vec;
+  const bool partial = key0 + 32 > n_keys;  // uniform: a partial (or empty) tile masks keys
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    // uniform; query tile 0 always runs (n_qv >= 1), so the tile's loads are used
-    // unconditionally and stay where they were issued
-    if (qt > 0 && qt * 32 >= n_qv) break;
     const T* qrow = qs + (qt * 32 + (lane & 31)) * DEC_QROW + 8 * (lane >> 5);
     f32x16 sc = f32x16{};
 #pragma unroll
     for (int i = 0; i < 8; ++i) sc = MfmaT<T>::mma(kc[i], *(const vec*)(qrow + 16 * i), sc);
-    float tmax = -INFINITY;
+    if (partial) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const bool vis = key0 + mfma_row(r, lane) < n_keys;
-      sc[r] = vis ? sc[r] * scale : -INFINITY;
-      tmax = fmaxf(tmax, sc[r]);
+      for (int r = 0; r < 16; ++r) sc[r] = key0 + mfma_row(r, lane) < n_keys ? sc[r] : -INFINITY;
     }
+    float tmax = sc[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, sc[r]);
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run[qt], tmax);
-    const float basev = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __expf(m_run[qt] - basev);
+    const float mc = tmax * c;  // -inf for a query vector with no visible key in the tile
+    const bool up = mc > m_run[qt] + DEC_RESCALE_LOG2;
+    if (__ballot(up)) {  // uniform: some base has to rise
+      const float alpha = up ? __builtin_amdgcn_exp2f(m_run[qt] - mc) : 1.f;  // 0 from -inf
+      if (__ballot(up && m_run[qt] != -INFINITY)) {  // O is still zero before the first key
+#pragma unroll
+        for (int hb = 0; hb < 4; ++hb) o[qt][hb] *= alpha;
+      }
+      l_run[qt] *= alpha;
+      m_run[qt] = up ? mc : m_run[qt];
+    }
+    const float base = m_run[qt] == -INFINITY ? 0.f : m_run[qt];  // no key yet: p = 0
     float pr[16];
     float psum = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      pr[r] = __expf(sc[r] - basev);
+      pr[r] = __builtin_amdgcn_exp2f(fmaf(sc[r], c, -base));
       psum += pr[r];
     }
-    l_run[qt] = l_run[qt] * alpha + psum;
-    m_run[qt] = m_new;
-#pragma unroll
-    for (int hb = 0; hb < 4; ++hb) o[qt][hb] *= alpha;
+    l_run[qt] += psum;
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
       vec pf;
@@ -314,6 +329,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   const int n_qv = n_rows * G;
   const int R = gridDim.x, rg = blockIdx.x, kvh = blockIdx.y;
   const int n_keys = desc ? desc->n_keys : n_keys_arg;
+  const float c = scale * 1.44269504088896340736f;  // scores to base-2 exponents
   const int n_tiles = (n_keys + 31) >> 5;
   const int t_begin = (int)((int64_t)n_tiles * rg / R);
   const int t_end = (int)((int64_t)n_tiles * (rg + 1) / R);
@@ -374,12 +390,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 #pragma unroll
   for (int u = 0; u < UP; ++u) {
     const int t = t0 + 4 * u;
-    attend_tile<T, QT>(kt[u], vt[u], qs, t * 32, t < t_end ? n_keys : 0, n_qv, scale, lane,
-                       m_run, l_run, o);
+    attend_tile<T, QT>(kt[u], vt[u], qs, t * 32, t < t_end ? n_keys : 0, c, lane, m_run, l_run,
+                       o);
   }
   for (int t = t0 + 4 * UP; t < t_end; t += 4) {  // ranges longer than 4*UP tiles
     load_tile_nt<T>(base, t, lane, true, kt[0], vt[0]);
-    attend_tile<T, QT>(kt[0], vt[0], qs, t * 32, n_keys, n_qv, scale, lane, m_run, l_run, o);
+    attend_tile<T, QT>(kt[0], vt[0], qs, t * 32, n_keys, c, lane, m_run, l_run, o);
   }
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) l_run[qt] += __shfl_xor(l_run[qt], 32, 64);
@@ -413,7 +429,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     float ll = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      wgt[qt][w] = mw[w] == -INFINITY ? 0.f : __expf(mw[w] - mm);
+      wgt[qt][w] = mw[w] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw[w] - mm);
       ll += wgt[qt][w] * lw[w];
     }
     if (wave == 0 && lane < 32) {
@@ -472,7 +488,7 @@ __global__ __launch_bounds__(256) void attn_decode_combine_kernel(
     for (int r = pg; r < R; r += 8) {
       const int64_t mi = (((int64_t)r * Hkv + kvh) * (QT * 32) + qt * 32 + c) * 2;
       const float m_r = ml_part[mi];
-      const float w = m_r == -INFINITY ? 0.f : __expf(m_r - mm);
+      const float w = m_r == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_r - mm);
       wts[r * 32 + c] = w;
       l_loc += w * ml_part[mi + 1];
     }

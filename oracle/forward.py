@@ -25,47 +25,59 @@ def _lin(weights, key, x, kind):
     return ops.linear(x, w, b, weight_kind=kind)
 
 
-def layer_forward(weights, cfg, i, hidden, cos, sin, visible, kv_hook=None):
+def _keep(x):
+    return x
+
+
+def layer_forward(weights, cfg, i, hidden, cos, sin, visible, kv_hook=None, operand_round=None):
     """One decoder layer over all rows of ``hidden`` (fp32 ``[S, d]``).
 
     ``h += o(attn(rope(qnorm(q(n))), rope(knorm(k(n))), v(n)))`` with
     ``n = rmsnorm(h)``, then ``h += down(swiglu(gate(n2), up(n2)))`` with
     ``n2 = rmsnorm(h)`` (``mlx_forward.py:1164-1309``; op order fixed by
     ``graph/ir.py:106``).
+
+    ``operand_round`` (a precision model, not reference semantics) is applied to
+    every tensor that a lower-precision device path stores in its operand type:
+    the linears' inputs (n, attention output, n2, swiglu output), Q, and the
+    cached K/V. ``None`` is the reference computation.
     """
+    rnd = operand_round or _keep
     kind = cfg["weight_kind"]
     eps = cfg["eps"]
     hq, hkv, hd = cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"]
     p = f"model.layers.{i}."
     s = hidden.shape[0]
-    n = ops.rms_norm(hidden, weights[p + "input_layernorm.weight"], eps)
+    n = rnd(ops.rms_norm(hidden, weights[p + "input_layernorm.weight"], eps))
     q = _lin(weights, p + "self_attn.q_proj", n, kind).reshape(s, hq, hd)
     if cfg["qk_norm"]:
         q = ops.rms_norm(q, weights[p + "self_attn.q_norm.weight"], eps)
-    q = ops.apply_split_half_rope(q, cos, sin)
+    q = rnd(ops.apply_split_half_rope(q, cos, sin))
     k = _lin(weights, p + "self_attn.k_proj", n, kind).reshape(s, hkv, hd)
-    v = _lin(weights, p + "self_attn.v_proj", n, kind).reshape(s, hkv, hd)
+    v = rnd(_lin(weights, p + "self_attn.v_proj", n, kind).reshape(s, hkv, hd))
     if cfg["qk_norm"]:
         k = ops.rms_norm(k, weights[p + "self_attn.k_norm.weight"], eps)
-    k = ops.apply_split_half_rope(k, cos, sin)
+    k = rnd(ops.apply_split_half_rope(k, cos, sin))
     if kv_hook is not None:
         kv_hook(i, k, v)
-    attn = ops.attention(q, k, v, visible=visible, dtype=np.float32).astype(np.float32)
+    attn = rnd(ops.attention(q, k, v, visible=visible, dtype=np.float32).astype(np.float32))
     hidden = (hidden + _lin(weights, p + "self_attn.o_proj", attn, kind)).astype(np.float32)
-    n2 = ops.rms_norm(hidden, weights[p + "post_attention_layernorm.weight"], eps)
+    n2 = rnd(ops.rms_norm(hidden, weights[p + "post_attention_layernorm.weight"], eps))
     gate = _lin(weights, p + "mlp.gate_proj", n2, kind)
     up = _lin(weights, p + "mlp.up_proj", n2, kind)
-    mlp = _lin(weights, p + "mlp.down_proj", ops.swiglu(gate, up), kind)
+    mlp = _lin(weights, p + "mlp.down_proj", rnd(ops.swiglu(gate, up)), kind)
     return (hidden + mlp).astype(np.float32)
 
 
 def forward_full(weights, cfg, token_ids, *, mask_kind, mask_geometry=None,
-                 output_rows=None, n_layers=None, kv_hook=None):
+                 output_rows=None, n_layers=None, kv_hook=None, operand_round=None):
     """Raw fp32 logits for ``output_rows`` (default: every row) of ``token_ids``.
 
     ``mask_kind`` is ``"d2f_hybrid"`` (``mask_geometry = (prompt_len,
     block_size)``; BD3 uses origin 0) or ``"bidirectional"`` (Dream, no mask).
     ``n_layers`` limits the layer count (the CPU baseline's bounded sample).
+    ``operand_round``: see :func:`layer_forward`; also applied to the final
+    norm's output (the LM head's input).
     """
     ids = np.asarray(token_ids, dtype=np.int64)
     s = ids.shape[0]
@@ -82,10 +94,10 @@ def forward_full(weights, cfg, token_ids, *, mask_kind, mask_geometry=None,
         raise ValueError(f"unsupported mask kind {mask_kind!r}")
     layers = cfg["n_layers"] if n_layers is None else n_layers
     for i in range(layers):
-        hidden = layer_forward(weights, cfg, i, hidden, cos, sin, visible, kv_hook)
+        hidden = layer_forward(weights, cfg, i, hidden, cos, sin, visible, kv_hook, operand_round)
     rows = list(range(s)) if output_rows is None else [int(r) for r in output_rows]
     h = hidden[rows]
-    h = ops.rms_norm(h, weights["model.norm.weight"], cfg["eps"])
+    h = (operand_round or _keep)(ops.rms_norm(h, weights["model.norm.weight"], cfg["eps"]))
     logits = ops.linear(h, weights["lm_head.weight"], None, weight_kind=cfg["weight_kind"])
     return logits.astype(np.float32)
 

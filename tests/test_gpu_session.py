@@ -8,8 +8,8 @@ from oracle import forward as F
 from oracle import ops as O
 from oracle import policy as P
 
-from helpers import (LOGITS_REL_TOL, compare_proposals, oracle_weights, rel_err_rows,
-                      tiny_dream_geometry, tiny_geometry)
+from helpers import (LOGITS_REL_TOL, OPERAND_TIE_REL, compare_proposals, oracle_weights,
+                     rel_err_rows, tiny_dream_geometry, tiny_geometry)
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -247,7 +247,7 @@ def test_reference_mask_cases_against_golden(kind):
                 if tokens[r] != w["argmax"]:
                     margin = w["max"] - w["second"]
                     band = (2 * 2.0 ** (np.floor(np.log2(scale)) - 7) if kind == "bf16"
-                            else -np.log1p(-1e-3))
+                            else -np.log1p(-OPERAND_TIE_REL))
                     assert margin <= band, (c["name"], r, tokens[r], w["argmax"], margin)
                     _say(f"  near-tie row {r}: {tokens[r]} vs {w['argmax']} margin {margin:.3g}")
                 else:

@@ -168,3 +168,46 @@ def test_kv_hook_sees_roped_keys():
     k0 = seen["k"][0].astype(np.float64)
     np.testing.assert_allclose(np.sqrt((k0 ** 2).mean(axis=-1)), 1.0, rtol=1e-4)
     assert seen["v"].shape == (8, g.num_kv_heads, g.head_dim)
+
+
+@pytest.mark.parametrize("seed", [21, 22])
+def test_fp16_operand_margin_perturbation(seed):
+    """The operand-precision tie band (helpers.OPERAND_TIE_REL) is measured, not
+    chosen: rounding the tensors the device path keeps in fp16 (linear inputs, Q,
+    K/V) moves the margins between the top token and the next seven by less than
+    0.8x the band at the BD3 layer shapes (2 layers, all 128 rows of a 96-token
+    prompt + one masked block)."""
+    import dataclasses
+
+    from helpers import OPERAND_TIE_REL
+
+    geom = dataclasses.replace(syn.BD3_QWEN3_06B, layer_count=2, vocab_size=4096,
+                               mask_token_id=4000, eos_token_id=4001)
+    model = syn.build_model(geom, "q4", seed)
+    W, cfg = oracle_weights(model), syn.oracle_config(geom, "q4")
+    x = np.random.default_rng(5).integers(0, 3900, 96).tolist() + [4000] * 32
+
+    def r16(a):
+        return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+    ref = F.forward_full(W, cfg, x, mask_kind="d2f_hybrid", mask_geometry=(0, 32))
+    got = F.forward_full(W, cfg, x, mask_kind="d2f_hybrid", mask_geometry=(0, 32),
+                         operand_round=r16)
+    ref, got = ref.astype(np.float64), got.astype(np.float64)
+    order = np.argsort(-ref, axis=-1)[:, :8]
+    rows = np.arange(ref.shape[0])
+    top = order[:, 0]
+    shift = max(np.abs((got[rows, order[:, j]] - got[rows, top]) -
+                       (ref[rows, order[:, j]] - ref[rows, top])).max() for j in range(1, 8))
+    assert 0 < shift < 0.8 * OPERAND_TIE_REL, shift
+    # the rounding does reach the margins (the band is not vacuous) ...
+    assert shift > 0.2 * OPERAND_TIE_REL
+    # ... and a planted fp16 -> bf16 operand precision breaks the bound
+    def r_bf16(a):
+        return O.bf16_round(np.asarray(a, np.float32))
+
+    coarse = F.forward_full(W, cfg, x, mask_kind="d2f_hybrid", mask_geometry=(0, 32),
+                            operand_round=r_bf16).astype(np.float64)
+    shift_bf16 = max(np.abs((coarse[rows, order[:, j]] - coarse[rows, top]) -
+                            (ref[rows, order[:, j]] - ref[rows, top])).max() for j in range(1, 8))
+    assert shift_bf16 > OPERAND_TIE_REL
