@@ -258,33 +258,58 @@ DRT_DEV void load_tile_nt(const T* __restrict__ base, int t, int lane, bool real
 // VGPRs, is rare instead of once per tile. Any base gives the same o / l.
 constexpr float DEC_RESCALE_LOG2 = 8.f;
 
-// One 32-key tile for all query tiles: S^T = K Q^T, softmax weights against the
-// running base, O^T += V^T P^T. Keys at or beyond n_keys get zero weight
-// (n_keys <= key0 makes the tile a no-op). Every query tile runs (the kernel is
-// instantiated with QT = ceil(n_qv / 32)); rows beyond n_qv hold Q = 0.
-// c = scale * log2(e); m_run is the base in scaled units (-inf before any key).
-template <typename T, int QT>
-DRT_DEV void attend_tile(const typename MfmaT<T>::vec (&kc)[8],
-                         const typename MfmaT<T>::vec (&vc)[8], const T* __restrict__ qs,
-                         int key0, int n_keys, float c, int lane, float (&m_run)[QT],
-                         float (&l_run)[QT], f32x16 (&o)[QT][4]) {
+// max(v[l], v[l ^ 32]) on every lane (gfx950 v_permlane32_swap, no LDS trip).
+DRT_DEV float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// NG 32-key tiles for all query tiles at once: S^T = K Q^T for every (tile,
+// query tile) as independent MFMA chains, one max over the group, softmax
+// weights against the running base, O^T += V^T P^T. Keys at or beyond nk[g]
+// get zero weight (nk[g] <= key0[g] makes tile g a no-op). Every query tile runs
+// (the kernel is instantiated with QT = ceil(n_qv / 32)); rows beyond n_qv hold
+// Q = 0. c = scale * log2(e); m_run is the base in scaled units (-inf before
+// any key). key0 / nk are wave-uniform.
+template <typename T, int QT, int NG>
+DRT_DEV void attend_group(const typename MfmaT<T>::vec (&kc)[NG][8],
+                          const typename MfmaT<T>::vec (&vc)[NG][8], const T* __restrict__ qs,
+                          const int (&key0)[NG], const int (&nk)[NG], float c, int lane,
+                          float (&m_run)[QT], float (&l_run)[QT], f32x16 (&o)[QT][4]) {
   typedef typename MfmaT<T>::vec vec;
-  const bool partial = key0 + 32 > n_keys;  // uniform: a partial (or empty) tile masks keys
+  f32x16 sc[NG][QT];
+#pragma unroll
+  for (int g = 0; g < NG; ++g)
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) sc[g][qt] = f32x16{};
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const vec qf =
+          *(const vec*)(qs + (qt * 32 + (lane & 31)) * DEC_QROW + 8 * (lane >> 5) + 16 * i);
+#pragma unroll
+      for (int g = 0; g < NG; ++g) sc[g][qt] = MfmaT<T>::mma(kc[g][i], qf, sc[g][qt]);
+    }
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    if (key0[g] + 32 > nk[g]) {  // uniform: a partial (or empty) tile masks its keys
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          sc[g][qt][r] = key0[g] + mfma_row(r, lane) < nk[g] ? sc[g][qt][r] : -INFINITY;
+    }
+  }
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    const T* qrow = qs + (qt * 32 + (lane & 31)) * DEC_QROW + 8 * (lane >> 5);
-    f32x16 sc = f32x16{};
+    float tmax = sc[0][qt][0];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) sc = MfmaT<T>::mma(kc[i], *(const vec*)(qrow + 16 * i), sc);
-    if (partial) {
+    for (int g = 0; g < NG; ++g)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sc[r] = key0 + mfma_row(r, lane) < n_keys ? sc[r] : -INFINITY;
-    }
-    float tmax = sc[0];
-#pragma unroll
-    for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, sc[r]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float mc = tmax * c;  // -inf for a query vector with no visible key in the tile
+      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sc[g][qt][r]);
+    const float mc = max_xor32(tmax) * c;  // -inf: no visible key in the group
     const bool up = mc > m_run[qt] + DEC_RESCALE_LOG2;
     if (__ballot(up)) {  // uniform: some base has to rise
       const float alpha = up ? __builtin_amdgcn_exp2f(m_run[qt] - mc) : 1.f;  // 0 from -inf
@@ -295,24 +320,30 @@ DRT_DEV void attend_tile(const typename MfmaT<T>::vec (&kc)[8],
       l_run[qt] *= alpha;
       m_run[qt] = up ? mc : m_run[qt];
     }
-    const float base = m_run[qt] == -INFINITY ? 0.f : m_run[qt];  // no key yet: p = 0
-    float pr[16];
-    float psum = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      pr[r] = __builtin_amdgcn_exp2f(fmaf(sc[r], c, -base));
-      psum += pr[r];
-    }
-    l_run[qt] += psum;
-#pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
-      vec pf;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) pf[j] = MfmaT<T>::from_float(pr[kh * 8 + j]);
-#pragma unroll
-      for (int hb = 0; hb < 4; ++hb) o[qt][hb] = MfmaT<T>::mma(vc[hb * 2 + kh], pf, o[qt][hb]);
-    }
   }
+#pragma unroll
+  for (int g = 0; g < NG; ++g)
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const float base = m_run[qt] == -INFINITY ? 0.f : m_run[qt];  // no key yet: p = 0
+      float pr[16];
+      float psum = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        pr[r] = __builtin_amdgcn_exp2f(fmaf(sc[g][qt][r], c, -base));
+        psum += pr[r];
+      }
+      l_run[qt] += psum;
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+        vec pf;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pf[j] = MfmaT<T>::from_float(pr[kh * 8 + j]);
+#pragma unroll
+        for (int hb = 0; hb < 4; ++hb)
+          o[qt][hb] = MfmaT<T>::mma(vc[g][hb * 2 + kh], pf, o[qt][hb]);
+      }
+    }
 }
 
 template <typename T, int QT>
@@ -324,7 +355,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   constexpr int SLOTS = QT * 4096;              // O slots of one partial
   constexpr int SLOT = SLOTS + QT * 64 * 2;     // + (m, l) per lane, one wave's LDS share
   constexpr int UP = DEC_TILES_UP_FRONT;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform tile choices
   const int G = Hq / Hkv;
   const int n_qv = n_rows * G;
   const int R = gridDim.x, rg = blockIdx.x, kvh = blockIdx.y;
@@ -387,34 +419,43 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 #pragma unroll
     for (int hb = 0; hb < 4; ++hb) o[qt][hb] = f32x16{};
   }
+  {
+    int key0[UP], nk[UP];
 #pragma unroll
-  for (int u = 0; u < UP; ++u) {
-    const int t = t0 + 4 * u;
-    attend_tile<T, QT>(kt[u], vt[u], qs, t * 32, t < t_end ? n_keys : 0, c, lane, m_run, l_run,
-                       o);
+    for (int u = 0; u < UP; ++u) {
+      key0[u] = (t0 + 4 * u) * 32;
+      nk[u] = t0 + 4 * u < t_end ? n_keys : 0;
+    }
+    attend_group<T, QT, UP>(kt, vt, qs, key0, nk, c, lane, m_run, l_run, o);
   }
   for (int t = t0 + 4 * UP; t < t_end; t += 4) {  // ranges longer than 4*UP tiles
-    load_tile_nt<T>(base, t, lane, true, kt[0], vt[0]);
-    attend_tile<T, QT>(kt[0], vt[0], qs, t * 32, n_keys, c, lane, m_run, l_run, o);
+    vec k1[1][8], v1[1][8];
+    load_tile_nt<T>(base, t, lane, true, k1[0], v1[0]);
+    const int key0[1] = {t * 32}, nk[1] = {n_keys};
+    attend_group<T, QT, 1>(k1, v1, qs, key0, nk, c, lane, m_run, l_run, o);
   }
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) l_run[qt] += __shfl_xor(l_run[qt], 32, 64);
 
-  // every wave stores its (O, m, l); slot (qt*64 + hb*16 + r)*64 + lane
+  // every wave stores its (O, m, l); O as 16-byte units of 4 accumulator rows,
+  // unit ((qt*4 + hb)*4 + r/4)*64 + lane
   float* mine = mrg + wave * SLOT;
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
 #pragma unroll
     for (int hb = 0; hb < 4; ++hb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mine[(qt * 64 + hb * 16 + r) * 64 + lane] = o[qt][hb][r];
+      for (int r4 = 0; r4 < 4; ++r4)
+        ((f32x4*)mine)[((qt * 4 + hb) * 4 + r4) * 64 + lane] =
+            f32x4{o[qt][hb][4 * r4], o[qt][hb][4 * r4 + 1], o[qt][hb][4 * r4 + 2],
+                  o[qt][hb][4 * r4 + 3]};
     mine[SLOTS + (qt * 64 + lane) * 2] = m_run[qt];
     mine[SLOTS + (qt * 64 + lane) * 2 + 1] = l_run[qt];
   }
   __syncthreads();
-  // combine the four waves; slot s = threadIdx.x + 256*i has lane (s & 63) = lane.
-  // A wave without keys holds O = 0 and weight 0 (its O is finite: the cache
-  // tiles are zero-initialised and invisible keys get probability 0).
+  // combine the four waves; unit e = threadIdx.x + 256*i has lane (e & 63) = lane
+  // and query tile i / 4. A wave without keys holds O = 0 and weight 0 (its O is
+  // finite: the cache tiles are zero-initialised and invisible keys get p = 0).
   float wgt[QT][4];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
@@ -437,26 +478,27 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       ml_part[(part * (QT * 32) + qt * 32 + lane) * 2 + 1] = ll;
     }
   }
-  float* op = o_part + part * SLOTS;
+  f32x4* op = (f32x4*)(o_part + part * SLOTS);
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int sl = qt * 4096 + threadIdx.x + 256 * i;
-      float v = 0.f;
+    for (int i = 0; i < 4; ++i) {
+      const int e = qt * 1024 + threadIdx.x + 256 * i;
+      f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int w = 0; w < 4; ++w) v = fmaf(wgt[qt][w], mrg[w * SLOT + sl], v);
-      op[sl] = v;
+      for (int w = 0; w < 4; ++w) v += wgt[qt][w] * ((const f32x4*)(mrg + w * SLOT))[e];
+      op[e] = v;
     }
   }
 }
 
-// Combine the ranges of the decode attention. Slot (qt*64 + hb*16 + r)*64 + l of a
-// partial holds query vector qt*32 + (l & 31) and head dim hb*32 + 8*(r >> 2) +
-// 4*(l >> 5) + (r & 3) (the MFMA result layout). Work-group (kvh, qt, hb*4 + rq)
-// owns the 256 slots with r in [4rq, 4rq + 4): 32 query vectors x the 8
-// consecutive head dims hb*32 + 8rq .. +8, one thread per slot, so 256
-// work-groups share the reads. Each query vector's 8 dims are one 8-element
+// Combine the ranges of the decode attention. Float ((qt*4 + hb)*4 + r/4)*256 +
+// l*4 + (r & 3) of a partial holds accumulator row r of lane l of the MFMA result
+// (qt, hb): query vector qt*32 + (l & 31), head dim hb*32 + 8*(r >> 2) +
+// 4*(l >> 5) + (r & 3). Work-group (kvh, qt, hb*4 + rq) owns the 256 contiguous
+// floats with r in [4rq, 4rq + 4): 32 query vectors x the 8 consecutive head
+// dims hb*32 + 8rq .. +8, one thread per float, so 256 work-groups share the
+// reads. Each query vector's 8 dims are one 8-element
 // chunk of the output row. Empty ranges (m = -inf) are skipped.
 // out_fmt: 0 = ACT_F16P (no group sums: its consumer sums the fp16 values
 // itself), 1 = ACT_BF16, 2 = fp32 plain, 3 = bf16 plain.
@@ -495,12 +537,12 @@ __global__ __launch_bounds__(256) void attn_decode_combine_kernel(
     ls[pg][c] = l_loc;
     __syncthreads();
   }
-  // 2. this thread's slot: r = 4rq + (j >> 6), lane l = j & 63
-  const int l = j & 63, r = 4 * rq + (j >> 6), c = l & 31;
+  // 2. this thread's float: lane l = j >> 2, r = 4rq + (j & 3)
+  const int l = j >> 2, r = 4 * rq + (j & 3), c = l & 31;
   float lsum = 0.f;
 #pragma unroll
   for (int g = 0; g < 8; ++g) lsum += ls[g][c];
-  const int64_t sl = (int64_t)qt * 4096 + (hb * 16 + r) * 64 + l;
+  const int64_t sl = (int64_t)qt * 4096 + (hb * 4 + rq) * 256 + j;
   float acc = 0.f;
   int rr = 0;
   for (; rr + 8 <= R; rr += 8) {
