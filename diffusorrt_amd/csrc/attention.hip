@@ -359,7 +359,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform tile choices
   const int G = Hq / Hkv;
   const int n_qv = n_rows * G;
-  const int R = gridDim.x, rg = blockIdx.x, kvh = blockIdx.y;
+  // grid (Hkv, R): with Hkv = 8 every range of a head runs on one XCD (work-group
+  // i runs on XCD i % 8), where the range combine of that head reads the partials
+  const int R = gridDim.y, rg = blockIdx.y, kvh = blockIdx.x;
   const int n_keys = desc ? desc->n_keys : n_keys_arg;
   const float c = scale * 1.44269504088896340736f;  // scores to base-2 exponents
   const int n_tiles = (n_keys + 31) >> 5;
@@ -515,49 +517,74 @@ __global__ __launch_bounds__(256) void attn_decode_combine_kernel(
   __shared__ float ls[8][32];
   __shared__ float tile[32][9];
   extern __shared__ float wts[];  // [R][32] unnormalised weights
-  // 1. per query vector c: max over ranges, weights, normaliser (8 range groups)
+  // this thread's float: lane l = j >> 2, r = 4rq + (j & 3)
+  const int l = j >> 2, r = 4 * rq + (j & 3);
+  const int64_t sl = (int64_t)qt * 4096 + (hb * 4 + rq) * 256 + j;
+  // the O values of the first RB ranges are loaded before (and independently
+  // of) the statistics, so one memory latency covers both
+  constexpr int RB = 32;
+  float v[RB];
+#pragma unroll
+  for (int e = 0; e < RB; ++e)
+    v[e] = o_part[((int64_t)min(e, R - 1) * Hkv + kvh) * SLOTS + sl];  // e >= R: unused
+  // 1. per query vector c: max over ranges, weights, normaliser (8 range groups;
+  // a thread holds ranges pg, pg + 8, ... < R <= 128)
   {
     const int c = j & 31, pg = j >> 5;
+    constexpr int MLR = 16;
+    float mr[MLR], lr[MLR];
+#pragma unroll
+    for (int k = 0; k < MLR; ++k) {
+      const int rr = pg + 8 * k;
+      const int64_t mi = (((int64_t)min(rr, R - 1) * Hkv + kvh) * (QT * 32) + qt * 32 + c) * 2;
+      mr[k] = rr < R ? ml_part[mi] : -INFINITY;
+      lr[k] = rr < R ? ml_part[mi + 1] : 0.f;
+    }
     float m_loc = -INFINITY;
-    for (int r = pg; r < R; r += 8)
-      m_loc = fmaxf(m_loc, ml_part[(((int64_t)r * Hkv + kvh) * (QT * 32) + qt * 32 + c) * 2]);
+#pragma unroll
+    for (int k = 0; k < MLR; ++k) m_loc = fmaxf(m_loc, mr[k]);
     mx[pg][c] = m_loc;
     __syncthreads();
     float mm = -INFINITY;
 #pragma unroll
     for (int g = 0; g < 8; ++g) mm = fmaxf(mm, mx[g][c]);
     float l_loc = 0.f;
-    for (int r = pg; r < R; r += 8) {
-      const int64_t mi = (((int64_t)r * Hkv + kvh) * (QT * 32) + qt * 32 + c) * 2;
-      const float m_r = ml_part[mi];
-      const float w = m_r == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_r - mm);
-      wts[r * 32 + c] = w;
-      l_loc += w * ml_part[mi + 1];
+#pragma unroll
+    for (int k = 0; k < MLR; ++k) {
+      const int rr = pg + 8 * k;
+      const float w = mr[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mr[k] - mm);
+      if (rr < R) wts[rr * 32 + c] = w;
+      l_loc += w * lr[k];
     }
     ls[pg][c] = l_loc;
     __syncthreads();
   }
-  // 2. this thread's float: lane l = j >> 2, r = 4rq + (j & 3)
-  const int l = j >> 2, r = 4 * rq + (j & 3), c = l & 31;
+  // 2. weighted sum over the ranges (a zero weight never multiplies its O,
+  // which an empty range does not write)
+  const int c = l & 31;
   float lsum = 0.f;
 #pragma unroll
   for (int g = 0; g < 8; ++g) lsum += ls[g][c];
-  const int64_t sl = (int64_t)qt * 4096 + (hb * 4 + rq) * 256 + j;
   float acc = 0.f;
-  int rr = 0;
-  for (; rr + 8 <= R; rr += 8) {
-    float v[8], w[8];
+#pragma unroll
+  for (int e = 0; e < RB; ++e) {
+    if (e < R) {
+      const float w = wts[e * 32 + c];
+      acc = fmaf(w, w == 0.f ? 0.f : v[e], acc);
+    }
+  }
+  for (int rr = RB; rr < R; rr += 8) {
+    float u[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      u[e] = o_part[((int64_t)min(rr + e, R - 1) * Hkv + kvh) * SLOTS + sl];  // >= R: unused
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      w[e] = wts[(rr + e) * 32 + c];
-      v[e] = w[e] == 0.f ? 0.f : o_part[((int64_t)(rr + e) * Hkv + kvh) * SLOTS + sl];
+      if (rr + e < R) {
+        const float w = wts[(rr + e) * 32 + c];
+        acc = fmaf(w, w == 0.f ? 0.f : u[e], acc);
+      }
     }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc = fmaf(w[e], v[e], acc);
-  }
-  for (; rr < R; ++rr) {
-    const float w = wts[rr * 32 + c];
-    if (w != 0.f) acc = fmaf(w, o_part[((int64_t)rr * Hkv + kvh) * SLOTS + sl], acc);
   }
   // 3. gather each query vector's 8 dims: dim offset 4*(l >> 5) + (r & 3)
   tile[c][4 * (l >> 5) + (r & 3)] = acc / lsum;
@@ -805,7 +832,7 @@ void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv
   const int qt = (n_rows * G + 31) / 32;
   const float scale = 1.0f / sqrtf(128.0f);
   const size_t lds = (size_t)qt * 32 * DEC_QROW * 2 + (size_t)4 * (qt * 4096 + qt * 128) * 4;
-  const dim3 grid(ranges, Hkv);
+  const dim3 grid(Hkv, ranges);
   const double bytes = 2.0 * n_rows * Hq * 128 + 4.0 * n_keys * Hkv * 128;
   float* o_part = part;
   float* ml_part = part + (size_t)ranges * Hkv * qt * 4096;
