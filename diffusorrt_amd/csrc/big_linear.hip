@@ -1,0 +1,324 @@
+// Large-M q4 linear for gfx950: the forwards of more than 32 rows (Dream's
+// full canvas, BD3 prefix commits). At these sizes the contraction is MFMA
+// bound, so the weights are dequantized once per work-group into fp16 MFMA
+// operands (w = s * q + b, one fp16 rounding; backends/mlx_ops.py:97-130 for the
+// linear, :43-60 for the MLX q4 g64 packing) instead of the per-group scaled
+// accumulators of the weight-streaming kernels, whose two FMAs per output and
+// group would cost as much VALU time as the MFMAs.
+//
+// Work-group tile: 128 rows x 256 columns, 4 waves side by side in N; a wave
+// owns 128 x 64 (4 x 2 MFMA 32x32x16 tiles, 128 fp32 accumulators per lane).
+//   A (the ACT_F16P activation [M][K]) is staged per 64-k group in LDS, double
+//     buffered; every wave reads all 128 rows (16 KiB per group).
+//   B (q4 tile layout: per 32-column n-tile and 64-k group, 1 KiB of words and
+//     32 scale|bias pairs) goes straight from global memory to registers and is
+//     dequantized there: 2 n-tiles per wave per group.
+// A register ring keeps the next group's loads in flight during the MFMAs, and
+// two work-groups per CU (<= 256 registers per lane) hide each other's waits.
+// Split-K over blockIdx.z (KS slices) writes fp32 partial slices y + ks * M * N
+// that a reduce pass sums (residual_norm_kernel).
+// Epilogues run on 32-row pieces of the tile staged through LDS:
+//   EPI_STORE : y (+ bias on slice 0)
+//   EPI_SWIGLU: [gate 64 | up 64] column blocks -> silu(g) * u -> ACT_F16P
+//   EPI_QKV   : (+ bias), q/k RMSNorm, RoPE, Q out / K,V into the tiled cache
+#include "fused.h"
+#include "gemm_core.h"
+#include "launch.h"
+
+#include "linear_dev.h"
+
+namespace {
+
+constexpr int BG_WM = 128;                     // rows per work-group
+constexpr int BG_WN = 256;                     // columns per work-group (4 waves x 64)
+constexpr int BG_AROW = 72;                    // fp16 elements per LDS A row (64 + 16 B pad)
+constexpr int BG_ABUF = BG_WM * BG_AROW;       // fp16 elements per A buffer
+constexpr int BG_EROW = BG_WN + 4;             // floats per LDS row of an epilogue piece
+constexpr int BG_STAGE_BYTES = 2 * BG_ABUF * 2 > 32 * BG_EROW * 4 ? 2 * BG_ABUF * 2
+                                                                   : 32 * BG_EROW * 4;
+constexpr int BG_V_OFF = (BG_STAGE_BYTES + 15) / 16 * 16;
+constexpr int BG_LDS = BG_V_OFF + 4096 * 2;    // + one V tile half for the QKV epilogue
+
+template <int S> struct Slot { static constexpr int value = S; };
+// register ring of group loads: RING - 1 groups in flight ahead of the MFMAs
+// (2: two work-groups per CU, the other work-group hides the latency)
+constexpr int BG_RING = 2;
+
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+
+// fp16 B fragments of one 64-k group of one 32-column n-tile: word t of the lane
+// holds the 8 k of MFMA step t in the ACT_F16P order (0,4,1,5,2,6,3,7); nibble
+// pairs become (1024 + q) halves by bit placement, then q * s + b in one fma.
+DRT_DEV void dequant_q4_group(const u32x4 w, uint32_t sbv, f16x8 (&b)[4]) {
+  const _Float16 s = (_Float16)bf16_bits_to_float(sbv & 0xffffu);
+  const _Float16 z = (_Float16)bf16_bits_to_float(sbv >> 16);
+  const h2v s2 = {s, s}, z2 = {z, z};
+  const h2v k2 = {(_Float16)-1024.f, (_Float16)-1024.f};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const h2v h = __builtin_bit_cast(h2v, ((w[t] >> (4 * e)) & 0x000F000Fu) | 0x64006400u);
+      o[e] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(h + k2, s2, z2));
+    }
+    b[t] = __builtin_bit_cast(f16x8, o);
+  }
+}
+
+}  // namespace
+
+template <int EPI>
+__global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int KS) {
+  constexpr int RING = BG_RING;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int M = a.M, N = a.N, K = a.K, G = K >> 6;
+  const int n0 = blockIdx.x * BG_WN, m0 = blockIdx.y * BG_WM, ks = blockIdx.z;
+  const int g_lo = (int)((int64_t)G * ks / KS), g_hi = (int)((int64_t)G * (ks + 1) / KS);
+  const int n_g = g_hi - g_lo;
+  const int NT = N >> 5;
+  // this wave's two n-tiles, clamped so that loads stay in bounds (columns
+  // beyond N are computed from the last n-tile and never stored)
+  const int nt0 = min((n0 >> 5) + 2 * wave, NT - 1);
+  const int nt1 = min((n0 >> 5) + 2 * wave + 1, NT - 1);
+  extern __shared__ __align__(16) char smem[];
+  _Float16* as = (_Float16*)smem;  // [2][BG_WM][BG_AROW]
+  const _Float16* act = (const _Float16*)a.act;
+
+  u32x4 ra[RING][4];
+  u32x4 wq[RING][2];
+  uint32_t wsb[RING][2];
+  // A chunk c = threadIdx.x + 256 i of a group: row c >> 3, 16-byte part c & 7
+  auto issue = [&](int g, auto slot) {
+    constexpr int S = decltype(slot)::value;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int m = min(m0 + (c >> 3), M - 1);  // rows past M are zeroed when stashed
+      ra[S][i] = *(const u32x4*)(act + (int64_t)m * K + g * 64 + (c & 7) * 8);
+    }
+    wq[S][0] = *q4_tile_words(a.qw, nt0, G, g, lane);
+    wq[S][1] = *q4_tile_words(a.qw, nt1, G, g, lane);
+    wsb[S][0] = q4_tile_sb(a.sb, nt0, G, g, lane);
+    wsb[S][1] = q4_tile_sb(a.sb, nt1, G, g, lane);
+  };
+  auto stash = [&](int buf, auto slot) {
+    constexpr int S = decltype(slot)::value;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const bool ok = m0 + (c >> 3) < M;
+      *(u32x4*)(as + buf * BG_ABUF + (c >> 3) * BG_AROW + (c & 7) * 8) =
+          ok ? ra[S][i] : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i][0] = acc[i][1] = f32x16{};
+
+  if (n_g > 0) issue(g_lo, Slot<0>{});
+  if (RING > 2 && n_g > 1) issue(g_lo + 1, Slot<1 % RING>{});
+  if (RING > 3 && n_g > 2) issue(g_lo + 2, Slot<2 % RING>{});
+  if (n_g > 0) stash(0, Slot<0>{});
+  __syncthreads();
+
+  // group gi (relative) lives in ring slot gi % RING and LDS buffer gi & 1
+  auto step = [&](int gi, auto slot) {
+    constexpr int S = decltype(slot)::value;
+    f16x8 bf[2][4];
+    dequant_q4_group(wq[S][0], wsb[S][0], bf[0]);
+    dequant_q4_group(wq[S][1], wsb[S][1], bf[1]);
+    // the slot of group gi + RING - 1 held group gi - 1: consumed (B) and stashed (A)
+    if (gi + RING - 1 < n_g) issue(g_lo + gi + RING - 1, Slot<(S + RING - 1) % RING>{});
+    const _Float16* ab = as + (gi & 1) * BG_ABUF;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f16x8 af =
+            *(const f16x8*)(ab + (i * 32 + (lane & 31)) * BG_AROW + 32 * (lane >> 5) + 8 * t);
+        acc[i][0] = mfma_f16(af, bf[0][t], acc[i][0]);
+        acc[i][1] = mfma_f16(af, bf[1][t], acc[i][1]);
+      }
+    }
+    // the other buffer was last read before the previous step's barrier
+    if (gi + 1 < n_g) stash((gi + 1) & 1, Slot<(S + 1) % RING>{});
+    __syncthreads();
+  };
+  for (int gb = 0; gb < n_g; gb += RING) {
+    step(gb, Slot<0>{});
+    if (gb + 1 < n_g) step(gb + 1, Slot<1 % RING>{});
+    if (RING > 2 && gb + 2 < n_g) step(gb + 2, Slot<2 % RING>{});
+    if (RING > 3 && gb + 3 < n_g) step(gb + 3, Slot<3 % RING>{});
+  }
+
+  // Epilogue in 32-row pieces (MFMA m-tile p of every wave) through LDS.
+  float* e = (float*)smem;  // [32][BG_EROW]
+  uint16_t* vbuf = (uint16_t*)(smem + BG_V_OFF);
+  const int row0 = a.desc ? a.desc->row0 : 0;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int mp = m0 + 32 * p;  // forward row of local row 0
+    if (mp >= M) break;          // uniform
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        e[mfma_row(r, lane) * BG_EROW + wave * 64 + j * 32 + (lane & 31)] = acc[p][j][r];
+    __syncthreads();
+    if (EPI == EPI_STORE) {
+      float* y = a.y + (int64_t)ks * M * N;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int c = threadIdx.x + 256 * i;
+        const int r = c >> 6, n = n0 + (c & 63) * 4;
+        if (mp + r < M && n < N) {
+          f32x4 v = *(const f32x4*)(e + r * BG_EROW + (c & 63) * 4);
+          if (a.bias && ks == 0) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] += bf16_bits_to_float(a.bias[n + k]);
+          }
+          *(f32x4*)(y + (int64_t)(mp + r) * N + n) = v;
+        }
+      }
+    } else if (EPI == EPI_SWIGLU) {
+      // output chunk q: block q >> 3 of [gate 64 | up 64], 8 outputs at (q & 7) * 8
+      const int F = N >> 1;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int c = threadIdx.x + 256 * i;
+        const int r = c >> 4, q = c & 15, blk = q >> 3, c8 = (q & 7) * 8;
+        if (mp + r < M && n0 + blk * 128 < N) {
+          _Float16 h[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const float g = e[r * BG_EROW + blk * 128 + c8 + k];
+            const float u = e[r * BG_EROW + blk * 128 + 64 + c8 + k];
+            h[f16p_index(k)] = (_Float16)(g * (1.f / (1.f + expf(-g))) * u);
+          }
+          *(u32x4*)((_Float16*)a.act_out + (int64_t)(mp + r) * F + (n0 >> 1) + blk * 64 + c8) =
+              __builtin_bit_cast(u32x4, h);
+        }
+      }
+    } else if (EPI == EPI_QKV) {
+      const int rows = min(32, M - mp);
+#pragma unroll
+      for (int hl = 0; hl < 2; ++hl) {
+        const int head = (n0 >> 7) + hl;
+        if (head * 128 >= N) break;  // uniform
+        if (hl) __syncthreads();     // the V tile buffer of head 0 has been copied out
+        auto get = [&](int m, int d) { return e[m * BG_EROW + hl * 128 + d]; };
+        if (a.kv_bf16) qkv_epilogue<__bf16>(a, head, mp, row0 + mp, rows, get, vbuf);
+        else qkv_epilogue<_Float16>(a, head, mp, row0 + mp, rows, get, vbuf);
+      }
+    }
+    __syncthreads();  // the piece's LDS is read before the next piece is written
+  }
+}
+
+template __global__ void big_q4_kernel<EPI_STORE>(const FusedArgs, int);
+template __global__ void big_q4_kernel<EPI_SWIGLU>(const FusedArgs, int);
+template __global__ void big_q4_kernel<EPI_QKV>(const FusedArgs, int);
+
+// The QKV epilogue of a split-K q|k|v projection: work-group (head, 32-row
+// block) sums the KS fp32 partial slices of its head's 128 columns (bias
+// excluded, added by the epilogue) into LDS - every slice's loads issued before
+// the first add - and runs the same per-head epilogue from there.
+template <typename T>
+__global__ __launch_bounds__(256) void big_qkv_epilogue_kernel(const FusedArgs a,
+                                                               const float* __restrict__ part,
+                                                               int KS) {
+  __shared__ __align__(16) float tile[32][132];
+  __shared__ __align__(16) uint16_t vbuf[4096];
+  const int M = a.M, N = a.N;
+  const int head = blockIdx.x, mp = blockIdx.y * 32;
+  const int rows = min(32, M - mp);
+  const int row0 = a.desc ? a.desc->row0 : 0;
+  // 32 rows x 32 float4 per slice: thread t takes rows t >> 5 + 8j, float4 t & 31
+  constexpr int KMAX = drt::BG_QKV_MAX_KS;
+  f32x4 v[KMAX][4];
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = min((threadIdx.x >> 5) + 8 * j, rows - 1);
+      v[k][j] = *(const f32x4*)(part + (int64_t)min(k, KS - 1) * M * N + (int64_t)(mp + m) * N +
+                                head * 128 + (threadIdx.x & 31) * 4);
+    }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    f32x4 sum = v[0][j];
+#pragma unroll
+    for (int k = 1; k < KMAX; ++k)
+      if (k < KS) sum += v[k][j];
+    *(f32x4*)&tile[(threadIdx.x >> 5) + 8 * j][(threadIdx.x & 31) * 4] = sum;
+  }
+  __syncthreads();
+  auto get = [&](int m, int d) { return tile[m][d]; };
+  qkv_epilogue<T>(a, head, mp, row0 + mp, rows, get, vbuf);
+}
+
+template __global__ void big_qkv_epilogue_kernel<_Float16>(const FusedArgs, const float*, int);
+template __global__ void big_qkv_epilogue_kernel<__bf16>(const FusedArgs, const float*, int);
+
+namespace drt {
+
+// K slices for a large-M q4 linear of M x N x K: enough work-groups for two per
+// CU (the kernel's register budget), at most max_ks slices and at least 8 groups
+// of 64 k per slice.
+int big_linear_splits(int M, int N, int K, int max_ks) {
+  const int tiles = ((M + BG_WM - 1) / BG_WM) * ((N + BG_WN - 1) / BG_WN);
+  if (tiles >= 384) return 1;
+  int ks = std::min(max_ks, (448 + tiles - 1) / tiles);
+  ks = std::min(ks, std::max(1, (K / 64) / 8));
+  return std::max(1, ks);
+}
+
+bool big_linear_supported(const FusedArgs& a, int kind) {
+  if (!a.qw || !a.sb || a.M <= 32 || a.N % 32 != 0 || a.K % 64 != 0) return false;
+  if ((kind == FL_QKV || kind == FL_SWIGLU) && a.N % 128 != 0) return false;
+  if (kind == FL_SWIGLU && a.act_fmt != ACT_F16P) return false;
+  return kind == FL_QKV || kind == FL_SWIGLU || kind == FL_STORE;
+}
+
+void big_linear(const FusedArgs& a, int kind, int KS, hipStream_t s) {
+  require(big_linear_supported(a, kind), "large-M linear: unsupported shape or kind");
+  require(KS >= 1 && KS <= a.K / 64 && (KS == 1 || kind == FL_STORE),
+          "large-M linear: split-K only for plain stores");
+  const dim3 grid((a.N + BG_WN - 1) / BG_WN, (a.M + BG_WM - 1) / BG_WM, KS);
+  const double bytes = (double)a.N * a.K / 2 + (double)a.N * a.K / 16 + 2.0 * a.M * a.K +
+                       (kind == FL_STORE ? 4.0 * KS : 2.0) * a.M * a.N;
+#define DRT_BG(E)                                                                        \
+  {                                                                                      \
+    auto fn = big_q4_kernel<E>;                                                          \
+    static size_t granted = 0;                                                           \
+    grant_lds((const void*)fn, BG_LDS, granted);                                         \
+    DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(256), BG_LDS, s, a, KS);            \
+  }
+  if (kind == FL_QKV) DRT_BG(EPI_QKV)
+  else if (kind == FL_SWIGLU) DRT_BG(EPI_SWIGLU)
+  else DRT_BG(EPI_STORE)
+#undef DRT_BG
+  DRT_HIP(hipGetLastError());
+}
+
+void big_qkv(const FusedArgs& a, float* part, size_t part_floats, hipStream_t s) {
+  const int ks = big_linear_splits(a.M, a.N, a.K, BG_QKV_MAX_KS);
+  if (ks == 1 || ks > BG_QKV_MAX_KS || !part || (size_t)ks * a.M * a.N > part_floats) {
+    big_linear(a, FL_QKV, 1, s);
+    return;
+  }
+  FusedArgs g = a;
+  g.bias = nullptr;  // the epilogue adds it
+  g.y = part;
+  big_linear(g, FL_STORE, ks, s);
+  const dim3 grid(a.N / 128, (a.M + 31) / 32);
+  if (a.kv_bf16)
+    hipLaunchKernelGGL(big_qkv_epilogue_kernel<__bf16>, grid, dim3(256), 0, s, a, part, ks);
+  else
+    hipLaunchKernelGGL(big_qkv_epilogue_kernel<_Float16>, grid, dim3(256), 0, s, a, part, ks);
+  DRT_HIP(hipGetLastError());
+}
+
+}  // namespace drt

@@ -2,8 +2,9 @@
 //
 //   * embed_kernel:         token rows of the bf16 table -> fp32 residual stream.
 //   * residual_norm_kernel: (optional split partials added to) the residual
-//     stream, then RMSNorm(h) * w of selected rows in an activation format;
-//     the runtime uses it for the final norm of the LM-head rows.
+//     stream, then RMSNorm(h) * w of selected rows in an activation format:
+//     the final norm of the LM-head rows, and the reduce + next norm of the
+//     large-M forwards' split-K projections.
 //   * per-op fp32 kernels of the kernel-table seam: rms_norm, rope, swiglu.
 // The decoder layer's other epilogues are fused into fused_linear.hip.
 // Reference math: backends/mlx_ops.py:21-35 (rms_norm), :97-130 (linear
@@ -32,23 +33,6 @@ DRT_DEV float block_sum_256(float v, float* red) {
   for (int i = 0; i < nw; ++i) t += red[i];
   return t;
 }
-
-// Write one activation element. F16P also needs a wave-wide group sum, done by
-// the caller (each wave covers exactly one 64-wide group per call).
-DRT_DEV void write_act(int fmt, void* row, int k, float v, float* xsum_row, int lane) {
-  if (fmt == ACT_F16P) {
-    const _Float16 h = (_Float16)v;
-    ((_Float16*)row)[f16p_index(k)] = h;
-    const float s = wave_sum((float)h);
-    if (lane == 0) xsum_row[k >> 6] = s;
-  } else if (fmt == ACT_BF16) {
-    ((uint16_t*)row)[k] = float_to_bf16_bits(v);
-  } else {
-    ((float*)row)[k] = v;
-  }
-}
-
-DRT_DEV size_t act_row_bytes(int fmt, int d) { return fmt == 2 ? (size_t)d * 4 : (size_t)d * 2; }
 
 }  // namespace
 
@@ -82,48 +66,122 @@ extern "C" __global__ void embed_kernel(const int32_t* __restrict__ tokens,
   }
 }
 
-// One 256-thread WG per output row. Requires d % 256 == 0 (true for every
-// geometry here: 1024, 3584 = 14 * 256).
+// One wave per output row (4 rows per 256-thread work-group). Lane l owns the
+// 8-element chunks l, l + 64, ... of the row (d % 64 == 0, d <= 4096), loaded
+// and stored 16 bytes at a time; the 8 chunks of a 64-wide group are 8
+// consecutive lanes.
 //   src row  = src_rows ? src_rows[i] : i
 //   v        = hidden[src] + R(sum_s part[s][src])          (part may be null)
-//   hidden_out[src] = v                                     (if non-null)
+//   hidden_out[src] = v                                     (if write_hidden)
 //   act[i]   = fmt(v * rsqrt(mean(v^2) + eps) * w)          (if norm_w non-null)
-extern "C" __global__ void residual_norm_kernel(
+// (backends/mlx_ops.py:21-35 for the norm; R rounds to bf16 when rnd_bf16.)
+constexpr int RN_MAX_SPLITS = 8;  // partial slices a reduce takes
+
+extern "C" __global__ __launch_bounds__(256) void residual_norm_kernel(
     float* __restrict__ hidden, const float* __restrict__ part, int splits, int M_part,
     int rnd_bf16, const int32_t* __restrict__ src_rows, int write_hidden,
     const uint16_t* __restrict__ norm_w, float eps, int d, int fmt, void* __restrict__ act,
-    float* __restrict__ xsum) {
-  __shared__ float red[8];
-  const int i = blockIdx.x;
-  const int src = src_rows ? src_rows[i] : i;
+    float* __restrict__ xsum, int n_rows) {
+  constexpr int NC = 8;  // chunks per lane for d <= 4096
   const int lane = threadIdx.x & 63;
-  constexpr int MAXV = 14;  // d <= 3584
-  float v[MAXV];
-  const int nv = d / 256;
-  float ss = 0.f;
-  for (int j = 0; j < nv; ++j) {
-    const int k = j * 256 + threadIdx.x;
-    float x = hidden[(int64_t)src * d + k];
-    if (part) {
-      float s = 0.f;
-      for (int p = 0; p < splits; ++p) s += part[((int64_t)p * M_part + src) * d + k];
-      if (rnd_bf16) s = round_bf16(s);
-      x += s;
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (i >= n_rows) return;  // whole waves
+  const int src = src_rows ? src_rows[i] : i;
+  f32x4 v[NC][2];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int k = (lane + 64 * c) * 8;
+    if (k < d) {
+      const f32x4* hp = (const f32x4*)(hidden + (int64_t)src * d + k);
+      v[c][0] = hp[0];
+      v[c][1] = hp[1];
+    } else {
+      v[c][0] = v[c][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    v[j] = x;
-    ss += x * x;
   }
-  if (write_hidden)
-    for (int j = 0; j < nv; ++j) hidden[(int64_t)src * d + j * 256 + threadIdx.x] = v[j];
+  if (part) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int k = (lane + 64 * c) * 8;
+      if (k < d) {
+        // every slice's loads are issued before the first add (one latency)
+        f32x4 ps[RN_MAX_SPLITS][2];
+#pragma unroll
+        for (int p = 0; p < RN_MAX_SPLITS; ++p) {
+          const f32x4* pp =
+              (const f32x4*)(part + ((int64_t)min(p, splits - 1) * M_part + src) * d + k);
+          ps[p][0] = pp[0];
+          ps[p][1] = pp[1];
+        }
+        f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
+#pragma unroll
+        for (int p = 0; p < RN_MAX_SPLITS; ++p) {
+          if (p < splits) {
+            s0 += ps[p][0];
+            s1 += ps[p][1];
+          }
+        }
+        if (rnd_bf16) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            s0[e] = round_bf16(s0[e]);
+            s1[e] = round_bf16(s1[e]);
+          }
+        }
+        v[c][0] += s0;
+        v[c][1] += s1;
+        if (write_hidden) {
+          f32x4* hp = (f32x4*)(hidden + (int64_t)src * d + k);
+          hp[0] = v[c][0];
+          hp[1] = v[c][1];
+        }
+      }
+    }
+  }
   if (!norm_w) return;
-  const float tot = block_sum_256(ss, red);
-  const float inv = 1.f / sqrtf(tot / (float)d + eps);
-  char* arow = (char*)act + (size_t)i * act_row_bytes(fmt, d);
-  float* xs_row = xsum ? xsum + (int64_t)i * (d >> 6) : nullptr;
-  for (int j = 0; j < nv; ++j) {
-    const int k = j * 256 + threadIdx.x;
-    const float n = (v[j] * inv) * bf16_bits_to_float(norm_w[k]);
-    write_act(fmt, arow, k, n, xs_row, lane);
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ss += v[c][0][e] * v[c][0][e] + v[c][1][e] * v[c][1][e];
+  const float inv = 1.f / sqrtf(wave_sum(ss) / (float)d + eps);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int k = (lane + 64 * c) * 8;
+    if (k >= d) break;  // uniform across each 8-lane group (d % 64 == 0)
+    const u32x4 wv = *(const u32x4*)(norm_w + k);
+    float n[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      n[2 * e] = (v[c][e >> 1][(2 * e) & 3] * inv) * bf16_bits_to_float(wv[e] & 0xffffu);
+      n[2 * e + 1] = (v[c][e >> 1][(2 * e + 1) & 3] * inv) * bf16_bits_to_float(wv[e] >> 16);
+    }
+    if (fmt == ACT_F16P) {
+      _Float16 h[8];
+      float gs = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const _Float16 he = (_Float16)n[e];
+        h[f16p_index(e)] = he;
+        gs += (float)he;
+      }
+      *(u32x4*)((_Float16*)act + (int64_t)i * d + k) = __builtin_bit_cast(u32x4, h);
+      if (xsum) {
+        gs += __shfl_xor(gs, 1, 64);
+        gs += __shfl_xor(gs, 2, 64);
+        gs += __shfl_xor(gs, 4, 64);
+        if ((lane & 7) == 0) xsum[(int64_t)i * (d >> 6) + (k >> 6)] = gs;
+      }
+    } else if (fmt == ACT_BF16) {
+      uint16_t h[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) h[e] = float_to_bf16_bits(n[e]);
+      *(u32x4*)((uint16_t*)act + (int64_t)i * d + k) = __builtin_bit_cast(u32x4, h);
+    } else {
+      f32x4* o = (f32x4*)((float*)act + (int64_t)i * d + k);
+      o[0] = f32x4{n[0], n[1], n[2], n[3]};
+      o[1] = f32x4{n[4], n[5], n[6], n[7]};
+    }
   }
 }
 
@@ -188,11 +246,12 @@ void embed(const int32_t* tokens, const uint16_t* table, float* hidden, int M, i
 void residual_norm(float* hidden, const float* part, int splits, int M_part, bool rnd_bf16,
                    const int32_t* src_rows, bool write_hidden, const uint16_t* norm_w, float eps,
                    int d, int fmt, void* act, float* xsum, int n_out_rows, hipStream_t s) {
-  require(d % 256 == 0 && d <= 14 * 256, "residual_norm needs d % 256 == 0 and d <= 3584");
+  require(d % 64 == 0 && d <= 4096, "residual_norm needs d % 64 == 0 and d <= 4096");
+  require(!part || (splits >= 1 && splits <= RN_MAX_SPLITS), "residual_norm takes 1..8 slices");
   if (n_out_rows <= 0) return;
-  hipLaunchKernelGGL(residual_norm_kernel, dim3(n_out_rows), dim3(256), 0, s, hidden, part, splits,
-                     M_part, (int)rnd_bf16, src_rows, (int)write_hidden, norm_w, eps, d, fmt, act,
-                     xsum);
+  hipLaunchKernelGGL(residual_norm_kernel, dim3((n_out_rows + 3) / 4), dim3(256), 0, s, hidden,
+                     part, splits, M_part, (int)rnd_bf16, src_rows, (int)write_hidden, norm_w, eps,
+                     d, fmt, act, xsum, n_out_rows);
   DRT_HIP(hipGetLastError());
 }
 

@@ -64,4 +64,15 @@ bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s);
 // Workspace the skinny kernels need for a linear of N outputs and K inputs.
 size_t skinny_part_floats(int N, int K);
 int skinny_counters(int N);
+// The large-M q4 kernels (M > 32): ACT_F16P activation in, kinds FL_QKV,
+// FL_SWIGLU (ACT_F16P out) and FL_STORE (KS > 1: fp32 partial slices
+// y + ks * M * N for a reduce pass).
+bool big_linear_supported(const FusedArgs& a, int kind);
+int big_linear_splits(int M, int N, int K, int max_ks);
+void big_linear(const FusedArgs& a, int kind, int KS, hipStream_t s);
+// q|k|v projection + epilogue: split-K into `part` (when the tiles alone would
+// leave CUs idle and part_floats suffices) and a separate epilogue pass.
+void big_qkv(const FusedArgs& a, float* part, size_t part_floats, hipStream_t s);
+constexpr int BG_QKV_MAX_KS = 4;    // split-K slices of the q|k|v projection
+constexpr int BG_RESID_MAX_KS = 8;  // ... of o_proj / down_proj (reduced with the next norm)
 }

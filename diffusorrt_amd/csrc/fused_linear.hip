@@ -381,6 +381,10 @@ constexpr size_t FUSED_LDS = 32 * (1024 + 8) * 2 + 16 * 32 * 4 + 32 * 4 + 32 * 2
 void fused_linear(const FusedArgs& a, int kind, hipStream_t s) {
   require(a.N % 32 == 0, "fused linear needs N % 32 == 0");
   if (skinny_linear(a, kind, s)) return;
+  if (kind == FL_STORE && big_linear_supported(a, kind)) {  // > 32 rows, q4
+    big_linear(a, FL_STORE, 1, s);
+    return;
+  }
   require(a.K % (a.qw ? 64 : 16) == 0, "fused linear needs K % 64 (q4) or K % 16 (bf16)");
   static_assert(FUSED_LDS >= 16 * 32 * 33 * 4, "LDS staging must also hold the reduction");
   const bool q4 = a.qw != nullptr;

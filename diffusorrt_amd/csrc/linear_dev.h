@@ -106,4 +106,133 @@ DRT_DEV void qkv_head_store(const FusedArgs& a, int head, int m, int pos, float 
   }
 }
 
+// Epilogue of one q/k/v head over 32 rows of a forward (backends/mlx_forward.py:
+// 1164-1361): (+ bias), per-head RMSNorm of q/k (mlx_ops.py:21-35), split-half
+// RoPE at the row's absolute position (mlx_ops.py:133-144), then Q out or K/V
+// into the tiled cache. 256 threads: thread t owns local row t >> 3 and the head
+// dims 8c .. 8c+7 and 64+8c .. 64+8c+7 (c = t & 7): the RoPE pairs of its dims
+// are its own, the norm is a sum over 8 lanes, and every store is 16 bytes -
+// except V, whose tile layout spreads a key over the tile: a whole aligned
+// 32-key tile is assembled in LDS first (lds_v, 4096 elements; the call then
+// holds a work-group barrier, so every thread must make it), otherwise V is
+// written element-wise.
+//   mrow0: forward row of local row 0 (Q rows are forward rows)
+//   pos0 : absolute position of local row 0
+//   rows : valid local rows (<= 32)
+//   get(m, d): the linear's output (before bias) of local row m, head dim d
+template <typename T, typename Get>
+DRT_DEV void qkv_epilogue(const FusedArgs& a, int head, int mrow0, int pos0, int rows, Get get,
+                          uint16_t* lds_v) {
+  const int Hq = a.Hq, Hkv = a.Hkv;
+  const int m = threadIdx.x >> 3, c = threadIdx.x & 7;
+  const bool is_q = head < Hq, is_k = !is_q && head < Hq + Hkv, is_v = !is_q && !is_k;
+  const int pos = pos0 + m;
+  const int pos_t = m < rows ? pos : pos0;  // rows past the end read a valid table row
+  float x[8], y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    x[e] = get(m, 8 * c + e);
+    y[e] = get(m, 64 + 8 * c + e);
+  }
+  if (a.bias) {
+    const u32x4 b0 = *(const u32x4*)(a.bias + head * 128 + 8 * c);
+    const u32x4 b1 = *(const u32x4*)(a.bias + head * 128 + 64 + 8 * c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] += bf16_bits_to_float(b0[e] & 0xffffu);
+      x[2 * e + 1] += bf16_bits_to_float(b0[e] >> 16);
+      y[2 * e] += bf16_bits_to_float(b1[e] & 0xffffu);
+      y[2 * e + 1] += bf16_bits_to_float(b1[e] >> 16);
+    }
+  }
+  if (!is_v) {
+    const uint16_t* nw = is_q ? a.q_norm : a.k_norm;
+    // rotary tables: cos/sin [pos][64] fp32, angle i shared by dims i and i + 64
+    const f32x4* cp = (const f32x4*)(a.rope_cos + (int64_t)pos_t * 64 + 8 * c);
+    const f32x4* sp = (const f32x4*)(a.rope_sin + (int64_t)pos_t * 64 + 8 * c);
+    const f32x4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+    if (nw) {
+      const u32x4 w0 = *(const u32x4*)(nw + 8 * c), w1 = *(const u32x4*)(nw + 64 + 8 * c);
+      float q = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) q += x[e] * x[e] + y[e] * y[e];
+      q += __shfl_xor(q, 1, 64);
+      q += __shfl_xor(q, 2, 64);
+      q += __shfl_xor(q, 4, 64);
+      const float inv = 1.f / sqrtf(q / 128.f + a.eps);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[2 * e] = (x[2 * e] * inv) * bf16_bits_to_float(w0[e] & 0xffffu);
+        x[2 * e + 1] = (x[2 * e + 1] * inv) * bf16_bits_to_float(w0[e] >> 16);
+        y[2 * e] = (y[2 * e] * inv) * bf16_bits_to_float(w1[e] & 0xffffu);
+        y[2 * e + 1] = (y[2 * e + 1] * inv) * bf16_bits_to_float(w1[e] >> 16);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float cs = e < 4 ? c0[e] : c1[e - 4], sn = e < 4 ? s0[e] : s1[e - 4];
+      const float r0 = x[e] * cs - y[e] * sn;
+      const float r1 = y[e] * cs + x[e] * sn;
+      x[e] = r0;
+      y[e] = r1;
+    }
+  }
+  T hx[8], hy[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    hx[e] = cvt_to<T>(x[e]);
+    hy[e] = cvt_to<T>(y[e]);
+  }
+  if (is_q) {
+    if (m < rows) {
+      T* qo = (T*)a.q_out + ((int64_t)(mrow0 + m) * Hq + head) * 128 + 8 * c;
+      *(u32x4*)qo = __builtin_bit_cast(u32x4, hx);
+      *(u32x4*)(qo + 64) = __builtin_bit_cast(u32x4, hy);
+    }
+    return;
+  }
+  const int kvh = is_k ? head - Hq : head - Hq - Hkv;
+  if (is_k) {
+    if (m < rows) {
+      // K[kk][hd] at ((hd/16*2 + (hd/8)&1)*32 + kk)*8 + hd%8: dims 8c.. are chunk c
+      T* tile = (T*)a.kv_layer + (int64_t)kvh * a.kv_head_stride + (int64_t)(pos >> 5) * 8192;
+      const int kk = pos & 31;
+      *(u32x4*)(tile + (c * 32 + kk) * 8) = __builtin_bit_cast(u32x4, hx);
+      *(u32x4*)(tile + ((8 + c) * 32 + kk) * 8) = __builtin_bit_cast(u32x4, hy);
+    }
+    return;
+  }
+  // V[kk][hd] at 4096 + ((((hd/32)*2 + kk/16)*2 + h)*32 + hd%32)*8 + j with
+  // q = kk%16, h = (q/4)&1, j = q%4 + 4*(q/8)
+  auto v_off = [](int hd, int kk) {
+    const int q16 = kk & 15;
+    return 4096 + ((((hd >> 5) * 2 + (kk >> 4)) * 2 + ((q16 >> 2) & 1)) * 32 + (hd & 31)) * 8 +
+           (q16 & 3) + 4 * (q16 >> 3);
+  };
+  T* tile = (T*)a.kv_layer + (int64_t)kvh * a.kv_head_stride + (int64_t)(pos0 >> 5) * 8192;
+  if (rows == 32 && (pos0 & 31) == 0) {
+    T* vs = (T*)lds_v;  // the V half of the tile, [4096]
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      vs[v_off(8 * c + e, m) - 4096] = hx[e];
+      vs[v_off(64 + 8 * c + e, m) - 4096] = hy[e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int ch = threadIdx.x + 256 * i;  // 16-byte chunk of the 8 KiB half
+      *(u32x4*)(tile + 4096 + ch * 8) = *(const u32x4*)(vs + ch * 8);
+    }
+  } else if (m < rows) {
+    T* vt = (T*)a.kv_layer + (int64_t)kvh * a.kv_head_stride + (int64_t)(pos >> 5) * 8192;
+    const int kk = pos & 31;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      vt[v_off(8 * c + e, kk)] = hx[e];
+      vt[v_off(64 + 8 * c + e, kk)] = hy[e];
+    }
+  }
+  (void)tile;
+}
+
 }  // namespace

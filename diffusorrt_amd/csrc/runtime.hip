@@ -130,6 +130,10 @@ struct Runtime {
   // (zeroed once; every kernel leaves them zero) and the residual stream's
   // per-32-column partial sums of squares
   DevBuf sk_part, sk_counters, sk_ss;
+  // large-M (> 32 rows) q4 forwards: the down projection's input activation and
+  // the split-K partial slices of o_proj / down_proj
+  DevBuf act2, big_part;
+  size_t big_part_floats = 0;
   size_t sk_part_floats = 0;
   int sk_n_counters = 0;
   int n_xcc = 1;
@@ -411,6 +415,19 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
     rt->sk_counters.alloc((size_t)std::max(nc, 1) * 4);
     DRT_HIP(hipMemsetAsync(rt->sk_counters.p, 0, rt->sk_counters.bytes, s));
     rt->sk_ss.alloc((size_t)d * 4);  // [d/32][32]
+    if (rt->q4 && M > 32) {
+      rt->act2.alloc((size_t)M * widest * 2);
+      size_t bf = 0;
+      const int n_qkv = (Hq + 2 * Hkv) * hd;
+      for (int mt = 1; mt <= (M + 127) / 128; ++mt) {
+        const int rows = std::min(M, mt * 128);
+        for (int K2 : {Hq * hd, F})
+          bf = std::max(bf, (size_t)big_linear_splits(rows, d, K2, BG_RESID_MAX_KS) * rows * d);
+        bf = std::max(bf, (size_t)big_linear_splits(rows, n_qkv, d, BG_QKV_MAX_KS) * rows * n_qkv);
+      }
+      rt->big_part_floats = bf;
+      rt->big_part.alloc(bf * 4);
+    }
     int nx = 1;
     if (hipDeviceGetAttribute(&nx, hipDeviceAttributeNumberOfXccs, rt->device) != hipSuccess)
       nx = 1;
@@ -568,8 +585,26 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
   // <= 32-row forwards use the split-K linears, which carry the RMSNorm row
   // statistics from each residual update to the next norm
   float* ss = M <= 32 ? rt.sk_ss.as<float>() : nullptr;
+  // > 32-row q4 forwards use the large-M kernels: each linear reads an ACT_F16P
+  // activation, the RMSNorms run as their own passes, fused with the split-K
+  // reduce and residual add of the projection before them
+  const bool big = rt.q4 && M > 32;
+  float* bpart = big ? rt.big_part.as<float>() : nullptr;
   embed(p.tokens_rel, rt.embed.as<uint16_t>(), hidden, M, d, ss, s);
   const int L = (int)rt.layers.size();
+  if (big && L > 0)
+    residual_norm(hidden, nullptr, 0, M, false, nullptr, false,
+                  rt.layers[0].in_norm.as<uint16_t>(), eps, d, ACT_F16P, rt.act.p, xs, M, s);
+  // split-K projection (o_proj / down_proj) into partial slices, then
+  // hidden += sum of the slices and the next norm's activation
+  auto big_resid = [&](FusedArgs f, const uint16_t* next_norm) {
+    const int ks = big_linear_splits(M, f.N, f.K, BG_RESID_MAX_KS);
+    require((size_t)ks * M * f.N <= rt.big_part_floats, "large-M partials exceed the workspace");
+    f.y = bpart;
+    big_linear(f, FL_STORE, ks, s);
+    residual_norm(hidden, bpart, ks, M, false, nullptr, true, next_norm, eps, d, ACT_F16P,
+                  rt.act.p, xs, M, s);
+  };
   for (int l = 0; l < L; ++l) {
     LayerW& w = rt.layers[l];
     auto base = [&](const LinearW& lw) {
@@ -607,7 +642,12 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
       f.Hkv = Hkv;
       f.kv_bf16 = rt.kv_bf16;
       f.ss_in = ss;
-      fused_linear(f, FL_QKV, s);
+      if (big) {
+        f.act = rt.act.p;
+        big_qkv(f, bpart, rt.big_part_floats, s);
+      } else {
+        fused_linear(f, FL_QKV, s);
+      }
     }
     if (decode_attn)
       attention_decode(rt.kv_bf16, rt.qbuf.p, kv_layer(l), head_stride, M, Hq, Hkv, a.n_keys, desc,
@@ -618,6 +658,20 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
                 fmt, s);
     const bool last = l == L - 1;
     if (last && a.n_lm == 0) break;  // commit-only forward: every layer's K/V is written
+    if (big) {
+      FusedArgs fo = base(w.o);
+      fo.act = rt.act.p;
+      big_resid(fo, w.post_norm.as<uint16_t>());  // act = post-attention norm
+      FusedArgs fg = base(w.gu);
+      fg.act = rt.act.p;
+      fg.act_out = rt.act2.p;
+      fg.act_fmt = ACT_F16P;
+      big_linear(fg, FL_SWIGLU, 1, s);
+      FusedArgs fd = base(w.down);
+      fd.act = rt.act2.p;
+      big_resid(fd, last ? nullptr : rt.layers[l + 1].in_norm.as<uint16_t>());
+      continue;
+    }
     {  // o_proj + residual
       FusedArgs f = base(w.o);
       f.act = rt.act.p;

@@ -46,8 +46,16 @@ def test_q4_linear_config3(m, n, k):
     W = O.Q4Weight(q.w_q.numpy().view(np.uint32), q.scales.float().numpy(),
                    q.biases.float().numpy())
     xf = x.float().numpy()
-    # what the kernel multiplies: fp16 activations, exact integer nibbles
-    ref16 = O.q4_linear64(xf.astype(np.float16).astype(np.float64), W)
+    x16 = xf.astype(np.float16).astype(np.float64)
+    if m <= 32:
+        # what the weight-streaming kernels multiply: fp16 activations, exact
+        # integer nibbles (scale and bias applied in fp32)
+        ref16 = O.q4_linear64(x16, W)
+    else:
+        # the large-M kernels dequantize each weight once to fp16: s * q + b with
+        # a single rounding (exact products and sum in float64, then fp16)
+        w16 = O.q4_dequant(W.w_q, W.scales, W.biases, dtype=np.float64).astype(np.float16)
+        ref16 = x16 @ w16.astype(np.float64).T
     scale = np.abs(ref16).max()
     err16 = np.abs(y - ref16).max() / scale
     # the reference's semantics: fp32 activation into mx.quantized_matmul
@@ -55,7 +63,34 @@ def test_q4_linear_config3(m, n, k):
     err = np.abs(y - ref).max() / np.abs(ref).max()
     _say(f"  err_vs_fp16_input={err16:.2e} err_vs_reference={err:.2e}")
     assert err16 < 2e-5  # fp32 accumulation only
-    assert err < 2e-3    # bf16 inputs are exact in fp16, so this is accumulation too
+    # bf16 inputs are exact in fp16: accumulation (and for m > 32 the fp16 weights)
+    assert err < 2e-3
+
+
+def test_q4_linear_large_m_ragged_with_bias():
+    """The large-M kernels on ragged shapes: 200 rows (a partial 128-row tile),
+    352 columns (a partial 256-column tile, 11 n-tiles) and 3 groups of 64 k,
+    with a bias, against fp16-dequantized weights in float64."""
+    from diffusorrt_amd import kernels
+
+    m, n, k = 200, 352, 192
+    _say("q4_linear large-M ragged", m, n, k)
+    # independent biases (centred ones, b = -8s, make s * q + b exact in fp16)
+    gen, q = _q4_case(n, k, seed=8, centred=False)
+    x = torch.randn((m, k), generator=gen)
+    bias = (torch.randn(n, generator=gen) * 0.1).to(torch.bfloat16)
+    w = kernels.DeviceQ4Weight(q.w_q.cuda(), q.scales.cuda(), q.biases.cuda())
+    y = kernels.linear(x.cuda(), w, bias.cuda()).cpu().numpy().astype(np.float64)
+    W = O.Q4Weight(q.w_q.numpy().view(np.uint32), q.scales.float().numpy(),
+                   q.biases.float().numpy())
+    w16 = O.q4_dequant(W.w_q, W.scales, W.biases, dtype=np.float64).astype(np.float16)
+    x16 = x.numpy().astype(np.float16).astype(np.float64)
+    ref = x16 @ w16.astype(np.float64).T + bias.float().numpy()
+    assert np.abs(y - ref).max() / np.abs(ref).max() < 2e-5
+    # the bound separates fp16-rounded weights from exact ones: a kernel that
+    # skipped or misplaced the rounding would not pass it
+    exact = O.q4_linear64(x16, W) + bias.float().numpy()
+    assert np.abs(exact - ref).max() / np.abs(ref).max() > 2e-5
 
 
 def test_q4_linear_fp32_input_and_bias():
