@@ -259,6 +259,26 @@ __global__ __launch_bounds__(256) void big_qkv_epilogue_kernel(const FusedArgs a
   qkv_epilogue<T>(a, head, mp, row0 + mp, rows, get, vbuf);
 }
 
+// y = sum of the KS slices (slice order) + bias, 4 floats per thread.
+__global__ __launch_bounds__(256) void sum_slices_kernel(const float* __restrict__ part, int KS,
+                                                         int64_t n, const uint16_t* __restrict__ bias,
+                                                         int N, float* __restrict__ y) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= n) return;
+  f32x4 v[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) v[k] = *(const f32x4*)(part + (int64_t)min(k, KS - 1) * n + i);
+  f32x4 sum = v[0];
+#pragma unroll
+  for (int k = 1; k < 8; ++k)
+    if (k < KS) sum += v[k];
+  if (bias) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sum[e] += bf16_bits_to_float(bias[(i + e) % N]);
+  }
+  *(f32x4*)(y + i) = sum;
+}
+
 template __global__ void big_qkv_epilogue_kernel<_Float16>(const FusedArgs, const float*, int);
 template __global__ void big_qkv_epilogue_kernel<__bf16>(const FusedArgs, const float*, int);
 
@@ -300,6 +320,15 @@ void big_linear(const FusedArgs& a, int kind, int KS, hipStream_t s) {
   else if (kind == FL_SWIGLU) DRT_BG(EPI_SWIGLU)
   else DRT_BG(EPI_STORE)
 #undef DRT_BG
+  DRT_HIP(hipGetLastError());
+}
+
+void sum_slices(const float* part, int KS, int64_t n, const uint16_t* bias, int N, float* y,
+                hipStream_t s) {
+  require(KS >= 1 && KS <= 8 && n % 4 == 0 && N % 4 == 0, "sum_slices: 1..8 slices of n % 4 == 0");
+  const int64_t blocks = (n / 4 + 255) / 256;
+  hipLaunchKernelGGL(sum_slices_kernel, dim3((unsigned)blocks), dim3(256), 0, s, part, KS, n,
+                     bias, N, y);
   DRT_HIP(hipGetLastError());
 }
 

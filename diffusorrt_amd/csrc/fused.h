@@ -75,4 +75,8 @@ void big_linear(const FusedArgs& a, int kind, int KS, hipStream_t s);
 void big_qkv(const FusedArgs& a, float* part, size_t part_floats, hipStream_t s);
 constexpr int BG_QKV_MAX_KS = 4;    // split-K slices of the q|k|v projection
 constexpr int BG_RESID_MAX_KS = 8;  // ... of o_proj / down_proj (reduced with the next norm)
+constexpr int BG_OP_MAX_KS = 8;     // ... of the per-op linear (summed into its output)
+// y[i] = sum_k part[k * n + i] (+ bias[i % N]) in slice order (the per-op linear's reduce)
+void sum_slices(const float* part, int KS, int64_t n, const uint16_t* bias, int N, float* y,
+                hipStream_t s);
 }

@@ -1269,9 +1269,16 @@ int32_t drt_session_set_profiling(uint64_t session, int32_t enable) {
 
 // ------------------------------------------------------------------ per-op
 
+// fp16 activation + group sums, then (more than 32 rows) the split-K slices
+static size_t q4_op_act_bytes(int32_t m, int32_t k) {
+  return ((size_t)m * k * 2 + (size_t)m * (k / 64) * 4 + 255) / 256 * 256;
+}
+
 size_t drt_op_q4_linear_workspace_bytes(int32_t m, int32_t n, int32_t k) {
   if (m <= 0 || k <= 0) return 0;
-  return (size_t)m * k * 2 + (size_t)m * (k / 64) * 4 + 256;
+  size_t b = q4_op_act_bytes(m, k) + 256;
+  if (m > 32 && n > 0) b += (size_t)big_linear_splits(m, n, k, BG_OP_MAX_KS) * m * n * 4;
+  return b;
 }
 
 int32_t drt_op_q4_repack(const void* w_q, const void* scales, const void* biases, int32_t n,
@@ -1307,7 +1314,18 @@ int32_t drt_op_q4_linear(const void* qw, const void* sb, const void* x, int32_t 
     f.act = xp;
     f.act_xsum = xs;
     f.y = y;
-    fused_linear(f, FL_STORE, st);
+    const int ks = m > 32 ? big_linear_splits(m, n, k, BG_OP_MAX_KS) : 1;
+    if (ks > 1 && big_linear_supported(f, FL_STORE)) {
+      // split-K slices in the workspace, summed (+ bias) into y in a fixed order
+      float* part = (float*)(ws + q4_op_act_bytes(m, k));
+      FusedArgs g = f;
+      g.bias = nullptr;
+      g.y = part;
+      big_linear(g, FL_STORE, ks, st);
+      sum_slices(part, ks, (int64_t)m * n, (const uint16_t*)bias, n, y, st);
+    } else {
+      fused_linear(f, FL_STORE, st);
+    }
   });
 }
 

@@ -67,13 +67,15 @@ def test_q4_linear_config3(m, n, k):
     assert err < 2e-3
 
 
-def test_q4_linear_large_m_ragged_with_bias():
+@pytest.mark.parametrize("k", [192, 1024])
+def test_q4_linear_large_m_ragged_with_bias(k):
     """The large-M kernels on ragged shapes: 200 rows (a partial 128-row tile),
-    352 columns (a partial 256-column tile, 11 n-tiles) and 3 groups of 64 k,
-    with a bias, against fp16-dequantized weights in float64."""
+    352 columns (a partial 256-column tile, 11 n-tiles), with a bias, against
+    fp16-dequantized weights in float64. k = 192 (3 groups) runs one K slice with
+    the bias in the kernel; k = 1024 splits K and adds the bias in the slice sum."""
     from diffusorrt_amd import kernels
 
-    m, n, k = 200, 352, 192
+    m, n = 200, 352
     _say("q4_linear large-M ragged", m, n, k)
     # independent biases (centred ones, b = -8s, make s * q + b exact in fp16)
     gen, q = _q4_case(n, k, seed=8, centred=False)
