@@ -216,10 +216,14 @@ __global__ __launch_bounds__(64 * QW) void attn_split_kernel(
 }
 
 // Decode attention: rows of one mask segment (every key in [0, n_keys) is
-// visible to every row) with at most 32*QT query vectors per KV head.
+// visible to every row) with at most 32*QT query vectors per KV head. Two
+// kernels share the partial layout and the range combine: attn_decode_kernel
+// (below: K/V streamed into LDS by a producer wave) and attn_decode_reg_kernel
+// (this one: every wave loads its own tiles into registers; kept as the
+// DRT_ATTN_NO_DMA alternative).
 //
-// Grid (R ranges, Hkv), 4 waves per work-group, one work-group per CU (the
-// host keeps R * Hkv <= 256). Range r owns the tiles [n_tiles*r/R,
+// attn_decode_reg_kernel: grid (Hkv, R ranges), 4 waves per work-group, one
+// work-group per CU (the host keeps R * Hkv <= 256). Range r owns the tiles [n_tiles*r/R,
 // n_tiles*(r+1)/R) of its KV head; wave w takes tiles t0 + w, t0 + w + 4 and
 // t0 + w + 8 and issues all three tiles' K/V loads (nontemporal: the cache is
 // streamed once per layer) before anything else, so one memory latency covers
@@ -347,7 +351,7 @@ DRT_DEV void attend_group(const typename MfmaT<T>::vec (&kc)[NG][8],
 }
 
 template <typename T, int QT>
-__global__ __launch_bounds__(256) void attn_decode_kernel(
+__global__ __launch_bounds__(256) void attn_decode_reg_kernel(
     const T* __restrict__ q, const T* __restrict__ kv, int64_t kv_head_stride, int n_rows,
     int Hq, int Hkv, int n_keys_arg, const StepDesc* __restrict__ desc,
     float* __restrict__ o_part, float* __restrict__ ml_part, float scale) {
@@ -458,6 +462,246 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   // combine the four waves; unit e = threadIdx.x + 256*i has lane (e & 63) = lane
   // and query tile i / 4. A wave without keys holds O = 0 and weight 0 (its O is
   // finite: the cache tiles are zero-initialised and invisible keys get p = 0).
+  float wgt[QT][4];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    float mw[4], lw[4];
+    float mm = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      mw[w] = mrg[w * SLOT + SLOTS + (qt * 64 + lane) * 2];
+      lw[w] = mrg[w * SLOT + SLOTS + (qt * 64 + lane) * 2 + 1];
+      mm = fmaxf(mm, mw[w]);
+    }
+    float ll = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      wgt[qt][w] = mw[w] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw[w] - mm);
+      ll += wgt[qt][w] * lw[w];
+    }
+    if (wave == 0 && lane < 32) {
+      ml_part[(part * (QT * 32) + qt * 32 + lane) * 2] = mm;
+      ml_part[(part * (QT * 32) + qt * 32 + lane) * 2 + 1] = ll;
+    }
+  }
+  f32x4* op = (f32x4*)(o_part + part * SLOTS);
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = qt * 1024 + threadIdx.x + 256 * i;
+      f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < 4; ++w) v += wgt[qt][w] * ((const f32x4*)(mrg + w * SLOT))[e];
+      op[e] = v;
+    }
+  }
+}
+
+// attn_decode_kernel, the producer / consumer form (same grid, partial layout
+// and combine as attn_decode_reg_kernel). With every wave loading its own tiles
+// a wave cannot compute while its loads wait to issue (the memory system paces
+// them), so the compute started only once the range had nearly streamed.
+// Here five waves split the roles: wave 4 streams the range's 16 KiB K/V tiles
+// with direct-to-LDS loads (global_load_lds, no registers held) into a ring of
+// DECR_SLOTS tile slots, and after each s_waitcnt that proves a tile complete
+// writes the tile's number (+1) into the slot's ready flag; waves 0-3 take tiles
+// t = wave, wave + 4, ... as their flags appear, so the tiles are computed while
+// the rest of the range is still streaming, and release each slot (freed flag)
+// after reading it into registers. Every wait on a flag is bounded: a wait that
+// runs out sets *err (the host reports it) and the kernel still finishes.
+constexpr int DECR_SLOTS = 8;
+constexpr int DECR_SPIN = 1 << 22;
+// s_waitcnt immediates (gfx9: vmcnt bits 3:0 + 15:14, expcnt 6:4, lgkmcnt 11:8)
+constexpr int DECR_VM48 = 0xCF70, DECR_VM32 = 0x8F70, DECR_VM16 = 0x4F70, DECR_VM0 = 0x0F70;
+constexpr int DECR_LGKM0 = 0xC07F;
+// cache policy of the tile loads: nontemporal (the K/V stream is read once per
+// step; cached, it evicts the weights the linears find in the memory-side cache)
+constexpr int DECR_NT = 2;
+
+// s_waitcnt that the compiler may not move memory operations across
+template <int IMM> DRT_DEV void decr_waitcnt() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(IMM);
+  asm volatile("" ::: "memory");
+}
+
+// The flags are read and written with inline ds_read / ds_write: the compiler
+// would otherwise put an s_waitcnt vmcnt(0) before every LDS access that follows
+// a direct-to-LDS load (it cannot tell the flags from the tile slots), which
+// would make the producer wait for every tile in flight before each signal.
+DRT_DEV int decr_lds_read(const int* p) {
+  int v;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)"
+               : "=v"(v)
+               : "v"((uint32_t)(uintptr_t)p)
+               : "memory");
+  return v;
+}
+DRT_DEV void decr_lds_write(int* p, int v) {
+  asm volatile("ds_write_b32 %0, %1" : : "v"((uint32_t)(uintptr_t)p), "v"(v) : "memory");
+}
+
+// LDS accesses after the wait stay after it (compiler barrier; one wave's LDS
+// operations execute in order).
+DRT_DEV bool decr_wait(const int* flag, int want, int* err) {
+  bool ok = false;
+  for (int it = 0; it < DECR_SPIN && !ok; ++it) {
+    ok = decr_lds_read(flag) == want;
+    if (!ok) __builtin_amdgcn_s_sleep(1);
+  }
+  if (!ok && err && (threadIdx.x & 63) == 0) atomicOr(err, 2);
+  asm volatile("" ::: "memory");
+  return ok;
+}
+
+template <typename T, int QT>
+__global__ __launch_bounds__(320) void attn_decode_kernel(
+    const T* __restrict__ q, const T* __restrict__ kv, int64_t kv_head_stride, int n_rows,
+    int Hq, int Hkv, int n_keys_arg, const StepDesc* __restrict__ desc,
+    float* __restrict__ o_part, float* __restrict__ ml_part, float scale, int* err) {
+  typedef typename MfmaT<T>::vec vec;
+  constexpr int SLOTS = QT * 4096;
+  constexpr int SLOT = SLOTS + QT * 64 * 2;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int G = Hq / Hkv;
+  const int n_qv = n_rows * G;
+  const int R = gridDim.y, rg = blockIdx.y, kvh = blockIdx.x;
+  const int n_keys = desc ? desc->n_keys : n_keys_arg;
+  const float c = scale * 1.44269504088896340736f;
+  const int n_tiles = (n_keys + 31) >> 5;
+  const int t_begin = (int)((int64_t)n_tiles * rg / R);
+  const int t_end = (int)((int64_t)n_tiles * (rg + 1) / R);
+  const int n = t_end - t_begin;
+  const int64_t part = (int64_t)rg * Hkv + kvh;
+  extern __shared__ __align__(16) char smem[];
+  int* ready = (int*)smem;                               // [DECR_SLOTS]
+  int* freed = ready + DECR_SLOTS;                       // [DECR_SLOTS]
+  T* qs = (T*)(smem + 128);                              // [QT*32][DEC_QROW]
+  char* tiles = smem + 128 + QT * 32 * DEC_QROW * 2;     // [DECR_SLOTS][16 KiB]
+  float* mrg = (float*)(smem + 128);                     // [4][SLOT], over Q and the tiles
+
+  if (n <= 0) {
+    if (threadIdx.x < QT * 32) {
+      ml_part[(part * (QT * 32) + threadIdx.x) * 2] = -INFINITY;
+      ml_part[(part * (QT * 32) + threadIdx.x) * 2 + 1] = 0.f;
+    }
+    return;
+  }
+  const T* base = kv + (int64_t)kvh * kv_head_stride + (int64_t)t_begin * KV_TILE_ELEMS;
+  // tile t of the range into its slot: 16 wave-wide 1 KiB loads, LDS image = HBM image
+  auto dma_tile = [&](int t) {
+    const u32x4* src = (const u32x4*)(base + (int64_t)t * KV_TILE_ELEMS) + lane;
+    char* dst = tiles + (t % DECR_SLOTS) * 16384;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(src + i * 64),
+                                       (__attribute__((address_space(3))) void*)(dst + i * 1024),
+                                       16, 0, DECR_NT);
+  };
+  auto signal = [&](int t) {  // tile t's loads are complete
+    asm volatile("" ::: "memory");
+    decr_lds_write(&ready[t % DECR_SLOTS], t + 1);  // every lane writes the same value
+  };
+
+  constexpr int QCH = QT * 2;  // Q chunks per consumer thread
+  if (wave == 4) {
+    const int n0 = min(n, 4);
+    for (int t = 0; t < n0; ++t) dma_tile(t);
+  } else {
+    u32x4 qraw[QCH];
+#pragma unroll
+    for (int i = 0; i < QCH; ++i) {
+      const int ch = threadIdx.x + 256 * i;
+      const int qvc = min(ch >> 4, n_qv - 1);
+      const int row = qvc / G, head = kvh * G + (qvc - row * G);
+      qraw[i] = *(const u32x4*)(q + ((int64_t)row * Hq + head) * 128 + (ch & 15) * 8);
+    }
+    if (threadIdx.x < 2 * DECR_SLOTS) ready[threadIdx.x] = 0;  // ready and freed
+#pragma unroll
+    for (int i = 0; i < QCH; ++i) {
+      const int ch = threadIdx.x + 256 * i;
+      *(u32x4*)(qs + (ch >> 4) * DEC_QROW + (ch & 15) * 8) =
+          (ch >> 4) < n_qv ? qraw[i] : u32x4{0u, 0u, 0u, 0u};
+    }
+    decr_waitcnt<DECR_LGKM0>();  // Q and the flags are written
+  }
+  // Q in LDS, flags zero. A bare s_barrier: __syncthreads() would first wait for
+  // the producer's four tiles in flight.
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  float m_run[QT], l_run[QT];
+  f32x16 o[QT][4];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    m_run[qt] = -INFINITY;
+    l_run[qt] = 0.f;
+#pragma unroll
+    for (int hb = 0; hb < 4; ++hb) o[qt][hb] = f32x16{};
+  }
+  if (wave == 4) {
+    // the loads after tile t's are 16 per later tile: vmcnt(48) proves tile t - 3
+    if (n >= 4) {
+      decr_waitcnt<DECR_VM48>();
+      signal(0);
+    }
+    for (int t = 4; t < n; ++t) {
+      if (t >= DECR_SLOTS) decr_wait(&freed[t % DECR_SLOTS], t - DECR_SLOTS + 1, err);
+      dma_tile(t);
+      decr_waitcnt<DECR_VM48>();
+      signal(t - 3);
+    }
+    if (n >= 3) {
+      decr_waitcnt<DECR_VM32>();
+      signal(n - 3);
+    }
+    if (n >= 2) {
+      decr_waitcnt<DECR_VM16>();
+      signal(n - 2);
+    }
+    decr_waitcnt<DECR_VM0>();
+    signal(n - 1);
+  } else {
+    for (int t = wave; t < n; t += 4) {
+      decr_wait(&ready[t % DECR_SLOTS], t + 1, err);
+      const vec* tp = (const vec*)(tiles + (t % DECR_SLOTS) * 16384);
+      vec kc[1][8], vc[1][8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        kc[0][i] = tp[i * 64 + lane];
+        vc[0][i] = tp[512 + i * 64 + lane];
+      }
+      if (t + DECR_SLOTS < n) {  // the producer reuses the slot for tile t + 8
+        decr_waitcnt<DECR_LGKM0>();  // the slot's reads are complete
+        decr_lds_write(&freed[t % DECR_SLOTS], t + 1);
+      }
+      const int key0[1] = {(t_begin + t) * 32}, nk[1] = {n_keys};
+      attend_group<T, QT, 1>(kc, vc, qs, key0, nk, c, lane, m_run, l_run, o);
+    }
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) l_run[qt] += __shfl_xor(l_run[qt], 32, 64);
+  }
+  __syncthreads();  // every tile consumed: Q and the slots become the merge area
+  if (wave < 4) {
+    float* mine = mrg + wave * SLOT;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+      for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          ((f32x4*)mine)[((qt * 4 + hb) * 4 + r4) * 64 + lane] =
+              f32x4{o[qt][hb][4 * r4], o[qt][hb][4 * r4 + 1], o[qt][hb][4 * r4 + 2],
+                    o[qt][hb][4 * r4 + 3]};
+      mine[SLOTS + (qt * 64 + lane) * 2] = m_run[qt];
+      mine[SLOTS + (qt * 64 + lane) * 2 + 1] = l_run[qt];
+    }
+  }
+  __syncthreads();
+  if (wave >= 4) return;
   float wgt[QT][4];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
@@ -730,18 +974,32 @@ template __global__ void attn_split_kernel<__bf16, 2>(const __bf16*, const __bf1
 template __global__ void attn_split_kernel<__bf16, 4>(const __bf16*, const __bf16*, int64_t, int,
                                                       int, int, int, int, int, int, int, int,
                                                       float*, float*, float);
+template __global__ void attn_decode_reg_kernel<_Float16, 1>(const _Float16*, const _Float16*,
+                                                         int64_t, int, int, int, int,
+                                                         const StepDesc*, float*, float*, float);
+template __global__ void attn_decode_reg_kernel<_Float16, 2>(const _Float16*, const _Float16*,
+                                                         int64_t, int, int, int, int,
+                                                         const StepDesc*, float*, float*, float);
+template __global__ void attn_decode_reg_kernel<__bf16, 1>(const __bf16*, const __bf16*, int64_t, int,
+                                                       int, int, int, const StepDesc*, float*,
+                                                       float*, float);
+template __global__ void attn_decode_reg_kernel<__bf16, 2>(const __bf16*, const __bf16*, int64_t, int,
+                                                       int, int, int, const StepDesc*, float*,
+                                                       float*, float);
 template __global__ void attn_decode_kernel<_Float16, 1>(const _Float16*, const _Float16*,
-                                                         int64_t, int, int, int, int,
-                                                         const StepDesc*, float*, float*, float);
+                                                          int64_t, int, int, int, int,
+                                                          const StepDesc*, float*, float*, float,
+                                                          int*);
 template __global__ void attn_decode_kernel<_Float16, 2>(const _Float16*, const _Float16*,
-                                                         int64_t, int, int, int, int,
-                                                         const StepDesc*, float*, float*, float);
+                                                          int64_t, int, int, int, int,
+                                                          const StepDesc*, float*, float*, float,
+                                                          int*);
 template __global__ void attn_decode_kernel<__bf16, 1>(const __bf16*, const __bf16*, int64_t, int,
-                                                       int, int, int, const StepDesc*, float*,
-                                                       float*, float);
+                                                        int, int, int, const StepDesc*, float*,
+                                                        float*, float, int*);
 template __global__ void attn_decode_kernel<__bf16, 2>(const __bf16*, const __bf16*, int64_t, int,
-                                                       int, int, int, const StepDesc*, float*,
-                                                       float*, float);
+                                                        int, int, int, const StepDesc*, float*,
+                                                        float*, float, int*);
 template __global__ void kv_pack_kernel<_Float16>(const void*, const void*, int, int, int, int,
                                                   _Float16*, int64_t);
 template __global__ void kv_pack_kernel<__bf16>(const void*, const void*, int, int, int, int,
@@ -825,7 +1083,7 @@ int attention_decode_ranges(int n_keys, int Hkv) {
 // `part` holds attention_decode_part_bytes(ranges, Hkv, n_rows * Hq / Hkv).
 void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_stride,
                       int n_rows, int Hq, int Hkv, int n_keys, const StepDesc* desc, int ranges,
-                      float* part, void* out, float* xsum, int out_fmt, hipStream_t s) {
+                      float* part, void* out, float* xsum, int out_fmt, hipStream_t s, int* err) {
   const int G = Hq / Hkv;
   require(Hq % Hkv == 0 && n_rows * G <= 64, "decode attention needs <= 64 query vectors per head");
   require(ranges >= 1 && ranges <= 128, "decode attention takes 1..128 key ranges");
@@ -838,18 +1096,36 @@ void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv
   float* ml_part = part + (size_t)ranges * Hkv * qt * 4096;
 #define DRT_DEC(T, QT)                                                                      \
   {                                                                                         \
-    auto fn = attn_decode_kernel<T, QT>;                                                    \
+    auto fn = attn_decode_reg_kernel<T, QT>;                                                    \
     static size_t granted = 0;                                                              \
     grant_lds((const void*)fn, lds, granted);                                               \
     DRT_LAUNCH(Profiler::ATTN, bytes, fn, grid, dim3(256), lds, s, (const T*)q,             \
                (const T*)kv_layer, kv_head_stride, n_rows, Hq, Hkv, n_keys, desc, o_part,   \
                ml_part, scale);                                                             \
   }
-  if (bf16) {
+#define DRT_DECR(T, QT)                                                                     \
+  {                                                                                         \
+    auto fn = attn_decode_kernel<T, QT>;                                                   \
+    static size_t granted = 0;                                                              \
+    grant_lds((const void*)fn, ldsr, granted);                                              \
+    DRT_LAUNCH(Profiler::ATTN, bytes, fn, grid, dim3(320), ldsr, s, (const T*)q,            \
+               (const T*)kv_layer, kv_head_stride, n_rows, Hq, Hkv, n_keys, desc, o_part,   \
+               ml_part, scale, err);                                                        \
+  }
+  static const bool reg_tiles = getenv("DRT_ATTN_NO_DMA") != nullptr;
+  const size_t ldsr = 128 + (size_t)qt * 32 * DEC_QROW * 2 + (size_t)DECR_SLOTS * 16384;
+  if (!reg_tiles) {
+    if (bf16) {
+      if (qt == 1) DRT_DECR(__bf16, 1) else DRT_DECR(__bf16, 2)
+    } else {
+      if (qt == 1) DRT_DECR(_Float16, 1) else DRT_DECR(_Float16, 2)
+    }
+  } else if (bf16) {
     if (qt == 1) DRT_DEC(__bf16, 1) else DRT_DEC(__bf16, 2)
   } else {
     if (qt == 1) DRT_DEC(_Float16, 1) else DRT_DEC(_Float16, 2)
   }
+#undef DRT_DECR
 #undef DRT_DEC
   DRT_HIP(hipGetLastError());
   (void)xsum;  // the F16P output's consumer computes its own group sums

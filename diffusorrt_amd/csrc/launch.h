@@ -186,7 +186,8 @@ size_t attention_decode_part_bytes(int ranges, int Hkv, int n_qv);
 int attention_decode_ranges(int n_keys, int Hkv);
 void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_stride,
                       int n_rows, int Hq, int Hkv, int n_keys, const StepDesc* desc, int ranges,
-                      float* part, void* out, float* xsum, int out_fmt, hipStream_t s);
+                      float* part, void* out, float* xsum, int out_fmt, hipStream_t s,
+                      int* err = nullptr);
 void kv_pack(bool kv_bf16, const void* k, const void* v, bool src_bf16, int n, int Hkv, int pos0,
              void* kv_layer, int64_t kv_head_stride, hipStream_t s);
 

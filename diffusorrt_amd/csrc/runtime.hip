@@ -651,7 +651,7 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
     }
     if (decode_attn)
       attention_decode(rt.kv_bf16, rt.qbuf.p, kv_layer(l), head_stride, M, Hq, Hkv, a.n_keys, desc,
-                       ranges, o_part, rt.act.p, xs, fmt, s);
+                       ranges, o_part, rt.act.p, xs, fmt, s, rt.placement_err.as<int>());
     else
       attention(rt.kv_bf16, rt.qbuf.p, kv_layer(l), head_stride, M, Hq, Hkv, a.n_keys, a.row0,
                 a.mask_kind, a.mask_prompt_len, a.mask_block, ap, o_part, ml_part, rt.act.p, xs,
@@ -710,8 +710,15 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
 
 // The split-K linears rely on work-group i running on XCD i % n_xcc; a kernel
 // that observed otherwise left a flag (read back with the forward's results).
+// Bit 2 of the same flag: a wave of the decode attention gave up waiting for a K/V
+// tile (its bounded wait ran out), so that forward's attention is not valid.
 void check_placement(const Runtime& rt) {
-  if (*rt.placement_host != 0)
+  const int e = *rt.placement_host;
+  if (e & 2)
+    fail(INTERNAL_ERROR,
+         "decode attention: a bounded wait for a K/V tile expired; results of this runtime "
+         "are not valid");
+  if (e != 0)
     fail(INTERNAL_ERROR,
          "a split-K linear ran on an unexpected XCD (work-group placement is not the "
          "round-robin the kernels assume); results of this runtime are not valid");
