@@ -209,8 +209,9 @@ __global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int K
         if (head * 128 >= N) break;  // uniform
         if (hl) __syncthreads();     // the V tile buffer of head 0 has been copied out
         auto get = [&](int m, int d) { return e[m * BG_EROW + hl * 128 + d]; };
-        if (a.kv_bf16) qkv_epilogue<__bf16>(a, head, mp, row0 + mp, rows, get, vbuf);
-        else qkv_epilogue<_Float16>(a, head, mp, row0 + mp, rows, get, vbuf);
+        const QkvTables qt = qkv_tables(a, head, row0 + mp, rows);
+        if (a.kv_bf16) qkv_epilogue<__bf16>(a, qt, head, mp, row0 + mp, rows, get, vbuf);
+        else qkv_epilogue<_Float16>(a, qt, head, mp, row0 + mp, rows, get, vbuf);
       }
     }
     __syncthreads();  // the piece's LDS is read before the next piece is written
@@ -237,6 +238,7 @@ __global__ __launch_bounds__(256) void big_qkv_epilogue_kernel(const FusedArgs a
   const int row0 = a.desc ? a.desc->row0 : 0;
   // 32 rows x 32 float4 per slice: thread t takes rows t >> 5 + 8j, float4 t & 31
   constexpr int KMAX = drt::BG_QKV_MAX_KS;
+  const QkvTables qt = qkv_tables(a, head, row0 + mp, rows);
   f32x4 v[KMAX][4];
 #pragma unroll
   for (int k = 0; k < KMAX; ++k)
@@ -256,7 +258,7 @@ __global__ __launch_bounds__(256) void big_qkv_epilogue_kernel(const FusedArgs a
   }
   __syncthreads();
   auto get = [&](int m, int d) { return tile[m][d]; };
-  qkv_epilogue<T>(a, head, mp, row0 + mp, rows, get, vbuf);
+  qkv_epilogue<T>(a, qt, head, mp, row0 + mp, rows, get, vbuf);
 }
 
 // y = sum of the KS slices (slice order) + bias, 4 floats per thread.

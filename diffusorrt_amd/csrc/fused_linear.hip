@@ -178,7 +178,8 @@ __global__ __launch_bounds__(64 * WN * WK) void fused_linear_kernel(const FusedA
         const int u = ub + p;
         if (u < u_hi) {
           if (WKIND == W_Q4) {
-            q4_group_mma1_lane(acc, af[p], wq[p], wsb[p], lane);
+            // (the LDS staging area is unused on this path: 32 floats per wave)
+            q4_group_mma1_lane(acc, af[p], wq[p], wsb[p], lane, (float*)smem + (threadIdx.x >> 6) * 32);
           } else {
             acc = mfma_bf16(ab[p], wbf[p], acc);
           }

@@ -24,36 +24,61 @@ DRT_DEV void q4_group_mma1(f32x16& acc, const f16x8 (&a)[4], const float (&xsr)[
   for (int r = 0; r < 16; ++r) acc[r] = fmaf(s, c[r], fmaf(bp, xsr[r], acc[r]));
 }
 
-// Same as q4_group_mma1 with the group sum of each row computed here from the
-// A fragments (lane l holds 32 of the 64 values of row l & 31; the two halves
-// are added by one shuffle) and fetched by shuffle as the rows are consumed.
+// v[l] + v[l ^ 32] on every lane (gfx950 v_permlane32_swap, no LDS trip); both
+// lanes of a pair add the same two operands in the same order.
+DRT_DEV float sum_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// The 16 row sums a lane needs in accumulator order (rows 8j + 4(lane >> 5) + i
+// for r = 4j + i) from a [32] array of row sums in LDS: four 16-byte reads.
+DRT_DEV void load_row_sums(const float* rs, int lane, float (&xsr)[16]) {
+  const f32x4* p = (const f32x4*)rs + (lane >> 5);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const f32x4 v = p[2 * j];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xsr[4 * j + i] = v[i];
+  }
+}
+
+// Group sums of the A fragments of UW units (lane l holds 32 of the 64 values
+// of row l & 31 for each unit): the lane's half-sums, the two halves added
+// across lanes, staged through this wave's LDS scratch (UW x 32 floats) and
+// read back in accumulator order. The wave's LDS operations run in order, so
+// no barrier is needed; the scratch may be rewritten by the next call.
+template <int UW>
+DRT_DEV void row_sums_lane(const u32x4 (&a)[UW][4], float* scratch, int lane,
+                           float (&xsr)[UW][16]) {
+#pragma unroll
+  for (int i = 0; i < UW; ++i) {
+    float v = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const f16x8 h = __builtin_bit_cast(f16x8, a[i][t]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v += (float)h[e];
+    }
+    v = sum_xor32(v);
+    if (lane < 32) scratch[i * 32 + lane] = v;
+  }
+#pragma unroll
+  for (int i = 0; i < UW; ++i) load_row_sums(scratch + i * 32, lane, xsr[i]);
+}
+
+// q4_group_mma1 for one unit whose A fragments came straight from global
+// memory (row sums through this wave's LDS scratch of 32 floats).
 DRT_DEV void q4_group_mma1_lane(f32x16& acc, const u32x4 (&a)[4], const u32x4 w,
-                                const uint32_t sbv, int lane) {
-  float xs_lane = 0.f;
+                                const uint32_t sbv, int lane, float* scratch) {
+  const u32x4(&a1)[1][4] = reinterpret_cast<const u32x4(&)[1][4]>(a);
+  float xsr[1][16];
+  row_sums_lane<1>(a1, scratch, lane, xsr);
+  f16x8 ah[4];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const f16x8 h = __builtin_bit_cast(f16x8, a[t]);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) xs_lane += (float)h[e];
-  }
-  xs_lane += __shfl_xor(xs_lane, 32, 64);
-  f32x16 c = f32x16{};
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const uint32_t wt = w[t];
-    u32x4 bw;
-    bw[0] = (wt & 0x000F000Fu) | 0x64006400u;
-    bw[1] = ((wt >> 4) & 0x000F000Fu) | 0x64006400u;
-    bw[2] = ((wt >> 8) & 0x000F000Fu) | 0x64006400u;
-    bw[3] = ((wt >> 12) & 0x000F000Fu) | 0x64006400u;
-    c = mfma_f16(__builtin_bit_cast(f16x8, a[t]), __builtin_bit_cast(f16x8, bw), c);
-  }
-  const float s = bf16_bits_to_float(sbv & 0xffffu);
-  const float b = bf16_bits_to_float(sbv >> 16);
-  const float bp = fmaf(-1024.f, s, b);
-#pragma unroll
-  for (int r = 0; r < 16; ++r)
-    acc[r] = fmaf(s, c[r], fmaf(bp, __shfl(xs_lane, mfma_row(r, lane), 64), acc[r]));
+  for (int t = 0; t < 4; ++t) ah[t] = __builtin_bit_cast(f16x8, a[t]);
+  q4_group_mma1(acc, ah, xsr[0], w, sbv);
 }
 
 template <typename T> DRT_DEV T cvt_to(float f);
@@ -120,14 +145,54 @@ DRT_DEV void qkv_head_store(const FusedArgs& a, int head, int m, int pos, float 
 //   pos0 : absolute position of local row 0
 //   rows : valid local rows (<= 32)
 //   get(m, d): the linear's output (before bias) of local row m, head dim d
+// The per-thread inputs of qkv_epilogue besides the linear's output: bias, q/k
+// norm weights and the rotary angles of the thread's row and dims. Loaded by
+// every thread without branches (absent tables read a valid stand-in and are
+// not used), so a caller can issue them together with its last loads and the
+// epilogue waits for no further memory round trip.
+struct QkvTables {
+  f32x4 c0, c1, s0, s1;  // cos / sin of angles 8c .. 8c+7
+  u32x4 w0, w1;          // norm weights of dims 8c.., 64+8c.. (bf16 pairs)
+  u32x4 b0, b1;          // bias of the same dims (bf16 pairs)
+};
+DRT_DEV QkvTables qkv_tables(const FusedArgs& a, int head, int pos0, int rows) {
+  const int m = threadIdx.x >> 3, c = threadIdx.x & 7;
+  const int pos_t = m < rows ? pos0 + m : pos0;  // rows past the end read a valid table row
+  QkvTables t;
+  // rotary tables: cos/sin [pos][64] fp32, angle i shared by dims i and i + 64
+  const f32x4* cp = (const f32x4*)(a.rope_cos + (int64_t)pos_t * 64 + 8 * c);
+  const f32x4* sp = (const f32x4*)(a.rope_sin + (int64_t)pos_t * 64 + 8 * c);
+  t.c0 = cp[0];
+  t.c1 = cp[1];
+  t.s0 = sp[0];
+  t.s1 = sp[1];
+  const uint16_t* stand_in = (const uint16_t*)a.rope_cos;  // >= 64 floats
+  const uint16_t* nw = head < a.Hq ? a.q_norm : a.k_norm;
+  nw = nw ? nw : stand_in;
+  t.w0 = *(const u32x4*)(nw + 8 * c);
+  t.w1 = *(const u32x4*)(nw + 64 + 8 * c);
+  const uint16_t* bias = a.bias ? a.bias + head * 128 : stand_in;
+  t.b0 = *(const u32x4*)(bias + 8 * c);
+  t.b1 = *(const u32x4*)(bias + 64 + 8 * c);
+  return t;
+}
+
+// Sum over the 8 lanes of an aligned 8-lane group, with DPP moves (no LDS):
+// two quad swaps, then the half-row mirror pairs quad 0 with quad 1.
+DRT_DEV float sum8_dpp(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  return v;
+}
+
 template <typename T, typename Get>
-DRT_DEV void qkv_epilogue(const FusedArgs& a, int head, int mrow0, int pos0, int rows, Get get,
-                          uint16_t* lds_v) {
+DRT_DEV void qkv_epilogue(const FusedArgs& a, const QkvTables& t, int head, int mrow0, int pos0,
+                          int rows, Get get, uint16_t* lds_v) {
   const int Hq = a.Hq, Hkv = a.Hkv;
   const int m = threadIdx.x >> 3, c = threadIdx.x & 7;
   const bool is_q = head < Hq, is_k = !is_q && head < Hq + Hkv, is_v = !is_q && !is_k;
   const int pos = pos0 + m;
-  const int pos_t = m < rows ? pos : pos0;  // rows past the end read a valid table row
   float x[8], y[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -135,30 +200,22 @@ DRT_DEV void qkv_epilogue(const FusedArgs& a, int head, int mrow0, int pos0, int
     y[e] = get(m, 64 + 8 * c + e);
   }
   if (a.bias) {
-    const u32x4 b0 = *(const u32x4*)(a.bias + head * 128 + 8 * c);
-    const u32x4 b1 = *(const u32x4*)(a.bias + head * 128 + 64 + 8 * c);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      x[2 * e] += bf16_bits_to_float(b0[e] & 0xffffu);
-      x[2 * e + 1] += bf16_bits_to_float(b0[e] >> 16);
-      y[2 * e] += bf16_bits_to_float(b1[e] & 0xffffu);
-      y[2 * e + 1] += bf16_bits_to_float(b1[e] >> 16);
+      x[2 * e] += bf16_bits_to_float(t.b0[e] & 0xffffu);
+      x[2 * e + 1] += bf16_bits_to_float(t.b0[e] >> 16);
+      y[2 * e] += bf16_bits_to_float(t.b1[e] & 0xffffu);
+      y[2 * e + 1] += bf16_bits_to_float(t.b1[e] >> 16);
     }
   }
   if (!is_v) {
-    const uint16_t* nw = is_q ? a.q_norm : a.k_norm;
-    // rotary tables: cos/sin [pos][64] fp32, angle i shared by dims i and i + 64
-    const f32x4* cp = (const f32x4*)(a.rope_cos + (int64_t)pos_t * 64 + 8 * c);
-    const f32x4* sp = (const f32x4*)(a.rope_sin + (int64_t)pos_t * 64 + 8 * c);
-    const f32x4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
-    if (nw) {
-      const u32x4 w0 = *(const u32x4*)(nw + 8 * c), w1 = *(const u32x4*)(nw + 64 + 8 * c);
+    const f32x4 c0 = t.c0, c1 = t.c1, s0 = t.s0, s1 = t.s1;
+    if (is_q ? a.q_norm : a.k_norm) {
+      const u32x4 w0 = t.w0, w1 = t.w1;
       float q = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) q += x[e] * x[e] + y[e] * y[e];
-      q += __shfl_xor(q, 1, 64);
-      q += __shfl_xor(q, 2, 64);
-      q += __shfl_xor(q, 4, 64);
+      q = sum8_dpp(q);
       const float inv = 1.f / sqrtf(q / 128.f + a.eps);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {

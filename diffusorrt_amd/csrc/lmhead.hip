@@ -117,8 +117,8 @@ __global__ __launch_bounds__(64 * WAVES) void lmhead_kernel(
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
           const int g = gbase + min(p, ng - 1);
-          wbuf[p][j] = *q4_tile_words(qw, nt0 + j, G, g, lane);
-          sbuf[p][j] = q4_tile_sb(sb, nt0 + j, G, g, lane);
+          wbuf[p][j] = __builtin_nontemporal_load(q4_tile_words(qw, nt0 + j, G, g, lane));
+          sbuf[p][j] = __builtin_nontemporal_load(&sb[((int64_t)(nt0 + j) * G + g) * 32 + (lane & 31)]);
         }
       for (int gb = 0; gb < ng; gb += P) {
 #pragma unroll
@@ -136,8 +136,9 @@ __global__ __launch_bounds__(64 * WAVES) void lmhead_kernel(
             if (gn < ng) {
 #pragma unroll
               for (int j = 0; j < NT; ++j) {
-                wbuf[p][j] = *q4_tile_words(qw, nt0 + j, G, gbase + gn, lane);
-                sbuf[p][j] = q4_tile_sb(sb, nt0 + j, G, gbase + gn, lane);
+                wbuf[p][j] = __builtin_nontemporal_load(q4_tile_words(qw, nt0 + j, G, gbase + gn, lane));
+                sbuf[p][j] = __builtin_nontemporal_load(
+                    &sb[((int64_t)(nt0 + j) * G + gbase + gn) * 32 + (lane & 31)]);
               }
             }
           }

@@ -75,6 +75,34 @@ DRT_DEV bool last_to_arrive(int* counter, int arrivals, int* flag) {
   return *flag != 0;
 }
 
+// The last work-group's sum of the KS <= KSC partial tiles of a wide block into
+// the [4][32][33] LDS tile: 1024 16-byte chunks, 4 per thread; every slice's
+// chunks are loaded before any is added (then added in slice order), and the
+// caller's further loads (after()) are issued behind them. Slices past KS reload
+// the last one and are added times 0: a load under a branch makes the compiler
+// wait for it, and for everything issued before it, inside the branch.
+template <int KSC, typename After>
+DRT_DEV void sk_wide_sum_slices(const float* pbase, int KS, float* red, After after) {
+  f32x4 pv[KSC][4];
+#pragma unroll
+  for (int k2 = 0; k2 < KSC; ++k2)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      pv[k2][i] = *(const f32x4*)(pbase + (size_t)min(k2, KS - 1) * 4096 + 4 * (threadIdx.x + 256 * i));
+  after();
+  __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the first wait
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k2 = 0; k2 < KSC; ++k2) sum += pv[k2][i] * (k2 < KS ? 1.f : 0.f);
+    const int q = threadIdx.x + 256 * i, tn = q >> 8, c4 = q & 255;
+    const int ln = c4 & 63, col = ln & 31, r0 = 8 * (c4 >> 6) + 4 * (ln >> 5);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) red[(tn * 32 + r0 + e) * 33 + col] = sum[e];
+  }
+}
+
 }  // namespace
 
 template <int EPI, int U>
@@ -104,7 +132,11 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
     wq[u] = *q4_tile_words(a.qw, nt, G, u0 + u, lane);
     wsb[u] = q4_tile_sb(a.sb, nt, G, u0 + u, lane);
   }
-  // 2. the hidden slice (8-wide items: U per thread) and the matching norm weights
+  // 2. the hidden slice (8-wide items: U per thread) and the matching norm weights.
+  // Every load of steps 1-3 is unconditional (rows past M read row M - 1 and are
+  // zeroed by their norm factor, partial sums past the last are clamped and
+  // masked after the wait): a load under a branch makes the compiler wait for it
+  // inside the branch, i.e. for every load issued before it.
   f32x4 hv[U][2];
   u32x4 nw[U];
 #pragma unroll
@@ -112,14 +144,9 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
     const int it = threadIdx.x + 256 * j;
     const int r = it / (8 * U), c8 = it - r * (8 * U);
     const int k = kc0 + c8 * 8;
-    if (r < M) {
-      const f32x4* src = (const f32x4*)(a.hidden + (int64_t)r * K + k);
-      hv[j][0] = src[0];
-      hv[j][1] = src[1];
-    } else {
-      hv[j][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-      hv[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    const f32x4* src = (const f32x4*)(a.hidden + (int64_t)min(r, M - 1) * K + k);
+    hv[j][0] = src[0];
+    hv[j][1] = src[1];
     nw[j] = *(const u32x4*)(a.norm_w + k);
   }
   // 3. row statistics from the producer's partial sums of squares: thread
@@ -130,15 +157,11 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
     const int r = threadIdx.x & 31, g8 = threadIdx.x >> 5;
     float sv[SK_SS_PER_THREAD];
 #pragma unroll
-    for (int e = 0; e < SK_SS_PER_THREAD; ++e) {
-      const int p = g8 + 8 * e;
-      sv[e] = 0.f;
-      if (8 * e < np)  // wave-uniform: only the rounds that exist are issued
-        sv[e] = p < np ? a.ss_in[p * 32 + r] : 0.f;
-    }
+    for (int e = 0; e < SK_SS_PER_THREAD; ++e) sv[e] = a.ss_in[min(g8 + 8 * e, np - 1) * 32 + r];
     float q = 0.f;
 #pragma unroll
-    for (int e = 0; e < SK_SS_PER_THREAD; ++e) q += sv[e];
+    for (int e = 0; e < SK_SS_PER_THREAD; ++e)  // a product, not a select, so that
+      q += sv[e] * (g8 + 8 * e < np ? 1.f : 0.f);  // the load is not sunk into a branch
     red[g8 * 32 + r] = q;
   }
   __syncthreads();
@@ -154,7 +177,7 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
   for (int j = 0; j < U; ++j) {
     const int it = threadIdx.x + 256 * j;
     const int r = it / (8 * U), c8 = it - r * (8 * U);
-    const float inv = rinv[r];
+    const float inv = r < M ? rinv[r] : 0.f;
     float x[8];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -172,10 +195,7 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
     float gs = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) gs += (float)h[e];
-    // a 64-k group is 8 consecutive items of one row = 8 consecutive lanes
-    gs += __shfl_xor(gs, 1, 64);
-    gs += __shfl_xor(gs, 2, 64);
-    gs += __shfl_xor(gs, 4, 64);
+    gs = sum8_dpp(gs);  // a 64-k group is 8 consecutive items of one row = 8 lanes
     if ((c8 & 7) == 0) xss[(c8 >> 3) * 32 + r] = gs;
   }
   __syncthreads();
@@ -188,11 +208,13 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
 #pragma unroll
     for (int t = 0; t < 4; ++t) af[t] = *(const f16x8*)(arow + 8 * t);
     float xsr[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) xsr[r] = xss[u * 32 + mfma_row(r, lane)];
+    load_row_sums(xss + u * 32, lane, xsr);
     q4_group_mma1(acc, af, xsr, wq[u], wsb[u]);
   }
   // 6. K slices meet: the last work-group of the column block adds the partials
+  // (the epilogue's tables are loaded with the partials)
+  const int row0 = a.desc ? a.desc->row0 : 0;
+  QkvTables qt;
   if (KS > 1) {
     // partial tile of this wave in accumulator order: chunk jj*64 + lane holds
     // rows 8jj + 4(lane >> 5) .. +3 of column lane & 31, so each store
@@ -202,29 +224,16 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
     for (int jj = 0; jj < 4; ++jj)
       *(f32x4*)(pw + 256 * jj) = f32x4{acc[4 * jj], acc[4 * jj + 1], acc[4 * jj + 2], acc[4 * jj + 3]};
     if (!last_to_arrive(&a.counters[grp], KS, flag)) return;
-    // 1024 16-byte chunks of the 4 tiles, 4 per thread; every slice's chunks are
-    // loaded before any is added (then added in slice order)
     const float* pbase = a.part + (size_t)grp * KS * 4096;
-    f32x4 pv[SK_KS_MAX][4];
-#pragma unroll
-    for (int k2 = 0; k2 < SK_KS_MAX; ++k2)
-      if (k2 < KS)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          pv[k2][i] = *(const f32x4*)(pbase + (size_t)k2 * 4096 + 4 * (threadIdx.x + 256 * i));
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int k2 = 0; k2 < SK_KS_MAX; ++k2)
-        if (k2 < KS) sum += pv[k2][i];
-      const int q = threadIdx.x + 256 * i, tn = q >> 8, c4 = q & 255;
-      const int ln = c4 & 63, col = ln & 31, row0 = 8 * (c4 >> 6) + 4 * (ln >> 5);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) red[(tn * 32 + row0 + e) * 33 + col] = sum[e];
-    }
+    auto tables = [&]() {
+      if (EPI == EPI_QKV) qt = qkv_tables(a, grp, row0, M);
+    };
+    if (KS <= 2) sk_wide_sum_slices<2>(pbase, KS, red, tables);
+    else if (KS <= 4) sk_wide_sum_slices<4>(pbase, KS, red, tables);
+    else sk_wide_sum_slices<SK_KS_MAX>(pbase, KS, red, tables);
     if (threadIdx.x == 0) a.counters[grp] = 0;
   } else {
+    if (EPI == EPI_QKV) qt = qkv_tables(a, grp, row0, M);
 #pragma unroll
     for (int r = 0; r < 16; ++r) red[(wave * 32 + mfma_row(r, lane)) * 33 + (lane & 31)] = acc[r];
   }
@@ -260,10 +269,9 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
       *(u32x4*)dst = pk;
     }
   } else if (EPI == EPI_QKV) {
-    const int row0 = a.desc ? a.desc->row0 : 0;
     auto get = [&](int m, int d) { return red[((d >> 5) * 32 + m) * 33 + (d & 31)]; };
-    if (a.kv_bf16) qkv_epilogue<__bf16>(a, grp, 0, row0, M, get, vbuf);
-    else qkv_epilogue<_Float16>(a, grp, 0, row0, M, get, vbuf);
+    if (a.kv_bf16) qkv_epilogue<__bf16>(a, qt, grp, 0, row0, M, get, vbuf);
+    else qkv_epilogue<_Float16>(a, qt, grp, 0, row0, M, get, vbuf);
   }
 #undef TT
 }
@@ -301,8 +309,15 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
 #pragma unroll
       for (int t = 0; t < 4; ++t) af[i][t] = row_ok ? ap[t] : u32x4{0u, 0u, 0u, 0u};
     }
+    float xsr[UW][16];
+    row_sums_lane<UW>(af, red + wave * 32 * 33, lane, xsr);
 #pragma unroll
-    for (int i = 0; i < UW; ++i) q4_group_mma1_lane(acc, af[i], wq[i], wsb[i], lane);
+    for (int i = 0; i < UW; ++i) {
+      f16x8 ah[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) ah[t] = __builtin_bit_cast(f16x8, af[i][t]);
+      q4_group_mma1(acc, ah, xsr[i], wq[i], wsb[i]);
+    }
     if (ub + UW >= u_hi) break;
   }
   // the four waves' K ranges, in order; thread t owns row t >> 3, columns
@@ -326,12 +341,10 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
     const float* pp = a.part + (size_t)nt * KS * 1024 + m * 32 + c0;
     f32x4 pv[SK_KS_MAX];
 #pragma unroll
-    for (int k2 = 0; k2 < SK_KS_MAX; ++k2)
-      if (k2 < KS) pv[k2] = *(const f32x4*)(pp + (size_t)k2 * 1024);
+    for (int k2 = 0; k2 < SK_KS_MAX; ++k2) pv[k2] = *(const f32x4*)(pp + (size_t)min(k2, KS - 1) * 1024);
     v = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int k2 = 0; k2 < SK_KS_MAX; ++k2)
-      if (k2 < KS) v += pv[k2];
+    for (int k2 = 0; k2 < SK_KS_MAX; ++k2) v += pv[k2] * (k2 < KS ? 1.f : 0.f);  // unconditional loads
     if (threadIdx.x == 0) a.counters[nt] = 0;
   }
   if (a.bias) {
@@ -348,10 +361,7 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
       *(f32x4*)(a.hidden_out + (int64_t)m * N + n) = h;
     }
     if (a.ss_out) {
-      float q = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];
-      q += __shfl_xor(q, 1, 64);
-      q += __shfl_xor(q, 2, 64);
-      q += __shfl_xor(q, 4, 64);
+      const float q = sum8_dpp(h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3]);
       if ((threadIdx.x & 7) == 0) a.ss_out[nt * 32 + m] = q;
     }
   } else if (m < M) {
