@@ -15,6 +15,11 @@ struct FusedArgs {
   const uint16_t* wb = nullptr;
   const uint16_t* bias = nullptr;
   int M = 0, N = 0, K = 0;
+  // XCDs of the device (work-group i runs on XCD i % n_xcc) and the flag a
+  // work-group sets if it finds itself on another XCD (next to M, N, K: the
+  // skinny kernels fetch these first, in one scalar load)
+  int n_xcc = 1;
+  int* placement_err = nullptr;
   // PRO_ACT: activation [M][K] (ACT_F16P + xsum[M][K/64], or ACT_BF16)
   const void* act = nullptr;
   const float* act_xsum = nullptr;
@@ -50,10 +55,6 @@ struct FusedArgs {
   int n_counters = 0;
   const float* ss_in = nullptr;  // PRO_NORM: partial sums of squares of `hidden` rows
   float* ss_out = nullptr;       // EPI_RESID: partial sums of squares of the new rows
-  // XCDs of the device (work-group i runs on XCD i % n_xcc) and the flag a
-  // work-group sets if it finds itself on another XCD
-  int n_xcc = 1;
-  int* placement_err = nullptr;
 };
 
 namespace drt {

@@ -47,18 +47,32 @@ constexpr int SK_SS_PER_THREAD = 14; // K / 32 <= 8 * 14 = 112 partial sums (d <
 #define SK_WIDE_V_OFF(U) (((32 * ((U) * 64 + 8) * 2 + (U) * 32 * 4 + 32 * 4 + SK_RED * 4 + 16) + 15) / 16 * 16)
 #define SK_WIDE_LDS(U) (SK_WIDE_V_OFF(U) + 4096 * 2)
 
+// Kernel arguments the first loads need are fetched in one batch at kernel
+// start: one empty asm that takes them all in scalar registers keeps the
+// compiler from fetching some only after a wait or behind a branch (a dependent
+// round trip each). Pointers pass through the global address space (a generic
+// pointer out of the asm would make every access through it a flat access,
+// which also counts on lgkmcnt).
+#define SK_GLOBAL(T) __attribute__((address_space(1))) T
+
 // Block and K slice of this work-group: with x = i % n_xcc and j = i / n_xcc,
 // block x + n_xcc * (j / KS) and slice j % KS, so a block's slices share an XCD.
-// Returns false for the padding work-groups past the last block.
-DRT_DEV bool sk_place(const FusedArgs& a, int n_blocks, int KS, int& blk, int& ks) {
-  const int i = blockIdx.x, x = i % a.n_xcc, j = i / a.n_xcc;
-  blk = x + a.n_xcc * (j / KS);
+// Returns false for the padding work-groups past the last block; those get
+// block 0 and must leave before their first store. (They run on past their
+// loads: an early return would let the compiler sink the loads, and the kernel
+// argument fetches they need, behind the branch - one more round trip for
+// every work-group.) n_xcc and perr are the pinned a.n_xcc, a.placement_err.
+DRT_DEV bool sk_place(int n_xcc, int* perr, int n_blocks, int KS, int& blk, int& ks) {
+  const int i = blockIdx.x, x = i % n_xcc, j = i / n_xcc;
+  blk = x + n_xcc * (j / KS);
   ks = j - (j / KS) * KS;
-  if (a.n_xcc > 1 && threadIdx.x == 0 && a.placement_err) {
+  if (n_xcc > 1 && threadIdx.x == 0 && perr) {
     const int xcc = (int)(__builtin_amdgcn_s_getreg((31 << 11) | 20) & 0xf);  // HW_REG_XCC_ID
-    if (xcc != x) __hip_atomic_fetch_or(a.placement_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (xcc != x) __hip_atomic_fetch_or(perr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  return blk < n_blocks;
+  const bool live = blk < n_blocks;
+  blk = live ? blk : 0;
+  return live;
 }
 
 // Called after this work-group stored its partial: returns true in the last
@@ -108,10 +122,25 @@ DRT_DEV void sk_wide_sum_slices(const float* pbase, int KS, float* red, After af
 template <int EPI, int U>
 __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int KS) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int M = a.M, N = a.N, K = a.K;
+  int M = a.M, N = a.N, K = a.K;
+  auto gqw = (SK_GLOBAL(const uint32_t)*)a.qw;
+  auto gsb = (SK_GLOBAL(const uint32_t)*)a.sb;
+  auto ghid = (SK_GLOBAL(const float)*)a.hidden;
+  auto gnw = (SK_GLOBAL(const uint16_t)*)a.norm_w;
+  auto gss = (SK_GLOBAL(const float)*)a.ss_in;
+  auto gerr = (SK_GLOBAL(int)*)a.placement_err;
+  int n_xcc = a.n_xcc;
+  asm volatile("" : "+s"(gqw), "+s"(gsb), "+s"(ghid), "+s"(gnw), "+s"(gss), "+s"(gerr), "+s"(M),
+               "+s"(N), "+s"(K), "+s"(n_xcc), "+s"(KS));
+  const uint32_t* qw = (const uint32_t*)gqw;
+  const uint32_t* sbp = (const uint32_t*)gsb;
+  const float* hidden = (const float*)ghid;
+  const uint16_t* norm_w = (const uint16_t*)gnw;
+  const float* ss_in = (const float*)gss;
+  int* perr = (int*)gerr;
   const int G = K >> 6;
   int grp, ks;
-  if (!sk_place(a, N / 128, KS, grp, ks)) return;
+  const bool live = sk_place(n_xcc, perr, N / 128, KS, grp, ks);
   const int nt = grp * 4 + wave;
   const int u0 = ks * U, kc0 = u0 * 64;
   constexpr int KCN = U * 64;
@@ -129,8 +158,8 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
   uint32_t wsb[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    wq[u] = *q4_tile_words(a.qw, nt, G, u0 + u, lane);
-    wsb[u] = q4_tile_sb(a.sb, nt, G, u0 + u, lane);
+    wq[u] = *q4_tile_words(qw, nt, G, u0 + u, lane);
+    wsb[u] = q4_tile_sb(sbp, nt, G, u0 + u, lane);
   }
   // 2. the hidden slice (8-wide items: U per thread) and the matching norm weights.
   // Every load of steps 1-3 is unconditional (rows past M read row M - 1 and are
@@ -144,10 +173,10 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
     const int it = threadIdx.x + 256 * j;
     const int r = it / (8 * U), c8 = it - r * (8 * U);
     const int k = kc0 + c8 * 8;
-    const f32x4* src = (const f32x4*)(a.hidden + (int64_t)min(r, M - 1) * K + k);
+    const f32x4* src = (const f32x4*)(hidden + (int64_t)min(r, M - 1) * K + k);
     hv[j][0] = src[0];
     hv[j][1] = src[1];
-    nw[j] = *(const u32x4*)(a.norm_w + k);
+    nw[j] = *(const u32x4*)(norm_w + k);
   }
   // 3. row statistics from the producer's partial sums of squares: thread
   // (group g = tid / 32, row r = tid % 32) loads partials g, g + 8, ... all at
@@ -157,7 +186,7 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
     const int r = threadIdx.x & 31, g8 = threadIdx.x >> 5;
     float sv[SK_SS_PER_THREAD];
 #pragma unroll
-    for (int e = 0; e < SK_SS_PER_THREAD; ++e) sv[e] = a.ss_in[min(g8 + 8 * e, np - 1) * 32 + r];
+    for (int e = 0; e < SK_SS_PER_THREAD; ++e) sv[e] = ss_in[min(g8 + 8 * e, np - 1) * 32 + r];
     float q = 0.f;
 #pragma unroll
     for (int e = 0; e < SK_SS_PER_THREAD; ++e)  // a product, not a select, so that
@@ -211,6 +240,7 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
     load_row_sums(xss + u * 32, lane, xsr);
     q4_group_mma1(acc, af, xsr, wq[u], wsb[u]);
   }
+  if (!live) return;  // work-group-uniform, before any global store
   // 6. K slices meet: the last work-group of the column block adds the partials
   // (the epilogue's tables are loaded with the partials)
   const int row0 = a.desc ? a.desc->row0 : 0;
@@ -281,11 +311,22 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
 template <int EPI, int UW>
 __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, int KS) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int M = a.M, N = a.N, K = a.K;
+  int M = a.M, N = a.N, K = a.K;
+  auto gqw = (SK_GLOBAL(const uint32_t)*)a.qw;
+  auto gsb = (SK_GLOBAL(const uint32_t)*)a.sb;
+  auto gact = (SK_GLOBAL(const uint16_t)*)a.act;
+  auto gerr = (SK_GLOBAL(int)*)a.placement_err;
+  int n_xcc = a.n_xcc;
+  asm volatile("" : "+s"(gqw), "+s"(gsb), "+s"(gact), "+s"(gerr), "+s"(M), "+s"(N), "+s"(K),
+               "+s"(n_xcc), "+s"(KS));
+  const uint32_t* qw = (const uint32_t*)gqw;
+  const uint32_t* sbp = (const uint32_t*)gsb;
+  const uint16_t* act = (const uint16_t*)gact;
+  int* perr = (int*)gerr;
   const int G = K >> 6;
   const int U = G / KS;
   int nt, ks;
-  if (!sk_place(a, N / 32, KS, nt, ks)) return;
+  const bool live = sk_place(n_xcc, perr, N / 32, KS, nt, ks);
   const int u_lo = ks * U + (U * wave) / 4, u_hi = ks * U + (U * (wave + 1)) / 4;
   const int mr = lane & 31;
   const bool row_ok = mr < M;
@@ -302,9 +343,9 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
       // clamped to a valid unit; a unit beyond the wave's range gets scale and
       // bias 0, an exact no-op, so every load is used unconditionally
       const int u = min(ub + i, max(u_hi, u_lo + 1) - 1);
-      wq[i] = *q4_tile_words(a.qw, nt, G, u, lane);
-      wsb[i] = ub + i < u_hi ? q4_tile_sb(a.sb, nt, G, u, lane) : 0u;
-      const u32x4* ap = (const u32x4*)((const uint16_t*)a.act + (int64_t)(row_ok ? mr : 0) * K +
+      wq[i] = *q4_tile_words(qw, nt, G, u, lane);
+      wsb[i] = ub + i < u_hi ? q4_tile_sb(sbp, nt, G, u, lane) : 0u;
+      const u32x4* ap = (const u32x4*)(act + (int64_t)(row_ok ? mr : 0) * K +
                                        u * 64 + 32 * (lane >> 5));
 #pragma unroll
       for (int t = 0; t < 4; ++t) af[i][t] = row_ok ? ap[t] : u32x4{0u, 0u, 0u, 0u};
@@ -320,6 +361,7 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
     }
     if (ub + UW >= u_hi) break;
   }
+  if (!live) return;  // work-group-uniform, before any barrier or store
   // the four waves' K ranges, in order; thread t owns row t >> 3, columns
   // 4*(t & 7) .. +3 of the tile (one 16-byte chunk everywhere below)
 #pragma unroll
