@@ -46,6 +46,10 @@ constexpr int SK_SS_PER_THREAD = 14; // K / 32 <= 8 * 14 = 112 partial sums (d <
 // red [4][32][33], flag (16 B), then the V tile half [4096] halves.
 #define SK_WIDE_V_OFF(U) (((32 * ((U) * 64 + 8) * 2 + (U) * 32 * 4 + 32 * 4 + SK_RED * 4 + 16) + 15) / 16 * 16)
 #define SK_WIDE_LDS(U) (SK_WIDE_V_OFF(U) + 4096 * 2)
+// LDS of the narrow kernel: red [4][32][33] floats, flag (16 B), then the A
+// staging of the four waves, [4][UW][32][144 B]
+#define SK_NARROW_STG (SK_RED * 4 + 16)
+#define SK_NARROW_LDS(UW) (SK_NARROW_STG + 4 * (UW) * 32 * 144)
 
 // Kernel arguments the first loads need are fetched in one batch at kernel
 // start: one empty asm that takes them all in scalar registers keeps the
@@ -328,15 +332,15 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
   int nt, ks;
   const bool live = sk_place(n_xcc, perr, N / 32, KS, nt, ks);
   const int u_lo = ks * U + (U * wave) / 4, u_hi = ks * U + (U * (wave + 1)) / 4;
-  const int mr = lane & 31;
-  const bool row_ok = mr < M;
   extern __shared__ __align__(16) char smem[];
   float* red = (float*)smem;  // [4][32][33]
   int* flag = (int*)(red + SK_RED);
 
   f32x16 acc = f32x16{};
+  // this wave's A staging: [UW][32 rows][144 B] (128 B of a unit's row + pad)
+  char* stg = smem + SK_NARROW_STG + wave * (UW * 32 * 144);
   for (int ub = u_lo; ub < u_hi || ub == u_lo; ub += UW) {
-    u32x4 wq[UW], af[UW][4];
+    u32x4 wq[UW], craw[UW][4], af[UW][4];
     uint32_t wsb[UW];
 #pragma unroll
     for (int i = 0; i < UW; ++i) {
@@ -345,11 +349,26 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
       const int u = min(ub + i, max(u_hi, u_lo + 1) - 1);
       wq[i] = *q4_tile_words(qw, nt, G, u, lane);
       wsb[i] = ub + i < u_hi ? q4_tile_sb(sbp, nt, G, u, lane) : 0u;
-      const u32x4* ap = (const u32x4*)(act + (int64_t)(row_ok ? mr : 0) * K +
-                                       u * 64 + 32 * (lane >> 5));
+      // the unit's 32 x 64 activation block as four coalesced loads of 8 rows x
+      // 128 B (rows past M read row M - 1: their outputs are never stored)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) af[i][t] = row_ok ? ap[t] : u32x4{0u, 0u, 0u, 0u};
+      for (int j = 0; j < 4; ++j)
+        craw[i][j] = *(const u32x4*)(act + (int64_t)min(8 * j + (lane >> 3), M - 1) * K +
+                                     u * 64 + (lane & 7) * 8);
     }
+    // through LDS into the q4 fragment order: lane l takes row l & 31, 16-byte
+    // chunks 4(l >> 5) + t, i.e. k = 32(l >> 5) + 8t .. +8 (one wave's LDS
+    // operations run in order: no barrier)
+#pragma unroll
+    for (int i = 0; i < UW; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *(u32x4*)(stg + (i * 32 + 8 * j + (lane >> 3)) * 144 + (lane & 7) * 16) = craw[i][j];
+#pragma unroll
+    for (int i = 0; i < UW; ++i)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        af[i][t] = *(const u32x4*)(stg + (i * 32 + (lane & 31)) * 144 + (4 * (lane >> 5) + t) * 16);
     float xsr[UW][16];
     row_sums_lane<UW>(af, red + wave * 32 * 33, lane, xsr);
 #pragma unroll
@@ -515,12 +534,13 @@ bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
     if (KS > SK_KS_MAX || (size_t)NT * KS * 1024 > a.part_floats || NT > a.n_counters)
       return false;
     const int per_wave = (G / KS + 3) / 4;
-    const size_t lds = SK_RED * 4 + 16;
     const dim3 grid((unsigned)((NT + a.n_xcc - 1) / a.n_xcc * a.n_xcc * KS));
 #define DRT_SN(E, UW)                                                              \
   {                                                                                \
     auto fn = skinny_narrow_kernel<E, UW>;                                         \
-    DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(256), lds, s, a, KS);         \
+    static size_t granted = 0;                                                     \
+    grant_lds((const void*)fn, SK_NARROW_LDS(UW), granted);                        \
+    DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(256), SK_NARROW_LDS(UW), s, a, KS); \
   }
     if (kind == FL_RESID) {
       if (per_wave <= 1) DRT_SN(EPI_RESID, 1) else if (per_wave <= 2) DRT_SN(EPI_RESID, 2) else DRT_SN(EPI_RESID, 4)
