@@ -781,8 +781,16 @@ __global__ __launch_bounds__(256) void attn_decode_combine_kernel(
     for (int k = 0; k < MLR; ++k) {
       const int rr = pg + 8 * k;
       const int64_t mi = (((int64_t)min(rr, R - 1) * Hkv + kvh) * (QT * 32) + qt * 32 + c) * 2;
-      mr[k] = rr < R ? ml_part[mi] : -INFINITY;
-      lr[k] = rr < R ? ml_part[mi + 1] : 0.f;
+      mr[k] = ml_part[mi];
+      lr[k] = ml_part[mi + 1];
+    }
+    // every load above is issued before the ranges past R are masked (the
+    // compiler would otherwise load under a branch and wait inside it)
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int k = 0; k < MLR; ++k) {
+      mr[k] = pg + 8 * k < R ? mr[k] : -INFINITY;
+      lr[k] = pg + 8 * k < R ? lr[k] : 0.f;
     }
     float m_loc = -INFINITY;
 #pragma unroll
@@ -809,13 +817,16 @@ __global__ __launch_bounds__(256) void attn_decode_combine_kernel(
   float lsum = 0.f;
 #pragma unroll
   for (int g = 0; g < 8; ++g) lsum += ls[g][c];
+  // all RB weights read before any is used (one LDS latency, no branches)
+  float wv[RB];
+#pragma unroll
+  for (int e = 0; e < RB; ++e) wv[e] = wts[min(e, R - 1) * 32 + c];
+  asm volatile("" ::: "memory");
   float acc = 0.f;
 #pragma unroll
   for (int e = 0; e < RB; ++e) {
-    if (e < R) {
-      const float w = wts[e * 32 + c];
-      acc = fmaf(w, w == 0.f ? 0.f : v[e], acc);
-    }
+    const float w = e < R ? wv[e] : 0.f;
+    acc = fmaf(w, w == 0.f ? 0.f : v[e], acc);
   }
   for (int rr = RB; rr < R; rr += 8) {
     float u[8];
