@@ -287,15 +287,38 @@ DRT_DEV void attend_group(const typename MfmaT<T>::vec (&kc)[NG][8],
   for (int g = 0; g < NG; ++g)
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) sc[g][qt] = f32x16{};
+  // Q fragments are read one k-step ahead: step i + 1's ds_reads are issued
+  // (inline asm, so the compiler does not sink them to their use) before step
+  // i's MFMAs, and waited for after them; the wait takes the registers as
+  // operands, so nothing reads them earlier.
+  const T* qrow = qs + (lane & 31) * DEC_QROW + 8 * (lane >> 5);
+  const uint32_t qaddr = (uint32_t)(uintptr_t)qrow;
+  vec qf[QT];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int qt = 0; qt < QT; ++qt) qf[qt] = *(const vec*)(qrow + qt * 32 * DEC_QROW);
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      const vec qf =
-          *(const vec*)(qs + (qt * 32 + (lane & 31)) * DEC_QROW + 8 * (lane >> 5) + 16 * i);
+  for (int i = 0; i < 8; ++i) {
+    vec qn[QT];
+    if (i < 7) {
 #pragma unroll
-      for (int g = 0; g < NG; ++g) sc[g][qt] = MfmaT<T>::mma(kc[g][i], qf, sc[g][qt]);
+      for (int qt = 0; qt < QT; ++qt)
+        asm volatile("ds_read_b128 %0, %1 offset:%2"
+                     : "=v"(qn[qt])
+                     : "v"(qaddr), "i"((qt * 32 * DEC_QROW + 16 * (i + 1)) * 2));
     }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int g = 0; g < NG; ++g) sc[g][qt] = MfmaT<T>::mma(kc[g][i], qf[qt], sc[g][qt]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (i < 7) {
+      if constexpr (QT == 1) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(qn[0]));
+      else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(qn[0]), "+v"(qn[1]));
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) qf[qt] = qn[qt];
+    }
+  }
 #pragma unroll
   for (int g = 0; g < NG; ++g) {
     if (key0[g] + 32 > nk[g]) {  // uniform: a partial (or empty) tile masks its keys
