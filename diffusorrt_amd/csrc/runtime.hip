@@ -139,6 +139,9 @@ struct Runtime {
   int n_xcc = 1;
   DevBuf placement_err;          // int, set by a kernel that finds itself on an unexpected XCD
   int* placement_host = nullptr; // pinned copy, read after each synchronized forward
+  // pinned landing area of a proposal's scores and tokens (the caller's arrays are
+  // pageable: a device-to-host copy into them takes the slow staged path)
+  char* out_host = nullptr;
   // Per-forward inputs: one pinned host slot + its device copy per forward, moved
   // by a single async copy. Slot 0 belongs to the commit graph, slot 1 to the
   // step graph; eager forwards rotate through the rest.
@@ -159,6 +162,7 @@ struct Runtime {
     if (stream) (void)hipStreamSynchronize(stream);
     if (up_host) (void)hipHostFree(up_host);
     if (placement_host) (void)hipHostFree(placement_host);
+    if (out_host) (void)hipHostFree(out_host);
     if (ev0) (void)hipEventDestroy(ev0);
     if (ev1) (void)hipEventDestroy(ev1);
     if (stream) (void)hipStreamDestroy(stream);
@@ -398,6 +402,7 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
   rt->stats.alloc(lmhead_stats_bytes(lm_cap, V));
   rt->scores.alloc((size_t)lm_cap * 8);
   rt->tokens_out.alloc((size_t)lm_cap * 4);
+  DRT_HIP(hipHostMalloc((void**)&rt->out_host, (size_t)lm_cap * 12 + 16, hipHostMallocDefault));
   rt->lm_rows.alloc((size_t)lm_cap * 4);
   rt->lm_pos.alloc((size_t)lm_cap * 4);
   {
@@ -1111,14 +1116,18 @@ int32_t drt_session_propose(uint64_t session, const int32_t* frontier, int32_t n
     r.up_next = 2;  // the stream is drained below before any slot is reused
     forwarded += a.n_rows;
     DRT_HIP(hipEventRecord(r.ev1, r.stream));
-    DRT_HIP(hipMemcpyAsync(out_scores, r.scores.p, (size_t)n_frontier * 8, hipMemcpyDeviceToHost,
+    char* land_scores = r.out_host;
+    char* land_tokens = r.out_host + (size_t)n_frontier * 8;
+    DRT_HIP(hipMemcpyAsync(land_scores, r.scores.p, (size_t)n_frontier * 8, hipMemcpyDeviceToHost,
                            r.stream));
-    DRT_HIP(hipMemcpyAsync(out_tokens, r.tokens_out.p, (size_t)n_frontier * 4,
+    DRT_HIP(hipMemcpyAsync(land_tokens, r.tokens_out.p, (size_t)n_frontier * 4,
                            hipMemcpyDeviceToHost, r.stream));
     DRT_HIP(hipMemcpyAsync(r.placement_host, r.placement_err.p, 4, hipMemcpyDeviceToHost,
                            r.stream));
     DRT_HIP(hipStreamSynchronize(r.stream));
     check_placement(r);
+    std::memcpy(out_scores, land_scores, (size_t)n_frontier * 8);
+    std::memcpy(out_tokens, land_tokens, (size_t)n_frontier * 4);
     s->finish_timing();
     s->publish_profile();
     s->proposals += 1;
