@@ -656,23 +656,26 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 
-  float m_run[QT], l_run[QT];
-  f32x16 o[QT][4];
+  // Consumer waves split each tile by query tile: wave w takes query tile
+  // w % QT of tiles w / QT, w / QT + 4 / QT, ..., so a tile's work is spread over
+  // QT waves (a shorter dependency chain per tile) and the merge adds 4 / QT
+  // partials per query tile.
+  constexpr int TSTRIDE = 4 / QT;
+  constexpr int SLOT1 = 4096 + 64 * 2;  // one wave's merge slot: O of one query tile + (m, l)
+  const int my_qt = wave % QT, phase = wave / QT;
+  float m_run[1] = {-INFINITY}, l_run[1] = {0.f};
+  f32x16 o[1][4];
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    m_run[qt] = -INFINITY;
-    l_run[qt] = 0.f;
-#pragma unroll
-    for (int hb = 0; hb < 4; ++hb) o[qt][hb] = f32x16{};
-  }
+  for (int hb = 0; hb < 4; ++hb) o[0][hb] = f32x16{};
   if (wave == 4) {
-    // the loads after tile t's are 16 per later tile: vmcnt(48) proves tile t - 3
+    // the loads after tile t's are 16 per later tile: vmcnt(48) proves tile t - 3;
+    // slot t % DECR_SLOTS is free once its previous tile has been read by QT waves
     if (n >= 4) {
       decr_waitcnt<DECR_VM48>();
       signal(0);
     }
     for (int t = 4; t < n; ++t) {
-      if (t >= DECR_SLOTS) decr_wait(&freed[t % DECR_SLOTS], t - DECR_SLOTS + 1, err);
+      if (t >= DECR_SLOTS) decr_wait(&freed[t % DECR_SLOTS], QT * (t / DECR_SLOTS), err);
       dma_tile(t);
       decr_waitcnt<DECR_VM48>();
       signal(t - 3);
@@ -688,7 +691,8 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
     decr_waitcnt<DECR_VM0>();
     signal(n - 1);
   } else {
-    for (int t = wave; t < n; t += 4) {
+    const T* my_q = qs + my_qt * 32 * DEC_QROW;
+    for (int t = phase; t < n; t += TSTRIDE) {
       decr_wait(&ready[t % DECR_SLOTS], t + 1, err);
       const vec* tp = (const vec*)(tiles + (t % DECR_SLOTS) * 16384);
       vec kc[1][8], vc[1][8];
@@ -699,64 +703,60 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
       }
       if (t + DECR_SLOTS < n) {  // the producer reuses the slot for tile t + 8
         decr_waitcnt<DECR_LGKM0>();  // the slot's reads are complete
-        decr_lds_write(&freed[t % DECR_SLOTS], t + 1);
+        if (lane == 0)
+          asm volatile("ds_add_u32 %0, %1"
+                       :
+                       : "v"((uint32_t)(uintptr_t)&freed[t % DECR_SLOTS]), "v"(1)
+                       : "memory");
       }
       const int key0[1] = {(t_begin + t) * 32}, nk[1] = {n_keys};
-      attend_group<T, QT, 1>(kc, vc, qs, key0, nk, c, lane, m_run, l_run, o);
+      attend_group<T, 1, 1>(kc, vc, my_q, key0, nk, c, lane, m_run, l_run, o);
     }
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) l_run[qt] += __shfl_xor(l_run[qt], 32, 64);
+    l_run[0] += __shfl_xor(l_run[0], 32, 64);
   }
   __syncthreads();  // every tile consumed: Q and the slots become the merge area
   if (wave < 4) {
-    float* mine = mrg + wave * SLOT;
+    float* mine = mrg + wave * SLOT1;
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
+    for (int hb = 0; hb < 4; ++hb)
 #pragma unroll
-      for (int hb = 0; hb < 4; ++hb)
-#pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4)
-          ((f32x4*)mine)[((qt * 4 + hb) * 4 + r4) * 64 + lane] =
-              f32x4{o[qt][hb][4 * r4], o[qt][hb][4 * r4 + 1], o[qt][hb][4 * r4 + 2],
-                    o[qt][hb][4 * r4 + 3]};
-      mine[SLOTS + (qt * 64 + lane) * 2] = m_run[qt];
-      mine[SLOTS + (qt * 64 + lane) * 2 + 1] = l_run[qt];
-    }
+      for (int r4 = 0; r4 < 4; ++r4)
+        ((f32x4*)mine)[(hb * 4 + r4) * 64 + lane] =
+            f32x4{o[0][hb][4 * r4], o[0][hb][4 * r4 + 1], o[0][hb][4 * r4 + 2], o[0][hb][4 * r4 + 3]};
+    mine[4096 + lane * 2] = m_run[0];
+    mine[4096 + lane * 2 + 1] = l_run[0];
   }
   __syncthreads();
   if (wave >= 4) return;
-  float wgt[QT][4];
+  // query tile qt: the waves qt + QT * p, p < TSTRIDE
+  f32x4* op = (f32x4*)(o_part + part * SLOTS);
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    float mw[4], lw[4];
+    float mw[TSTRIDE], lw[TSTRIDE], wgt[TSTRIDE];
     float mm = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      mw[w] = mrg[w * SLOT + SLOTS + (qt * 64 + lane) * 2];
-      lw[w] = mrg[w * SLOT + SLOTS + (qt * 64 + lane) * 2 + 1];
-      mm = fmaxf(mm, mw[w]);
+    for (int p = 0; p < TSTRIDE; ++p) {
+      mw[p] = mrg[(qt + QT * p) * SLOT1 + 4096 + lane * 2];
+      lw[p] = mrg[(qt + QT * p) * SLOT1 + 4096 + lane * 2 + 1];
+      mm = fmaxf(mm, mw[p]);
     }
     float ll = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      wgt[qt][w] = mw[w] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw[w] - mm);
-      ll += wgt[qt][w] * lw[w];
+    for (int p = 0; p < TSTRIDE; ++p) {
+      wgt[p] = mw[p] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw[p] - mm);
+      ll += wgt[p] * lw[p];
     }
     if (wave == 0 && lane < 32) {
       ml_part[(part * (QT * 32) + qt * 32 + lane) * 2] = mm;
       ml_part[(part * (QT * 32) + qt * 32 + lane) * 2 + 1] = ll;
     }
-  }
-  f32x4* op = (f32x4*)(o_part + part * SLOTS);
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int e = qt * 1024 + threadIdx.x + 256 * i;
+      const int e = threadIdx.x + 256 * i;  // float4 of the query tile (lane = e & 63)
       f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int w = 0; w < 4; ++w) v += wgt[qt][w] * ((const f32x4*)(mrg + w * SLOT))[e];
-      op[e] = v;
+      for (int p = 0; p < TSTRIDE; ++p) v += wgt[p] * ((const f32x4*)(mrg + (qt + QT * p) * SLOT1))[e];
+      op[qt * 1024 + e] = v;
     }
   }
 }
