@@ -630,7 +630,7 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
 
   constexpr int QCH = QT * 2;  // Q chunks per consumer thread
   if (wave == 4) {
-    const int n0 = min(n, 4);
+    const int n0 = min(n, 2);
     for (int t = 0; t < n0; ++t) dma_tile(t);
   } else {
     u32x4 qraw[QCH];
@@ -668,28 +668,35 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
 #pragma unroll
   for (int hb = 0; hb < 4; ++hb) o[0][hb] = f32x16{};
   if (wave == 4) {
-    // the loads after tile t's are 16 per later tile: vmcnt(48) proves tile t - 3;
-    // slot t % DECR_SLOTS is free once its previous tile has been read by QT waves
-    if (n >= 4) {
-      decr_waitcnt<DECR_VM48>();
-      signal(0);
-    }
-    for (int t = 4; t < n; ++t) {
+    // Tiles 0 and 1 were issued before the barrier. The first two tiles are
+    // proven with two newer tiles in flight (vmcnt(32) after issuing tiles 2, 3),
+    // so the consumers start as soon as tile 0 lands; tile 4 then goes out
+    // unproven and from tile 5 on each issue is followed by vmcnt(48), proving
+    // tile t - 3 with three newer tiles in flight. Slot t % DECR_SLOTS is free
+    // once its previous tile has been read by QT waves.
+    int next = 0;  // the next tile to signal
+    for (int t = 2; t < n; ++t) {
       if (t >= DECR_SLOTS) decr_wait(&freed[t % DECR_SLOTS], QT * (t / DECR_SLOTS), err);
       dma_tile(t);
-      decr_waitcnt<DECR_VM48>();
-      signal(t - 3);
+      if (t < 4) {
+        decr_waitcnt<DECR_VM32>();
+        signal(next++);
+      } else if (t > 4) {
+        decr_waitcnt<DECR_VM48>();
+        signal(next++);
+      }
     }
-    if (n >= 3) {
+    // the n - next tiles still unproven (<= 3) are the last ones issued
+    if (n - next == 3) {
       decr_waitcnt<DECR_VM32>();
-      signal(n - 3);
+      signal(next++);
     }
-    if (n >= 2) {
+    if (n - next == 2) {
       decr_waitcnt<DECR_VM16>();
-      signal(n - 2);
+      signal(next++);
     }
     decr_waitcnt<DECR_VM0>();
-    signal(n - 1);
+    while (next < n) signal(next++);
   } else {
     const T* my_q = qs + my_qt * 32 * DEC_QROW;
     for (int t = phase; t < n; t += TSTRIDE) {
