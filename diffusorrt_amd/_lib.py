@@ -103,6 +103,8 @@ SIGNATURES = {
     "drt_session_metrics": (_I32, [_U64, C.POINTER(Metrics)]),
     "drt_session_set_profiling": (_I32, [_U64, _I32]),
     "drt_op_q4_repack": (_I32, [_VP, _VP, _VP, _I32, _I32, _VP, _VP, _VP]),
+    "drt_op_q4_quantize": (_I32, [_VP, _I32, _I32, _I32, _VP, _VP, _VP, _VP]),
+    "drt_op_cast_bf16": (_I32, [_VP, _VP, _I64, _VP]),
     "drt_op_q4_linear_workspace_bytes": (_SZ, [_I32, _I32, _I32]),
     "drt_op_q4_linear": (_I32, [_VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _VP, _VP, _SZ,
                                 _VP]),

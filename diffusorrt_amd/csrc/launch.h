@@ -166,6 +166,9 @@ struct LinearW {
 void q4_repack(const uint32_t* w_q, const uint16_t* scales, const uint16_t* biases, int N, int K,
                uint32_t* qw, uint32_t* sb, hipStream_t s);
 void bf16_repack(const uint16_t* w, int N, int K, uint16_t* wb, hipStream_t s);
+// fp32 or bf16 W [N, K] -> MLX q4 g64 packing (w_q [N][K/8], scales/biases bf16 [N][K/64]).
+void q4_quantize(const void* w, bool w_f32, int N, int K, uint32_t* w_q, uint16_t* scales,
+                 uint16_t* biases, hipStream_t s);
 void q4_act_prep(const void* x, bool x_bf16, int M, int K, _Float16* xp, float* xsum,
                  hipStream_t s);
 

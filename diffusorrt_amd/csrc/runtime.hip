@@ -1306,6 +1306,24 @@ int32_t drt_op_q4_repack(const void* w_q, const void* scales, const void* biases
   });
 }
 
+int32_t drt_op_q4_quantize(const void* w, int32_t w_dtype, int32_t n, int32_t k, void* w_q,
+                           void* scales, void* biases, void* stream) {
+  return guarded([&] {
+    require(w && w_q && scales && biases && n > 0 && k > 0, "bad q4_quantize arguments");
+    require(w_dtype == DRT_F32 || w_dtype == DRT_BF16, "q4_quantize weight must be F32 or BF16");
+    if (k % 64 != 0) fail(UNSUPPORTED, "q4_quantize needs k % 64 == 0 (group size 64)");
+    q4_quantize(w, w_dtype == DRT_F32, n, k, (uint32_t*)w_q, (uint16_t*)scales,
+                (uint16_t*)biases, as_stream(stream));
+  });
+}
+
+int32_t drt_op_cast_bf16(const float* x, void* y, int64_t n, void* stream) {
+  return guarded([&] {
+    require(x && y && n > 0, "bad cast_bf16 arguments");
+    to_bf16(x, (uint16_t*)y, n, as_stream(stream));
+  });
+}
+
 int32_t drt_op_q4_linear(const void* qw, const void* sb, const void* x, int32_t x_dtype,
                          int32_t m, int32_t n, int32_t k, const void* bias, float* y,
                          void* workspace, size_t workspace_bytes, void* stream) {

@@ -4,7 +4,7 @@ Mirrors the compiled-provider contract the reference's host code drives
 (``model.py:873-920, 1026-1087`` and ``backends/device_runtime.py:108-183,
 277-365`` of the reference's ``python/src/edllm/``):
 
-    runtime = Runtime(weights, geometry, engine_config={...})
+    runtime = Runtime(package_dir_or_model, engine_config={...})
     with runtime.session(session_config={...}) as session:
         session.start_device(tokens, prompt_len=..., block_size=..., mask_token_id=...,
                              exact_kv=False, steps=..., memory_budget_bytes=0,
@@ -16,9 +16,11 @@ Mirrors the compiled-provider contract the reference's host code drives
         session.device_metrics()
 
 PyTorch is only the plumbing that puts the weights in device memory; all
-compute happens in the library's HIP kernels. The reference opens its runtime
-from an execution-package directory; here the caller supplies the weights
-mapping directly (synthetic models, or tensors it loaded itself).
+compute happens in the library's HIP kernels. As in the reference, the runtime
+opens an execution-package directory (``package.load_package``: manifest,
+verified weight store, bf16 cast and 4-bit quantization on the device when
+``engine_config["linear_quant_bits"] == 4``); it also takes a prepared model
+object (``geometry``, ``weight_kind``, ``weights``: the seeded synthetic models).
 """
 from __future__ import annotations
 
@@ -46,18 +48,18 @@ def _dtype_code(t) -> int:
         raise ValueError(f"dtype {t.dtype} has no ABI encoding") from None
 
 
-def rope_tables(positions: int, head_dim: int, rope_theta: float):
+def rope_tables(positions: int, head_dim: int, rope_theta: float, factor: float = 1.0):
     """Half-width fp32 rotary tables ``[positions, head_dim/2]``.
 
     Same float32 recipe as the reference's ``_rope_tables``
     (``backends/mlx_forward.py:1566-1595``): ``inv_freq = 1 / theta **
-    (arange(0, half, f32) / half)``, ``freqs = pos * inv_freq``; the kernels
-    duplicate the halves.
+    (arange(0, half, f32) / half) / max(1e-6, factor)`` (linear scaling),
+    ``freqs = pos * inv_freq``; the kernels duplicate the halves.
     """
     half = head_dim // 2
     inv_freq = np.float32(1.0) / (
         np.float32(rope_theta) ** (np.arange(0, half, dtype=np.float32) / np.float32(half)))
-    inv_freq = (inv_freq / np.float32(1.0)).astype(np.float32)
+    inv_freq = (inv_freq / np.float32(max(1e-6, float(factor)))).astype(np.float32)
     freqs = (np.arange(positions, dtype=np.float32)[:, None] * inv_freq[None, :]).astype(np.float32)
     return np.cos(freqs).astype(np.float32), np.sin(freqs).astype(np.float32)
 
@@ -78,10 +80,13 @@ class WindowLogits:
 class Runtime:
     """Owns the model in device layouts and one HIP stream (one per process is typical)."""
 
-    def __init__(self, model: SyntheticModel, *, device: str = "rocm",
-                 engine_config: dict | None = None, device_ordinal: int = 0,
-                 creation_memory_budget_bytes: int = 0, max_forward_rows: int = 2048,
-                 kv_dtype: str = "f16", max_positions: int | None = None):
+    def __init__(self, model, *, device: str = "rocm",
+                 engine_config: dict | None = None, precision: dict | None = None,
+                 device_ordinal: int = 0, creation_memory_budget_bytes: int = 0,
+                 max_forward_rows: int = 2048, kv_dtype: str = "f16",
+                 max_positions: int | None = None):
+        import os
+
         import torch
 
         if device != "rocm":
@@ -89,10 +94,20 @@ class Runtime:
         if not torch.cuda.is_available():
             raise RuntimeError("the rocm runtime needs a visible AMD GPU")
         lib = _lib.load()
-        g: ModelGeometry = model.geometry
         ec = dict(engine_config or {})
+        if isinstance(model, (str, os.PathLike)):
+            # an execution-package directory (model.py:888-920): weights read,
+            # cast and quantized on the device as the engine config asks
+            from .package import load_package
+
+            bits = ec.get("linear_quant_bits")
+            model = load_package(model, linear_quant_bits=None if bits in (None, -1) else int(bits),
+                                 linear_quant_group_size=int(ec.get("linear_quant_group_size", 64)),
+                                 device_ordinal=device_ordinal)
+        g: ModelGeometry = model.geometry
         quant_bits = 4 if model.weight_kind == "q4" else -1
-        if ec.get("linear_quant_bits", quant_bits) != quant_bits:
+        bits = ec.get("linear_quant_bits", quant_bits)
+        if (-1 if bits is None else bits) != quant_bits:
             raise ValueError("engine_config linear_quant_bits disagrees with the weights")
         for key in ("d2f_exact_kv_cache", "prefix_kv_cache", "block_kv_cache",
                     "layer0_kv_cache_enabled", "cross_request_cache", "canvas_cache"):
@@ -139,7 +154,8 @@ class Runtime:
                 add(base + ".biases", value.biases)
             else:
                 add(name, value)
-        cos, sin = rope_tables(positions, g.head_dim, g.rope_theta)
+        cos, sin = rope_tables(positions, g.head_dim, g.rope_theta,
+                               getattr(g, "rope_scaling_factor", 1.0))
         add("rope.cos", torch.from_numpy(cos))
         add("rope.sin", torch.from_numpy(sin))
         arr = (_lib.Tensor * len(descs))(*descs)

@@ -51,6 +51,9 @@ class ModelGeometry:
     eos_token_id: int
     tie_word_embeddings: bool
     max_position_embeddings: int = 40960
+    # linear RoPE scaling: positions are divided by this factor
+    # (backends/mlx_forward.py:1584-1588)
+    rope_scaling_factor: float = 1.0
 
     def scaled(self, **overrides) -> "ModelGeometry":
         values = dict(self.__dict__)

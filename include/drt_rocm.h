@@ -184,6 +184,16 @@ int32_t drt_session_set_profiling(uint64_t session, int32_t enable);
  * sb uint32 [N*K/64]. */
 int32_t drt_op_q4_repack(const void* w_q, const void* scales, const void* biases, int32_t n,
                          int32_t k, void* qw, void* sb, void* stream);
+/* quantize_linear_weight(w, group_size=64, bits=4) (mlx_ops.py:63-94, run once per load by
+ * backends/mlx_dream.py:2073-2108): fp32 or bf16 W [n, k] (rounded to bf16 first) -> the
+ * QuantizedWeight bundle in MLX packing: w_q uint32 [n, k/8], scales/biases bf16 [n, k/64].
+ * k % 64 != 0 is DRT_UNSUPPORTED (the reference keeps such a weight in floating point). */
+int32_t drt_op_q4_quantize(const void* w, int32_t w_dtype, int32_t n, int32_t k, void* w_q,
+                           void* scales, void* biases, void* stream);
+/* A floating-point package tensor cast to the resident bf16 dtype, round to nearest even
+ * (the `.astype(target)` of backends/mlx_dream.py:1957-1963, 1998-1999): fp32 x [n] ->
+ * bf16 y [n]. */
+int32_t drt_op_cast_bf16(const float* x, void* y, int64_t n, void* stream);
 /* linear(x, QuantizedWeight, bias) (mlx_ops.py:97-130): y fp32 [m, n] from x fp32 or
  * bf16 [m, k]; bias bf16 [n] or NULL. Needs drt_op_q4_linear_workspace_bytes(m, n, k). */
 size_t drt_op_q4_linear_workspace_bytes(int32_t m, int32_t n, int32_t k);

@@ -165,6 +165,59 @@ def q4_dequant(w_q, scales, biases, *, dtype=np.float32) -> np.ndarray:
     return (s * q + b).astype(dtype)
 
 
+def round_half_away(x) -> np.ndarray:
+    """float32 round to nearest, halves away from zero (C ``roundf``; Metal's
+    ``round``). ``x - trunc(x)`` is exact in float32, so no addition can
+    round a value just below a half up to it."""
+    a = np.asarray(x, dtype=np.float32)
+    t = np.trunc(a)
+    frac = a - t
+    step = np.where(np.abs(frac) >= np.float32(0.5), np.sign(a), np.float32(0)).astype(np.float32)
+    return (t + step).astype(np.float32)
+
+
+def q4_quantize(w, *, return_fp32: bool = False):
+    """4-bit affine group-64 quantization: ``mx.quantize(w, group_size=64, bits=4)``
+    as ``quantize_linear_weight`` calls it (``backends/mlx_ops.py:63-94``) on the
+    resident bf16 weight (``backends/mlx_dream.py:1957-1963, 2073-2108``).
+
+    MLX (``mlx>=0.31,<0.32``, absent here) is restated from its published affine
+    quantization, per group of 64 along K, in float32:
+      ``scale = max((w_max - w_min) / 15, 1e-7)``; the edge is ``w_min`` (scale
+      positive) when ``|w_min| > |w_max|``, else ``w_max`` (scale negated);
+      ``q0 = round(edge / scale)``; unless ``q0 == 0``: ``scale = edge / q0`` and
+      ``bias = edge``, else ``bias = 0``;
+      ``q = clip(round((w - bias) / scale), 0, 15)``;
+    scales/biases stored as bf16 (round to nearest even). ``round`` is taken as
+    halves away from zero (the Metal kernel's); MLX's CPU fallback rounds halves
+    to even, so an exact .5 quotient is where the two can differ.
+
+    Returns ``(w_q uint32 [N, K/8], scales, biases)`` (float32 values of bf16);
+    with ``return_fp32`` also the float32 scale and bias before the bf16 store.
+    """
+    a = bf16_round(np.asarray(w, dtype=np.float32))
+    n, k = a.shape
+    if k % Q4_GROUP:
+        raise ValueError(f"in-dim {k} not divisible by {Q4_GROUP}")
+    g = a.reshape(n, k // Q4_GROUP, Q4_GROUP)
+    f32 = np.float32
+    w_max = g.max(axis=-1)
+    w_min = g.min(axis=-1)
+    scale = np.maximum((w_max - w_min) / f32(15), f32(1e-7)).astype(f32)
+    side = np.abs(w_min) > np.abs(w_max)
+    scale = np.where(side, scale, -scale).astype(f32)
+    edge = np.where(side, w_min, w_max).astype(f32)
+    q0 = round_half_away(edge / scale)
+    at_zero = q0 == 0
+    with np.errstate(divide="ignore", invalid="ignore"):
+        scale = np.where(at_zero, scale, edge / q0).astype(f32)
+    bias = np.where(at_zero, f32(0), edge).astype(f32)
+    q = round_half_away((g - bias[..., None]) / scale[..., None])
+    q = np.clip(q, f32(0), f32(15)).astype(np.uint8).reshape(n, k)
+    out = (q4_pack(q), bf16_round(scale), bf16_round(bias))
+    return out + (scale, bias) if return_fp32 else out
+
+
 class Q4Weight:
     """A q4 g64 linear weight: packed words + float scales/biases (bf16 values).
 

@@ -1,0 +1,155 @@
+"""Package loading on the device: the HIP quantizer and bf16 cast bit-exact against
+the oracle, and runtimes opened from package directories against the oracle's
+forward on the same prepared weights."""
+from __future__ import annotations
+
+
+import numpy as np
+import pytest
+
+from oracle import forward as F
+from oracle import ops as O
+
+from helpers import LOGITS_REL_TOL, rel_err_rows, tiny_dream_geometry, tiny_geometry
+from package_writer import random_weights, write_package
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print("[case]", *a, flush=True)
+
+
+def _quantize_on_device(w: torch.Tensor):
+    from diffusorrt_amd import _lib
+
+    lib = _lib.load()
+    n, k = w.shape
+    src = w.contiguous().cuda()
+    w_q = torch.empty((n, k // 8), dtype=torch.int32, device="cuda")
+    s = torch.empty((n, k // 64), dtype=torch.bfloat16, device="cuda")
+    b = torch.empty((n, k // 64), dtype=torch.bfloat16, device="cuda")
+    code = _lib.F32 if w.dtype == torch.float32 else _lib.BF16
+    _lib.check(lib.drt_op_q4_quantize(src.data_ptr(), code, n, k, w_q.data_ptr(), s.data_ptr(),
+                                      b.data_ptr(), None))
+    torch.cuda.synchronize()
+    return (w_q.cpu().numpy().view(np.uint32), s.cpu().view(torch.int16).numpy().view(np.uint16),
+            b.cpu().view(torch.int16).numpy().view(np.uint16))
+
+
+def _special_groups(n_rows: int, k: int) -> np.ndarray:
+    """Rows of groups the quantizer treats specially: zero, constant, exact ramps
+    of both orientations, a .5 tie, tiny and large magnitudes, one-signed."""
+    rng = np.random.default_rng(7)
+    w = rng.normal(0, 0.02, (n_rows, k)).astype(np.float32)
+    ramp = np.arange(64) % 16
+    w[0, :64] = 0.0
+    w[0, 64:128] = 0.3
+    w[1, :64] = -1.0 + 0.125 * ramp
+    w[1, 64:128] = 1.0 - 0.125 * ramp
+    w[2, :64] = -1.0 + 0.125 * ramp
+    w[2, 2] = -0.6875  # q = 2.5 exactly
+    w[3, :64] = rng.normal(0, 1e-30, 64)
+    w[3, 64:128] = rng.normal(0, 300.0, 64)
+    w[4, :64] = np.abs(w[4, :64])
+    w[4, 64:128] = -np.abs(w[4, 64:128])
+    return w
+
+
+@pytest.mark.parametrize("n,k,dtype", [(64, 1024, "bf16"), (96, 3072, "f32"), (32, 128, "f32"),
+                                       (128, 18944, "bf16")])
+def test_q4_quantize_bit_exact(n, k, dtype):
+    _say("q4_quantize", n, k, dtype)
+    w = _special_groups(n, k)
+    t = torch.from_numpy(w)
+    if dtype == "bf16":
+        t = t.to(torch.bfloat16)
+    got_q, got_s, got_b = _quantize_on_device(t)
+    ref_q, ref_s, ref_b = O.q4_quantize(t.float().numpy())
+    assert np.array_equal(got_q, ref_q), np.argwhere(got_q != ref_q)[:5]
+    assert np.array_equal(got_s, O.bf16_bits(ref_s))
+    assert np.array_equal(got_b, O.bf16_bits(ref_b))
+    assert O.q4_unpack(got_q)[2, 2] == 3  # the tie, halves away from zero
+
+
+def test_q4_quantize_refuses_indivisible_k():
+    from diffusorrt_amd import _lib
+
+    lib = _lib.load()
+    buf = torch.empty(4096, dtype=torch.bfloat16, device="cuda")
+    status = lib.drt_op_q4_quantize(buf.data_ptr(), _lib.BF16, 32, 96, buf.data_ptr(),
+                                    buf.data_ptr(), buf.data_ptr(), None)
+    assert status == _lib.UNSUPPORTED
+
+
+def test_cast_bf16_bit_exact():
+    from diffusorrt_amd import _lib
+
+    lib = _lib.load()
+    x = np.random.default_rng(8).normal(0, 3, 100_003).astype(np.float32)
+    x[:6] = [0.0, -0.0, 1.0 + 2**-8, 1.0 + 3 * 2**-8, 3.4e38, -1e-40]
+    src = torch.from_numpy(x).cuda()
+    out = torch.empty(x.size, dtype=torch.bfloat16, device="cuda")
+    _lib.check(lib.drt_op_cast_bf16(src.data_ptr(), out.data_ptr(), x.size, None))
+    torch.cuda.synchronize()
+    got = out.cpu().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, O.bf16_bits(x))
+
+
+def _oracle_weights(host: dict, q4: bool) -> dict:
+    from diffusorrt_amd.package import is_quantized_linear
+
+    W = {}
+    for name, t in host.items():
+        a = t.float().numpy()
+        W[name] = O.Q4Weight(*O.q4_quantize(a)) if q4 and is_quantized_linear(name) else \
+            O.bf16_round(a)
+    return W
+
+
+@pytest.mark.parametrize("fmt,q4,dream", [("safetensors", True, False), ("npz", True, False),
+                                          ("safetensors", False, False), ("npz", True, True)])
+def test_runtime_from_package_matches_oracle(tmp_path, fmt, q4, dream):
+    from diffusorrt_amd import synthetic as syn
+    from diffusorrt_amd.package import load_package
+    from diffusorrt_amd.runtime import Runtime, bd3_session_config, fixed_quota_session_config
+
+    _say("package runtime", fmt, "q4" if q4 else "bf16", "dream" if dream else "bd3")
+    g = tiny_dream_geometry() if dream else tiny_geometry()
+    host = random_weights(g, seed=21, dtype=torch.bfloat16 if fmt == "safetensors" else torch.float32)
+    root = write_package(tmp_path / "pkg", g, host, fmt=fmt, max_shard_bytes=400_000)
+    ec = {"linear_quant_bits": 4, "linear_quant_group_size": 64} if q4 else {}
+    W = _oracle_weights(host, q4)
+    cfg = syn.oracle_config(g, "q4" if q4 else "bf16")
+    if q4:  # the device-prepared bundles are the oracle's, bit for bit
+        pm = load_package(root, linear_quant_bits=4)
+        for name, v in pm.weights.items():
+            if isinstance(v, syn.Q4Tensor):
+                assert np.array_equal(v.w_q.cpu().numpy().view(np.uint32), W[name].w_q), name
+                assert np.array_equal(v.scales.float().cpu().numpy(), W[name].scales), name
+                assert np.array_equal(v.biases.float().cpu().numpy(), W[name].biases), name
+            else:
+                assert np.array_equal(v.float().cpu().numpy(), W[name]), name
+        del pm
+    rt = Runtime(str(root), engine_config=ec, max_forward_rows=512, max_positions=1024)
+    assert rt.weight_kind == ("q4" if q4 else "bf16")
+    rng = np.random.default_rng(3)
+    if dream:
+        x = rng.integers(0, 900, 64).tolist() + [g.mask_token_id] * 64
+        scope = list(range(64, 128))
+        with rt.session(fixed_quota_session_config(256, 16, len(x))) as s:
+            got = s.execute_window(x, scope).array()
+        ref = F.window_logits(W, cfg, x, scope, mask_kind="bidirectional", mask_geometry=None,
+                              logits_convention="dream_ar_shift")
+    else:
+        x = rng.integers(0, 900, 64).tolist() + [g.mask_token_id] * 32
+        scope = list(range(64, 96))
+        with rt.session(bd3_session_config(32, 16, len(x))) as s:
+            got = s.execute_window(x, scope, mask_geometry=(0, 32)).array()
+        ref = F.forward_full(W, cfg, x, mask_kind="d2f_hybrid", mask_geometry=(0, 32),
+                             output_rows=scope)
+    err = rel_err_rows(got, ref)
+    _say(f"  logits rel err max={err.max():.2e}")
+    assert err.max() < LOGITS_REL_TOL
+    rt.close()

@@ -183,6 +183,94 @@ def test_q4_linear_matches_brute_force_loop():
 # --------------------------------------------------------------------------- linear
 
 
+def test_round_half_away_known_values():
+    x = np.array([2.5, -2.5, 0.5, -0.5, 1.5, 0.49999997, -0.49999997, 3.4999998, 7.0, -0.0],
+                 dtype=np.float32)
+    want = np.array([3, -3, 1, -1, 2, 0, 0, 3, 7, 0], dtype=np.float32)
+    assert np.array_equal(O.round_half_away(x), want)
+    # off the .5 points it is numpy's nearest rounding
+    r = np.random.default_rng(0).normal(0, 20, 10000).astype(np.float32)
+    r = r[np.abs(r - np.trunc(r)) != 0.5]
+    assert np.array_equal(O.round_half_away(r), np.round(r))
+
+
+def test_q4_quantize_exact_affine_ramps():
+    q = np.random.default_rng(1).integers(0, 16, (3, 128))
+    q[:, 0], q[:, 64], q[:, 1], q[:, 65] = 0, 0, 15, 15  # both extremes in every group
+    # |w_min| > |w_max|: positive scale, bias = w_min
+    w = (-1.0 + 0.125 * q).astype(np.float32)
+    wq, s, b = O.q4_quantize(w)
+    assert np.array_equal(O.q4_unpack(wq), q)
+    assert np.all(s == 0.125) and np.all(b == -1.0)
+    assert np.array_equal(O.q4_dequant(wq, s, b), w)
+    # |w_max| >= |w_min|: the scale is negated and the bias is w_max
+    w2 = (1.0 - 0.125 * q).astype(np.float32)
+    wq2, s2, b2 = O.q4_quantize(w2)
+    assert np.array_equal(O.q4_unpack(wq2), q)
+    assert np.all(s2 == -0.125) and np.all(b2 == 1.0)
+    assert np.array_equal(O.q4_dequant(wq2, s2, b2), w2)
+
+
+def test_q4_quantize_constant_and_zero_groups():
+    w = np.zeros((2, 128), dtype=np.float32)
+    w[1, :64] = 0.3
+    w[1, 64:] = -2.0
+    wq, s, b = O.q4_quantize(w)
+    assert np.all(O.q4_unpack(wq) == 0)
+    # an all-zero group keeps the negated minimum scale and a zero bias
+    assert s[0, 0] == O.bf16_round(np.float32(-1e-7)) and b[0, 0] == 0.0
+    # a constant group is its bias exactly (bf16 of the constant)
+    assert b[1, 0] == O.bf16_round(np.float32(0.3)) and b[1, 1] == -2.0
+    deq = O.q4_dequant(wq, s, b)
+    assert np.array_equal(deq[1], O.bf16_round(w[1]))
+
+
+def test_q4_quantize_rounds_halves_away_from_zero():
+    # scale 0.125, bias -1: -0.6875 sits at q = 2.5 exactly and goes to 3
+    w = np.full((1, 64), 0.0, dtype=np.float32)
+    w[0, 0], w[0, 1], w[0, 2] = -1.0, 0.875, -0.6875
+    w[0, 3:] = -1.0 + 0.125 * (np.arange(61) % 16)
+    q = O.q4_unpack(O.q4_quantize(w)[0])[0]
+    assert q[2] == 3
+
+
+def test_q4_quantize_is_nearest_grid_point():
+    rng = np.random.default_rng(2)
+    w = (rng.normal(0, 0.02, (16, 256)) + rng.normal(0, 0.01, (16, 1))).astype(np.float32)
+    w[3, :64] = np.abs(w[3, :64])   # one-signed groups
+    w[4, 64:128] = -np.abs(w[4, 64:128])
+    wq, s, b, s32, b32 = O.q4_quantize(w, return_fp32=True)
+    wb = O.bf16_round(w).astype(np.float64).reshape(16, 4, 64)
+    q = O.q4_unpack(wq).astype(np.float64).reshape(16, 4, 64)
+    grid = b32[..., None, None] + s32[..., None, None] * np.arange(16.0)  # [16, 4, 1, 16]
+    dist = np.abs(wb[..., None] - grid)                                     # [16, 4, 64, 16]
+    best = dist.min(axis=-1)
+    chosen = np.take_along_axis(dist, q[..., None].astype(np.int64), axis=-1)[..., 0]
+    # brute force over the 16 levels: the chosen level is a nearest one (fp32 slack)
+    assert np.all(chosen <= best + 1e-6 * np.abs(s32)[..., None])
+    # unclamped levels are within half a step, clamped ones within a step
+    err = np.abs(wb - (b32[..., None] + s32[..., None] * q))
+    assert np.all(err <= np.abs(s32)[..., None] * np.where(q == 15, 1.0, 0.5) * (1 + 1e-5))
+    # the edge value sits exactly on the fp32 grid (bias = edge)
+    edge_side = np.abs(wb.min(-1)) > np.abs(wb.max(-1))
+    edge = np.where(edge_side, wb.min(-1), wb.max(-1))
+    assert np.all(b32 == edge)
+    # zero lies on the grid: bias / scale is (minus) an integer level (the q0
+    # adjustment), not the raw (w_max - w_min) / 15 step
+    ratio = b32.astype(np.float64) / s32
+    assert np.all(np.abs(ratio - np.round(ratio)) < 1e-4)
+    raw = (wb.max(-1) - wb.min(-1)) / 15
+    assert np.mean(np.abs(np.abs(s32) - raw) > 1e-6 * raw) > 0.5
+    # stored scale/bias are the bf16 roundings of the fp32 ones
+    assert np.array_equal(s, O.bf16_round(s32)) and np.array_equal(b, O.bf16_round(b32))
+
+
+def test_q4_quantize_input_is_rounded_to_bf16_first():
+    w = np.random.default_rng(3).normal(0, 0.02, (4, 64)).astype(np.float32)
+    for a, b in zip(O.q4_quantize(w), O.q4_quantize(O.bf16_round(w))):
+        assert np.array_equal(a, b)
+
+
 def test_bf16_linear_matches_torch_bf16_matmul():
     """(x.astype(bf16) @ W.T) with a bf16 result, as torch's bf16 CPU matmul."""
     x = RNG.standard_normal((5, 96)).astype(np.float32)
