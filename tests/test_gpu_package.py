@@ -153,3 +153,31 @@ def test_runtime_from_package_matches_oracle(tmp_path, fmt, q4, dream):
     _say(f"  logits rel err max={err.max():.2e}")
     assert err.max() < LOGITS_REL_TOL
     rt.close()
+
+
+def test_engine_generates_from_package(tmp_path):
+    from diffusorrt_amd import decode
+    from diffusorrt_amd.engine import RocmEngine
+    from diffusorrt_amd.runtime import bd3_session_config
+
+    _say("engine from package")
+    g = tiny_geometry()
+    root = write_package(tmp_path / "pkg", g, random_weights(g, 22, dtype=torch.bfloat16))
+    prompt = np.random.default_rng(4).integers(0, 900, 64).tolist()
+    with RocmEngine(str(root), precision="q4", max_forward_rows=512, max_positions=256) as eng:
+        assert eng.plan.decode_strategy == "bd3_fixed_quota" and eng.runtime.weight_kind == "q4"
+        res = eng.generate_ids(prompt, max_tokens=64)
+        assert res.backend == "rocm" and res.decodes == 1 and res.steps == 128
+        # the engine is the session API plus its plan: the same tokens either way
+        with eng.runtime.session(bd3_session_config(32, res.steps, 128)) as s:
+            direct = decode.generate_device_tokens(
+                s, prompt, max_tokens=64, mask_token_id=g.mask_token_id,
+                eos_token_id=g.eos_token_id, steps=res.steps, block_size=32)
+        assert res.token_ids == direct.visible_generated_token_ids
+        # seeded sampling on the device is reproducible
+        a = eng.generate_ids(prompt, max_tokens=32, temperature=0.8, seed=7)
+        b = eng.generate_ids(prompt, max_tokens=32, temperature=0.8, seed=7)
+        assert a.seed == 7 and a.token_ids == b.token_ids
+        # no limit: one decode up to the sequence limit (256 - 64 positions)
+        c = eng.generate_ids(prompt, max_tokens=None)
+        assert c.decodes == 1 and c.budget == 192 and len(c.token_ids) <= 192
