@@ -103,7 +103,7 @@ def forward_full(weights, cfg, token_ids, *, mask_kind, mask_geometry=None,
 
 
 def window_logits(weights, cfg, token_ids, scope, *, mask_kind, mask_geometry,
-                  logits_convention):
+                  logits_convention, operand_round=None):
     """Convention-applied logits for ``scope`` positions (``execute_window``).
 
     Raw row selection per ``_required_raw_row`` (``mlx_d2f_forward.py:74-93``);
@@ -113,6 +113,7 @@ def window_logits(weights, cfg, token_ids, scope, *, mask_kind, mask_geometry,
                 for p in scope]
     uniq = sorted(set(raw_rows))
     logits = forward_full(weights, cfg, token_ids, mask_kind=mask_kind,
-                          mask_geometry=mask_geometry, output_rows=uniq)
+                          mask_geometry=mask_geometry, output_rows=uniq,
+                          operand_round=operand_round)
     index = {r: j for j, r in enumerate(uniq)}
     return logits[[index[r] for r in raw_rows]]
