@@ -86,5 +86,5 @@ struct StepDesc {
   int32_t step;             // sampling forward index
   uint64_t seed;
   float temperature;
-  int32_t pad;
+  int32_t exclude_col;      // vocabulary column left out of the scoring (-1: none)
 };

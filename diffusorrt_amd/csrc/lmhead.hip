@@ -61,11 +61,14 @@ __global__ __launch_bounds__(64 * WAVES) void lmhead_kernel(
     const float* __restrict__ xsum, int M, int N, int K, int chunk_k,
     float* __restrict__ logits_out, LmStat* __restrict__ stats, float temperature_arg,
     uint64_t seed_arg, int step_arg, const int32_t* __restrict__ positions,
-    const StepDesc* __restrict__ desc) {
+    const StepDesc* __restrict__ desc, int exclude_arg) {
   // sampling controls come from the step descriptor when one is given (graph replays)
   const float temperature = desc ? desc->temperature : temperature_arg;
   const uint64_t seed = desc ? desc->seed : seed_arg;
   const int step = desc ? desc->step : step_arg;
+  // a column left out of the statistics (the canvas MASK token of threshold
+  // policies, backends/diffusion_runtime.py:256-282): -inf for max, sum and draw
+  const int excl = desc ? desc->exclude_col : exclude_arg;
   constexpr int NT = 2;
   const int G = K >> 6, KC = K >> 4;
   const int NTILES = N >> 5, NB = N >> 6;
@@ -180,7 +183,8 @@ __global__ __launch_bounds__(64 * WAVES) void lmhead_kernel(
         float v = acc[j][r];
         if (WK == 1) v = round_bf16(v);
         const int row = mfma_row(r, lane);
-        ttile[row * 65 + j * 32 + (lane & 31)] = v;
+        ttile[row * 65 + j * 32 + (lane & 31)] =
+            (nt0 + j) * 32 + (lane & 31) == excl ? -INFINITY : v;
         if (logits_out && m0 + row < M)
           logits_out[(int64_t)(m0 + row) * N + (nt0 + j) * 32 + (lane & 31)] = v;
       }
@@ -302,11 +306,11 @@ extern "C" __global__ void lmhead_finalize_kernel(const LmStat* __restrict__ sta
 template __global__ void lmhead_kernel<0, 4, 4>(const uint32_t*, const uint32_t*, const uint16_t*,
                                                 const void*, const float*, int, int, int, int,
                                                 float*, LmStat*, float, uint64_t, int,
-                                                const int32_t*, const StepDesc*);
+                                                const int32_t*, const StepDesc*, int);
 template __global__ void lmhead_kernel<1, 4, 8>(const uint32_t*, const uint32_t*, const uint16_t*,
                                                 const void*, const float*, int, int, int, int,
                                                 float*, LmStat*, float, uint64_t, int,
-                                                const int32_t*, const StepDesc*);
+                                                const int32_t*, const StepDesc*, int);
 
 namespace drt {
 
@@ -314,7 +318,8 @@ size_t lmhead_stats_bytes(int M, int N) { return (size_t)M * (N / 64) * sizeof(L
 
 void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* logits_out,
             void* stats, float temperature, uint64_t seed, int step, const int32_t* positions,
-            double* scores, int32_t* tokens, hipStream_t s, const StepDesc* desc) {
+            double* scores, int32_t* tokens, hipStream_t s, const StepDesc* desc,
+            int exclude_col) {
   require(w.N % 64 == 0, "lm head needs vocab % 64 == 0");
   require(M >= 1, "lm head needs at least one row");
   const int chunk_k = std::min(512, w.K);
@@ -331,7 +336,8 @@ void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* 
     const double bytes = (double)w.N * w.K / 2 + (double)w.N * w.K / 16 + 2.0 * M * w.K;
     DRT_LAUNCH(Profiler::LMHEAD, bytes, fn, grid, dim3(64 * WAVES), lds, s, w.qw.as<uint32_t>(),
                w.sb.as<uint32_t>(), (const uint16_t*)nullptr, act, xsum, M, w.N, w.K, chunk_k,
-               logits_out, (LmStat*)stats, temperature, seed, step, positions, desc);
+               logits_out, (LmStat*)stats, temperature, seed, step, positions, desc,
+               exclude_col);
   } else {
     auto fn = lmhead_kernel<1, WAVES, 8>;
     static size_t granted = 0;
@@ -340,7 +346,7 @@ void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* 
     DRT_LAUNCH(Profiler::LMHEAD, bytes, fn, grid, dim3(64 * WAVES), lds, s,
                (const uint32_t*)nullptr, (const uint32_t*)nullptr, w.wb.as<uint16_t>(), act, xsum,
                M, w.N, w.K, chunk_k, logits_out, (LmStat*)stats, temperature, seed, step,
-               positions, desc);
+               positions, desc, exclude_col);
   }
   DRT_HIP(hipGetLastError());
   if (scores && tokens) {

@@ -471,6 +471,7 @@ struct ForwardArgs {
   float temperature = 0.f;
   uint64_t seed = 0;
   int step = 0;
+  int exclude_col = -1;  // vocabulary column left out of the scores (-1: none)
 };
 
 // Rows [row0, row0 + n_rows) sit in one mask segment and see every key in
@@ -522,6 +523,7 @@ ForwardPtrs stage_forward(Runtime& rt, const ForwardArgs& a, int slot, bool grap
   hd.step = a.step;
   hd.seed = a.seed;
   hd.temperature = a.temperature;
+  hd.exclude_col = a.exclude_col;
   ForwardPtrs p;
   p.desc = &d->desc;
   if (a.n_lm <= 32) {
@@ -709,7 +711,7 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
                   eps, d, fmt, rt.act_lm.p, rt.xsum_lm.as<float>(), p.n_lm_launch, s);
     lmhead(rt.lm_head, rt.act_lm.p, rt.xsum_lm.as<float>(), p.n_lm_launch, a.logits, rt.stats.p,
            a.temperature, a.seed, a.step, p.lm_pos, rt.scores.as<double>(),
-           rt.tokens_out.as<int32_t>(), s, desc);
+           rt.tokens_out.as<int32_t>(), s, desc, a.exclude_col);
   }
 }
 
@@ -971,15 +973,18 @@ int32_t drt_session_open(uint64_t runtime, const drt_session_config* config,
     const drt_session_config& c = *config;
     const bool bd3 = c.decode_strategy == DRT_DECODE_BD3_FIXED_QUOTA;
     const bool fq = c.decode_strategy == DRT_DECODE_FIXED_QUOTA;
+    const bool bt = c.decode_strategy == DRT_DECODE_BLOCK_THRESHOLD;
     const bool window_only = c.decode_strategy < 0;  // forward-only window session
-    if (!bd3 && !fq && !window_only)
-      fail(UNSUPPORTED, "rocm sessions run only fixed_quota and bd3_fixed_quota");
-    if (bd3) require(c.attention_mask_kind == DRT_MASK_D2F_HYBRID,
-                     "bd3_fixed_quota runs only on a d2f_hybrid graph");
+    if (!bd3 && !fq && !bt && !window_only)
+      fail(UNSUPPORTED, "rocm sessions run only block_threshold, fixed_quota and bd3_fixed_quota");
+    if (bd3 || bt) require(c.attention_mask_kind == DRT_MASK_D2F_HYBRID,
+                           "bd3_fixed_quota and block_threshold run only on a d2f_hybrid graph");
     if (fq) require(c.attention_mask_kind == DRT_MASK_BIDIRECTIONAL,
                     "fixed_quota runs only on a bidirectional graph");
-    if (!window_only) require(c.commit_policy == DRT_COMMIT_FIXED_QUOTA,
-                              "fixed-quota strategies need the fixed_quota commit policy");
+    if (bd3 || fq) require(c.commit_policy == DRT_COMMIT_FIXED_QUOTA,
+                           "fixed-quota strategies need the fixed_quota commit policy");
+    if (bt) require(c.commit_policy == DRT_COMMIT_THRESHOLD,
+                    "block_threshold needs the threshold commit policy");
     auto sess = std::make_shared<Session>();
     sess->rt = rt;
     sess->cfg = c;
@@ -1000,7 +1005,12 @@ int32_t drt_session_start(uint64_t session, const int32_t* tokens, int32_t n_tok
     require(block_size >= 1 && prompt_len >= 0 && prompt_len <= n_tokens, "bad block geometry");
     require(steps >= 1, "steps must be >= 1");
     require(!(temperature < 0.0) && std::isfinite(temperature), "temperature must be >= 0");
-    if (exact_kv) fail(UNSUPPORTED, "D2F exact K/V is not offered by the fixed-quota path");
+    const bool threshold = s->cfg.decode_strategy == DRT_DECODE_BLOCK_THRESHOLD;
+    // block_threshold runs over the exact prompt + frozen-block K/V either way:
+    // every cached row is what a full forward of the canvas computes for it
+    if (exact_kv && !threshold)
+      fail(UNSUPPORTED, "D2F exact K/V belongs to block_threshold, not the fixed-quota path");
+    if (threshold) require(temperature == 0.0, "block_threshold decodes greedily (temperature 0)");
     if (s->cfg.attention_mask_kind == DRT_MASK_BIDIRECTIONAL)
       require(n_tokens <= r.max_rows, "a bidirectional canvas must fit max_forward_rows");
     for (int i = 0; i < n_tokens; ++i)
@@ -1050,12 +1060,20 @@ int32_t drt_session_propose(uint64_t session, const int32_t* frontier, int32_t n
       require(frozen_prefix >= 0 && frozen_prefix < window_end, "frozen_prefix outside the window");
       require(Session::seg_start(frozen_prefix, s->origin, s->block) == frozen_prefix,
               "frozen_prefix must start a block of the session geometry");
+      // Under the Dream logits shift position p reads row p - 1, so the block's
+      // first position reads the last row before the block: the forward then
+      // starts one row early and recomputes that row over its own (cached)
+      // context -- the reference's shift-feeder row
+      // (backends/mlx_d2f_forward.py:226-232). Its K/V is rewritten with what
+      // the cache already holds for it.
+      int row0 = frozen_prefix;
       for (int i = 0; i < n_frontier; ++i) {
         const int p = frontier[i];
         require(p >= frozen_prefix && p < window_end,
                 "frontier position outside [frozen_prefix, window_end)");
         const int rr = s->raw_row(p);
-        require(rr >= frozen_prefix, "frontier reads a row before frozen_prefix");
+        require(rr >= frozen_prefix - 1, "frontier reads a row before frozen_prefix - 1");
+        row0 = std::min(row0, rr);
       }
       // An earlier frozen prefix shrinks the exact cache; a later one commits blocks.
       if (s->cache_len > frozen_prefix) s->cache_len = frozen_prefix;
@@ -1086,13 +1104,14 @@ int32_t drt_session_propose(uint64_t session, const int32_t* frontier, int32_t n
         forwarded += todo;
         s->cache_len = frozen_prefix;
       }
-      a.row0 = frozen_prefix;
-      a.n_rows = window_end - frozen_prefix;
+      a.row0 = row0;
+      a.n_rows = window_end - row0;
       a.n_keys = window_end;
       a.mask_kind = 1;
       a.mask_prompt_len = s->origin;
       a.mask_block = s->block;
-      if (!(s->graphable(a.n_rows) && n_frontier <= 32)) s->upload_tokens(frozen_prefix, window_end);
+      if (s->cfg.decode_strategy == DRT_DECODE_BLOCK_THRESHOLD) a.exclude_col = s->mask_id;
+      if (!(s->graphable(a.n_rows) && n_frontier <= 32)) s->upload_tokens(row0, window_end);
     } else {
       // Full bidirectional canvas, no cache (Dream / MDLM fixed_quota).
       for (int i = 0; i < n_frontier; ++i)

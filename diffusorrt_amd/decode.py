@@ -1,13 +1,16 @@
-"""Host control plane of the denoise loop for the two fixed-quota strategies.
+"""Host control plane of the denoise loop for the strategies the device session
+runs: the two fixed-quota policies and Dream's block threshold.
 
 Mirrors the reference's ``backends/diffusion_runtime.py`` (``MaskState``
-:387-558, ``BlockLayout`` :1099-1141, ``FixedQuotaCommit`` :1145-1196,
-``BD3FixedQuotaCommit`` :1200-1346, ``run_decode_loop`` :1829-1991),
+:387-558, ``BlockThresholdCommit`` :1023-1098, ``BlockLayout`` :1099-1141,
+``FixedQuotaCommit`` :1145-1196, ``BD3FixedQuotaCommit`` :1200-1346,
+``run_decode_loop`` :1829-1991),
 ``backends/decode_session.py`` (``DecodeRequest.prepare`` :113-210) and
 ``backends/device_runtime.py`` (``_run_device_state`` :108-183,
 ``generate_device_tokens`` :186-274), limited to what the device route needs:
 the device session scores each frontier row and the shared commit policy here
-picks the rows (``argsort(-score)[:quota]``) and commits them.
+picks the rows (``argsort(-score)[:quota]``, or every row at or above the
+confidence threshold) and commits them.
 """
 from __future__ import annotations
 
@@ -115,7 +118,57 @@ def topk_count_choices(scores, transfer_count: int) -> list:
     return [int(i) for i in chosen]
 
 
+def threshold_choices(scores, threshold: float) -> list:
+    """Rows at or above ``threshold``; the single most confident row when none
+    clears it (``diffusion_runtime.py:302-314``)."""
+    conf = np.asarray(scores, dtype=np.float64)
+    chosen = np.flatnonzero(conf >= float(threshold))
+    if chosen.size == 0:
+        return [int(np.argmax(conf))]
+    return [int(i) for i in chosen]
+
+
 # --------------------------------------------------------------------------- policies
+
+
+@dataclass
+class BlockThresholdCommit:
+    """Block-sequential threshold commit (``diffusion_runtime.py:1023-1098``): the
+    frontier is the current left-to-right block of ``block_size`` fillable
+    positions still masked; the pointer moves past fully committed blocks; STOP
+    when none remain. ``select`` commits every row at or above the threshold
+    (floor of one). The step budget is the request's ``steps``
+    (``:1854-1857``)."""
+
+    confidence_threshold: float
+    block_size: int
+    requested_steps: int
+    name: str = field(default="block_threshold", init=False)
+    _block_index: int = field(default=0, init=False)
+
+    def __post_init__(self):
+        if self.block_size <= 0 or self.requested_steps <= 0:
+            raise ValueError("block_threshold requires positive block_size and steps")
+        if not 0.0 <= float(self.confidence_threshold) <= 1.0:
+            raise ValueError("confidence_threshold must lie in [0, 1]")
+
+    @property
+    def iteration_limit(self) -> int:
+        return self.requested_steps
+
+    def plan(self, *, state: MaskState, step: int) -> StepPlan:
+        fillable = state.all_fillable_positions()
+        while self._block_index < len(fillable):
+            block = fillable[self._block_index:self._block_index + self.block_size]
+            masked = [p for p in block if state.x[p] == state.mask_token_id]
+            if masked:
+                return StepPlan(frontier=masked)
+            self._block_index += self.block_size
+        return StepPlan(frontier=[], stop=True)
+
+    def select(self, *, scores, step: int) -> list:
+        return threshold_choices(scores, self.confidence_threshold)
+
 
 
 @dataclass
@@ -291,14 +344,18 @@ def generate_device_tokens(session, prompt_token_ids: list, *, max_tokens: int,
                            decode_strategy: str = "bd3_fixed_quota",
                            requires_prompt_block_alignment: bool = True,
                            temperature: float = 0.0, seed: int = 0,
-                           memory_budget_bytes: int = 0,
+                           memory_budget_bytes: int = 0, confidence_threshold: float = 0.9,
                            cancelled: Callable[[], bool] | None = None,
                            trace: list | None = None) -> DecodeResult:
-    """Run a fixed-quota policy with scoring on the device
-    (``backends/device_runtime.py:108-274``)."""
-    if decode_strategy not in {"fixed_quota", "bd3_fixed_quota"}:
-        raise ValueError("the rocm device session runs fixed_quota and bd3_fixed_quota, "
-                         f"not {decode_strategy!r}")
+    """Run a policy with scoring on the device (``backends/device_runtime.py:108-274``).
+    ``block_threshold`` scores without the MASK column (the session leaves it out
+    of the softmax and argmax) and decodes greedily over the exact K/V of the
+    prompt and the frozen blocks."""
+    if decode_strategy not in {"fixed_quota", "bd3_fixed_quota", "block_threshold"}:
+        raise ValueError("the rocm device session runs block_threshold, fixed_quota and "
+                         f"bd3_fixed_quota, not {decode_strategy!r}")
+    if decode_strategy == "block_threshold" and temperature != 0:
+        raise ValueError("block_threshold decodes greedily; temperature must be 0")
     for name, value, minimum in (("max_tokens", max_tokens, 0), ("steps", steps, 1),
                                  ("block_size", block_size, 1),
                                  ("memory_budget_bytes", memory_budget_bytes, 0)):
@@ -314,7 +371,18 @@ def generate_device_tokens(session, prompt_token_ids: list, *, max_tokens: int,
     state = MaskState(x=[*prompt_token_ids, *([mask_token_id] * max_tokens)],
                       prompt_len=prompt_len, mask_token_id=mask_token_id,
                       eos_token_id=eos_token_id)
-    if decode_strategy == "bd3_fixed_quota":
+    exact_kv = False
+    if decode_strategy == "block_threshold":
+        # D2F over the exact prompt + frozen-block K/V: blocks count from the
+        # prompt, each proposal forwards the active block (and the Dream shift's
+        # feeder row) over the cached prefix (backends/device_runtime.py:108-183)
+        layout = None
+        policy = BlockThresholdCommit(confidence_threshold=confidence_threshold,
+                                      block_size=block_size, requested_steps=steps)
+        origin = prompt_len
+        exact_kv = True
+        loop_kind = "rocm_dream_block_threshold"
+    elif decode_strategy == "bd3_fixed_quota":
         layout = BlockLayout(start=prompt_len, length=max_tokens, block_size=block_size, origin=0)
         policy = BD3FixedQuotaCommit(block_size=block_size, requested_steps=steps,
                                      generated_token_count=max_tokens, block_layout=layout,
@@ -328,11 +396,17 @@ def generate_device_tokens(session, prompt_token_ids: list, *, max_tokens: int,
         origin = prompt_len
         loop_kind = "rocm_bidirectional_fixed_quota"
     session.start_device(state.x, prompt_len=origin, block_size=block_size,
-                         mask_token_id=mask_token_id, exact_kv=False, steps=steps,
+                         mask_token_id=mask_token_id, exact_kv=exact_kv, steps=steps,
                          memory_budget_bytes=memory_budget_bytes,
                          temperature=float(temperature), seed=int(seed))
 
     def propose(plan):
+        if decode_strategy == "block_threshold":
+            block = (min(plan.frontier) - origin) // block_size
+            frozen = origin + block * block_size
+            return session.propose_device(plan.frontier,
+                                          window_end=min(len(state.x), frozen + block_size),
+                                          frozen_prefix=frozen)
         if layout is None:
             return session.propose_device(plan.frontier, window_end=len(state.x),
                                           frozen_prefix=state.prompt_len)

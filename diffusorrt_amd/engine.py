@@ -49,6 +49,7 @@ class DecodePlan:
     block_size: int
     steps: int
     requires_prompt_block_alignment: bool = False
+    confidence_threshold: float = 0.9
 
     @property
     def whole_canvas(self) -> bool:
@@ -63,10 +64,12 @@ DECODE_POLICIES = {
                                      128, True),
     "fixed_quota_ragged_v1": DecodePlan("fixed_quota_ragged_v1", "bd3_fixed_quota", "d2f_hybrid",
                                         32, 128, False),
+    # Dream's policy: 8-token prompt-relative blocks, threshold 0.9, over the
+    # exact K/V of the prompt and the frozen blocks; the step budget is the
+    # device route's default (backends/device_runtime.py:186-197)
+    "block_threshold_v1": DecodePlan("block_threshold_v1", "block_threshold", "d2f_hybrid", 8,
+                                     512, False, 0.9),
 }
-# The reference's block-threshold policy (Dream's and LLaDA's default) needs the
-# D2F exact-K/V session, which this backend does not offer.
-UNSUPPORTED_POLICIES = ("block_threshold_v1",)
 ARCHITECTURE_POLICY = {"qwen2_dream": "block_threshold_v1",
                        "qwen3_mdlm": "bidirectional_fixed_quota_v1",
                        "qwen3_bd3lm": "bd3_fixed_quota_v1"}
@@ -80,19 +83,17 @@ def admit_decode_plan(architecture: str, model_config: dict | None = None, *,
                       policy: str | None = None, **overrides) -> DecodePlan:
     """The decode plan of a package: its architecture's policy (or ``policy``),
     with the BD3 contract's package keys checked (``model_definitions.py:303-331``)
-    and explicit ``block_size`` / ``steps`` / ``decode_strategy`` overrides for a
-    fixed-quota policy (the benchmark configurations pass them directly)."""
+    and explicit ``decode_strategy`` / ``block_size`` / ``steps`` /
+    ``confidence_threshold`` overrides (the benchmark configurations run Dream
+    with a fixed quota)."""
     key = policy or ARCHITECTURE_POLICY.get(architecture)
     if key is None:
         raise PlanNotAdmitted(f"no decode policy for architecture {architecture!r}")
-    if key in UNSUPPORTED_POLICIES and "decode_strategy" not in overrides:
-        raise PlanNotAdmitted(f"decode policy {key!r} needs the D2F exact-K/V session; the rocm "
-                              "backend runs fixed_quota and bd3_fixed_quota")
     base = DECODE_POLICIES.get(key)
-    if base is None and key not in UNSUPPORTED_POLICIES:
+    if base is None:
         raise ValueError(f"unknown decode policy {key!r}")
     cfg = model_config or {}
-    if base is not None and base.decode_strategy == "bd3_fixed_quota" and \
+    if base.decode_strategy == "bd3_fixed_quota" and \
             "mlx_diffusion_decode_strategy" in cfg:
         if cfg.get("mlx_diffusion_decode_strategy") != base.decode_strategy:
             raise ValueError(f"decode policy {key!r} requires "
@@ -104,22 +105,29 @@ def admit_decode_plan(architecture: str, model_config: dict | None = None, *,
                 base.requires_prompt_block_alignment:
             raise ValueError(f"decode policy {key!r} requires bd3_requires_prompt_block_alignment="
                              f"{base.requires_prompt_block_alignment!r}")
-    strategy = overrides.get("decode_strategy", base.decode_strategy if base else None)
-    if strategy not in ("fixed_quota", "bd3_fixed_quota"):
-        raise PlanNotAdmitted(f"decode_strategy {strategy!r}: the rocm backend runs fixed_quota "
-                              "and bd3_fixed_quota")
-    mask = "d2f_hybrid" if strategy == "bd3_fixed_quota" else "bidirectional"
-    block = int(overrides.get("block_size", base.block_size if base else 64))
-    steps = int(overrides.get("steps", base.steps if base else 256))
+    strategy = overrides.get("decode_strategy", base.decode_strategy)
+    if strategy not in ("fixed_quota", "bd3_fixed_quota", "block_threshold"):
+        raise PlanNotAdmitted(f"decode_strategy {strategy!r}: the rocm backend runs "
+                              "block_threshold, fixed_quota and bd3_fixed_quota")
+    mask = "bidirectional" if strategy == "fixed_quota" else "d2f_hybrid"
+    same = strategy == base.decode_strategy
+    block = int(overrides.get("block_size", base.block_size if same else 64))
+    steps = int(overrides.get("steps", base.steps if same else 256))
     align = bool(overrides.get("requires_prompt_block_alignment",
-                               base.requires_prompt_block_alignment if base else False))
+                               base.requires_prompt_block_alignment if same else False))
+    tau = float(overrides.get("confidence_threshold", base.confidence_threshold))
     if block < 1 or steps < 1:
         raise ValueError("block_size and steps must be positive")
-    return DecodePlan(key, strategy, mask, block, steps, align)
+    if not 0.0 <= tau <= 1.0:
+        raise ValueError("confidence_threshold must lie in [0, 1]")
+    return DecodePlan(key, strategy, mask, block, steps, align, tau)
 
 
 def request_steps(plan: DecodePlan, max_tokens: int) -> int:
-    """``model.py:2252-2266``: at least one step per token of each block."""
+    """``model.py:2252-2266``: at least one step per token of each block for the
+    fixed-quota policies; the plan's own steps otherwise."""
+    if plan.decode_strategy == "block_threshold":
+        return plan.steps
     blocks = (max_tokens + plan.block_size - 1) // plan.block_size
     return max(plan.steps, blocks * plan.block_size)
 
@@ -232,11 +240,14 @@ class RocmEngine:
 
     def _session_config(self, max_total: int, steps: int) -> dict:
         p = self.plan
-        strategy = DecodeStrategy.BD3_FIXED_QUOTA if p.decode_strategy == "bd3_fixed_quota" \
-            else DecodeStrategy.FIXED_QUOTA
+        strategy = {"bd3_fixed_quota": DecodeStrategy.BD3_FIXED_QUOTA,
+                    "fixed_quota": DecodeStrategy.FIXED_QUOTA,
+                    "block_threshold": DecodeStrategy.BLOCK_THRESHOLD}[p.decode_strategy]
+        commit = CommitPolicy.THRESHOLD if p.decode_strategy == "block_threshold" \
+            else CommitPolicy.FIXED_QUOTA
         mask = AttentionMaskKind.D2F_HYBRID if p.attention_mask_kind == "d2f_hybrid" \
             else AttentionMaskKind.BIDIRECTIONAL
-        return {"decode_strategy": int(strategy), "commit_policy": int(CommitPolicy.FIXED_QUOTA),
+        return {"decode_strategy": int(strategy), "commit_policy": int(commit),
                 "attention_mask_kind": int(mask), "block_size": p.block_size, "steps": steps,
                 "max_tokens": max_total}
 
@@ -245,6 +256,9 @@ class RocmEngine:
                      cancelled: Callable[[], bool] | None = None,
                      trace: list | None = None) -> GenerateResult:
         validate_request(max_tokens=max_tokens, temperature=temperature, seed=seed)
+        if temperature != 0 and self.plan.decode_strategy == "block_threshold":
+            raise ValueError("this model decodes with block_threshold, which is greedy; "
+                             "temperature sampling belongs to the fixed-quota policies")
         prompt_ids = [int(t) for t in prompt_ids]
         if not prompt_ids:
             raise ValueError("a request needs a non-empty prompt")
@@ -268,6 +282,7 @@ class RocmEngine:
                     decode_strategy=self.plan.decode_strategy,
                     requires_prompt_block_alignment=self.plan.requires_prompt_block_alignment,
                     temperature=float(temperature), seed=0 if seed is None else int(seed),
+                    confidence_threshold=self.plan.confidence_threshold,
                     cancelled=cancelled, trace=trace)
 
         with self._lock:

@@ -296,6 +296,13 @@ def bd3_session_config(block_size: int, steps: int, max_tokens: int) -> dict:
             "block_size": block_size, "steps": steps, "max_tokens": max_tokens}
 
 
+def block_threshold_session_config(block_size: int, steps: int, max_tokens: int) -> dict:
+    return {"decode_strategy": int(DecodeStrategy.BLOCK_THRESHOLD),
+            "commit_policy": int(CommitPolicy.THRESHOLD),
+            "attention_mask_kind": int(AttentionMaskKind.D2F_HYBRID),
+            "block_size": block_size, "steps": steps, "max_tokens": max_tokens}
+
+
 def fixed_quota_session_config(block_size: int, steps: int, max_tokens: int) -> dict:
     return {"decode_strategy": int(DecodeStrategy.FIXED_QUOTA),
             "commit_policy": int(CommitPolicy.FIXED_QUOTA),

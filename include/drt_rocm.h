@@ -43,8 +43,8 @@ enum {
 enum { DRT_F32 = 0, DRT_F64 = 1, DRT_BF16 = 2, DRT_I32 = 3, DRT_I64 = 4, DRT_U8 = 5, DRT_F16 = 6 };
 
 /* DecodeStrategy / CommitPolicy / AttentionMaskKind values (abi/enums.py:14-43). */
-enum { DRT_DECODE_FIXED_QUOTA = 6, DRT_DECODE_BD3_FIXED_QUOTA = 7 };
-enum { DRT_COMMIT_FIXED_QUOTA = 3 };
+enum { DRT_DECODE_BLOCK_THRESHOLD = 0, DRT_DECODE_FIXED_QUOTA = 6, DRT_DECODE_BD3_FIXED_QUOTA = 7 };
+enum { DRT_COMMIT_THRESHOLD = 2, DRT_COMMIT_FIXED_QUOTA = 3 };
 enum { DRT_MASK_BIDIRECTIONAL = 0, DRT_MASK_D2F_HYBRID = 1, DRT_MASK_FULL = 2 };
 
 /* Logits conventions (mlx_d2f_forward.py:74-93). */

@@ -8,6 +8,10 @@ Restates, for the two fixed-quota strategies on this path:
     (``:1200-1346``),
   * ``run_decode_loop`` forward -> score -> select -> commit (``:1829-1991``)
     with ``exclude_mask_token=False`` (``:2199-2264``),
+  * and Dream's block-threshold policy: the block walk of
+    ``_block_frontier_plan`` (``:1023-1052``), the threshold choice with its
+    floor of one (``:302-314``) and the MASK column left out of the scoring
+    (``exclude_mask_token=True``, ``:256-282, 1955-1958``),
   * ``DecodeRequest.prepare`` canvas + BD3 absolute layout
     (``backends/decode_session.py:113-160``).
 
@@ -143,6 +147,67 @@ def run_fixed_quota_decode(prompt_ids, *, max_tokens, mask_id, eos_id, block_siz
             trace.append({"step": step, "frontier": list(frontier), "window_end": wend,
                           "scores": [float(s) for s in scores], "tokens": list(tokens),
                           "chosen": list(chosen), "quota": quota})
+        for r in chosen:
+            x[frontier[r]] = int(tokens[r])
+        committed += len(chosen)
+    out = finalize(x, prompt_len, mask_id, eos_id)
+    out.update({"x": x, "forward_count": forwards, "committed_token_count": committed})
+    return out
+
+
+def excluded_max_prob(logits, mask_id):
+    """``_exclude_mask_token`` then the float64 max-prob (``diffusion_runtime.py:
+    256-282, 179-192``): the MASK column becomes -inf before softmax and argmax."""
+    import numpy as np
+
+    values = np.array(logits, dtype=np.float32, copy=True)
+    if 0 <= int(mask_id) < values.shape[1]:
+        values[:, int(mask_id)] = -np.inf
+    return ops.raw_max_prob(values)
+
+
+def threshold_pick(scores, threshold):
+    """Every row with ``score >= threshold``, else the first most confident row."""
+    picked = [i for i, s in enumerate(scores) if float(s) >= float(threshold)]
+    if picked:
+        return picked
+    best = 0
+    for i, s in enumerate(scores):
+        if float(s) > float(scores[best]):
+            best = i
+    return [best]
+
+
+def run_block_threshold_decode(prompt_ids, *, max_tokens, mask_id, eos_id, block_size, steps,
+                               threshold, frontier_logits_fn, trace=None):
+    """Drive Dream's block-threshold decode. ``frontier_logits_fn(x, frontier,
+    window_end)`` returns the frontier's fp32 logits (convention applied) for the
+    canvas forwarded up to ``window_end`` = the end of the active block (rows past
+    it are dead: the d2f mask hides them from the active rows)."""
+    x = list(prompt_ids) + [mask_id] * max_tokens
+    prompt_len = len(prompt_ids)
+    block_index = 0
+    forwards = committed = 0
+    for step in range(steps):
+        frontier = []
+        while block_index < max_tokens:
+            lo = prompt_len + block_index
+            hi = min(lo + block_size, len(x))
+            frontier = [p for p in range(lo, hi) if x[p] == mask_id]
+            if frontier:
+                break
+            block_index += block_size
+        if not frontier:
+            break
+        window_end = min(len(x), prompt_len + block_index + block_size)
+        logits = frontier_logits_fn(list(x), list(frontier), window_end)
+        forwards += 1
+        scores, tokens = excluded_max_prob(logits, mask_id)
+        chosen = threshold_pick(scores, threshold)
+        if trace is not None:
+            trace.append({"step": step, "frontier": list(frontier), "window_end": window_end,
+                          "scores": [float(s) for s in scores], "tokens": list(tokens),
+                          "chosen": list(chosen), "quota": len(chosen)})
         for r in chosen:
             x[frontier[r]] = int(tokens[r])
         committed += len(chosen)

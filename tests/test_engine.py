@@ -69,8 +69,11 @@ def test_backend_id_and_policies():
         ("fixed_quota", 64, 256, True)
     ragged = E.admit_decode_plan("qwen3_bd3lm", policy="fixed_quota_ragged_v1")
     assert not ragged.requires_prompt_block_alignment
-    with pytest.raises(E.PlanNotAdmitted):
-        E.admit_decode_plan("qwen2_dream")  # block_threshold needs the D2F session
+    bt = E.admit_decode_plan("qwen2_dream")  # Dream's own block-threshold policy
+    assert (bt.decode_strategy, bt.block_size, bt.steps, bt.confidence_threshold,
+            bt.attention_mask_kind, bt.whole_canvas) == ("block_threshold", 8, 512, 0.9,
+                                                         "d2f_hybrid", False)
+    assert E.request_steps(bt, 2000) == 512
     dream = E.admit_decode_plan("qwen2_dream", decode_strategy="fixed_quota", block_size=256,
                                 steps=64)
     assert (dream.decode_strategy, dream.block_size, dream.steps) == ("fixed_quota", 256, 64)
@@ -139,6 +142,8 @@ def test_whole_canvas_without_limit_decodes_in_chunks():
     g = tiny_dream_geometry(max_position_embeddings=64 + 300)
     eng, rt = _engine(g, plan_overrides={"decode_strategy": "fixed_quota", "block_size": 256,
                                          "steps": 64})
+    with pytest.raises(ValueError):  # block_threshold (Dream's default) is greedy
+        _engine(g)[0].generate_ids(list(range(64)), max_tokens=8, temperature=0.5)
     res = eng.generate_ids(list(range(64)), max_tokens=None)
     # limit = 364 - 64 = 300: chunks of 128, 128, 44, each joining the next prompt
     assert res.decodes == 3 and [len(c.visible_generated_token_ids) for c in res.chunks] == \

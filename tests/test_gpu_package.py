@@ -181,3 +181,24 @@ def test_engine_generates_from_package(tmp_path):
         # no limit: one decode up to the sequence limit (256 - 64 positions)
         c = eng.generate_ids(prompt, max_tokens=None)
         assert c.decodes == 1 and c.budget == 192 and len(c.token_ids) <= 192
+
+
+def test_engine_dream_block_threshold_from_package(tmp_path):
+    from diffusorrt_amd import decode
+    from diffusorrt_amd.engine import RocmEngine
+    from diffusorrt_amd.runtime import block_threshold_session_config
+
+    _say("engine dream block_threshold from package")
+    g = tiny_dream_geometry()
+    root = write_package(tmp_path / "pkg", g, random_weights(g, 23, dtype=torch.bfloat16))
+    prompt = np.random.default_rng(6).integers(0, 900, 45).tolist()
+    with RocmEngine(str(root), precision="q4", max_forward_rows=512, max_positions=256) as eng:
+        assert eng.plan.decode_strategy == "block_threshold" and eng.plan.block_size == 8
+        res = eng.generate_ids(prompt, max_tokens=16)
+        assert res.decodes == 1 and res.committed_token_count == 16
+        with eng.runtime.session(block_threshold_session_config(8, 512, 61)) as s:
+            direct = decode.generate_device_tokens(
+                s, prompt, max_tokens=16, mask_token_id=g.mask_token_id,
+                eos_token_id=g.eos_token_id, steps=512, block_size=8,
+                decode_strategy="block_threshold")
+        assert res.token_ids == direct.visible_generated_token_ids

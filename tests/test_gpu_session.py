@@ -324,3 +324,83 @@ def test_dream_real_shapes_window():
     _say(f"  dream window rel err max={err.max():.2e}")
     assert err.max() < LOGITS_REL_TOL
     rt.close()
+
+
+def test_dream_block_threshold_exact_kv():
+    """Dream's block-threshold policy on the device session: prompt-relative
+    8-row blocks over the exact K/V of the prompt and the frozen blocks, the
+    logits shift's feeder row, the MASK column left out of the scoring. The LM
+    head's MASK row is set to 4x the row of the first frontier row's top token,
+    so MASK would win that row if it were scored."""
+    from diffusorrt_amd import decode
+    from diffusorrt_amd import synthetic as syn
+    from diffusorrt_amd.runtime import Runtime, block_threshold_session_config
+
+    _say("dream block_threshold exact K/V")
+    geom = tiny_dream_geometry()
+    model = syn.build_model(geom, "q4", 13)
+    W, cfg = _oracle(model)
+    P_LEN, GEN, BS = 45, 24, 8
+    prompt = np.random.default_rng(5).integers(0, 900, P_LEN).tolist()
+    x = prompt + [geom.mask_token_id] * GEN
+
+    def ref_logits(W, canvas, frontier):
+        return F.window_logits(W, cfg, canvas, frontier, mask_kind="d2f_hybrid",
+                               mask_geometry=(P_LEN, BS), logits_convention="dream_ar_shift")
+
+    first = list(range(P_LEN, P_LEN + BS))
+    top = int(np.argmax(ref_logits(W, x, first)[0]))
+    lm = model.weights["lm_head.weight"]
+    m = geom.mask_token_id
+    lm.w_q[m] = lm.w_q[top]
+    lm.scales[m] = (lm.scales[top].float() * 4).to(torch.bfloat16)
+    lm.biases[m] = (lm.biases[top].float() * 4).to(torch.bfloat16)
+    W, cfg = _oracle(model)
+    raw = ref_logits(W, x, first)
+    assert int(np.argmax(raw[0])) == m  # MASK would win row 0
+
+    def excluded(logits):
+        out = np.array(logits, dtype=np.float32, copy=True)
+        out[:, m] = -np.inf
+        return out
+
+    rt = Runtime(model, max_forward_rows=512, max_positions=1024)
+    with rt.session(block_threshold_session_config(BS, 64, len(x))) as s:
+        with pytest.raises(ValueError):  # the threshold policy decodes greedily
+            s.start_device(x, prompt_len=P_LEN, block_size=BS, mask_token_id=m, exact_kv=True,
+                           steps=64, temperature=0.5)
+        # the prompt-relative d2f mask through execute_window (logits are raw)
+        win = s.execute_window(x[:P_LEN + BS], first, mask_geometry=(P_LEN, BS))
+        err = rel_err_rows(win.array(), raw)
+        _say(f"  window (prompt {P_LEN}, block {BS}) rel err max={err.max():.2e}")
+        assert err.max() < LOGITS_REL_TOL
+    trace = []
+    with rt.session(block_threshold_session_config(BS, 64, len(x))) as s:
+        res = decode.generate_device_tokens(
+            s, prompt, max_tokens=GEN, mask_token_id=m, eos_token_id=geom.eos_token_id,
+            steps=64, block_size=BS, decode_strategy="block_threshold", trace=trace)
+        metrics = s.device_metrics()
+    assert res.committed_token_count == GEN and res.remaining_mask_count == 0
+    assert all(m not in t["tokens"] for t in trace)
+    assert trace[0]["tokens"][0] == int(np.argmax(excluded(raw)[0]))
+    # the exact cache holds the prompt and the frozen blocks before the last block
+    assert metrics["rocm_kv_cache_len"] == P_LEN + GEN - BS
+    xx = list(x)
+    problems, ties = [], []
+    for t in trace:
+        ref = excluded(ref_logits(W, xx, t["frontier"]))
+        rep, bad = compare_proposals(t["scores"], t["tokens"], ref, quota=len(t["chosen"]),
+                                     gpu_chosen=t["chosen"])
+        ties += rep["report"]
+        problems += [(t["step"],) + tuple(b) for b in bad]
+        for r in t["chosen"]:
+            xx[t["frontier"][r]] = t["tokens"][r]
+    _say(f"  steps={len(trace)} near-ties reported: {ties}")
+    assert not problems, problems
+    if not ties:
+        ref_out = P.run_block_threshold_decode(
+            prompt, max_tokens=GEN, mask_id=m, eos_id=geom.eos_token_id, block_size=BS,
+            steps=64, threshold=0.9,
+            frontier_logits_fn=lambda c, f, w: ref_logits(W, c, f))
+        assert ref_out["x"] == res.full_token_ids
+    rt.close()

@@ -200,3 +200,81 @@ def test_topk_matches_oracle_and_numpy_quicksort():
         s = rng.random(rng.integers(1, 40))
         k = int(rng.integers(0, len(s) + 1))
         assert D.topk_count_choices(s, k) == O.topk_count_choices(s, k)
+
+
+def test_threshold_choices_closed_forms():
+    for pick in (D.threshold_choices, P.threshold_pick):
+        assert pick([0.95, 0.5, 0.91], 0.9) == [0, 2]
+        assert pick([0.9, 0.5], 0.9) == [0]            # at the threshold counts
+        assert pick([0.2, 0.7, 0.7], 0.9) == [1]        # floor of one: the first maximum
+        assert pick([0.3], 0.9) == [0]
+
+
+def test_excluded_max_prob_drops_the_mask_column():
+    logits = np.array([[0.0, 5.0, 1.0, 1.0], [2.0, 0.0, 0.0, 0.0]], dtype=np.float32)
+    scores, toks = P.excluded_max_prob(logits, mask_id=1)
+    # row 0: MASK (column 1) would win; without it columns 2, 3 tie -> first
+    assert toks == [2, 0]
+    e = np.exp(np.array([0.0, 1.0, 1.0]) - 1.0)
+    assert scores[0] == pytest.approx(e.max() / e.sum(), rel=1e-12)
+    # an out-of-vocabulary sentinel needs no exclusion
+    s2, t2 = P.excluded_max_prob(logits, mask_id=99)
+    assert t2 == [1, 0]
+
+
+def test_block_threshold_walk_closed_form():
+    """Blocks of 8 over 20 generated positions: [0, 8), [8, 16), [16, 20); each
+    step commits the rows at or above 0.9 (here: rows whose position is odd)
+    or the first most confident one; committed blocks are skipped."""
+    prompt, gen, bs = [1, 2, 3], 20, 8
+
+    def fn(x, frontier, wend):
+        out = np.full((len(frontier), 120), -4.0, dtype=np.float32)
+        for r, p in enumerate(frontier):
+            out[r, 7] = 12.0 if p % 2 else 1.0 + 0.01 * r
+        return out
+
+    trace = []
+    ref = P.run_block_threshold_decode(prompt, max_tokens=gen, mask_id=MASK, eos_id=EOS,
+                                       block_size=bs, steps=100, threshold=0.9,
+                                       frontier_logits_fn=fn, trace=trace)
+    assert [t["window_end"] for t in trace][:2] == [11, 11]
+    assert trace[0]["frontier"] == list(range(3, 11))
+    assert [trace[0]["frontier"][r] for r in trace[0]["chosen"]] == [3, 5, 7, 9]
+    # then the even positions one per step, highest 0.01*r bonus first (the last row)
+    assert [trace[1]["frontier"][r] for r in trace[1]["chosen"]] == [10]
+    assert ref["x"][3:] == [7] * gen and ref["committed_token_count"] == gen
+    # per block: 1 step for the odd rows + one per even row: 1+4, 1+4, 1+2
+    assert ref["forward_count"] == 5 + 5 + 3
+
+
+@pytest.mark.parametrize("prompt_len,gen,bs,steps,thr", [(5, 24, 8, 60, 0.9),
+                                                         (16, 33, 8, 40, 0.02),
+                                                         (8, 16, 4, 6, 0.5)])
+def test_product_block_threshold_matches_oracle(prompt_len, gen, bs, steps, thr):
+    vocab = 120
+    fn = _fake_logits(vocab)
+    prompt = list(np.random.default_rng(prompt_len).integers(0, 90, prompt_len))
+    trace_o = []
+    ref = P.run_block_threshold_decode(prompt, max_tokens=gen, mask_id=MASK, eos_id=EOS,
+                                       block_size=bs, steps=steps, threshold=thr,
+                                       frontier_logits_fn=fn, trace=trace_o)
+    state = D.MaskState(x=[*prompt, *([MASK] * gen)], prompt_len=prompt_len,
+                        mask_token_id=MASK, eos_token_id=EOS)
+    pol = D.BlockThresholdCommit(confidence_threshold=thr, block_size=bs, requested_steps=steps)
+
+    def propose(plan):
+        frozen = prompt_len + (min(plan.frontier) - prompt_len) // bs * bs
+        wend = min(len(state.x), frozen + bs)
+        scores, toks = P.excluded_max_prob(fn(list(state.x), plan.frontier, wend), MASK)
+        return scores, toks, len(plan.frontier)
+
+    trace_p = []
+    fwd, committed, _ = D.run_decode_loop(state, commit_policy=pol,
+                                          iteration_limit=pol.iteration_limit,
+                                          propose_fn=propose, commit_device_fn=lambda p, t: None,
+                                          trace=trace_p)
+    assert state.x == ref["x"]
+    assert fwd == ref["forward_count"] and committed == ref["committed_token_count"]
+    assert [t["chosen"] for t in trace_p] == [t["chosen"] for t in trace_o]
+    assert MASK not in [t for tr in trace_p for t in tr["tokens"]]
