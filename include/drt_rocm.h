@@ -145,17 +145,24 @@ int32_t drt_release_handle(uint64_t handle);
 /* Runtime(package, device="rocm", engine_config, precision, device_ordinal, budget). */
 int32_t drt_runtime_create(const drt_engine_config* engine, const drt_model_geometry* geometry,
                            const drt_tensor* weights, int32_t n_weights, uint64_t* out_runtime);
-/* runtime.session(session_config=...). */
+/* runtime.session(session_config=...): bd3_fixed_quota (fixed_quota commit, d2f_hybrid),
+ * fixed_quota (fixed_quota commit, bidirectional) or block_threshold (threshold commit,
+ * d2f_hybrid; device_runtime.py:186-274); decode_strategy < 0 opens a window-only session. */
 int32_t drt_session_open(uint64_t runtime, const drt_session_config* config,
                          uint64_t* out_session);
 /* session.start_device(tokens, prompt_len=origin, block_size, mask_token_id, exact_kv,
- *                      steps, memory_budget_bytes, temperature, seed). */
+ *                      steps, memory_budget_bytes, temperature, seed). exact_kv is for
+ * block_threshold sessions only (greedy: temperature 0); their scores leave the MASK
+ * column out of the softmax and argmax (diffusion_runtime.py:256-282). */
 int32_t drt_session_start(uint64_t session, const int32_t* tokens, int32_t n_tokens,
                           int32_t prompt_len, int32_t block_size, int32_t mask_token_id,
                           int32_t exact_kv, int32_t steps, int64_t memory_budget_bytes,
                           double temperature, uint64_t seed);
 /* session.propose_device(frontier, window_end, frozen_prefix) -> (scores f64, tokens,
- * forwarded_rows). Only these cross to the host. */
+ * forwarded_rows). Only these cross to the host. On a d2f_hybrid session rows
+ * [0, frozen_prefix) are served from the exact K/V cache (forwarded once when they
+ * freeze); under the Dream logits shift the forward also recomputes row
+ * frozen_prefix - 1, which the block's first position reads (mlx_d2f_forward.py:226-232). */
 int32_t drt_session_propose(uint64_t session, const int32_t* frontier, int32_t n_frontier,
                             int32_t window_end, int32_t frozen_prefix, double* out_scores,
                             int32_t* out_tokens, int32_t* out_forwarded_rows);
