@@ -207,7 +207,7 @@ size_t lmhead_stats_bytes(int M, int N);
 void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* logits_out,
             void* stats, float temperature, uint64_t seed, int step, const int32_t* positions,
             double* scores, int32_t* tokens, hipStream_t s, const StepDesc* desc = nullptr,
-            int exclude_col = -1);
+            int exclude_col = -1, const int* err_dev = nullptr, int* err_host = nullptr);
 
 // y = round_bf16(y) (+ bias after rounding); x fp32 -> bf16 bits.
 void round_bf16_inplace(float* y, int64_t n, const uint16_t* bias, int N, hipStream_t s);

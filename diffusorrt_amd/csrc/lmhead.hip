@@ -234,12 +234,17 @@ __global__ __launch_bounds__(64 * WAVES) void lmhead_kernel(
   }
 }
 
-// One 256-thread WG per row: join the N/64 block statistics in float64.
+// One 256-thread WG per row: join the N/64 block statistics in float64. scores
+// and tokens may be pinned host memory (the session's landing area: no copy
+// after the forward); err_host, when given, receives the forward's placement
+// and bounded-wait flags (*err_dev, final once the earlier kernels are done).
 extern "C" __global__ void lmhead_finalize_kernel(const LmStat* __restrict__ stats, int NB,
                                                   int sampling_arg,
                                                   const StepDesc* __restrict__ desc,
                                                   double* __restrict__ scores,
-                                                  int32_t* __restrict__ tokens) {
+                                                  int32_t* __restrict__ tokens,
+                                                  const int* __restrict__ err_dev,
+                                                  int* __restrict__ err_host) {
   const int sampling = desc ? (desc->temperature > 0.f) : sampling_arg;
   __shared__ float red_f[4];
   __shared__ int red_i[4];
@@ -247,6 +252,8 @@ extern "C" __global__ void lmhead_finalize_kernel(const LmStat* __restrict__ sta
   __shared__ int red_j[4];
   const int row = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (err_host && row == 0 && threadIdx.x == 0)
+    *err_host = __hip_atomic_load(err_dev, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const LmStat* st = stats + (int64_t)row * NB;
   // pass 1: global max and its first block
   float mx = -INFINITY;
@@ -319,7 +326,7 @@ size_t lmhead_stats_bytes(int M, int N) { return (size_t)M * (N / 64) * sizeof(L
 void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* logits_out,
             void* stats, float temperature, uint64_t seed, int step, const int32_t* positions,
             double* scores, int32_t* tokens, hipStream_t s, const StepDesc* desc,
-            int exclude_col) {
+            int exclude_col, const int* err_dev, int* err_host) {
   require(w.N % 64 == 0, "lm head needs vocab % 64 == 0");
   require(M >= 1, "lm head needs at least one row");
   const int chunk_k = std::min(512, w.K);
@@ -351,7 +358,7 @@ void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* 
   DRT_HIP(hipGetLastError());
   if (scores && tokens) {
     hipLaunchKernelGGL(lmhead_finalize_kernel, dim3(M), dim3(256), 0, s, (const LmStat*)stats, NB,
-                       (int)(temperature > 0.f), desc, scores, tokens);
+                       (int)(temperature > 0.f), desc, scores, tokens, err_dev, err_host);
     DRT_HIP(hipGetLastError());
   }
 }

@@ -124,7 +124,7 @@ struct Runtime {
   int max_rows = 0;
 
   // workspace (sized for max_rows)
-  DevBuf hidden, act, xsum, act_lm, xsum_lm, qbuf, attn_part, stats, scores, tokens_out, lm_rows,
+  DevBuf hidden, act, xsum, act_lm, xsum_lm, qbuf, attn_part, stats, lm_rows,
       lm_pos, logits;
   // split-K linears of <= 32-row forwards: partial tiles, arrival counters
   // (zeroed once; every kernel leaves them zero) and the residual stream's
@@ -139,9 +139,12 @@ struct Runtime {
   int n_xcc = 1;
   DevBuf placement_err;          // int, set by a kernel that finds itself on an unexpected XCD
   int* placement_host = nullptr; // pinned copy, read after each synchronized forward
-  // pinned landing area of a proposal's scores and tokens (the caller's arrays are
-  // pageable: a device-to-host copy into them takes the slow staged path)
+  // pinned landing area of a forward's scores and tokens, written by the LM head's
+  // last kernel (the caller's arrays are pageable)
   char* out_host = nullptr;
+  int lm_cap = 0;
+  double* scores_host() const { return (double*)out_host; }
+  int32_t* tokens_host() const { return (int32_t*)(out_host + (size_t)lm_cap * 8); }
   // Per-forward inputs: one pinned host slot + its device copy per forward, moved
   // by a single async copy. Slot 0 belongs to the commit graph, slot 1 to the
   // step graph; eager forwards rotate through the rest.
@@ -400,9 +403,10 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
   rt->act_lm.alloc((size_t)lm_cap * d * 2);
   rt->xsum_lm.alloc((size_t)lm_cap * (d / 64) * 4);
   rt->stats.alloc(lmhead_stats_bytes(lm_cap, V));
-  rt->scores.alloc((size_t)lm_cap * 8);
-  rt->tokens_out.alloc((size_t)lm_cap * 4);
-  DRT_HIP(hipHostMalloc((void**)&rt->out_host, (size_t)lm_cap * 12 + 16, hipHostMallocDefault));
+  // the forwards' scores and tokens land in pinned host memory, written by the
+  // LM head's last kernel: [lm_cap] doubles, then [lm_cap] ints
+  rt->lm_cap = lm_cap;
+  DRT_HIP(hipHostMalloc((void**)&rt->out_host, (size_t)lm_cap * 12 + 16, hipHostMallocCoherent));
   rt->lm_rows.alloc((size_t)lm_cap * 4);
   rt->lm_pos.alloc((size_t)lm_cap * 4);
   {
@@ -439,7 +443,7 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
     rt->n_xcc = std::max(1, nx);
     rt->placement_err.alloc(4);
     DRT_HIP(hipMemsetAsync(rt->placement_err.p, 0, 4, s));
-    DRT_HIP(hipHostMalloc((void**)&rt->placement_host, 4, hipHostMallocDefault));
+    DRT_HIP(hipHostMalloc((void**)&rt->placement_host, 4, hipHostMallocCoherent));
     *rt->placement_host = 0;
   }
   DRT_HIP(hipStreamSynchronize(s));
@@ -710,8 +714,8 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
     residual_norm(hidden, nullptr, 0, M, false, p.lm_rows, false, rt.final_norm.as<uint16_t>(),
                   eps, d, fmt, rt.act_lm.p, rt.xsum_lm.as<float>(), p.n_lm_launch, s);
     lmhead(rt.lm_head, rt.act_lm.p, rt.xsum_lm.as<float>(), p.n_lm_launch, a.logits, rt.stats.p,
-           a.temperature, a.seed, a.step, p.lm_pos, rt.scores.as<double>(),
-           rt.tokens_out.as<int32_t>(), s, desc, a.exclude_col);
+           a.temperature, a.seed, a.step, p.lm_pos, rt.scores_host(), rt.tokens_host(), s, desc,
+           a.exclude_col, rt.placement_err.as<int>(), rt.placement_host);
   }
 }
 
@@ -1135,18 +1139,12 @@ int32_t drt_session_propose(uint64_t session, const int32_t* frontier, int32_t n
     r.up_next = 2;  // the stream is drained below before any slot is reused
     forwarded += a.n_rows;
     DRT_HIP(hipEventRecord(r.ev1, r.stream));
-    char* land_scores = r.out_host;
-    char* land_tokens = r.out_host + (size_t)n_frontier * 8;
-    DRT_HIP(hipMemcpyAsync(land_scores, r.scores.p, (size_t)n_frontier * 8, hipMemcpyDeviceToHost,
-                           r.stream));
-    DRT_HIP(hipMemcpyAsync(land_tokens, r.tokens_out.p, (size_t)n_frontier * 4,
-                           hipMemcpyDeviceToHost, r.stream));
-    DRT_HIP(hipMemcpyAsync(r.placement_host, r.placement_err.p, 4, hipMemcpyDeviceToHost,
-                           r.stream));
+    // the LM head's last kernel wrote scores, tokens and the placement flags
+    // into pinned host memory: nothing to copy once the stream has drained
     DRT_HIP(hipStreamSynchronize(r.stream));
     check_placement(r);
-    std::memcpy(out_scores, land_scores, (size_t)n_frontier * 8);
-    std::memcpy(out_tokens, land_tokens, (size_t)n_frontier * 4);
+    std::memcpy(out_scores, r.scores_host(), (size_t)n_frontier * 8);
+    std::memcpy(out_tokens, r.tokens_host(), (size_t)n_frontier * 4);
     s->finish_timing();
     s->publish_profile();
     s->proposals += 1;

@@ -253,22 +253,30 @@ class BD3FixedQuotaCommit:
         return self.block_layout.count * self.steps_per_block
 
     def plan(self, *, state: MaskState, step: int) -> StepPlan:
-        if len(state.all_fillable_positions()) != self.generated_token_count:
+        x, prompt_len = state.x, state.prompt_len
+        if len(x) - prompt_len != self.generated_token_count:
             raise ValueError("BD3LM generated-token count changed during decode")
+        if (self.block_layout.start, self.block_layout.length) != (prompt_len,
+                                                                   self.generated_token_count):
+            raise ValueError("BD3LM block layout does not cover the generated region")
         if step >= self.iteration_limit:
             return StepPlan(frontier=[], stop=True)
-        if self.requires_prompt_block_alignment and state.prompt_len % self.block_size:
+        if self.requires_prompt_block_alignment and prompt_len % self.block_size:
             raise ValueError("BD3LM Candidate prompt length must be a multiple of block_size")
         spb = self.steps_per_block
+        generated = x[prompt_len:]
         # EOS ends the decode only at a block boundary (:1305-1309).
-        if step % spb == 0 and state.eos_token_id in state.x[state.prompt_len:]:
+        if step % spb == 0 and state.eos_token_id in generated:
             return StepPlan(frontier=[], stop=True)
-        masked = state.masked_positions()
-        if not masked:
+        mask = state.mask_token_id
+        if mask not in generated:  # no masked position left
             return StepPlan(frontier=[], stop=True)
         block_id = step // spb
+        # the block's span lies inside the generated region (the layout covers
+        # exactly [prompt_len, len(x)), checked above), so its masked positions
+        # are the masked positions of the canvas that fall in the span
         start, end = self.block_layout.span(block_id)
-        frontier = [p for p in masked if start <= p < end]
+        frontier = [p for p in range(start, end) if x[p] == mask]
         if self._active_block_id != block_id:
             self._active_block_id = block_id
             self._base, self._remainder = divmod(len(frontier), spb)
