@@ -660,6 +660,10 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
         fused_linear(f, FL_QKV, s);
       }
     }
+    const bool last = l == L - 1;
+    // commit-only forward: the last layer's K/V is written by its q|k|v epilogue;
+    // nothing after it is read
+    if (last && a.n_lm == 0) break;
     if (decode_attn)
       attention_decode(rt.kv_bf16, rt.qbuf.p, kv_layer(l), head_stride, M, Hq, Hkv, a.n_keys, desc,
                        ranges, o_part, rt.act.p, xs, fmt, s, rt.placement_err.as<int>());
@@ -667,8 +671,6 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
       attention(rt.kv_bf16, rt.qbuf.p, kv_layer(l), head_stride, M, Hq, Hkv, a.n_keys, a.row0,
                 a.mask_kind, a.mask_prompt_len, a.mask_block, ap, o_part, ml_part, rt.act.p, xs,
                 fmt, s);
-    const bool last = l == L - 1;
-    if (last && a.n_lm == 0) break;  // commit-only forward: every layer's K/V is written
     if (big) {
       FusedArgs fo = base(w.o);
       fo.act = rt.act.p;
