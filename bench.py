@@ -55,7 +55,8 @@ def parse_args():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="time a 256 MiB device-to-device copy and exit")
     ap.add_argument("--workload", default="bd3_q4_8k",
-                    choices=["bd3_q4_8k", "bd3_bf16", "dream_q4", "attention", "q4_linear"],
+                    choices=["bd3_q4_8k", "bd3_bf16", "dream_q4", "dream_q4_threshold",
+                             "attention", "q4_linear"],
                     help="bd3_q4_8k is the headline line; the others print one JSON line per "
                          "case of the remaining configurations")
     return ap.parse_args()
@@ -252,10 +253,15 @@ def bench_decode_config(args, which: str) -> None:
 
     from diffusorrt_amd import decode
     from diffusorrt_amd import synthetic as syn
-    from diffusorrt_amd.runtime import Runtime, bd3_session_config, fixed_quota_session_config
+    from diffusorrt_amd.runtime import (Runtime, bd3_session_config, block_threshold_session_config,
+                                        fixed_quota_session_config)
 
     if which == "bd3_bf16":
         g, kind, seed, prompt_len, gen_len, steps, block = syn.BD3_QWEN3_06B, "bf16", 0, 64, 128, 32, 32
+    elif which == "dream_q4_threshold":
+        # Dream's own policy: 8-token blocks over the exact prompt + frozen-block
+        # K/V, threshold 0.9 (random weights never reach it: one token per step)
+        g, kind, seed, prompt_len, gen_len, steps, block = syn.DREAM_QWEN25_7B, "q4", 3, 256, 64, 512, 8
     else:
         g, kind, seed, prompt_len, gen_len, steps, block = syn.DREAM_QWEN25_7B, "q4", 3, 256, 256, 64, 256
     t = time.perf_counter()
@@ -264,9 +270,11 @@ def bench_decode_config(args, which: str) -> None:
     log(f"{which}: model generated in {time.perf_counter() - t:.1f}s")
     rt = Runtime(model, max_forward_rows=max(512, prompt_len + gen_len),
                  max_positions=prompt_len + gen_len + 64)
-    strategy = "bd3_fixed_quota" if which == "bd3_bf16" else "fixed_quota"
-    cfg = (bd3_session_config(block, steps, prompt_len + gen_len) if which == "bd3_bf16"
-           else fixed_quota_session_config(block, steps, prompt_len + gen_len))
+    strategy = {"bd3_bf16": "bd3_fixed_quota", "dream_q4": "fixed_quota",
+                "dream_q4_threshold": "block_threshold"}[which]
+    make = {"bd3_fixed_quota": bd3_session_config, "fixed_quota": fixed_quota_session_config,
+            "block_threshold": block_threshold_session_config}[strategy]
+    cfg = make(block, steps, prompt_len + gen_len)
 
     def run():
         with rt.session(cfg) as s:

@@ -761,6 +761,13 @@ struct Session {
   int proposals = 0;
   // execute_window identity of the cached prefix
   int win_prompt_len = -1, win_block = -1;
+  // Under the Dream logits shift the first position of a d2f block reads the
+  // last row before the block, which is frozen: its score and token stay fixed
+  // while the block decodes, so they are computed once (a one-row forward with
+  // the LM head) and kept here for position feeder_pos (-1: none).
+  int feeder_pos = -1;
+  double feeder_score = 0.0;
+  int32_t feeder_token = 0;
   std::vector<int32_t> win_tokens;
   drt_metrics m{};
   Profiler prof;
@@ -1026,6 +1033,7 @@ int32_t drt_session_start(uint64_t session, const int32_t* tokens, int32_t n_tok
     s->tokens_dev.ensure((size_t)n_tokens * 4);
     s->ensure_cache(n_tokens);
     s->cache_len = 0;  // a new request: nothing in the cache belongs to it yet
+    s->feeder_pos = -1;
     s->origin = prompt_len;
     s->block = block_size;
     s->mask_id = mask_token_id;
@@ -1041,6 +1049,15 @@ int32_t drt_session_start(uint64_t session, const int32_t* tokens, int32_t n_tok
     s->upload_tokens(0, n_tokens);
     DRT_HIP(hipStreamSynchronize(r.stream));
   });
+}
+
+// The frontier entry whose raw row precedes the forward's first row (the Dream
+// shift's feeder position), or -1.
+static int feeder_i_of(const std::shared_ptr<Session>& s, const int32_t* frontier, int n,
+                       int row0) {
+  for (int i = 0; i < n; ++i)
+    if (s->raw_row(frontier[i]) < row0) return i;
+  return -1;
 }
 
 int32_t drt_session_propose(uint64_t session, const int32_t* frontier, int32_t n_frontier,
@@ -1072,17 +1089,23 @@ int32_t drt_session_propose(uint64_t session, const int32_t* frontier, int32_t n
       // context -- the reference's shift-feeder row
       // (backends/mlx_d2f_forward.py:226-232). Its K/V is rewritten with what
       // the cache already holds for it.
-      int row0 = frozen_prefix;
+      int feeder_i = -1;  // the frontier entry that reads row frozen_prefix - 1
       for (int i = 0; i < n_frontier; ++i) {
         const int p = frontier[i];
         require(p >= frozen_prefix && p < window_end,
                 "frontier position outside [frozen_prefix, window_end)");
         const int rr = s->raw_row(p);
         require(rr >= frozen_prefix - 1, "frontier reads a row before frozen_prefix - 1");
-        row0 = std::min(row0, rr);
+        if (rr < frozen_prefix) {
+          require(feeder_i < 0, "a position appears twice in the frontier");
+          feeder_i = i;
+        }
       }
       // An earlier frozen prefix shrinks the exact cache; a later one commits blocks.
-      if (s->cache_len > frozen_prefix) s->cache_len = frozen_prefix;
+      if (s->cache_len > frozen_prefix) {
+        s->cache_len = frozen_prefix;
+        s->feeder_pos = -1;
+      }
       DRT_HIP(hipEventRecord(r.ev0, r.stream));
       if (s->cache_len < frozen_prefix) {
         const int todo = frozen_prefix - s->cache_len;
@@ -1110,14 +1133,41 @@ int32_t drt_session_propose(uint64_t session, const int32_t* frontier, int32_t n
         forwarded += todo;
         s->cache_len = frozen_prefix;
       }
-      a.row0 = row0;
-      a.n_rows = window_end - row0;
+      if (s->cfg.decode_strategy == DRT_DECODE_BLOCK_THRESHOLD) a.exclude_col = s->mask_id;
+      if (feeder_i >= 0 && s->feeder_pos != frozen_prefix) {
+        // the frozen row's score and token: one row over its own (cached) context
+        ForwardArgs f;
+        f.tokens_dev = s->tokens_dev.as<int32_t>();
+        f.row0 = frozen_prefix - 1;
+        f.n_rows = 1;
+        f.n_keys = frozen_prefix;
+        f.mask_kind = 1;
+        f.mask_prompt_len = s->origin;
+        f.mask_block = s->block;
+        f.exclude_col = a.exclude_col;
+        f.temperature = a.temperature;
+        f.seed = a.seed;
+        f.step = a.step;
+        f.n_lm = 1;
+        f.lm_rows.push_back(0);
+        f.lm_pos.push_back(frozen_prefix);
+        s->upload_tokens(frozen_prefix - 1, frozen_prefix);
+        run_forward(r, s->kv.p, s->head_stride, s->layer_stride, f);
+        DRT_HIP(hipStreamSynchronize(r.stream));
+        r.up_next = 2;
+        check_placement(r);
+        s->feeder_pos = frozen_prefix;
+        s->feeder_score = r.scores_host()[0];
+        s->feeder_token = r.tokens_host()[0];
+        forwarded += 1;
+      }
+      a.row0 = frozen_prefix;
+      a.n_rows = window_end - frozen_prefix;
       a.n_keys = window_end;
       a.mask_kind = 1;
       a.mask_prompt_len = s->origin;
       a.mask_block = s->block;
-      if (s->cfg.decode_strategy == DRT_DECODE_BLOCK_THRESHOLD) a.exclude_col = s->mask_id;
-      if (!(s->graphable(a.n_rows) && n_frontier <= 32)) s->upload_tokens(row0, window_end);
+      if (!(s->graphable(a.n_rows) && n_frontier <= 32)) s->upload_tokens(frozen_prefix, window_end);
     } else {
       // Full bidirectional canvas, no cache (Dream / MDLM fixed_quota).
       for (int i = 0; i < n_frontier; ++i)
@@ -1129,24 +1179,37 @@ int32_t drt_session_propose(uint64_t session, const int32_t* frontier, int32_t n
       a.n_keys = n;
       a.mask_kind = 0;
     }
-    a.n_lm = n_frontier;
+    // the feeder position (if any) is served from the session, not the forward
+    const int skip = a.mask_kind == 1 ? feeder_i_of(s, frontier, n_frontier, a.row0) : -1;
     for (int i = 0; i < n_frontier; ++i) {
+      if (i == skip) continue;
       a.lm_rows.push_back(s->raw_row(frontier[i]) - a.row0);
       a.lm_pos.push_back(frontier[i]);
     }
-    if (a.mask_kind == 1 && s->graphable(a.n_rows) && n_frontier <= 32)
-      s->graph_forward(false, a);
-    else
-      run_forward(r, s->kv.p, s->head_stride, s->layer_stride, a);
+    a.n_lm = (int)a.lm_rows.size();
+    if (a.n_lm > 0) {
+      if (a.mask_kind == 1 && s->graphable(a.n_rows) && a.n_lm <= 32)
+        s->graph_forward(false, a);
+      else
+        run_forward(r, s->kv.p, s->head_stride, s->layer_stride, a);
+      forwarded += a.n_rows;
+    }
     r.up_next = 2;  // the stream is drained below before any slot is reused
-    forwarded += a.n_rows;
     DRT_HIP(hipEventRecord(r.ev1, r.stream));
     // the LM head's last kernel wrote scores, tokens and the placement flags
     // into pinned host memory: nothing to copy once the stream has drained
     DRT_HIP(hipStreamSynchronize(r.stream));
     check_placement(r);
-    std::memcpy(out_scores, r.scores_host(), (size_t)n_frontier * 8);
-    std::memcpy(out_tokens, r.tokens_host(), (size_t)n_frontier * 4);
+    for (int i = 0, j = 0; i < n_frontier; ++i) {
+      if (i == skip) {
+        out_scores[i] = s->feeder_score;
+        out_tokens[i] = s->feeder_token;
+      } else {
+        out_scores[i] = r.scores_host()[j];
+        out_tokens[i] = r.tokens_host()[j];
+        ++j;
+      }
+    }
     s->finish_timing();
     s->publish_profile();
     s->proposals += 1;
