@@ -404,3 +404,42 @@ def test_dream_block_threshold_exact_kv():
             frontier_logits_fn=lambda c, f, w: ref_logits(W, c, f))
         assert ref_out["x"] == res.full_token_ids
     rt.close()
+
+
+def test_dream_real_shapes_block_threshold():
+    """Dream's layer shapes through the block-threshold path: the 40-row prompt
+    commit (large-M kernels), the one-row feeder and the 8-row steps (at these
+    shapes the <= 32-row linears run on the single-pass kernels), teacher-forced
+    against the oracle with MASK left out of the scoring."""
+    from diffusorrt_amd import decode
+    from diffusorrt_amd.runtime import block_threshold_session_config
+
+    _say("dream real shapes block_threshold")
+    geom = _real_shape_geometry("dream")
+    model, rt = _build(geom, "q4", seed=23)
+    W, cfg = _oracle(model)
+    P_LEN, GEN, BS = 40, 16, 8
+    prompt = np.random.default_rng(7).integers(0, 3900, P_LEN).tolist()
+    trace = []
+    with rt.session(block_threshold_session_config(BS, 32, P_LEN + GEN)) as s:
+        res = decode.generate_device_tokens(
+            s, prompt, max_tokens=GEN, mask_token_id=geom.mask_token_id,
+            eos_token_id=geom.eos_token_id, steps=32, block_size=BS,
+            decode_strategy="block_threshold", trace=trace)
+    assert res.committed_token_count == GEN
+    xx = prompt + [geom.mask_token_id] * GEN
+    problems, ties = [], []
+    for t in trace:
+        ref = F.window_logits(W, cfg, xx, t["frontier"], mask_kind="d2f_hybrid",
+                              mask_geometry=(P_LEN, BS), logits_convention="dream_ar_shift")
+        ref = np.array(ref, dtype=np.float32)
+        ref[:, geom.mask_token_id] = -np.inf
+        rep, bad = compare_proposals(t["scores"], t["tokens"], ref, quota=len(t["chosen"]),
+                                     gpu_chosen=t["chosen"])
+        ties += rep["report"]
+        problems += [(t["step"],) + tuple(b) for b in bad]
+        for r in t["chosen"]:
+            xx[t["frontier"][r]] = t["tokens"][r]
+    _say(f"  steps={len(trace)} near-ties reported: {ties}")
+    assert not problems, problems
+    rt.close()
