@@ -49,6 +49,9 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=64, help="timed denoise steps")
     ap.add_argument("--warmup", type=int, default=8, help="untimed denoise steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--host-loop", action="store_true",
+                    help="drive the step loop from Python (propose/commit per step) instead of "
+                         "the library's native loop")
     ap.add_argument("--cpu-sample-layers", type=int, default=1)
     ap.add_argument("--profile-steps", type=int, default=None,
                     help="eager steps timed per dispatch for the roofline (default: --steps; 0 = none)")
@@ -351,6 +354,13 @@ def main():
     step_iter = iter(range(policy.iteration_limit))
 
     def one_step() -> int:
+        if not args.host_loop:  # the library's own loop: one step per call
+            fwd, com, done = sess.bd3_decode(prompt_len=PREFIX, max_tokens=max_tokens,
+                                             steps=steps_budget,
+                                             eos_token_id=g.eos_token_id, max_forwards=1)
+            if fwd != 1:
+                raise RuntimeError("decode stopped early (EOS at a block boundary)")
+            return com
         for step in step_iter:
             plan = policy.plan(state=state, step=step)
             if plan.stop:

@@ -98,6 +98,9 @@ SIGNATURES = {
                                  C.c_double, _U64]),
     "drt_session_propose": (_I32, [_U64, _PI32, _I32, _I32, _I32, _PF64, _PI32, _PI32]),
     "drt_session_commit": (_I32, [_U64, _PI32, _PI32, _I32]),
+    "drt_session_bd3_decode": (_I32, [_U64, _I32, _I32, _I32, _I32, _I32, _I32, _PI32, _PI32,
+                                      _PI32]),
+    "drt_session_canvas": (_I32, [_U64, _PI32, _I32, _PI32]),
     "drt_session_execute_window": (_I32, [_U64, _PI32, _I32, _PI32, _I32, _I32, _I32, _PF32,
                                           _I64, _PI32, _PI32]),
     "drt_session_metrics": (_I32, [_U64, C.POINTER(Metrics)]),

@@ -775,6 +775,13 @@ struct Session {
   int feeder_pos = -1;
   double feeder_score = 0.0;
   int32_t feeder_token = 0;
+  // the native BD3 fixed-quota loop (drt_session_bd3_decode): its policy state
+  struct Bd3Loop {
+    bool on = false;
+    int prompt_len = 0, gen = 0, steps = 0, eos = 0, spb = 0, count = 0, limit = 0;
+    bool align = true;
+    int step = 0, active = -1, base = 0, rem = 0;
+  } loop;
   std::vector<int32_t> win_tokens;
   drt_metrics m{};
   Profiler prof;
@@ -1041,6 +1048,7 @@ int32_t drt_session_start(uint64_t session, const int32_t* tokens, int32_t n_tok
     s->ensure_cache(n_tokens);
     s->cache_len = 0;  // a new request: nothing in the cache belongs to it yet
     s->feeder_pos = -1;
+    s->loop = Session::Bd3Loop{};
     s->origin = prompt_len;
     s->block = block_size;
     s->mask_id = mask_token_id;
@@ -1067,10 +1075,10 @@ static int feeder_i_of(const std::shared_ptr<Session>& s, const int32_t* frontie
   return -1;
 }
 
-int32_t drt_session_propose(uint64_t session, const int32_t* frontier, int32_t n_frontier,
-                            int32_t window_end, int32_t frozen_prefix, double* out_scores,
-                            int32_t* out_tokens, int32_t* out_forwarded_rows) {
-  return guarded([&] {
+static void propose_impl(uint64_t session, const int32_t* frontier, int32_t n_frontier,
+                         int32_t window_end, int32_t frozen_prefix, double* out_scores,
+                         int32_t* out_tokens, int32_t* out_forwarded_rows) {
+  {
     auto s = handles().get<Session>(session, Kind::SESSION);
     Runtime& r = *s->rt;
     require(s->started, "propose_device before start_device");
@@ -1225,6 +1233,118 @@ int32_t drt_session_propose(uint64_t session, const int32_t* frontier, int32_t n
     s->m.lm_rows += n_frontier;
     s->m.kv_cache_len = s->cache_len;
     if (out_forwarded_rows) *out_forwarded_rows = forwarded;
+  }
+}
+
+int32_t drt_session_propose(uint64_t session, const int32_t* frontier, int32_t n_frontier,
+                            int32_t window_end, int32_t frozen_prefix, double* out_scores,
+                            int32_t* out_tokens, int32_t* out_forwarded_rows) {
+  return guarded([&] {
+    propose_impl(session, frontier, n_frontier, window_end, frozen_prefix, out_scores, out_tokens,
+                 out_forwarded_rows);
+  });
+}
+
+// The BD3 fixed-quota loop of decode.py (BD3FixedQuotaCommit over absolute blocks,
+// diffusion_runtime.py:1200-1346, driven as run_decode_loop does, :1829-1991) run
+// natively: plan, propose, pick the quota's best rows, commit, with no return to
+// the caller between steps. Same schedule and commits as the host loop; rows with
+// exactly equal float64 scores are taken lowest index first.
+int32_t drt_session_bd3_decode(uint64_t session, int32_t prompt_len, int32_t max_tokens,
+                               int32_t steps, int32_t eos_token_id, int32_t requires_alignment,
+                               int32_t max_forwards, int32_t* out_forwards,
+                               int32_t* out_committed, int32_t* out_done) {
+  return guarded([&] {
+    auto s = handles().get<Session>(session, Kind::SESSION);
+    require(s->started, "bd3_decode before start_device");
+    require(s->cfg.decode_strategy == DRT_DECODE_BD3_FIXED_QUOTA && s->origin == 0,
+            "bd3_decode runs a bd3_fixed_quota session (block origin 0)");
+    const int n = (int)s->canvas.size();
+    require(prompt_len >= 0 && max_tokens >= 0 && prompt_len + max_tokens == n,
+            "bd3_decode: prompt_len + max_tokens must equal the canvas length");
+    require(steps >= 1 && max_forwards >= 0, "bd3_decode: steps >= 1, max_forwards >= 0");
+    const int B = s->block;
+    Session::Bd3Loop& L = s->loop;
+    if (!L.on || L.prompt_len != prompt_len || L.gen != max_tokens || L.steps != steps) {
+      L = Session::Bd3Loop{};
+      L.on = true;
+      L.prompt_len = prompt_len;
+      L.gen = max_tokens;
+      L.steps = steps;
+      L.eos = eos_token_id;
+      L.align = requires_alignment != 0;
+      if (max_tokens > 0) {
+        const int first = prompt_len / B, last = (prompt_len + max_tokens - 1) / B;
+        L.count = last - first + 1;
+        const int sched = (max_tokens + B - 1) / B;
+        L.spb = (steps + sched - 1) / sched;
+      }
+      L.limit = L.count * L.spb;
+    }
+    int forwards = 0, committed = 0, done = 0;
+    std::vector<int32_t> frontier, pos, tok;
+    std::vector<double> sc;
+    std::vector<int32_t> tk, order;
+    while (forwards < max_forwards) {
+      const int step = L.step;
+      if (step >= L.limit) { done = 1; break; }
+      if (L.align && prompt_len % B)
+        fail(INVALID_ARGUMENT, "BD3LM Candidate prompt length must be a multiple of block_size");
+      const int32_t* gen = s->canvas.data() + prompt_len;
+      // EOS ends the decode only at a block boundary
+      if (step % L.spb == 0 && std::find(gen, gen + max_tokens, L.eos) != gen + max_tokens) {
+        done = 1;
+        break;
+      }
+      if (std::find(gen, gen + max_tokens, s->mask_id) == gen + max_tokens) { done = 1; break; }
+      const int block_id = step / L.spb;
+      const int grid = (prompt_len / B + block_id) * B;
+      const int lo = std::max(prompt_len, grid), hi = std::min(prompt_len + max_tokens, grid + B);
+      frontier.clear();
+      for (int p = lo; p < hi; ++p)
+        if (s->canvas[p] == s->mask_id) frontier.push_back(p);
+      if (L.active != block_id) {
+        L.active = block_id;
+        L.base = (int)frontier.size() / L.spb;
+        L.rem = (int)frontier.size() % L.spb;
+      }
+      const int quota = L.base + (step % L.spb < L.rem ? 1 : 0);
+      L.step = step + 1;
+      if (frontier.empty() || quota == 0) continue;
+      const int nf = (int)frontier.size();
+      sc.assign(nf, 0.0);
+      tk.assign(nf, 0);
+      int32_t fwd = 0;
+      propose_impl(session, frontier.data(), nf, hi, (frontier[0] / B) * B, sc.data(), tk.data(),
+                   &fwd);
+      ++forwards;
+      order.resize(nf);
+      for (int i = 0; i < nf; ++i) order[i] = i;
+      std::stable_sort(order.begin(), order.end(),
+                       [&](int a, int b) { return sc[a] > sc[b]; });
+      const int k = std::min(quota, nf);
+      for (int i = 0; i < k; ++i) {
+        const int r = order[i];
+        require(tk[r] >= 0 && tk[r] < s->rt->V(), "proposed token outside the vocabulary");
+        s->canvas[frontier[r]] = tk[r];
+      }
+      committed += k;
+    }
+    if (out_forwards) *out_forwards = forwards;
+    if (out_committed) *out_committed = committed;
+    if (out_done) *out_done = done;
+  });
+}
+
+// The session's canvas (the committed tokens of a native loop): n_out >= its length.
+int32_t drt_session_canvas(uint64_t session, int32_t* out, int32_t n_out, int32_t* out_len) {
+  return guarded([&] {
+    auto s = handles().get<Session>(session, Kind::SESSION);
+    require(s->started, "canvas before start_device");
+    const int n = (int)s->canvas.size();
+    if (out_len) *out_len = n;
+    require(out && n_out >= n, "canvas output buffer too small");
+    std::memcpy(out, s->canvas.data(), (size_t)n * 4);
   });
 }
 

@@ -353,12 +353,15 @@ def generate_device_tokens(session, prompt_token_ids: list, *, max_tokens: int,
                            requires_prompt_block_alignment: bool = True,
                            temperature: float = 0.0, seed: int = 0,
                            memory_budget_bytes: int = 0, confidence_threshold: float = 0.9,
+                           native: bool = True,
                            cancelled: Callable[[], bool] | None = None,
                            trace: list | None = None) -> DecodeResult:
     """Run a policy with scoring on the device (``backends/device_runtime.py:108-274``).
     ``block_threshold`` scores without the MASK column (the session leaves it out
     of the softmax and argmax) and decodes greedily over the exact K/V of the
-    prompt and the frozen blocks."""
+    prompt and the frozen blocks. With ``native`` (and no trace or cancellation
+    hook) ``bd3_fixed_quota`` runs the same loop inside the library
+    (``drt_session_bd3_decode``)."""
     if decode_strategy not in {"fixed_quota", "bd3_fixed_quota", "block_threshold"}:
         raise ValueError("the rocm device session runs block_threshold, fixed_quota and "
                          f"bd3_fixed_quota, not {decode_strategy!r}")
@@ -423,10 +426,20 @@ def generate_device_tokens(session, prompt_token_ids: list, *, max_tokens: int,
         return session.propose_device(plan.frontier, window_end=plan.window_end,
                                       frozen_prefix=frozen)
 
-    forwards, committed, iterations = run_decode_loop(
-        state, commit_policy=policy, iteration_limit=policy.iteration_limit,
-        propose_fn=propose, commit_device_fn=session.commit_device, cancelled=cancelled,
-        trace=trace)
+    if (native and decode_strategy == "bd3_fixed_quota" and trace is None and cancelled is None
+            and hasattr(session, "bd3_decode")):
+        # the same loop run inside the library: no return to Python between steps
+        forwards, committed, _done = session.bd3_decode(
+            prompt_len=prompt_len, max_tokens=max_tokens, steps=steps, eos_token_id=eos_token_id,
+            requires_prompt_block_alignment=requires_prompt_block_alignment,
+            max_forwards=policy.iteration_limit)
+        iterations = forwards
+        state.x = session.canvas()
+    else:
+        forwards, committed, iterations = run_decode_loop(
+            state, commit_policy=policy, iteration_limit=policy.iteration_limit,
+            propose_fn=propose, commit_device_fn=session.commit_device, cancelled=cancelled,
+            trace=trace)
     fin = state.finalize()
     return DecodeResult(
         visible_generated_token_ids=fin["visible_token_ids"], iteration_count=iterations,

@@ -226,6 +226,7 @@ class DeviceSession:
                      exact_kv: bool, steps: int, memory_budget_bytes: int = 0,
                      temperature: float = 0.0, seed: int = 0) -> None:
         toks = _lib.i32_array(tokens)
+        self._canvas_len = len(tokens)
         _lib.check(self._lib.drt_session_start(
             self.handle, toks, len(tokens), int(prompt_len), int(block_size), int(mask_token_id),
             int(bool(exact_kv)), int(steps), int(memory_budget_bytes), float(temperature),
@@ -246,6 +247,26 @@ class DeviceSession:
             raise ValueError("commit_device needs one token per position")
         _lib.check(self._lib.drt_session_commit(
             self.handle, _lib.i32_array(positions), _lib.i32_array(tokens), len(positions)))
+
+    def bd3_decode(self, *, prompt_len: int, max_tokens: int, steps: int, eos_token_id: int,
+                   requires_prompt_block_alignment: bool = True, max_forwards: int) -> tuple:
+        """Run up to ``max_forwards`` steps of the BD3 fixed-quota loop natively (the
+        policy state persists in the session between calls). Returns
+        ``(forwards, committed, done)``."""
+        fwd, com, done = C.c_int32(0), C.c_int32(0), C.c_int32(0)
+        _lib.check(self._lib.drt_session_bd3_decode(
+            self.handle, int(prompt_len), int(max_tokens), int(steps), int(eos_token_id),
+            int(bool(requires_prompt_block_alignment)), int(max_forwards), C.byref(fwd),
+            C.byref(com), C.byref(done)))
+        return fwd.value, com.value, bool(done.value)
+
+    def canvas(self) -> list:
+        """The session's canvas (prompt + generated positions, as committed)."""
+        n = int(self._canvas_len)
+        out = (C.c_int32 * max(1, n))()
+        size = C.c_int32(0)
+        _lib.check(self._lib.drt_session_canvas(self.handle, out, n, C.byref(size)))
+        return list(out[:size.value])
 
     def execute_window(self, token_ids, scope, mask_geometry=None) -> WindowLogits:
         n_scope = len(scope)

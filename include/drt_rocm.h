@@ -166,6 +166,16 @@ int32_t drt_session_start(uint64_t session, const int32_t* tokens, int32_t n_tok
 int32_t drt_session_propose(uint64_t session, const int32_t* frontier, int32_t n_frontier,
                             int32_t window_end, int32_t frozen_prefix, double* out_scores,
                             int32_t* out_tokens, int32_t* out_forwarded_rows);
+/* The BD3 fixed-quota loop (diffusion_runtime.py:1200-1346 driven as in :1829-1991) run inside
+ * the library: up to max_forwards plan/propose/select/commit steps with no return to the caller
+ * in between; the policy state persists in the session. No counterpart in the reference, whose
+ * loop runs on the host; rows with exactly equal float64 scores commit lowest index first. */
+int32_t drt_session_bd3_decode(uint64_t session, int32_t prompt_len, int32_t max_tokens,
+                               int32_t steps, int32_t eos_token_id, int32_t requires_alignment,
+                               int32_t max_forwards, int32_t* out_forwards,
+                               int32_t* out_committed, int32_t* out_done);
+/* The session's canvas: n_out >= its length (the length is returned in *out_len). */
+int32_t drt_session_canvas(uint64_t session, int32_t* out, int32_t n_out, int32_t* out_len);
 /* session.commit_device(positions, tokens). */
 int32_t drt_session_commit(uint64_t session, const int32_t* positions, const int32_t* tokens,
                            int32_t n);

@@ -443,3 +443,42 @@ def test_dream_real_shapes_block_threshold():
     _say(f"  steps={len(trace)} near-ties reported: {ties}")
     assert not problems, problems
     rt.close()
+
+
+@pytest.mark.parametrize("kind", ["q4", "bf16"])
+def test_bd3_native_loop_matches_host_loop(kind):
+    """drt_session_bd3_decode runs the same schedule and commits as the host loop:
+    whole decodes, an end token that stops at a block boundary, and a decode
+    split into several calls."""
+    from diffusorrt_amd import decode
+    from diffusorrt_amd.runtime import bd3_session_config
+
+    _say("bd3 native loop vs host loop", kind)
+    geom = tiny_geometry()
+    _, rt = _build(geom, kind, seed=14)
+    prompt = np.random.default_rng(9).integers(0, 900, 64).tolist()
+
+    def run(native, eos):
+        with rt.session(bd3_session_config(32, 24, 64 + 96)) as s:
+            return decode.generate_device_tokens(
+                s, prompt, max_tokens=96, mask_token_id=geom.mask_token_id, eos_token_id=eos,
+                steps=24, block_size=32, native=native)
+
+    host, nat = run(False, geom.eos_token_id), run(True, geom.eos_token_id)
+    assert nat.full_token_ids == host.full_token_ids
+    assert (nat.forward_count, nat.committed_token_count) == (host.forward_count,
+                                                              host.committed_token_count)
+    eos = host.full_token_ids[64 + 5]  # committed in the first block: stop at its boundary
+    host_e, nat_e = run(False, eos), run(True, eos)
+    assert host_e.hit_eos and nat_e.full_token_ids == host_e.full_token_ids
+    assert nat_e.forward_count == host_e.forward_count < host.forward_count
+    with rt.session(bd3_session_config(32, 24, 64 + 96)) as s:
+        s.start_device(prompt + [geom.mask_token_id] * 96, prompt_len=0, block_size=32,
+                       mask_token_id=geom.mask_token_id, exact_kv=False, steps=24)
+        total, done = 0, False
+        while not done:
+            f, _, done = s.bd3_decode(prompt_len=64, max_tokens=96, steps=24,
+                                      eos_token_id=geom.eos_token_id, max_forwards=5)
+            total += f
+        assert total == host.forward_count and s.canvas() == host.full_token_ids
+    rt.close()
