@@ -353,14 +353,18 @@ def main():
                       exact_kv=False, steps=steps_budget)
     step_iter = iter(range(policy.iteration_limit))
 
+    def native_steps(k: int) -> int:
+        """k steps of the library's own loop in one call (as the product runs it)."""
+        fwd, com, _done = sess.bd3_decode(prompt_len=PREFIX, max_tokens=max_tokens,
+                                          steps=steps_budget, eos_token_id=g.eos_token_id,
+                                          max_forwards=k)
+        if fwd != k:
+            raise RuntimeError("decode stopped early (EOS at a block boundary)")
+        return com
+
     def one_step() -> int:
-        if not args.host_loop:  # the library's own loop: one step per call
-            fwd, com, done = sess.bd3_decode(prompt_len=PREFIX, max_tokens=max_tokens,
-                                             steps=steps_budget,
-                                             eos_token_id=g.eos_token_id, max_forwards=1)
-            if fwd != 1:
-                raise RuntimeError("decode stopped early (EOS at a block boundary)")
-            return com
+        if not args.host_loop:
+            return native_steps(1)
         for step in step_iter:
             plan = policy.plan(state=state, step=step)
             if plan.stop:
@@ -389,8 +393,11 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     committed = 0
-    for _ in range(args.steps):
-        committed += one_step()
+    if args.host_loop:
+        for _ in range(args.steps):
+            committed += one_step()
+    else:
+        committed = native_steps(args.steps)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     m1 = sess.device_metrics()
