@@ -162,7 +162,7 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
   uint32_t wsb[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    wq[u] = *q4_tile_words(qw, nt, G, u0 + u, lane);
+    wq[u] = __builtin_nontemporal_load(q4_tile_words(qw, nt, G, u0 + u, lane));
     wsb[u] = q4_tile_sb(sbp, nt, G, u0 + u, lane);
   }
   // 2. the hidden slice (8-wide items: U per thread) and the matching norm weights.
@@ -347,7 +347,7 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
       // clamped to a valid unit; a unit beyond the wave's range gets scale and
       // bias 0, an exact no-op, so every load is used unconditionally
       const int u = min(ub + i, max(u_hi, u_lo + 1) - 1);
-      wq[i] = *q4_tile_words(qw, nt, G, u, lane);
+      wq[i] = __builtin_nontemporal_load(q4_tile_words(qw, nt, G, u, lane));
       wsb[i] = ub + i < u_hi ? q4_tile_sb(sbp, nt, G, u, lane) : 0u;
       // the unit's 32 x 64 activation block as four coalesced loads of 8 rows x
       // 128 B (rows past M read row M - 1: their outputs are never stored)
