@@ -8,11 +8,12 @@ GPU invocation) and the ``cpu_baseline`` leg of ``bench.py``.
 Every function cites the reference file:line it restates (paths relative to the
 reference's ``python/src/edllm/``). The reference's MLX code cannot run here
 (no ``mlx``, Python 3.10 < 3.11), so each function is pinned instead by known
-answers, closed forms and invariants in ``tests/test_oracle_*.py``; a function
-with no such check is marked "parity unpinned" in its docstring (the sampling
-hash's key chaining, ``ops.sampling_uniform_bits``). MLX's own last-bit
-behaviour (quantized_matmul accumulation order, fused SDPA, bf16 matmul
-rounding) is parity unpinned as well: no reference test or golden logits ship.
+answers, closed forms and invariants in ``tests/test_oracle_*.py``; the
+temperature sampler (whose key chaining only the reference's code fixes) by
+vectors that the reference's own sampler wrote (``tests/golden/
+sampling_vectors.json``, ``tests/test_sampling_vectors.py``). MLX's own
+last-bit behaviour (quantized_matmul accumulation order, fused SDPA, bf16
+matmul rounding) is parity unpinned: no reference test or golden logits ship.
 
 Modules:
   ops      -- per-op math: RMSNorm, RoPE tables + split-half RoPE, SwiGLU,

@@ -386,10 +386,10 @@ def sampling_uniform_bits(seed: int, step: int, position: int, token: int) -> in
     ``key = mix(key + (position+1) G)``; ``bits = mix(key + (token+1) G)``
     (``backends/diffusion_runtime.py:203-253``).
 
-    Parity unpinned for the chaining order: ``mix64`` is pinned by the published
-    splitmix64 sequence and the noise by its Gumbel statistics, but no reference
-    fixture holds sampled tokens, so the key order itself is checked only by
-    reading the cited lines.
+    Pinned by ``tests/golden/sampling_vectors.json``: noise rows and sampled
+    tokens/scores written by the reference's own ``sampling_noise`` and
+    ``_sampled_max_prob_confidence`` (``tests/golden/make_sampling_vectors.py``),
+    matched bit for bit; ``mix64`` also by the published splitmix64 sequence.
     """
     g = SAMPLING_STEP
     key = mix64((seed & MASK64) + g)
