@@ -66,7 +66,8 @@ class SessionConfig(C.Structure):
     _fields_ = [("decode_strategy", C.c_int32), ("commit_policy", C.c_int32),
                 ("attention_mask_kind", C.c_int32), ("block_size", C.c_int32),
                 ("steps", C.c_int32), ("max_tokens", C.c_int32),
-                ("trace_canvas", C.c_int32), ("error_fixing", C.c_int32)]
+                ("trace_canvas", C.c_int32), ("error_fixing", C.c_int32),
+                ("reserved", C.c_int32 * 8)]
 
 
 class Tensor(C.Structure):

@@ -315,8 +315,10 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
   if (e.linear_quant_bits == 4)
     require(e.linear_quant_group_size == 64, "only group size 64 is supported");
   if (e.layer0_kv_cache_enabled || e.prefix_kv_cache || e.block_kv_cache ||
-      e.d2f_exact_kv_cache || e.cross_request_cache || e.canvas_cache)
-    fail(UNSUPPORTED, "the fixed-quota denoise step admits no approximate or D2F caches");
+      e.cross_request_cache || e.canvas_cache)
+    fail(UNSUPPORTED, "the rocm runtime admits no approximate, cross-request or canvas caches");
+  require(e.d2f_exact_kv_cache == 0 || e.d2f_exact_kv_cache == 1,
+          "d2f_exact_kv_cache must be 0 or 1");
   require(e.kv_dtype == DRT_F16 || e.kv_dtype == DRT_BF16, "kv_dtype must be DRT_F16 or DRT_BF16");
   require(e.max_forward_rows >= 32, "max_forward_rows must be >= 32");
 
@@ -998,6 +1000,7 @@ int32_t drt_session_open(uint64_t runtime, const drt_session_config* config,
     require(config && out_session, "drt_session_open needs a config and an output handle");
     auto rt = handles().get<Runtime>(runtime, Kind::RUNTIME);
     const drt_session_config& c = *config;
+    for (int i = 0; i < 8; ++i) require(c.reserved[i] == 0, "session config reserved fields must be 0");
     const bool bd3 = c.decode_strategy == DRT_DECODE_BD3_FIXED_QUOTA;
     const bool fq = c.decode_strategy == DRT_DECODE_FIXED_QUOTA;
     const bool bt = c.decode_strategy == DRT_DECODE_BLOCK_THRESHOLD;

@@ -77,6 +77,34 @@ class WindowLogits:
         return np.frombuffer(self.logits, dtype="<f4").reshape(self.n_rows, self.n_vocab)
 
 
+def engine_request(engine_config: dict, weight_kind: str) -> tuple:
+    """Validate an engine request (``EngineConfig``, ``abi/lifetimes.py:30-43``) for
+    weights of ``weight_kind``; returns ``(linear_quant_bits, d2f_exact_kv_cache)``.
+
+    ``d2f_exact_kv_cache = 1`` is what ``cuda_engine_config(precision,
+    exact_kv=True)`` sends for Dream's block_threshold (``model.py:905-916, 991``;
+    ``backends/device_runtime.py:53-58``): accepted, since this runtime's
+    block_threshold sessions always run over the exact prompt + frozen-block K/V;
+    fixed-quota sessions refuse ``exact_kv`` at ``start_device``. The approximate,
+    cross-request and canvas caches are not offered.
+    """
+    ec = dict(engine_config or {})
+    quant_bits = 4 if weight_kind == "q4" else -1
+    bits = ec.get("linear_quant_bits", quant_bits)
+    if (-1 if bits is None else bits) != quant_bits:
+        raise ValueError("engine_config linear_quant_bits disagrees with the weights")
+    for key in ("prefix_kv_cache", "block_kv_cache", "layer0_kv_cache_enabled",
+                "cross_request_cache", "canvas_cache"):
+        if int(ec.get(key, 0)):
+            raise ValueError(f"engine_config {key} is not offered by the rocm runtime")
+    exact_kv_cache = ec.get("d2f_exact_kv_cache", 0)
+    if exact_kv_cache not in (0, 1):
+        raise ValueError("engine_config d2f_exact_kv_cache must be 0 or 1")
+    if int(ec.get("compute_dtype", 0)) != 0:
+        raise ValueError("engine_config compute_dtype must be 0 (bf16)")
+    return quant_bits, int(exact_kv_cache)
+
+
 class Runtime:
     """Owns the model in device layouts and one HIP stream (one per process is typical)."""
 
@@ -105,23 +133,18 @@ class Runtime:
                                  linear_quant_group_size=int(ec.get("linear_quant_group_size", 64)),
                                  device_ordinal=device_ordinal)
         g: ModelGeometry = model.geometry
-        quant_bits = 4 if model.weight_kind == "q4" else -1
-        bits = ec.get("linear_quant_bits", quant_bits)
-        if (-1 if bits is None else bits) != quant_bits:
-            raise ValueError("engine_config linear_quant_bits disagrees with the weights")
-        for key in ("d2f_exact_kv_cache", "prefix_kv_cache", "block_kv_cache",
-                    "layer0_kv_cache_enabled", "cross_request_cache", "canvas_cache"):
-            if int(ec.get(key, 0)):
-                raise ValueError(f"engine_config {key} is not offered by the rocm runtime")
+        quant_bits, exact_kv_cache = engine_request(ec, model.weight_kind)
+        self.d2f_exact_kv_cache = bool(exact_kv_cache)
         self.geometry = g
         self.weight_kind = model.weight_kind
         self._device = torch.device("cuda", device_ordinal)
         positions = int(max_positions or g.max_position_embeddings)
         self._engine = _lib.EngineConfig(
-            compute_dtype=int(ec.get("compute_dtype", 0)), linear_quant_bits=quant_bits,
+            compute_dtype=0, linear_quant_bits=quant_bits,
             linear_quant_group_size=64, window_exec=0, device_ordinal=device_ordinal,
             max_forward_rows=int(max_forward_rows),
             kv_dtype=_lib.BF16 if kv_dtype == "bf16" else _lib.F16,
+            d2f_exact_kv_cache=exact_kv_cache,
             creation_memory_budget_bytes=int(creation_memory_budget_bytes))
         self._geo = _lib.ModelGeometry(
             layer_count=g.layer_count, hidden_size=g.hidden_size, num_heads=g.num_heads,
@@ -182,7 +205,14 @@ class Runtime:
             attention_mask_kind=int(session_config.get("attention_mask_kind", 0)),
             block_size=int(session_config.get("block_size", 0)),
             steps=int(session_config.get("steps", 0)),
-            max_tokens=int(session_config.get("max_tokens", 0)))
+            max_tokens=int(session_config.get("max_tokens", 0)),
+            trace_canvas=int(session_config.get("trace_canvas", 0)),
+            error_fixing=int(session_config.get("error_fixing", 0)))
+        reserved = tuple(session_config.get("reserved", (0,) * 8))
+        if len(reserved) != 8:
+            raise ValueError("session_config reserved holds 8 ints")
+        for i, v in enumerate(reserved):
+            sc.reserved[i] = int(v)
         out = C.c_uint64(0)
         _lib.check(self._lib.drt_session_open(self.handle, C.byref(sc), C.byref(out)))
         return DeviceSession(self, out.value, sc)

@@ -59,7 +59,12 @@ typedef struct drt_engine_config {
   int32_t layer0_kv_cache_enabled;  /* must be 0 */
   int32_t prefix_kv_cache;          /* must be 0 (approximate caches are not offered) */
   int32_t block_kv_cache;           /* must be 0 */
-  int32_t d2f_exact_kv_cache;       /* must be 0 (D2F exact K/V is not on this path) */
+  int32_t d2f_exact_kv_cache;       /* 0 or 1: 1 is what cuda_engine_config(exact_kv=True)
+                                     * sends for Dream's block_threshold (model.py:913, 991;
+                                     * backends/device_runtime.py:53-58). Sessions of this
+                                     * runtime serve block_threshold over the exact prompt +
+                                     * frozen-block K/V either way; fixed-quota sessions refuse
+                                     * exact_kv at start (device_runtime.py:223-231). */
   int32_t cross_request_cache;      /* must be 0 */
   int32_t canvas_cache;             /* must be 0 */
   int64_t canvas_cache_budget_bytes;
@@ -98,6 +103,7 @@ typedef struct drt_session_config {
   int32_t max_tokens;
   int32_t trace_canvas;
   int32_t error_fixing;
+  int32_t reserved[8];              /* must be 0 (SessionDecodeConfig.reserved) */
 } drt_session_config;
 
 /* A borrowed device tensor (TensorDesc + BufferView, abi/buffers.py:45-75),

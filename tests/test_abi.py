@@ -92,3 +92,37 @@ def test_product_package_never_imports_the_oracle():
     for path in pkg.rglob("*.py"):
         text = path.read_text()
         assert not re.search(r"^\s*(from|import)\s+oracle\b", text, flags=re.M), path
+
+
+def _reference_engine_config(scheme: str, exact_kv: bool) -> dict:
+    """The dict ``cuda_engine_config`` builds (``backends/device_runtime.py:53-58``)."""
+    config = {"compute_dtype": 0, "d2f_exact_kv_cache": int(exact_kv)}
+    if scheme == "int8_weight_only":
+        config.update(linear_quant_bits=8, linear_quant_group_size=64)
+    return config
+
+
+def test_engine_request_takes_the_reference_dream_block_threshold_config():
+    """model.py:905-916 opens Dream's block_threshold runtime with
+    cuda_engine_config(precision, exact_kv=True) (exact_kv from model.py:991)."""
+    for kind in ("q4", "bf16"):
+        assert runtime.engine_request(_reference_engine_config("bf16", True), kind)[1] == 1
+        assert runtime.engine_request(_reference_engine_config("bf16", False), kind)[1] == 0
+    assert runtime.engine_request({}, "q4") == (4, 0)
+    with pytest.raises(ValueError):  # 8-bit linears are not offered
+        runtime.engine_request(_reference_engine_config("int8_weight_only", True), "q4")
+    for bad in ({"d2f_exact_kv_cache": 2}, {"prefix_kv_cache": 1}, {"canvas_cache": 1},
+                {"compute_dtype": 1}):
+        with pytest.raises(ValueError):
+            runtime.engine_request(bad, "q4")
+
+
+def test_session_config_struct_matches_the_reference_fields():
+    """SessionDecodeConfig (abi/lifetimes.py:57-69): eight int32 fields then
+    ``reserved`` (8 ints)."""
+    names = [n for n, _ in _lib.SessionConfig._fields_]
+    assert names == ["decode_strategy", "commit_policy", "attention_mask_kind", "block_size",
+                     "steps", "max_tokens", "trace_canvas", "error_fixing", "reserved"]
+    assert C.sizeof(_lib.SessionConfig) == 16 * 4
+    text = HEADER.read_text()
+    assert re.search(r"int32_t reserved\[8\];[^\n]*\n\} drt_session_config;", text)
