@@ -79,13 +79,18 @@ __global__ __launch_bounds__(64 * QW) void attn_split_kernel(
   const bool q_ok = qv < n_qv;
   const int qrow = q_ok ? qv / G : 0;
   const int qhead = kvh * G + (q_ok ? qv - (qv / G) * G : 0);
-  vec qf[8];
+  vec qf[8], qfl[8];  // Q hi / lo planes (lo at + n_rows * Hq * 128)
   {
     const T* qp = q + ((int64_t)qrow * Hq + qhead) * 128 + 8 * (lane >> 5);
+    const T* qpl = qp + (int64_t)n_rows * Hq * 128;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      if (q_ok) qf[i] = *(const vec*)(qp + 16 * i);
-      else qf[i] = vec{};
+      if (q_ok) {
+        qf[i] = *(const vec*)(qp + 16 * i);
+        qfl[i] = *(const vec*)(qpl + 16 * i);
+      } else {
+        qf[i] = qfl[i] = vec{};
+      }
     }
   }
   const int qpos = row_pos0 + qrow;
@@ -145,6 +150,7 @@ __global__ __launch_bounds__(64 * QW) void attn_split_kernel(
       for (int i = 0; i < 8; ++i) {
         const vec kf = *(const vec*)(kt + (i * 64 + lane) * 8);
         s = MfmaT<T>::mma(kf, qf[i], s);
+        s = MfmaT<T>::mma(kf, qfl[i], s);
       }
       float tmax = -INFINITY;
 #pragma unroll
@@ -236,6 +242,7 @@ __global__ __launch_bounds__(64 * QW) void attn_split_kernel(
 // m = -inf, l = 0; the combine then skips their O.
 // n_keys comes from `desc` when it is set (graph replays), else from the argument.
 constexpr int DEC_QROW = 136;  // 16-bit elements per Q row in LDS (+16 B pad)
+constexpr int DEC_QLO = 64 * DEC_QROW;  // elements from the Q hi plane to the lo plane in LDS
 constexpr int DEC_TILES_UP_FRONT = 3;
 
 // K/V fragments of tile t. With real == false every lane reads the first 16
@@ -291,32 +298,49 @@ DRT_DEV void attend_group(const typename MfmaT<T>::vec (&kc)[NG][8],
   // (inline asm, so the compiler does not sink them to their use) before step
   // i's MFMAs, and waited for after them; the wait takes the registers as
   // operands, so nothing reads them earlier.
+  // The lo plane of Q sits DEC_QLO elements after the hi plane: every score
+  // MFMA has a twin on the lo fragments (Q carried to ~22 bits, K exact).
   const T* qrow = qs + (lane & 31) * DEC_QROW + 8 * (lane >> 5);
   const uint32_t qaddr = (uint32_t)(uintptr_t)qrow;
-  vec qf[QT];
+  vec qf[QT], qfl[QT];
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt) qf[qt] = *(const vec*)(qrow + qt * 32 * DEC_QROW);
+  for (int qt = 0; qt < QT; ++qt) {
+    qf[qt] = *(const vec*)(qrow + qt * 32 * DEC_QROW);
+    qfl[qt] = *(const vec*)(qrow + DEC_QLO + qt * 32 * DEC_QROW);
+  }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    vec qn[QT];
+    vec qn[QT], qnl[QT];
     if (i < 7) {
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt)
+      for (int qt = 0; qt < QT; ++qt) {
         asm volatile("ds_read_b128 %0, %1 offset:%2"
                      : "=v"(qn[qt])
                      : "v"(qaddr), "i"((qt * 32 * DEC_QROW + 16 * (i + 1)) * 2));
+        asm volatile("ds_read_b128 %0, %1 offset:%2"
+                     : "=v"(qnl[qt])
+                     : "v"(qaddr), "i"((DEC_QLO + qt * 32 * DEC_QROW + 16 * (i + 1)) * 2));
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
-      for (int g = 0; g < NG; ++g) sc[g][qt] = MfmaT<T>::mma(kc[g][i], qf[qt], sc[g][qt]);
+      for (int g = 0; g < NG; ++g) {
+        sc[g][qt] = MfmaT<T>::mma(kc[g][i], qf[qt], sc[g][qt]);
+        sc[g][qt] = MfmaT<T>::mma(kc[g][i], qfl[qt], sc[g][qt]);
+      }
     __builtin_amdgcn_sched_barrier(0);
     if (i < 7) {
-      if constexpr (QT == 1) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(qn[0]));
-      else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(qn[0]), "+v"(qn[1]));
+      if constexpr (QT == 1) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(qn[0]), "+v"(qnl[0]));
+      else
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(qn[0]), "+v"(qn[1]), "+v"(qnl[0]), "+v"(qnl[1]));
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt) qf[qt] = qn[qt];
+      for (int qt = 0; qt < QT; ++qt) {
+        qf[qt] = qn[qt];
+        qfl[qt] = qnl[qt];
+      }
     }
   }
 #pragma unroll
@@ -396,8 +420,8 @@ __global__ __launch_bounds__(256) void attn_decode_reg_kernel(
   const int t_end = (int)((int64_t)n_tiles * (rg + 1) / R);
   const int64_t part = (int64_t)rg * Hkv + kvh;
   extern __shared__ __align__(16) char smem[];
-  T* qs = (T*)smem;                                       // [QT*32][DEC_QROW]
-  float* mrg = (float*)(smem + QT * 32 * DEC_QROW * 2);   // [4][SLOT]
+  T* qs = (T*)smem;    // [QT*32][DEC_QROW] hi, lo plane at + DEC_QLO
+  float* mrg = (float*)smem;  // [4][SLOT], over the Q planes once every wave is done
 
   if (t_begin >= t_end) {  // no keys in this range
     if (threadIdx.x < QT * 32) {
@@ -410,13 +434,16 @@ __global__ __launch_bounds__(256) void attn_decode_reg_kernel(
   // unconditional (clamped rows) so the wait for Q below does not also wait for
   // the K/V loads issued after it.
   constexpr int QCH = QT * 2;  // QT*32 rows x 16 chunks / 256 threads
-  u32x4 qraw[QCH];
+  const T* q_lo = q + (int64_t)n_rows * Hq * 128;  // the Q lo plane
+  u32x4 qraw[QCH], qrawl[QCH];
 #pragma unroll
   for (int i = 0; i < QCH; ++i) {
     const int c = threadIdx.x + 256 * i;
     const int qvc = min(c >> 4, n_qv - 1);
     const int row = qvc / G, head = kvh * G + (qvc - row * G);
-    qraw[i] = *(const u32x4*)(q + ((int64_t)row * Hq + head) * 128 + (c & 15) * 8);
+    const int64_t off = ((int64_t)row * Hq + head) * 128 + (c & 15) * 8;
+    qraw[i] = *(const u32x4*)(q + off);
+    qrawl[i] = *(const u32x4*)(q_lo + off);
   }
   __builtin_amdgcn_sched_barrier(0);
   const T* base = kv + (int64_t)kvh * kv_head_stride;
@@ -434,8 +461,10 @@ __global__ __launch_bounds__(256) void attn_decode_reg_kernel(
 #pragma unroll
   for (int i = 0; i < QCH; ++i) {
     const int c = threadIdx.x + 256 * i;
-    *(u32x4*)(qs + (c >> 4) * DEC_QROW + (c & 15) * 8) =
-        (c >> 4) < n_qv ? qraw[i] : u32x4{0u, 0u, 0u, 0u};
+    const bool ok = (c >> 4) < n_qv;
+    T* d = qs + (c >> 4) * DEC_QROW + (c & 15) * 8;
+    *(u32x4*)d = ok ? qraw[i] : u32x4{0u, 0u, 0u, 0u};
+    *(u32x4*)(d + DEC_QLO) = ok ? qrawl[i] : u32x4{0u, 0u, 0u, 0u};
   }
   __syncthreads();
 
@@ -467,7 +496,9 @@ __global__ __launch_bounds__(256) void attn_decode_reg_kernel(
   for (int qt = 0; qt < QT; ++qt) l_run[qt] += __shfl_xor(l_run[qt], 32, 64);
 
   // every wave stores its (O, m, l); O as 16-byte units of 4 accumulator rows,
-  // unit ((qt*4 + hb)*4 + r/4)*64 + lane
+  // unit ((qt*4 + hb)*4 + r/4)*64 + lane (the merge area overlays Q: every
+  // wave has read its last Q fragment first)
+  __syncthreads();
   float* mine = mrg + wave * SLOT;
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
@@ -533,7 +564,9 @@ __global__ __launch_bounds__(256) void attn_decode_reg_kernel(
 // the rest of the range is still streaming, and release each slot (freed flag)
 // after reading it into registers. Every wait on a flag is bounded: a wait that
 // runs out sets *err (the host reports it) and the kernel still finishes.
-constexpr int DECR_SLOTS = 8;
+// Tile slots of the ring: 8, or 7 when the Q planes of 64 query vectors leave
+// no room for an eighth (160 KiB of LDS per work-group).
+template <int QT> constexpr int decr_slots() { return QT == 1 ? 8 : 7; }
 constexpr int DECR_SPIN = 1 << 22;
 // s_waitcnt immediates (gfx9: vmcnt bits 3:0 + 15:14, expcnt 6:4, lgkmcnt 11:8)
 constexpr int DECR_VM48 = 0xCF70, DECR_VM32 = 0x8F70, DECR_VM16 = 0x4F70, DECR_VM0 = 0x0F70;
@@ -584,6 +617,7 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
     int Hq, int Hkv, int n_keys_arg, const StepDesc* __restrict__ desc,
     float* __restrict__ o_part, float* __restrict__ ml_part, float scale, int* err) {
   typedef typename MfmaT<T>::vec vec;
+  constexpr int DECR_SLOTS = decr_slots<QT>();
   constexpr int SLOTS = QT * 4096;
   constexpr int SLOT = SLOTS + QT * 64 * 2;
   const int lane = threadIdx.x & 63;
@@ -601,8 +635,8 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
   extern __shared__ __align__(16) char smem[];
   int* ready = (int*)smem;                               // [DECR_SLOTS]
   int* freed = ready + DECR_SLOTS;                       // [DECR_SLOTS]
-  T* qs = (T*)(smem + 128);                              // [QT*32][DEC_QROW]
-  char* tiles = smem + 128 + QT * 32 * DEC_QROW * 2;     // [DECR_SLOTS][16 KiB]
+  T* qs = (T*)(smem + 128);  // [QT*32][DEC_QROW] hi, lo plane at + DEC_QLO
+  char* tiles = smem + 128 + (DEC_QLO + QT * 32 * DEC_QROW) * 2;  // [DECR_SLOTS][16 KiB]
   float* mrg = (float*)(smem + 128);                     // [4][SLOT], over Q and the tiles
 
   if (n <= 0) {
@@ -633,20 +667,25 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
     const int n0 = min(n, 2);
     for (int t = 0; t < n0; ++t) dma_tile(t);
   } else {
-    u32x4 qraw[QCH];
+    const T* q_lo = q + (int64_t)n_rows * Hq * 128;  // the Q lo plane
+    u32x4 qraw[QCH], qrawl[QCH];
 #pragma unroll
     for (int i = 0; i < QCH; ++i) {
       const int ch = threadIdx.x + 256 * i;
       const int qvc = min(ch >> 4, n_qv - 1);
       const int row = qvc / G, head = kvh * G + (qvc - row * G);
-      qraw[i] = *(const u32x4*)(q + ((int64_t)row * Hq + head) * 128 + (ch & 15) * 8);
+      const int64_t off = ((int64_t)row * Hq + head) * 128 + (ch & 15) * 8;
+      qraw[i] = *(const u32x4*)(q + off);
+      qrawl[i] = *(const u32x4*)(q_lo + off);
     }
     if (threadIdx.x < 2 * DECR_SLOTS) ready[threadIdx.x] = 0;  // ready and freed
 #pragma unroll
     for (int i = 0; i < QCH; ++i) {
       const int ch = threadIdx.x + 256 * i;
-      *(u32x4*)(qs + (ch >> 4) * DEC_QROW + (ch & 15) * 8) =
-          (ch >> 4) < n_qv ? qraw[i] : u32x4{0u, 0u, 0u, 0u};
+      const bool ok = (ch >> 4) < n_qv;
+      T* d = qs + (ch >> 4) * DEC_QROW + (ch & 15) * 8;
+      *(u32x4*)d = ok ? qraw[i] : u32x4{0u, 0u, 0u, 0u};
+      *(u32x4*)(d + DEC_QLO) = ok ? qrawl[i] : u32x4{0u, 0u, 0u, 0u};
     }
     decr_waitcnt<DECR_LGKM0>();  // Q and the flags are written
   }
@@ -708,7 +747,7 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
         kc[0][i] = tp[i * 64 + lane];
         vc[0][i] = tp[512 + i * 64 + lane];
       }
-      if (t + DECR_SLOTS < n) {  // the producer reuses the slot for tile t + 8
+      if (t + DECR_SLOTS < n) {  // the producer reuses the slot for tile t + DECR_SLOTS
         decr_waitcnt<DECR_LGKM0>();  // the slot's reads are complete
         if (lane == 0)
           asm volatile("ds_add_u32 %0, %1"
@@ -776,12 +815,13 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
 // dims hb*32 + 8rq .. +8, one thread per float, so 256 work-groups share the
 // reads. Each query vector's 8 dims are one 8-element
 // chunk of the output row. Empty ranges (m = -inf) are skipped.
-// out_fmt: 0 = ACT_F16P (no group sums: its consumer sums the fp16 values
-// itself), 1 = ACT_BF16, 2 = fp32 plain, 3 = bf16 plain.
+// out_fmt: 0 = ACT_F16P (no group sums: its consumer sums the hi + lo values
+// itself), 1 = ACT_BF16, 2 = fp32 plain, 3 = bf16 plain. A value beyond the
+// fp16 range sets DRT_ERR_F16_RANGE in *err.
 template <int QT>
 __global__ __launch_bounds__(256) void attn_decode_combine_kernel(
     const float* __restrict__ o_part, const float* __restrict__ ml_part, int R, int n_rows,
-    int Hq, int Hkv, void* __restrict__ out, int out_fmt) {
+    int Hq, int Hkv, void* __restrict__ out, int out_fmt, int* __restrict__ err) {
   constexpr int SLOTS = QT * 4096;
   const int kvh = blockIdx.x, qt = blockIdx.y, hb = blockIdx.z >> 2, rq = blockIdx.z & 3;
   const int j = threadIdx.x;
@@ -883,11 +923,20 @@ __global__ __launch_bounds__(256) void attn_decode_combine_kernel(
   float vals[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) vals[e] = tile[j][e];
-  if (out_fmt == 0) {
-    _Float16 pk[8];
+  if (out_fmt == 0) {  // ACT_F16P: hi plane, lo plane at + n_rows * D
+    _Float16 pk[8], pl[8];
+    bool over = false;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) pk[f16p_index(e)] = (_Float16)vals[e];
-    *(u32x4*)((_Float16*)out + (int64_t)row * D + col0) = __builtin_bit_cast(u32x4, pk);
+    for (int e = 0; e < 8; ++e) {
+      const _Float16 h = (_Float16)vals[e];
+      pk[f16p_index(e)] = h;
+      pl[f16p_index(e)] = f16_lo(vals[e], h);
+      over = over || f16_overflows(vals[e]);
+    }
+    _Float16* o = (_Float16*)out + (int64_t)row * D + col0;
+    *(u32x4*)o = __builtin_bit_cast(u32x4, pk);
+    *(u32x4*)(o + (int64_t)n_rows * D) = __builtin_bit_cast(u32x4, pl);
+    if (over && err) atomicOr(err, DRT_ERR_F16_RANGE);
   } else if (out_fmt == 1 || out_fmt == 3) {
     uint16_t pk[8];
 #pragma unroll
@@ -908,7 +957,8 @@ __global__ __launch_bounds__(256) void attn_decode_combine_kernel(
 extern "C" __global__ void attn_combine_kernel(const float* __restrict__ o_part,
                                                const float* __restrict__ ml_part, int n_splits,
                                                int n_rows, int Hq, int Hkv, void* __restrict__ out,
-                                               float* __restrict__ xsum, int out_fmt) {
+                                               float* __restrict__ xsum, int out_fmt,
+                                               int* __restrict__ err) {
   const int lane = threadIdx.x & 63;
   const int64_t wid = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
   if (wid >= (int64_t)n_rows * Hq) return;
@@ -949,12 +999,18 @@ extern "C" __global__ void attn_combine_kernel(const float* __restrict__ o_part,
   const float v0 = a0 * inv, v1 = a1 * inv;
   const int D = Hq * 128;
   const int c0 = head * 128 + lane, c1 = c0 + 64;
-  if (out_fmt == 0) {
+  if (out_fmt == 0) {  // ACT_F16P: hi plane, lo plane at + n_rows * D
     _Float16* o = (_Float16*)out + (int64_t)row * D;
+    _Float16* ol = o + (int64_t)n_rows * D;
     const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
+    const _Float16 l0 = f16_lo(v0, h0), l1 = f16_lo(v1, h1);
     o[f16p_index(c0)] = h0;
     o[f16p_index(c1)] = h1;
-    const float s0 = wave_sum((float)h0), s1 = wave_sum((float)h1);
+    ol[f16p_index(c0)] = l0;
+    ol[f16p_index(c1)] = l1;
+    if (__ballot(f16_overflows(v0) || f16_overflows(v1)) && lane == 0 && err)
+      atomicOr(err, DRT_ERR_F16_RANGE);
+    const float s0 = wave_sum((float)h0 + (float)l0), s1 = wave_sum((float)h1 + (float)l1);
     if (lane == 0) {
       xsum[(int64_t)row * (D >> 6) + (c0 >> 6)] = s0;
       xsum[(int64_t)row * (D >> 6) + (c0 >> 6) + 1] = s1;
@@ -1074,7 +1130,7 @@ size_t attention_part_bytes(const AttnPlan& p, int n_rows, int Hq, int Hkv) {
 void attention(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_stride,
                int n_rows, int Hq, int Hkv, int n_keys, int row_pos0, int mask_kind,
                int mask_prompt_len, int mask_block, const AttnPlan& plan, float* o_part,
-               float* ml_part, void* out, float* xsum, int out_fmt, hipStream_t s) {
+               float* ml_part, void* out, float* xsum, int out_fmt, hipStream_t s, int* err) {
   require(Hq % Hkv == 0, "attention needs Hq % Hkv == 0");
   require(n_keys >= 1 && n_rows >= 1, "attention needs at least one query row and key");
   const float scale = 1.0f / sqrtf(128.0f);
@@ -1102,7 +1158,7 @@ void attention(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_s
   DRT_HIP(hipGetLastError());
   const int64_t waves = (int64_t)n_rows * Hq;
   hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s,
-                     o_part, ml_part, plan.splits, n_rows, Hq, Hkv, out, xsum, out_fmt);
+                     o_part, ml_part, plan.splits, n_rows, Hq, Hkv, out, xsum, out_fmt, err);
   DRT_HIP(hipGetLastError());
 }
 
@@ -1130,7 +1186,8 @@ void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv
   require(ranges >= 1 && ranges <= 128, "decode attention takes 1..128 key ranges");
   const int qt = (n_rows * G + 31) / 32;
   const float scale = 1.0f / sqrtf(128.0f);
-  const size_t lds = (size_t)qt * 32 * DEC_QROW * 2 + (size_t)4 * (qt * 4096 + qt * 128) * 4;
+  const size_t lds = std::max((size_t)(DEC_QLO + qt * 32 * DEC_QROW) * 2,
+                              (size_t)4 * (qt * 4096 + qt * 128) * 4);
   const dim3 grid(Hkv, ranges);
   const double bytes = 2.0 * n_rows * Hq * 128 + 4.0 * n_keys * Hkv * 128;
   float* o_part = part;
@@ -1154,7 +1211,8 @@ void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv
                ml_part, scale, err);                                                        \
   }
   static const bool reg_tiles = getenv("DRT_ATTN_NO_DMA") != nullptr;
-  const size_t ldsr = 128 + (size_t)qt * 32 * DEC_QROW * 2 + (size_t)DECR_SLOTS * 16384;
+  const size_t ldsr = 128 + (size_t)(DEC_QLO + qt * 32 * DEC_QROW) * 2 +
+                      (size_t)(qt == 1 ? decr_slots<1>() : decr_slots<2>()) * 16384;
   if (!reg_tiles) {
     if (bf16) {
       if (qt == 1) DRT_DECR(__bf16, 1) else DRT_DECR(__bf16, 2)
@@ -1174,10 +1232,10 @@ void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv
   const size_t clds = (size_t)ranges * 32 * 4;
   if (qt == 1)
     hipLaunchKernelGGL(attn_decode_combine_kernel<1>, cgrid, dim3(256), clds, s, o_part, ml_part,
-                       ranges, n_rows, Hq, Hkv, out, out_fmt);
+                       ranges, n_rows, Hq, Hkv, out, out_fmt, err);
   else
     hipLaunchKernelGGL(attn_decode_combine_kernel<2>, cgrid, dim3(256), clds, s, o_part, ml_part,
-                       ranges, n_rows, Hq, Hkv, out, out_fmt);
+                       ranges, n_rows, Hq, Hkv, out, out_fmt, err);
   DRT_HIP(hipGetLastError());
 }
 

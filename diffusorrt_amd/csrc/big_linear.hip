@@ -8,13 +8,18 @@
 //
 // Work-group tile: 128 rows x 256 columns, 4 waves side by side in N; a wave
 // owns 128 x 64 (4 x 2 MFMA 32x32x16 tiles, 128 fp32 accumulators per lane).
-//   A (the ACT_F16P activation [M][K]) is staged per 64-k group in LDS, double
-//     buffered; every wave reads all 128 rows (16 KiB per group).
+//   A (the ACT_F16P activation: hi and lo planes of [M][K]) is streamed per
+//     64-k group straight into LDS (global_load_lds, no registers held),
+//     double buffered: 2 planes x 128 rows x 128 B per group. Rows are stored
+//     unpadded with the 16-byte chunks of row r permuted (chunk c at position
+//     c ^ (r & 7)), so the MFMA fragment reads of 8 consecutive rows hit 8
+//     different bank groups. Each MFMA step multiplies hi and lo by the same B.
 //   B (q4 tile layout: per 32-column n-tile and 64-k group, 1 KiB of words and
 //     32 scale|bias pairs) goes straight from global memory to registers and is
-//     dequantized there: 2 n-tiles per wave per group.
-// A register ring keeps the next group's loads in flight during the MFMAs, and
-// two work-groups per CU (<= 256 registers per lane) hide each other's waits.
+//     dequantized there, one k step at a time: 2 n-tiles per wave per group.
+// Group g + 1's loads are issued right after the barrier that proves group g
+// in LDS, so they stream during g's MFMAs; two work-groups per CU (<= 256
+// registers per lane) hide each other's waits.
 // Split-K over blockIdx.z (KS slices) writes fp32 partial slices y + ks * M * N
 // that a reduce pass sums (residual_norm_kernel).
 // Epilogues run on 32-row pieces of the tile staged through LDS:
@@ -31,46 +36,45 @@ namespace {
 
 constexpr int BG_WM = 128;                     // rows per work-group
 constexpr int BG_WN = 256;                     // columns per work-group (4 waves x 64)
-constexpr int BG_AROW = 72;                    // fp16 elements per LDS A row (64 + 16 B pad)
-constexpr int BG_ABUF = BG_WM * BG_AROW;       // fp16 elements per A buffer
+constexpr int BG_PLANE_BYTES = BG_WM * 128;    // one plane of one group: 128 rows x 64 halves
+constexpr int BG_BUF_BYTES = 2 * BG_PLANE_BYTES;  // hi + lo planes of one group
 constexpr int BG_EROW = BG_WN + 4;             // floats per LDS row of an epilogue piece
-constexpr int BG_STAGE_BYTES = 2 * BG_ABUF * 2 > 32 * BG_EROW * 4 ? 2 * BG_ABUF * 2
-                                                                   : 32 * BG_EROW * 4;
-constexpr int BG_V_OFF = (BG_STAGE_BYTES + 15) / 16 * 16;
-constexpr int BG_LDS = BG_V_OFF + 4096 * 2;    // + one V tile half for the QKV epilogue
+constexpr int BG_V_OFF = (32 * BG_EROW * 4 + 15) / 16 * 16;  // V tile half, after the piece
+constexpr int BG_LDS = 2 * BG_BUF_BYTES;       // two group buffers (the epilogue reuses them)
+static_assert(BG_V_OFF + 4096 * 2 <= BG_LDS, "epilogue piece + V tile must fit the A buffers");
 
 template <int S> struct Slot { static constexpr int value = S; };
-// register ring of group loads: RING - 1 groups in flight ahead of the MFMAs
-// (2: two work-groups per CU, the other work-group hides the latency)
-constexpr int BG_RING = 2;
 
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 
-// fp16 B fragments of one 64-k group of one 32-column n-tile: word t of the lane
-// holds the 8 k of MFMA step t in the ACT_F16P order (0,4,1,5,2,6,3,7); nibble
-// pairs become (1024 + q) halves by bit placement, then q * s + b in one fma.
-DRT_DEV void dequant_q4_group(const u32x4 w, uint32_t sbv, f16x8 (&b)[4]) {
+// fp16 B fragment of k step t of one 64-k group of one 32-column n-tile: word t
+// of the lane holds the 8 k of the step in the ACT_F16P order (0,4,1,5,2,6,3,7);
+// nibble pairs become (1024 + q) halves by bit placement, then q * s + b in one fma.
+DRT_DEV f16x8 dequant_q4_step(uint32_t wt, uint32_t sbv) {
   const _Float16 s = (_Float16)bf16_bits_to_float(sbv & 0xffffu);
   const _Float16 z = (_Float16)bf16_bits_to_float(sbv >> 16);
   const h2v s2 = {s, s}, z2 = {z, z};
   const h2v k2 = {(_Float16)-1024.f, (_Float16)-1024.f};
+  u32x4 o;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    u32x4 o;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const h2v h = __builtin_bit_cast(h2v, ((w[t] >> (4 * e)) & 0x000F000Fu) | 0x64006400u);
-      o[e] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(h + k2, s2, z2));
-    }
-    b[t] = __builtin_bit_cast(f16x8, o);
+  for (int e = 0; e < 4; ++e) {
+    const h2v h = __builtin_bit_cast(h2v, ((wt >> (4 * e)) & 0x000F000Fu) | 0x64006400u);
+    o[e] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(h + k2, s2, z2));
   }
+  return __builtin_bit_cast(f16x8, o);
+}
+
+// LDS fragment read the compiler does not see: a plain read after a
+// direct-to-LDS load makes it wait for every global load in flight first
+// (it cannot tell the group being read from the one being filled).
+DRT_DEV void lds_read16(f16x8& v, uint32_t addr) {
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
 }
 
 }  // namespace
 
 template <int EPI>
 __global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int KS) {
-  constexpr int RING = BG_RING;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int M = a.M, N = a.N, K = a.K, G = K >> 6;
   const int n0 = blockIdx.x * BG_WN, m0 = blockIdx.y * BG_WM, ks = blockIdx.z;
@@ -82,76 +86,80 @@ __global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int K
   const int nt0 = min((n0 >> 5) + 2 * wave, NT - 1);
   const int nt1 = min((n0 >> 5) + 2 * wave + 1, NT - 1);
   extern __shared__ __align__(16) char smem[];
-  _Float16* as = (_Float16*)smem;  // [2][BG_WM][BG_AROW]
   const _Float16* act = (const _Float16*)a.act;
 
-  u32x4 ra[RING][4];
-  u32x4 wq[RING][2];
-  uint32_t wsb[RING][2];
-  // A chunk c = threadIdx.x + 256 i of a group: row c >> 3, 16-byte part c & 7
-  auto issue = [&](int g, auto slot) {
+  u32x4 wq[2][2];
+  uint32_t wsb[2][2];
+  // A of group g into buffer buf: plane pl, 8-row block blk = wave + 4i is one
+  // wave instruction (lane l: row blk*8 + (l >> 3), LDS position l & 7, which
+  // holds the row's chunk (l & 7) ^ (row & 7)); rows past M re-read row M - 1,
+  // whose copies feed only outputs that are never stored.
+  auto issue = [&](int g, int buf, auto slot) {
     constexpr int S = decltype(slot)::value;
+    const int r_in = lane >> 3, c = (lane & 7) ^ (r_in & 7);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = threadIdx.x + 256 * i;
-      const int m = min(m0 + (c >> 3), M - 1);  // rows past M are zeroed when stashed
-      ra[S][i] = *(const u32x4*)(act + (int64_t)m * K + g * 64 + (c & 7) * 8);
-    }
+    for (int pl = 0; pl < 2; ++pl)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int blk = wave + 4 * i;
+        const int m = min(m0 + blk * 8 + r_in, M - 1);
+        const _Float16* src = act + ((int64_t)pl * M + m) * K + g * 64 + c * 8;
+        char* dst = smem + buf * BG_BUF_BYTES + pl * BG_PLANE_BYTES + blk * 1024;
+        __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)src,
+                                         (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+      }
     wq[S][0] = *q4_tile_words(a.qw, nt0, G, g, lane);
     wq[S][1] = *q4_tile_words(a.qw, nt1, G, g, lane);
     wsb[S][0] = q4_tile_sb(a.sb, nt0, G, g, lane);
     wsb[S][1] = q4_tile_sb(a.sb, nt1, G, g, lane);
-  };
-  auto stash = [&](int buf, auto slot) {
-    constexpr int S = decltype(slot)::value;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = threadIdx.x + 256 * i;
-      const bool ok = m0 + (c >> 3) < M;
-      *(u32x4*)(as + buf * BG_ABUF + (c >> 3) * BG_AROW + (c & 7) * 8) =
-          ok ? ra[S][i] : u32x4{0u, 0u, 0u, 0u};
-    }
   };
 
   f32x16 acc[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i) acc[i][0] = acc[i][1] = f32x16{};
 
-  if (n_g > 0) issue(g_lo, Slot<0>{});
-  if (RING > 2 && n_g > 1) issue(g_lo + 1, Slot<1 % RING>{});
-  if (RING > 3 && n_g > 2) issue(g_lo + 2, Slot<2 % RING>{});
-  if (n_g > 0) stash(0, Slot<0>{});
-  __syncthreads();
+  if (n_g > 0) issue(g_lo, 0, Slot<0>{});
+  // this lane's fragment row within each 32-row m-tile is lane & 31; its k
+  // chunk at step t is 4 * (lane >> 5) + t, stored at position chunk ^ (row & 7)
+  const uint32_t lds0 = (uint32_t)(uintptr_t)smem + (lane & 31) * 128;
 
-  // group gi (relative) lives in ring slot gi % RING and LDS buffer gi & 1
   auto step = [&](int gi, auto slot) {
     constexpr int S = decltype(slot)::value;
-    f16x8 bf[2][4];
-    dequant_q4_group(wq[S][0], wsb[S][0], bf[0]);
-    dequant_q4_group(wq[S][1], wsb[S][1], bf[1]);
-    // the slot of group gi + RING - 1 held group gi - 1: consumed (B) and stashed (A)
-    if (gi + RING - 1 < n_g) issue(g_lo + gi + RING - 1, Slot<(S + RING - 1) % RING>{});
-    const _Float16* ab = as + (gi & 1) * BG_ABUF;
+    // group gi's loads (issued one step ago) are complete in every lane, and
+    // every wave is done reading the buffer that group gi + 1 overwrites
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    if (gi + 1 < n_g) issue(g_lo + gi + 1, (gi + 1) & 1, Slot<(S + 1) % 2>{});
+    const uint32_t ab = lds0 + (gi & 1) * BG_BUF_BYTES;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
+      const uint32_t pos = (uint32_t)(((4 * (lane >> 5) + t) ^ (lane & 7)) * 16);
+      f16x8 ah[4], al[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const f16x8 af =
-            *(const f16x8*)(ab + (i * 32 + (lane & 31)) * BG_AROW + 32 * (lane >> 5) + 8 * t);
-        acc[i][0] = mfma_f16(af, bf[0][t], acc[i][0]);
-        acc[i][1] = mfma_f16(af, bf[1][t], acc[i][1]);
+        lds_read16(ah[i], ab + i * 32 * 128 + pos);
+        lds_read16(al[i], ab + BG_PLANE_BYTES + i * 32 * 128 + pos);
+      }
+      const f16x8 b0 = dequant_q4_step(wq[S][0][t], wsb[S][0]);
+      const f16x8 b1 = dequant_q4_step(wq[S][1][t], wsb[S][1]);
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(ah[0]), "+v"(ah[1]), "+v"(ah[2]), "+v"(ah[3]), "+v"(al[0]),
+                     "+v"(al[1]), "+v"(al[2]), "+v"(al[3]));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[i][0] = mfma_f16(ah[i], b0, acc[i][0]);
+        acc[i][1] = mfma_f16(ah[i], b1, acc[i][1]);
+        acc[i][0] = mfma_f16(al[i], b0, acc[i][0]);
+        acc[i][1] = mfma_f16(al[i], b1, acc[i][1]);
       }
     }
-    // the other buffer was last read before the previous step's barrier
-    if (gi + 1 < n_g) stash((gi + 1) & 1, Slot<(S + 1) % RING>{});
-    __syncthreads();
   };
-  for (int gb = 0; gb < n_g; gb += RING) {
+  for (int gb = 0; gb < n_g; gb += 2) {
     step(gb, Slot<0>{});
-    if (gb + 1 < n_g) step(gb + 1, Slot<1 % RING>{});
-    if (RING > 2 && gb + 2 < n_g) step(gb + 2, Slot<2 % RING>{});
-    if (RING > 3 && gb + 3 < n_g) step(gb + 3, Slot<3 % RING>{});
+    if (gb + 1 < n_g) step(gb + 1, Slot<1>{});
   }
+  __syncthreads();  // every wave's last fragment reads are done: the epilogue reuses the LDS
 
   // Epilogue in 32-row pieces (MFMA m-tile p of every wave) through LDS.
   float* e = (float*)smem;  // [32][BG_EROW]
@@ -183,24 +191,32 @@ __global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int K
         }
       }
     } else if (EPI == EPI_SWIGLU) {
-      // output chunk q: block q >> 3 of [gate 64 | up 64], 8 outputs at (q & 7) * 8
+      // output chunk q: block q >> 3 of [gate 64 | up 64], 8 outputs at (q & 7) * 8;
+      // ACT_F16P hi plane, then the lo plane at + M * F
       const int F = N >> 1;
+      bool over = false;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int c = threadIdx.x + 256 * i;
         const int r = c >> 4, q = c & 15, blk = q >> 3, c8 = (q & 7) * 8;
         if (mp + r < M && n0 + blk * 128 < N) {
-          _Float16 h[8];
+          _Float16 h[8], lo[8];
 #pragma unroll
           for (int k = 0; k < 8; ++k) {
             const float g = e[r * BG_EROW + blk * 128 + c8 + k];
             const float u = e[r * BG_EROW + blk * 128 + 64 + c8 + k];
-            h[f16p_index(k)] = (_Float16)(g * (1.f / (1.f + expf(-g))) * u);
+            const float y = g * (1.f / (1.f + expf(-g))) * u;
+            const _Float16 hk = (_Float16)y;
+            h[f16p_index(k)] = hk;
+            lo[f16p_index(k)] = f16_lo(y, hk);
+            over = over || f16_overflows(y);
           }
-          *(u32x4*)((_Float16*)a.act_out + (int64_t)(mp + r) * F + (n0 >> 1) + blk * 64 + c8) =
-              __builtin_bit_cast(u32x4, h);
+          _Float16* dst = (_Float16*)a.act_out + (int64_t)(mp + r) * F + (n0 >> 1) + blk * 64 + c8;
+          *(u32x4*)dst = __builtin_bit_cast(u32x4, h);
+          *(u32x4*)(dst + (int64_t)M * F) = __builtin_bit_cast(u32x4, lo);
         }
       }
+      if (over) raise_range(a);
     } else if (EPI == EPI_QKV) {
       const int rows = min(32, M - mp);
 #pragma unroll

@@ -12,6 +12,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -61,10 +63,41 @@ DRT_DEV double wave_sum_d(double v) {
 }
 
 // Activation formats written by producers and read by the linear kernels.
+//  ACT_F16P: an fp32 value x carried as two fp16 planes of [M][K] each, hi =
+//    fp16(x) first, then lo = fp16(x - hi) at + M*K elements (x - hi is exact in
+//    fp32, so hi + lo holds x to about 22 significant bits); each 8-element chunk
+//    of a row stored in the order (0,4,1,5,2,6,3,7). Group sums, where a
+//    producer writes them, are fp32 sums of hi + lo over 64-wide k groups.
+//  ACT_BF16: bf16, natural order (bf16-weight linears: the reference rounds
+//    their inputs to bf16 itself).
 enum ActFmt : int {
-  ACT_F16P = 0,  // fp16, each 8-chunk stored (0,4,1,5,2,6,3,7) + fp32 group sums
-  ACT_BF16 = 1,  // bf16, natural order (bf16-weight linears)
+  ACT_F16P = 0,
+  ACT_BF16 = 1,
 };
+
+// hi/lo fp16 pair of a float (ACT_F16P, and the Q planes of the attention)
+DRT_DEV _Float16 f16_lo(float x, _Float16 hi) { return (_Float16)(x - (float)hi); }
+template <typename T> DRT_DEV T lo_part(float x, T hi);
+template <> DRT_DEV _Float16 lo_part<_Float16>(float x, _Float16 hi) { return f16_lo(x, hi); }
+template <> DRT_DEV __bf16 lo_part<__bf16>(float x, __bf16 hi) {
+  const float r = x - bf16_bits_to_float(__builtin_bit_cast(uint16_t, hi));
+  return __builtin_bit_cast(__bf16, float_to_bf16_bits(r));
+}
+
+// Bit set in the runtime's error word when a producer met a value beyond the
+// fp16 range (|x| >= 65520 rounds to infinity): the forward's results are not
+// valid and the host reports it.
+constexpr int DRT_ERR_F16_RANGE = 4;
+DRT_DEV bool f16_overflows(float x) { return !(fabsf(x) < 65504.f); }
+
+// Two q4 nibbles at bits 0-3 and 16-19 of w as a pair of exact fp16 integers
+// q: the nibble placed under the exponent of 1024 is the fp16 1024 + q, and one
+// packed fp16 subtraction of 1024 (exact) leaves q.
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+DRT_DEV uint32_t q4_pair_to_f16(uint32_t w) {
+  const f16x2 k = {(_Float16)-1024.f, (_Float16)-1024.f};
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, w | 0x64006400u) + k);
+}
 
 // Position of element k within an ACT_F16P row: chunk order (0,4,1,5,2,6,3,7).
 DRT_DEV int f16p_index(int k) {

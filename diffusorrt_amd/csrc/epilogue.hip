@@ -81,7 +81,7 @@ extern "C" __global__ __launch_bounds__(256) void residual_norm_kernel(
     float* __restrict__ hidden, const float* __restrict__ part, int splits, int M_part,
     int rnd_bf16, const int32_t* __restrict__ src_rows, int write_hidden,
     const uint16_t* __restrict__ norm_w, float eps, int d, int fmt, void* __restrict__ act,
-    float* __restrict__ xsum, int n_rows) {
+    float* __restrict__ xsum, int n_rows, int* __restrict__ err) {
   constexpr int NC = 8;  // chunks per lane for d <= 4096
   const int lane = threadIdx.x & 63;
   const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -156,16 +156,22 @@ extern "C" __global__ __launch_bounds__(256) void residual_norm_kernel(
       n[2 * e] = (v[c][e >> 1][(2 * e) & 3] * inv) * bf16_bits_to_float(wv[e] & 0xffffu);
       n[2 * e + 1] = (v[c][e >> 1][(2 * e + 1) & 3] * inv) * bf16_bits_to_float(wv[e] >> 16);
     }
-    if (fmt == ACT_F16P) {
-      _Float16 h[8];
+    if (fmt == ACT_F16P) {  // hi plane, lo plane at + n_rows * d
+      _Float16 h[8], lo[8];
       float gs = 0.f;
+      bool over = false;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const _Float16 he = (_Float16)n[e];
+        const _Float16 he = (_Float16)n[e], le = f16_lo(n[e], he);
         h[f16p_index(e)] = he;
-        gs += (float)he;
+        lo[f16p_index(e)] = le;
+        gs += (float)he + (float)le;
+        over = over || f16_overflows(n[e]);
       }
-      *(u32x4*)((_Float16*)act + (int64_t)i * d + k) = __builtin_bit_cast(u32x4, h);
+      _Float16* dst = (_Float16*)act + (int64_t)i * d + k;
+      *(u32x4*)dst = __builtin_bit_cast(u32x4, h);
+      *(u32x4*)(dst + (int64_t)n_rows * d) = __builtin_bit_cast(u32x4, lo);
+      if (over && err) atomicOr(err, DRT_ERR_F16_RANGE);
       if (xsum) {
         gs += __shfl_xor(gs, 1, 64);
         gs += __shfl_xor(gs, 2, 64);
@@ -245,13 +251,14 @@ void embed(const int32_t* tokens, const uint16_t* table, float* hidden, int M, i
 
 void residual_norm(float* hidden, const float* part, int splits, int M_part, bool rnd_bf16,
                    const int32_t* src_rows, bool write_hidden, const uint16_t* norm_w, float eps,
-                   int d, int fmt, void* act, float* xsum, int n_out_rows, hipStream_t s) {
+                   int d, int fmt, void* act, float* xsum, int n_out_rows, hipStream_t s,
+                   int* err) {
   require(d % 64 == 0 && d <= 4096, "residual_norm needs d % 64 == 0 and d <= 4096");
   require(!part || (splits >= 1 && splits <= RN_MAX_SPLITS), "residual_norm takes 1..8 slices");
   if (n_out_rows <= 0) return;
   hipLaunchKernelGGL(residual_norm_kernel, dim3((n_out_rows + 3) / 4), dim3(256), 0, s, hidden,
                      part, splits, M_part, (int)rnd_bf16, src_rows, (int)write_hidden, norm_w, eps,
-                     d, fmt, act, xsum, n_out_rows);
+                     d, fmt, act, xsum, n_out_rows, err);
   DRT_HIP(hipGetLastError());
 }
 

@@ -68,19 +68,30 @@ DRT_DEV void stage_norm_items(const FusedArgs& a, int m0, int kc0, int kcn, uint
     x[6] = (v[j][1][2] * inv) * bf16_bits_to_float(w67 & 0xffffu);
     x[7] = (v[j][1][3] * inv) * bf16_bits_to_float(w67 >> 16);
     if (WKIND == W_Q4) {
-      // ACT_F16P: store the 8-chunk in the order (0,4,1,5,2,6,3,7)
-      _Float16 h[8];
+      // ACT_F16P hi / lo planes (the lo plane 32 rows after the hi plane in
+      // LDS): the 8-chunk stored in the order (0,4,1,5,2,6,3,7)
+      _Float16 h[8], lo[8];
+      bool over = false;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) h[e] = (_Float16)x[e];
-      u32x4 pk;
-      pk[0] = (uint32_t)half_bits(h[0]) | ((uint32_t)half_bits(h[4]) << 16);
-      pk[1] = (uint32_t)half_bits(h[1]) | ((uint32_t)half_bits(h[5]) << 16);
-      pk[2] = (uint32_t)half_bits(h[2]) | ((uint32_t)half_bits(h[6]) << 16);
-      pk[3] = (uint32_t)half_bits(h[3]) | ((uint32_t)half_bits(h[7]) << 16);
-      if (c8 < ipr) *(u32x4*)(xs + r * row_h + c8 * 8) = pk;
+      for (int e = 0; e < 8; ++e) {
+        h[e] = (_Float16)x[e];
+        lo[e] = f16_lo(x[e], h[e]);
+        over = over || f16_overflows(x[e]);
+      }
+      if (over && m0 + r < a.M && c8 < ipr) raise_range(a);
+      u32x4 pk, pl;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pk[e] = (uint32_t)half_bits(h[e]) | ((uint32_t)half_bits(h[e + 4]) << 16);
+        pl[e] = (uint32_t)half_bits(lo[e]) | ((uint32_t)half_bits(lo[e + 4]) << 16);
+      }
+      if (c8 < ipr) {
+        *(u32x4*)(xs + r * row_h + c8 * 8) = pk;
+        *(u32x4*)(xs + (32 + r) * row_h + c8 * 8) = pl;
+      }
       float gs = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) gs += (float)h[e];
+      for (int e = 0; e < 8; ++e) gs += (float)h[e] + (float)lo[e];
       // a 64-k group is 8 consecutive items = 8 consecutive lanes
       gs += __shfl_xor(gs, 1, 64);
       gs += __shfl_xor(gs, 2, 64);
@@ -137,8 +148,8 @@ __global__ __launch_bounds__(64 * WN * WK) void fused_linear_kernel(const FusedA
   const int KC = K >> 4;
 
   extern __shared__ __align__(16) char smem[];
-  uint16_t* xs = (uint16_t*)smem;                               // [32][ROW_H]
-  float* xss = (float*)(smem + 32 * ROW_H * 2);                  // [16][32]
+  uint16_t* xs = (uint16_t*)smem;                               // [2][32][ROW_H] (q4: hi, lo)
+  float* xss = (float*)(smem + 2 * 32 * ROW_H * 2);              // [16][32]
   float* rinv = xss + 16 * 32;                                   // [32]
   float* rss = rinv + 32;                                        // [32][NW] row partials
 
@@ -151,7 +162,7 @@ __global__ __launch_bounds__(64 * WN * WK) void fused_linear_kernel(const FusedA
     const int mrow = m0 + (lane & 31);
     const bool row_ok = mrow < M;
     const int mr = row_ok ? mrow : 0;
-    u32x4 wq[P], af[P][4];
+    u32x4 wq[P], af[P][4], afl[P][4];
     uint32_t wsb[P];
     bf16x8 wbf[P], ab[P];
     auto fetch = [&](int slot, int unit) {
@@ -161,8 +172,12 @@ __global__ __launch_bounds__(64 * WN * WK) void fused_linear_kernel(const FusedA
         wsb[slot] = q4_tile_sb(a.sb, ntc, G, unit, lane);
         const u32x4* ap = (const u32x4*)((const uint16_t*)a.act + (int64_t)mr * K + unit * 64 +
                                          32 * (lane >> 5));
+        const u32x4* apl = ap + (int64_t)M * K / 8;  // the lo plane
 #pragma unroll
-        for (int t = 0; t < 4; ++t) af[slot][t] = row_ok ? ap[t] : u32x4{0u, 0u, 0u, 0u};
+        for (int t = 0; t < 4; ++t) {
+          af[slot][t] = row_ok ? ap[t] : u32x4{0u, 0u, 0u, 0u};
+          afl[slot][t] = row_ok ? apl[t] : u32x4{0u, 0u, 0u, 0u};
+        }
       } else {
         wbf[slot] = *bf16_tile_frag(a.wb, ntc, KC, unit, lane);
         const bf16x8* ap = (const bf16x8*)((const uint16_t*)a.act + (int64_t)mr * K + unit * 16 +
@@ -179,7 +194,8 @@ __global__ __launch_bounds__(64 * WN * WK) void fused_linear_kernel(const FusedA
         if (u < u_hi) {
           if (WKIND == W_Q4) {
             // (the LDS staging area is unused on this path: 32 floats per wave)
-            q4_group_mma1_lane(acc, af[p], wq[p], wsb[p], lane, (float*)smem + (threadIdx.x >> 6) * 32);
+            q4_group_mma1_lane(acc, af[p], afl[p], wq[p], wsb[p], lane,
+                               (float*)smem + (threadIdx.x >> 6) * 32);
           } else {
             acc = mfma_bf16(ab[p], wbf[p], acc);
           }
@@ -244,12 +260,15 @@ __global__ __launch_bounds__(64 * WN * WK) void fused_linear_kernel(const FusedA
       __syncthreads();  // rinv ready / previous chunk's LDS reads done
       if (PRO == PRO_ACT) {
         const int vpr = kcn / 8;
-        for (int i = threadIdx.x; i < 32 * vpr; i += NTHR) {
-          const int r = i / vpr, v = i - r * vpr;
+        const int planes = WKIND == W_Q4 ? 2 : 1;  // ACT_F16P: hi and lo planes
+        for (int i = threadIdx.x; i < planes * 32 * vpr; i += NTHR) {
+          const int pr = i / vpr, v = i - pr * vpr;  // pr = plane * 32 + row
+          const int r = pr & 31, pl = pr >> 5;
           const int m = m0 + r;
           u32x4 val = {0u, 0u, 0u, 0u};
-          if (m < M) val = *(const u32x4*)((const uint16_t*)a.act + (int64_t)m * K + kc0 + v * 8);
-          *(u32x4*)(xs + r * ROW_H + v * 8) = val;
+          if (m < M)
+            val = *(const u32x4*)((const uint16_t*)a.act + ((int64_t)pl * M + m) * K + kc0 + v * 8);
+          *(u32x4*)(xs + pr * ROW_H + v * 8) = val;
         }
         if (WKIND == W_Q4) {
           for (int i = threadIdx.x; i < 32 * (kcn / 64); i += NTHR) {
@@ -273,13 +292,16 @@ __global__ __launch_bounds__(64 * WN * WK) void fused_linear_kernel(const FusedA
               if (WKIND == W_Q4) {
                 const _Float16* arow =
                     (const _Float16*)xs + (lane & 31) * ROW_H + uc * 64 + 32 * (lane >> 5);
-                f16x8 af[4];
+                f16x8 af[4], afl[4];
 #pragma unroll
-                for (int t = 0; t < 4; ++t) af[t] = *(const f16x8*)(arow + 8 * t);
+                for (int t = 0; t < 4; ++t) {
+                  af[t] = *(const f16x8*)(arow + 8 * t);
+                  afl[t] = *(const f16x8*)(arow + 32 * ROW_H + 8 * t);
+                }
                 float xsr[16];
 #pragma unroll
                 for (int r = 0; r < 16; ++r) xsr[r] = xss[uc * 32 + mfma_row(r, lane)];
-                q4_group_mma1(acc, af, xsr, wq[p], wsb[p]);
+                q4_group_mma1(acc, af, afl, xsr, wq[p], wsb[p]);
               } else {
                 const bf16x8 af =
                     *(const bf16x8*)(xs + (lane & 31) * ROW_H + uc * 16 + 8 * (lane >> 5));
@@ -334,9 +356,12 @@ __global__ __launch_bounds__(64 * WN * WK) void fused_linear_kernel(const FusedA
       const float g = TT(r, lane), u = TT(r, 64 + lane);
       const float y = g * (1.f / (1.f + expf(-g))) * u;
       if (a.act_fmt == ACT_F16P) {
-        const _Float16 h = (_Float16)y;
-        ((_Float16*)a.act_out)[(int64_t)m * F + f16p_index(f0 + lane)] = h;
-        const float s = wave_sum((float)h);
+        const _Float16 h = (_Float16)y, lo = f16_lo(y, h);
+        _Float16* o = (_Float16*)a.act_out + (int64_t)m * F + f16p_index(f0 + lane);
+        o[0] = h;
+        o[(int64_t)M * F] = lo;
+        if (__ballot(f16_overflows(y)) && lane == 0) raise_range(a);
+        const float s = wave_sum((float)h + (float)lo);
         if (lane == 0) a.xsum_out[(int64_t)m * (F >> 6) + (f0 >> 6)] = s;
       } else {
         ((uint16_t*)a.act_out)[(int64_t)m * F + f0 + lane] = float_to_bf16_bits(y);
@@ -363,10 +388,10 @@ __global__ __launch_bounds__(64 * WN * WK) void fused_linear_kernel(const FusedA
 
 #define DRT_INST(W, WN, WK, P, E) \
   template __global__ void fused_linear_kernel<W, WN, WK, P, E>(const FusedArgs);
-DRT_INST(W_Q4, 4, 4, PRO_NORM, EPI_QKV)
-DRT_INST(W_Q4, 1, 16, PRO_ACT, EPI_RESID)
-DRT_INST(W_Q4, 4, 4, PRO_NORM, EPI_SWIGLU)
-DRT_INST(W_Q4, 1, 16, PRO_ACT, EPI_STORE)
+DRT_INST(W_Q4, 4, 2, PRO_NORM, EPI_QKV)
+DRT_INST(W_Q4, 1, 8, PRO_ACT, EPI_RESID)
+DRT_INST(W_Q4, 4, 2, PRO_NORM, EPI_SWIGLU)
+DRT_INST(W_Q4, 1, 8, PRO_ACT, EPI_STORE)
 DRT_INST(W_Q4, 4, 4, PRO_ACT, EPI_RESID)
 DRT_INST(W_BF16, 4, 4, PRO_NORM, EPI_QKV)
 DRT_INST(W_BF16, 1, 16, PRO_ACT, EPI_RESID)
@@ -377,7 +402,7 @@ DRT_INST(W_BF16, 4, 4, PRO_ACT, EPI_RESID)
 
 namespace drt {
 
-constexpr size_t FUSED_LDS = 32 * (1024 + 8) * 2 + 16 * 32 * 4 + 32 * 4 + 32 * 2 * 4;
+constexpr size_t FUSED_LDS = 2 * 32 * (1024 + 8) * 2 + 16 * 32 * 4 + 32 * 4 + 32 * 2 * 4;
 
 void fused_linear(const FusedArgs& a, int kind, hipStream_t s) {
   require(a.N % 32 == 0, "fused linear needs N % 32 == 0");
@@ -402,24 +427,26 @@ void fused_linear(const FusedArgs& a, int kind, hipStream_t s) {
     DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(64 * WN * WK), FUSED_LDS, s, a);       \
   }
   switch (kind) {
+    // q4 kernels run 8 waves where the bf16 ones run 16: the hi and lo A
+    // fragments need the registers of 512-thread work-groups
     case FL_QKV:
       require(a.N % 128 == 0, "QKV epilogue needs whole heads");
-      if (q4) DRT_FL(W_Q4, 4, 4, PRO_NORM, EPI_QKV) else DRT_FL(W_BF16, 4, 4, PRO_NORM, EPI_QKV)
+      if (q4) DRT_FL(W_Q4, 4, 2, PRO_NORM, EPI_QKV) else DRT_FL(W_BF16, 4, 4, PRO_NORM, EPI_QKV)
       break;
     case FL_RESID:
       // decode-sized tiles read A straight from global; large M shares it via LDS
       if (a.M <= 32) {
-        if (q4) DRT_FL(W_Q4, 1, 16, PRO_ACT, EPI_RESID) else DRT_FL(W_BF16, 1, 16, PRO_ACT, EPI_RESID)
+        if (q4) DRT_FL(W_Q4, 1, 8, PRO_ACT, EPI_RESID) else DRT_FL(W_BF16, 1, 16, PRO_ACT, EPI_RESID)
       } else {
         if (q4) DRT_FL(W_Q4, 4, 4, PRO_ACT, EPI_RESID) else DRT_FL(W_BF16, 4, 4, PRO_ACT, EPI_RESID)
       }
       break;
     case FL_SWIGLU:
       require(a.N % 128 == 0, "SwiGLU epilogue needs 64-column gate/up blocks");
-      if (q4) DRT_FL(W_Q4, 4, 4, PRO_NORM, EPI_SWIGLU) else DRT_FL(W_BF16, 4, 4, PRO_NORM, EPI_SWIGLU)
+      if (q4) DRT_FL(W_Q4, 4, 2, PRO_NORM, EPI_SWIGLU) else DRT_FL(W_BF16, 4, 4, PRO_NORM, EPI_SWIGLU)
       break;
     case FL_STORE:
-      if (q4) DRT_FL(W_Q4, 1, 16, PRO_ACT, EPI_STORE) else DRT_FL(W_BF16, 1, 16, PRO_ACT, EPI_STORE)
+      if (q4) DRT_FL(W_Q4, 1, 8, PRO_ACT, EPI_STORE) else DRT_FL(W_BF16, 1, 16, PRO_ACT, EPI_STORE)
       break;
     default:
       fail(INVALID_ARGUMENT, "unknown fused linear kind");

@@ -4,11 +4,12 @@
 
 // One 64-wide k group of a q4 tile-32 weight for NT n-tiles (see q4_linear.hip
 // for the layout and the exact-integer B construction).
-//   a[t]   : ACT_F16P fragments of this lane's row, words t = 0..3 of the group
-//   xsr[r] : group sums of the 16 rows this lane holds in the MFMA result
+//   a[t], al[t] : ACT_F16P hi / lo fragments of this lane's row, words t = 0..3
+//   xsr[r]      : group sums (hi + lo) of the 16 rows this lane holds in the result
 template <int NT>
-DRT_DEV void q4_group_mma(f32x16 (&acc)[NT], const f16x8 (&a)[4], const float (&xsr)[16],
-                          const u32x4 (&w)[NT], const uint32_t (&sbv)[NT]) {
+DRT_DEV void q4_group_mma(f32x16 (&acc)[NT], const f16x8 (&a)[4], const f16x8 (&al)[4],
+                          const float (&xsr)[16], const u32x4 (&w)[NT],
+                          const uint32_t (&sbv)[NT]) {
 #pragma unroll
   for (int j = 0; j < NT; ++j) {
     f32x16 c = f32x16{};
@@ -16,17 +17,18 @@ DRT_DEV void q4_group_mma(f32x16 (&acc)[NT], const f16x8 (&a)[4], const float (&
     for (int t = 0; t < 4; ++t) {
       const uint32_t wt = w[j][t];
       u32x4 bw;
-      bw[0] = (wt & 0x000F000Fu) | 0x64006400u;
-      bw[1] = ((wt >> 4) & 0x000F000Fu) | 0x64006400u;
-      bw[2] = ((wt >> 8) & 0x000F000Fu) | 0x64006400u;
-      bw[3] = ((wt >> 12) & 0x000F000Fu) | 0x64006400u;
-      c = mfma_f16(a[t], __builtin_bit_cast(f16x8, bw), c);
+      bw[0] = q4_pair_to_f16((wt >> 0) & 0x000F000Fu);
+      bw[1] = q4_pair_to_f16((wt >> 4) & 0x000F000Fu);
+      bw[2] = q4_pair_to_f16((wt >> 8) & 0x000F000Fu);
+      bw[3] = q4_pair_to_f16((wt >> 12) & 0x000F000Fu);
+      const f16x8 b = __builtin_bit_cast(f16x8, bw);
+      c = mfma_f16(a[t], b, c);
+      c = mfma_f16(al[t], b, c);
     }
     const float s = bf16_bits_to_float(sbv[j] & 0xffffu);
     const float b = bf16_bits_to_float(sbv[j] >> 16);
-    const float bp = fmaf(-1024.f, s, b);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[j][r] = fmaf(s, c[r], fmaf(bp, xsr[r], acc[j][r]));
+    for (int r = 0; r < 16; ++r) acc[j][r] = fmaf(s, c[r], fmaf(b, xsr[r], acc[j][r]));
   }
 }
 

@@ -181,7 +181,8 @@ size_t attention_part_bytes(const AttnPlan& p, int n_rows, int Hq, int Hkv);
 void attention(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_stride,
                int n_rows, int Hq, int Hkv, int n_keys, int row_pos0, int mask_kind,
                int mask_prompt_len, int mask_block, const AttnPlan& plan, float* o_part,
-               float* ml_part, void* out, float* xsum, int out_fmt, hipStream_t s);
+               float* ml_part, void* out, float* xsum, int out_fmt, hipStream_t s,
+               int* err = nullptr);
 // Decode attention over `ranges` key ranges (attention_decode_ranges(n_keys, Hkv) when
 // the key count is known at launch) + the range combine; `part` is a workspace of
 // attention_decode_part_bytes(ranges, Hkv, n_rows * Hq / Hkv) bytes.
@@ -201,7 +202,8 @@ void embed(const int32_t* tokens, const uint16_t* table, float* hidden, int M, i
            float* ss_out, hipStream_t s);
 void residual_norm(float* hidden, const float* part, int splits, int M_part, bool rnd_bf16,
                    const int32_t* src_rows, bool write_hidden, const uint16_t* norm_w, float eps,
-                   int d, int fmt, void* act, float* xsum, int n_out_rows, hipStream_t s);
+                   int d, int fmt, void* act, float* xsum, int n_out_rows, hipStream_t s,
+                   int* err = nullptr);
 // LM head: per-row scores (f64) and tokens, optional raw logits.
 size_t lmhead_stats_bytes(int M, int N);
 void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* logits_out,

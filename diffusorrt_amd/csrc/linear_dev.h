@@ -4,24 +4,30 @@
 
 namespace {
 
-DRT_DEV void q4_group_mma1(f32x16& acc, const f16x8 (&a)[4], const float (&xsr)[16],
-                           const u32x4 w, const uint32_t sbv) {
+// One 64-wide k group of one q4 n-tile with an ACT_F16P activation: a / al are
+// the hi / lo fragments of this lane's row, xsr the group sums (hi + lo) of the
+// 16 rows this lane holds in the MFMA result. The B operand is the exact fp16
+// integer q (q4_pair_to_f16), so c = sum x q stays small (no large offset for
+// the fp32 accumulation to lose bits against) and y += s * c + b * sum x.
+DRT_DEV void q4_group_mma1(f32x16& acc, const f16x8 (&a)[4], const f16x8 (&al)[4],
+                           const float (&xsr)[16], const u32x4 w, const uint32_t sbv) {
   f32x16 c = f32x16{};
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const uint32_t wt = w[t];
     u32x4 bw;
-    bw[0] = (wt & 0x000F000Fu) | 0x64006400u;
-    bw[1] = ((wt >> 4) & 0x000F000Fu) | 0x64006400u;
-    bw[2] = ((wt >> 8) & 0x000F000Fu) | 0x64006400u;
-    bw[3] = ((wt >> 12) & 0x000F000Fu) | 0x64006400u;
-    c = mfma_f16(a[t], __builtin_bit_cast(f16x8, bw), c);
+    bw[0] = q4_pair_to_f16((wt >> 0) & 0x000F000Fu);
+    bw[1] = q4_pair_to_f16((wt >> 4) & 0x000F000Fu);
+    bw[2] = q4_pair_to_f16((wt >> 8) & 0x000F000Fu);
+    bw[3] = q4_pair_to_f16((wt >> 12) & 0x000F000Fu);
+    const f16x8 b = __builtin_bit_cast(f16x8, bw);
+    c = mfma_f16(a[t], b, c);
+    c = mfma_f16(al[t], b, c);
   }
   const float s = bf16_bits_to_float(sbv & 0xffffu);
   const float b = bf16_bits_to_float(sbv >> 16);
-  const float bp = fmaf(-1024.f, s, b);
 #pragma unroll
-  for (int r = 0; r < 16; ++r) acc[r] = fmaf(s, c[r], fmaf(bp, xsr[r], acc[r]));
+  for (int r = 0; r < 16; ++r) acc[r] = fmaf(s, c[r], fmaf(b, xsr[r], acc[r]));
 }
 
 // v[l] + v[l ^ 32] on every lane (gfx950 v_permlane32_swap, no LDS trip); both
@@ -44,22 +50,23 @@ DRT_DEV void load_row_sums(const float* rs, int lane, float (&xsr)[16]) {
   }
 }
 
-// Group sums of the A fragments of UW units (lane l holds 32 of the 64 values
-// of row l & 31 for each unit): the lane's half-sums, the two halves added
-// across lanes, staged through this wave's LDS scratch (UW x 32 floats) and
-// read back in accumulator order. The wave's LDS operations run in order, so
-// no barrier is needed; the scratch may be rewritten by the next call.
+// Group sums (hi + lo) of the A fragments of UW units (lane l holds 32 of the 64
+// values of row l & 31 for each unit): the lane's half-sums, the two halves
+// added across lanes, staged through this wave's LDS scratch (UW x 32 floats)
+// and read back in accumulator order. The wave's LDS operations run in order,
+// so no barrier is needed; the scratch may be rewritten by the next call.
 template <int UW>
-DRT_DEV void row_sums_lane(const u32x4 (&a)[UW][4], float* scratch, int lane,
-                           float (&xsr)[UW][16]) {
+DRT_DEV void row_sums_lane(const u32x4 (&a)[UW][4], const u32x4 (&al)[UW][4], float* scratch,
+                           int lane, float (&xsr)[UW][16]) {
 #pragma unroll
   for (int i = 0; i < UW; ++i) {
     float v = 0.f;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const f16x8 h = __builtin_bit_cast(f16x8, a[i][t]);
+      const f16x8 l = __builtin_bit_cast(f16x8, al[i][t]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v += (float)h[e];
+      for (int e = 0; e < 8; ++e) v += (float)h[e] + (float)l[e];
     }
     v = sum_xor32(v);
     if (lane < 32) scratch[i * 32 + lane] = v;
@@ -68,17 +75,34 @@ DRT_DEV void row_sums_lane(const u32x4 (&a)[UW][4], float* scratch, int lane,
   for (int i = 0; i < UW; ++i) load_row_sums(scratch + i * 32, lane, xsr[i]);
 }
 
-// q4_group_mma1 for one unit whose A fragments came straight from global
-// memory (row sums through this wave's LDS scratch of 32 floats).
-DRT_DEV void q4_group_mma1_lane(f32x16& acc, const u32x4 (&a)[4], const u32x4 w,
-                                const uint32_t sbv, int lane, float* scratch) {
+// q4_group_mma1 for one unit whose A fragments (hi, lo) came straight from
+// global memory (row sums through this wave's LDS scratch of 32 floats).
+DRT_DEV void q4_group_mma1_lane(f32x16& acc, const u32x4 (&a)[4], const u32x4 (&al)[4],
+                                const u32x4 w, const uint32_t sbv, int lane, float* scratch) {
   const u32x4(&a1)[1][4] = reinterpret_cast<const u32x4(&)[1][4]>(a);
+  const u32x4(&al1)[1][4] = reinterpret_cast<const u32x4(&)[1][4]>(al);
   float xsr[1][16];
-  row_sums_lane<1>(a1, scratch, lane, xsr);
-  f16x8 ah[4];
+  row_sums_lane<1>(a1, al1, scratch, lane, xsr);
+  f16x8 ah[4], alh[4];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) ah[t] = __builtin_bit_cast(f16x8, a[t]);
-  q4_group_mma1(acc, ah, xsr[0], w, sbv);
+  for (int t = 0; t < 4; ++t) {
+    ah[t] = __builtin_bit_cast(f16x8, a[t]);
+    alh[t] = __builtin_bit_cast(f16x8, al[t]);
+  }
+  q4_group_mma1(acc, ah, alh, xsr[0], w, sbv);
+}
+
+// Records a value beyond the fp16 range in the runtime's error word.
+DRT_DEV void raise_range(const FusedArgs& a) {
+  if (a.placement_err)
+    __hip_atomic_fetch_or(a.placement_err, DRT_ERR_F16_RANGE, __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A value the operand type T cannot hold (fp16 only: bf16 has fp32's range).
+template <typename T> DRT_DEV bool out_of_range(float x) {
+  if constexpr (std::is_same<T, _Float16>::value) return f16_overflows(x);
+  else return false;
 }
 
 template <typename T> DRT_DEV T cvt_to(float f);
@@ -108,10 +132,16 @@ DRT_DEV void qkv_head_store(const FusedArgs& a, int head, int m, int pos, float 
     x0 = r0;
     x1 = r1;
   }
+  if (out_of_range<T>(x0) || out_of_range<T>(x1)) raise_range(a);
   if (is_q) {
+    // Q as hi / lo planes: lo at + M * Hq * 128 elements
     T* qo = (T*)a.q_out + ((int64_t)m * Hq + head) * 128;
-    qo[lane] = cvt_to<T>(x0);
-    qo[lane + 64] = cvt_to<T>(x1);
+    T* ql = qo + (int64_t)a.M * Hq * 128;
+    const T h0 = cvt_to<T>(x0), h1 = cvt_to<T>(x1);
+    qo[lane] = h0;
+    qo[lane + 64] = h1;
+    ql[lane] = lo_part<T>(x0, h0);
+    ql[lane + 64] = lo_part<T>(x1, h1);
     return;
   }
   const int kvh = is_k ? head - Hq : head - Hq - Hkv;
@@ -235,16 +265,29 @@ DRT_DEV void qkv_epilogue(const FusedArgs& a, const QkvTables& t, int head, int 
     }
   }
   T hx[8], hy[8];
+  bool over = false;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     hx[e] = cvt_to<T>(x[e]);
     hy[e] = cvt_to<T>(y[e]);
+    over = over || out_of_range<T>(x[e]) || out_of_range<T>(y[e]);
   }
+  if (over && m < rows) raise_range(a);
   if (is_q) {
     if (m < rows) {
+      // Q as hi / lo planes: lo at + M * Hq * 128 elements
       T* qo = (T*)a.q_out + ((int64_t)(mrow0 + m) * Hq + head) * 128 + 8 * c;
+      T* ql = qo + (int64_t)a.M * Hq * 128;
+      T lx[8], ly[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        lx[e] = lo_part<T>(x[e], hx[e]);
+        ly[e] = lo_part<T>(y[e], hy[e]);
+      }
       *(u32x4*)qo = __builtin_bit_cast(u32x4, hx);
       *(u32x4*)(qo + 64) = __builtin_bit_cast(u32x4, hy);
+      *(u32x4*)ql = __builtin_bit_cast(u32x4, lx);
+      *(u32x4*)(ql + 64) = __builtin_bit_cast(u32x4, ly);
     }
     return;
   }

@@ -51,7 +51,8 @@ DRT_DEV float gumbel(uint64_t row_key, int token) {
 
 }  // namespace
 
-// WK = 0: q4 tile32-g64 weights + ACT_F16P activation; WK = 1: bf16 tile weights
+// WK = 0: q4 tile32-g64 weights + ACT_F16P activation (hi and lo planes of M
+// rows, group sums of hi + lo); WK = 1: bf16 tile weights
 // + ACT_BF16 activation (logits rounded to bf16, as the reference's bf16 matmul).
 // Grid: x = ceil(N / (64 * WAVES)), y = 1, z = ceil(M / 32). NT is fixed to 2.
 template <int WK, int WAVES, int P>
@@ -80,9 +81,11 @@ __global__ __launch_bounds__(64 * WAVES) void lmhead_kernel(
 
   extern __shared__ __align__(16) char smem[];
   const int row_h = chunk_k + 8;
-  char* xs_raw = smem;
-  float* xss = (float*)(smem + (size_t)32 * row_h * 2);
-  float* ttile = (float*)(smem + (size_t)32 * row_h * 2 + (size_t)32 * (chunk_k >> 6) * 4) +
+  constexpr int PLANES = WK == 0 ? 2 : 1;  // ACT_F16P: hi rows, then lo rows
+  char* xs_raw = smem;                      // [PLANES][32][row_h]
+  float* xss = (float*)(smem + (size_t)PLANES * 32 * row_h * 2);
+  float* ttile = (float*)(smem + (size_t)PLANES * 32 * row_h * 2 +
+                          (size_t)32 * (chunk_k >> 6) * 4) +
                  wave * (32 * 65);
 
   f32x16 acc[NT];
@@ -93,12 +96,13 @@ __global__ __launch_bounds__(64 * WAVES) void lmhead_kernel(
     const int ck = min(chunk_k, K - k0);
     __syncthreads();
     const int cpr = ck / 8;
-    for (int c = threadIdx.x; c < 32 * cpr; c += 64 * WAVES) {
-      const int r = c / cpr, cc = c - r * cpr;
-      const int m = m0 + r;
+    for (int c = threadIdx.x; c < PLANES * 32 * cpr; c += 64 * WAVES) {
+      const int pr = c / cpr, cc = c - pr * cpr;  // pr = plane * 32 + row
+      const int m = m0 + (pr & 31);
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (m < M) v = *(const u32x4*)((const uint16_t*)x + (int64_t)m * K + k0 + cc * 8);
-      *(u32x4*)((uint16_t*)xs_raw + r * row_h + cc * 8) = v;
+      if (m < M)
+        v = *(const u32x4*)((const uint16_t*)x + ((int64_t)(pr >> 5) * M + m) * K + k0 + cc * 8);
+      *(u32x4*)((uint16_t*)xs_raw + pr * row_h + cc * 8) = v;
     }
     if (WK == 0) {
       const int ngc = ck >> 6;
@@ -128,13 +132,16 @@ __global__ __launch_bounds__(64 * WAVES) void lmhead_kernel(
         for (int p = 0; p < P; ++p) {
           const int gg = gb + p;
           if (gg < ng) {
-            f16x8 a[4];
+            f16x8 a[4], al[4];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) a[t] = *(const f16x8*)(arow + gg * 64 + 8 * t);
+            for (int t = 0; t < 4; ++t) {
+              a[t] = *(const f16x8*)(arow + gg * 64 + 8 * t);
+              al[t] = *(const f16x8*)(arow + 32 * row_h + gg * 64 + 8 * t);
+            }
             float xsr[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) xsr[r] = xss[gg * 32 + mfma_row(r, lane)];
-            q4_group_mma<NT>(acc, a, xsr, wbuf[p], sbuf[p]);
+            q4_group_mma<NT>(acc, a, al, xsr, wbuf[p], sbuf[p]);
             const int gn = gg + P;
             if (gn < ng) {
 #pragma unroll
@@ -329,12 +336,14 @@ void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* 
             int exclude_col, const int* err_dev, int* err_host) {
   require(w.N % 64 == 0, "lm head needs vocab % 64 == 0");
   require(M >= 1, "lm head needs at least one row");
-  const int chunk_k = std::min(512, w.K);
+  // k per LDS chunk: q4 stages hi and lo rows, so half the k of bf16 keeps the
+  // work-group at <= 66 KiB of LDS (two per CU)
+  const int chunk_k = std::min(w.q4 ? 256 : 512, w.K);
   require(w.K % chunk_k == 0 || w.K % 64 == 0, "lm head K must be a multiple of 64");
   const int NB = w.N / 64;
   constexpr int WAVES = 4;
-  const size_t lds = (size_t)32 * (chunk_k + 8) * 2 + (size_t)32 * (chunk_k / 64) * 4 +
-                     (size_t)WAVES * 32 * 65 * 4;
+  const size_t lds = (size_t)(w.q4 ? 2 : 1) * 32 * (chunk_k + 8) * 2 +
+                     (size_t)32 * (chunk_k / 64) * 4 + (size_t)WAVES * 32 * 65 * 4;
   const dim3 grid((NB + WAVES - 1) / WAVES, 1, (M + 31) / 32);
   if (w.q4) {
     auto fn = lmhead_kernel<0, WAVES, 4>;

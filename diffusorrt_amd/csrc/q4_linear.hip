@@ -4,12 +4,16 @@
 //         = sum_g ( scale[n,g] * sum_{k in g} x[m,k] * q[n,k]  +  bias[n,g] * xsum[m,g] )
 //
 // The nibbles q enter the MFMA as exact fp16 integers: each 16-bit half is built
-// as 0x6400 | q, i.e. the fp16 value 1024 + q, by one shift and one and-or per
-// two nibbles. The 1024 offset is removed in fp32 together with the bias:
-//   y += scale * acc_g + (bias - 1024 * scale) * xsum[m, g]
-// so the weights are never rounded; the only rounding versus an fp32 reference
-// is the fp16 activation (2^-12 relative) and fp32 accumulation order.
-//
+// as 0x6400 | q, the fp16 value 1024 + q, by one shift and one and-or per two
+// nibbles, and one packed fp16 subtraction of 1024 (exact) leaves q. Scale and
+// bias are applied in fp32 per group:
+//   y += scale * acc_g + bias * xsum[m, g]
+// so the weights are never rounded, and acc_g = sum x q stays small (no large
+// offset for the fp32 accumulation to lose bits against). The activation enters
+// as an fp16 hi + lo pair (each MFMA step runs twice), so the only differences
+// from an fp32 reference are ~2^-22 relative on the activation and the fp32
+// summation order.
+
 // Device weight layout ("tile32-g64"), produced once by q4_repack_kernel from
 // the MLX layout w_q[N][K/8] (word j of row n holds k = 8j..8j+7, low nibble
 // first) and scales/biases[N][K/64] (bf16):
@@ -18,9 +22,9 @@
 // so one n-tile x group is a contiguous 1 KiB of words (one dwordx4 per lane)
 // plus 128 B of scale/bias.
 //
-// The activation is ACT_F16P: fp16 rows whose 8-chunks are stored in the order
-// (0,4,1,5,2,6,3,7), which is exactly the k order of the B halves above, plus
-// xsum[m][g] = sum over the group of the fp16-rounded values (fp32).
+// The activation is ACT_F16P: hi and lo planes of fp16 rows whose 8-chunks are
+// stored in the order (0,4,1,5,2,6,3,7), which is exactly the k order of the B
+// halves above, plus xsum[m][g] = sum over the group of hi + lo (fp32).
 #include "common.h"
 #include "launch.h"
 
@@ -53,7 +57,8 @@ extern "C" __global__ void q4_repack_kernel(const uint32_t* __restrict__ w_q,
   }
 }
 
-// fp32 (or bf16) activation rows -> ACT_F16P + group sums. One wave per (row, group).
+// fp32 (or bf16) activation rows -> ACT_F16P (hi plane, lo plane at + M*K) +
+// group sums of hi + lo. One wave per (row, group).
 extern "C" __global__ void q4_act_prep_kernel(const void* __restrict__ x, int x_is_bf16,
                                               _Float16* __restrict__ xp,
                                               float* __restrict__ xsum, int M, int K) {
@@ -66,9 +71,10 @@ extern "C" __global__ void q4_act_prep_kernel(const void* __restrict__ x, int x_
   float v;
   if (x_is_bf16) v = bf16_bits_to_float(((const uint16_t*)x)[m * K + k]);
   else v = ((const float*)x)[m * K + k];
-  const _Float16 h = (_Float16)v;
+  const _Float16 h = (_Float16)v, lo = f16_lo(v, h);
   xp[m * K + f16p_index(k)] = h;
-  const float s = wave_sum((float)h);
+  xp[(int64_t)M * K + m * K + f16p_index(k)] = lo;
+  const float s = wave_sum((float)h + (float)lo);
   if (lane == 0) xsum[m * G + g] = s;
 }
 

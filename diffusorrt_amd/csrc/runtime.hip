@@ -396,9 +396,10 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
   const int M = rt->max_rows;
   const int widest = std::max({d, Hq * hd, F});
   rt->hidden.alloc((size_t)M * d * 4);
-  rt->act.alloc((size_t)M * widest * 2);
+  // activations and Q carry hi and lo fp16 planes (ACT_F16P)
+  rt->act.alloc((size_t)2 * M * widest * 2);
   rt->xsum.alloc((size_t)M * (widest / 64) * 4);
-  rt->qbuf.alloc((size_t)M * Hq * hd * 2);
+  rt->qbuf.alloc((size_t)2 * M * Hq * hd * 2);
   DRT_HIP(hipHostMalloc((void**)&rt->up_host, sizeof(Runtime::StepUpload) * Runtime::UPLOAD_SLOTS,
                         hipHostMallocDefault));
   rt->up_dev.alloc(sizeof(Runtime::StepUpload) * Runtime::UPLOAD_SLOTS);
@@ -406,7 +407,7 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
                                           (size_t)Hkv * M * (Hq / Hkv) * 130 * 4);
   rt->attn_part.alloc(rt->attn_part_budget);
   const int lm_cap = M;  // LM rows per forward <= rows forwarded
-  rt->act_lm.alloc((size_t)lm_cap * d * 2);
+  rt->act_lm.alloc((size_t)2 * lm_cap * d * 2);
   rt->xsum_lm.alloc((size_t)lm_cap * (d / 64) * 4);
   rt->stats.alloc(lmhead_stats_bytes(lm_cap, V));
   // the forwards' scores and tokens land in pinned host memory, written by the
@@ -434,7 +435,7 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
     DRT_HIP(hipMemsetAsync(rt->sk_counters.p, 0, rt->sk_counters.bytes, s));
     rt->sk_ss.alloc((size_t)d * 4);  // [d/32][32]
     if (rt->q4 && M > 32) {
-      rt->act2.alloc((size_t)M * widest * 2);
+      rt->act2.alloc((size_t)2 * M * widest * 2);
       size_t bf = 0;
       const int n_qkv = (Hq + 2 * Hkv) * hd;
       for (int mt = 1; mt <= (M + 127) / 128; ++mt) {
@@ -614,7 +615,8 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
   const int L = (int)rt.layers.size();
   if (big && L > 0)
     residual_norm(hidden, nullptr, 0, M, false, nullptr, false,
-                  rt.layers[0].in_norm.as<uint16_t>(), eps, d, ACT_F16P, rt.act.p, xs, M, s);
+                  rt.layers[0].in_norm.as<uint16_t>(), eps, d, ACT_F16P, rt.act.p, xs, M, s,
+                  rt.placement_err.as<int>());
   // split-K projection (o_proj / down_proj) into partial slices, then
   // hidden += sum of the slices and the next norm's activation
   auto big_resid = [&](FusedArgs f, const uint16_t* next_norm) {
@@ -623,7 +625,7 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
     f.y = bpart;
     big_linear(f, FL_STORE, ks, s);
     residual_norm(hidden, bpart, ks, M, false, nullptr, true, next_norm, eps, d, ACT_F16P,
-                  rt.act.p, xs, M, s);
+                  rt.act.p, xs, M, s, rt.placement_err.as<int>());
   };
   for (int l = 0; l < L; ++l) {
     LayerW& w = rt.layers[l];
@@ -679,7 +681,7 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
     else
       attention(rt.kv_bf16, rt.qbuf.p, kv_layer(l), head_stride, M, Hq, Hkv, a.n_keys, a.row0,
                 a.mask_kind, a.mask_prompt_len, a.mask_block, ap, o_part, ml_part, rt.act.p, xs,
-                fmt, s);
+                fmt, s, rt.placement_err.as<int>());
     if (big) {
       FusedArgs fo = base(w.o);
       fo.act = rt.act.p;
@@ -723,7 +725,8 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
   }
   if (a.n_lm > 0) {
     residual_norm(hidden, nullptr, 0, M, false, p.lm_rows, false, rt.final_norm.as<uint16_t>(),
-                  eps, d, fmt, rt.act_lm.p, rt.xsum_lm.as<float>(), p.n_lm_launch, s);
+                  eps, d, fmt, rt.act_lm.p, rt.xsum_lm.as<float>(), p.n_lm_launch, s,
+                  rt.placement_err.as<int>());
     lmhead(rt.lm_head, rt.act_lm.p, rt.xsum_lm.as<float>(), p.n_lm_launch, a.logits, rt.stats.p,
            a.temperature, a.seed, a.step, p.lm_pos, rt.scores_host(), rt.tokens_host(), s, desc,
            a.exclude_col, rt.placement_err.as<int>(), rt.placement_host);
@@ -740,6 +743,10 @@ void check_placement(const Runtime& rt) {
     fail(INTERNAL_ERROR,
          "decode attention: a bounded wait for a K/V tile expired; results of this runtime "
          "are not valid");
+  if (e & DRT_ERR_F16_RANGE)
+    fail(INTERNAL_ERROR,
+         "an activation, Q, K or V value exceeded the fp16 range (|x| >= 65504); results of "
+         "this forward are not valid");
   if (e != 0)
     fail(INTERNAL_ERROR,
          "a split-K linear ran on an unexpected XCD (work-group placement is not the "
@@ -1497,9 +1504,10 @@ int32_t drt_session_set_profiling(uint64_t session, int32_t enable) {
 
 // ------------------------------------------------------------------ per-op
 
-// fp16 activation + group sums, then (more than 32 rows) the split-K slices
+// ACT_F16P activation (hi and lo planes) + group sums, then (more than 32
+// rows) the split-K slices
 static size_t q4_op_act_bytes(int32_t m, int32_t k) {
-  return ((size_t)m * k * 2 + (size_t)m * (k / 64) * 4 + 255) / 256 * 256;
+  return ((size_t)2 * m * k * 2 + (size_t)m * (k / 64) * 4 + 255) / 256 * 256;
 }
 
 size_t drt_op_q4_linear_workspace_bytes(int32_t m, int32_t n, int32_t k) {
@@ -1547,7 +1555,7 @@ int32_t drt_op_q4_linear(const void* qw, const void* sb, const void* x, int32_t 
             "q4_linear workspace too small");
     char* ws = (char*)workspace;
     _Float16* xp = (_Float16*)ws;
-    float* xs = (float*)(ws + (size_t)m * k * 2);
+    float* xs = (float*)(ws + (size_t)2 * m * k * 2);
     hipStream_t st = as_stream(stream);
     q4_act_prep(x, x_dtype == DRT_BF16, m, k, xp, xs, st);
     FusedArgs f;
@@ -1627,7 +1635,9 @@ size_t drt_op_attention_workspace_bytes(int32_t rows, int32_t hq, int32_t hkv, i
   const AttnPlan p = plan_attention(rows, hq, hkv, n_keys, (size_t)256 << 20);
   const size_t general = attention_part_bytes(p, rows, hq, hkv);
   const size_t decode = attention_decode_part_bytes(attention_decode_ranges(n_keys, hkv), hkv, rows * (hq / hkv));
-  return std::max(general, decode) + 256;
+  // + the kernels' Q operand: the caller's Q as the hi plane and a zero lo plane
+  const size_t q_planes = ((size_t)2 * rows * hq * 128 * 2 + 255) / 256 * 256;
+  return std::max(general, decode) + q_planes + 256;
 }
 
 int32_t drt_op_attention(const void* q, const void* cache, int64_t head_stride, int32_t kv_dtype,
@@ -1654,7 +1664,15 @@ int32_t drt_op_attention(const void* q, const void* cache, int64_t head_stride, 
     fa.mask_kind = mask_kind == DRT_MASK_D2F_HYBRID ? 1 : 0;
     fa.mask_prompt_len = mask_prompt_len;
     fa.mask_block = std::max(1, mask_block_size);
-    float* o_part = (float*)workspace;
+    // the kernels read Q as hi and lo planes: the caller's Q (already in the
+    // operand type) is the hi plane, the lo plane is zero
+    const size_t q_bytes = (size_t)rows * hq * 128 * 2;
+    char* qp = (char*)workspace;
+    hipStream_t st = as_stream(stream);
+    DRT_HIP(hipMemcpyAsync(qp, q, q_bytes, hipMemcpyDeviceToDevice, st));
+    DRT_HIP(hipMemsetAsync(qp + q_bytes, 0, q_bytes, st));
+    q = qp;
+    float* o_part = (float*)(qp + (2 * q_bytes + 255) / 256 * 256);
     const int ofmt = out_dtype == DRT_F32 ? 2 : 3;
     if (rows * (hq / hkv) <= 64 && one_segment(fa)) {
       const int ranges = attention_decode_ranges(n_keys, hkv);
@@ -1696,7 +1714,7 @@ int32_t drt_op_swiglu(const float* gate, const float* up, float* y, int64_t n, v
 
 size_t drt_op_lm_head_workspace_bytes(int32_t rows, int32_t n, int32_t k) {
   if (rows <= 0 || n <= 0 || k <= 0) return 0;
-  return (size_t)rows * k * 2 + (size_t)rows * (k / 64) * 4 + lmhead_stats_bytes(rows, n) + 512;
+  return (size_t)2 * rows * k * 2 + (size_t)rows * (k / 64) * 4 + lmhead_stats_bytes(rows, n) + 512;
 }
 
 int32_t drt_op_lm_head_score(const void* qw, const void* sb, const void* wb, int32_t rows,
@@ -1724,8 +1742,8 @@ int32_t drt_op_lm_head_score(const void* qw, const void* sb, const void* wb, int
     }
     char* ws = (char*)workspace;
     void* act = ws;
-    float* xs = (float*)(ws + (size_t)rows * k * 2);
-    void* stats = ws + (size_t)rows * k * 2 + (size_t)rows * (k / 64) * 4;
+    float* xs = (float*)(ws + (size_t)2 * rows * k * 2);  // after the hi and lo planes
+    void* stats = ws + (size_t)2 * rows * k * 2 + (size_t)rows * (k / 64) * 4;
     stats = (void*)(((uintptr_t)stats + 255) & ~(uintptr_t)255);
     hipStream_t st = as_stream(stream);
     auto release = [&] { w.qw.p = nullptr; w.sb.p = nullptr; w.wb.p = nullptr; };

@@ -42,14 +42,14 @@ constexpr int SK_RED = 4 * 32 * 33;  // floats of the [4][32][33] reduction tile
 constexpr int SK_KS_MAX = 8;         // K slices per output tile (host-enforced)
 constexpr int SK_SS_PER_THREAD = 14; // K / 32 <= 8 * 14 = 112 partial sums (d <= 3584)
 
-// LDS of the wide kernel: xs [32][64U + 8] halves, xss [U][32], rinv [32],
-// red [4][32][33], flag (16 B), then the V tile half [4096] halves.
-#define SK_WIDE_V_OFF(U) (((32 * ((U) * 64 + 8) * 2 + (U) * 32 * 4 + 32 * 4 + SK_RED * 4 + 16) + 15) / 16 * 16)
+// LDS of the wide kernel: xs [2][32][64U + 8] halves (hi, lo), xss [U][32],
+// rinv [32], red [4][32][33], flag (16 B), then the V tile half [4096] halves.
+#define SK_WIDE_V_OFF(U) (((2 * 32 * ((U) * 64 + 8) * 2 + (U) * 32 * 4 + 32 * 4 + SK_RED * 4 + 16) + 15) / 16 * 16)
 #define SK_WIDE_LDS(U) (SK_WIDE_V_OFF(U) + 4096 * 2)
 // LDS of the narrow kernel: red [4][32][33] floats, flag (16 B), then the A
-// staging of the four waves, [4][UW][32][144 B]
+// staging of the four waves, [4][2 planes][UW][32][144 B]
 #define SK_NARROW_STG (SK_RED * 4 + 16)
-#define SK_NARROW_LDS(UW) (SK_NARROW_STG + 4 * (UW) * 32 * 144)
+#define SK_NARROW_LDS(UW) (SK_NARROW_STG + 4 * 2 * (UW) * 32 * 144)
 
 // Kernel arguments the first loads need are fetched in one batch at kernel
 // start: one empty asm that takes them all in scalar registers keeps the
@@ -150,8 +150,9 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
   constexpr int KCN = U * 64;
   constexpr int ROW_H = KCN + 8;  // 16-bit elements per LDS row (+16 B pad)
   extern __shared__ __align__(16) char smem[];
-  uint16_t* xs = (uint16_t*)smem;                       // [32][ROW_H] ACT_F16P
-  float* xss = (float*)(smem + 32 * ROW_H * 2);         // [U][32] group sums
+  uint16_t* xs = (uint16_t*)smem;                       // [32][ROW_H] ACT_F16P hi
+  uint16_t* xsl = xs + 32 * ROW_H;                      // [32][ROW_H] ACT_F16P lo
+  float* xss = (float*)(smem + 2 * 32 * ROW_H * 2);     // [U][32] group sums
   float* rinv = xss + U * 32;                           // [32]
   float* red = rinv + 32;                               // [4][32][33]
   int* flag = (int*)(red + SK_RED);
@@ -205,7 +206,8 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
     rinv[threadIdx.x] = 1.f / sqrtf(ssum / (float)K + a.eps);
   }
   __syncthreads();
-  // 4. RMSNorm(h) * w -> ACT_F16P (chunk order 0,4,1,5,2,6,3,7) + group sums
+  // 4. RMSNorm(h) * w -> ACT_F16P hi / lo (chunk order 0,4,1,5,2,6,3,7) + group sums
+  bool over = false;
 #pragma unroll
   for (int j = 0; j < U; ++j) {
     const int it = threadIdx.x + 256 * j;
@@ -217,32 +219,43 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
       x[2 * e] = (hv[j][e >> 1][(2 * e) & 3] * inv) * bf16_bits_to_float(nw[j][e] & 0xffffu);
       x[2 * e + 1] = (hv[j][e >> 1][(2 * e + 1) & 3] * inv) * bf16_bits_to_float(nw[j][e] >> 16);
     }
-    _Float16 h[8];
+    _Float16 h[8], lo[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) h[e] = (_Float16)x[e];
-    u32x4 pk;
+    for (int e = 0; e < 8; ++e) {
+      h[e] = (_Float16)x[e];
+      lo[e] = f16_lo(x[e], h[e]);
+      over = over || f16_overflows(x[e]);
+    }
+    u32x4 pk, pl;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
+    for (int e = 0; e < 4; ++e) {
       pk[e] = (uint32_t)half_bits(h[e]) | ((uint32_t)half_bits(h[e + 4]) << 16);
+      pl[e] = (uint32_t)half_bits(lo[e]) | ((uint32_t)half_bits(lo[e + 4]) << 16);
+    }
     *(u32x4*)(xs + r * ROW_H + c8 * 8) = pk;
+    *(u32x4*)(xsl + r * ROW_H + c8 * 8) = pl;
     float gs = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) gs += (float)h[e];
+    for (int e = 0; e < 8; ++e) gs += (float)h[e] + (float)lo[e];
     gs = sum8_dpp(gs);  // a 64-k group is 8 consecutive items of one row = 8 lanes
     if ((c8 & 7) == 0) xss[(c8 >> 3) * 32 + r] = gs;
   }
+  if (over && live) raise_range(a);
   __syncthreads();
   // 5. this wave's n-tile over the U units
   f32x16 acc = f32x16{};
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const _Float16* arow = (const _Float16*)xs + (lane & 31) * ROW_H + u * 64 + 32 * (lane >> 5);
-    f16x8 af[4];
+    f16x8 af[4], afl[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) af[t] = *(const f16x8*)(arow + 8 * t);
+    for (int t = 0; t < 4; ++t) {
+      af[t] = *(const f16x8*)(arow + 8 * t);
+      afl[t] = *(const f16x8*)(arow + 32 * ROW_H + 8 * t);
+    }
     float xsr[16];
     load_row_sums(xss + u * 32, lane, xsr);
-    q4_group_mma1(acc, af, xsr, wq[u], wsb[u]);
+    q4_group_mma1(acc, af, afl, xsr, wq[u], wsb[u]);
   }
   if (!live) return;  // work-group-uniform, before any global store
   // 6. K slices meet: the last work-group of the column block adds the partials
@@ -276,8 +289,8 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
   if (EPI == EPI_SWIGLU) {
     // thread t: row t >> 3, outputs f0 + 8c .. +7 (c = t & 7) from gate columns
     // 8c.. and up columns 64 + 8c.. of the [gate 64 | up 64] block; one 16-byte
-    // store per thread (ACT_F16P chunk order 0,4,1,5,2,6,3,7). No group sums:
-    // the down projection computes them from the fp16 values it reads.
+    // store per thread (ACT_F16P chunk order 0,4,1,5,2,6,3,7; hi and lo planes).
+    // No group sums: the down projection computes them from the values it reads.
     const int F = N >> 1;
     const int f0 = grp * 64;
     const int m = threadIdx.x >> 3, c = threadIdx.x & 7;
@@ -291,9 +304,18 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
       uint16_t* dst = (uint16_t*)a.act_out + (int64_t)m * F + f0 + 8 * c;
       u32x4 pk;
       if (a.act_fmt == ACT_F16P) {
+        u32x4 pl;
+        bool over = false;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          pk[e] = (uint32_t)half_bits((_Float16)y[e]) | ((uint32_t)half_bits((_Float16)y[e + 4]) << 16);
+        for (int e = 0; e < 4; ++e) {
+          const _Float16 h0 = (_Float16)y[e], h1 = (_Float16)y[e + 4];
+          pk[e] = (uint32_t)half_bits(h0) | ((uint32_t)half_bits(h1) << 16);
+          pl[e] = (uint32_t)half_bits(f16_lo(y[e], h0)) |
+                  ((uint32_t)half_bits(f16_lo(y[e + 4], h1)) << 16);
+          over = over || f16_overflows(y[e]) || f16_overflows(y[e + 4]);
+        }
+        *(u32x4*)(dst + (int64_t)M * F) = pl;
+        if (over) raise_range(a);
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -337,10 +359,11 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
   int* flag = (int*)(red + SK_RED);
 
   f32x16 acc = f32x16{};
-  // this wave's A staging: [UW][32 rows][144 B] (128 B of a unit's row + pad)
-  char* stg = smem + SK_NARROW_STG + wave * (UW * 32 * 144);
+  // this wave's A staging: [2 planes][UW][32 rows][144 B] (128 B of a unit's row + pad)
+  char* stg = smem + SK_NARROW_STG + wave * (2 * UW * 32 * 144);
+  const uint16_t* act_lo = act + (int64_t)M * K;  // ACT_F16P lo plane
   for (int ub = u_lo; ub < u_hi || ub == u_lo; ub += UW) {
-    u32x4 wq[UW], craw[UW][4], af[UW][4];
+    u32x4 wq[UW], craw[UW][4], crawl[UW][4], af[UW][4], afl[UW][4];
     uint32_t wsb[UW];
 #pragma unroll
     for (int i = 0; i < UW; ++i) {
@@ -352,31 +375,43 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
       // the unit's 32 x 64 activation block as four coalesced loads of 8 rows x
       // 128 B (rows past M read row M - 1: their outputs are never stored)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        craw[i][j] = *(const u32x4*)(act + (int64_t)min(8 * j + (lane >> 3), M - 1) * K +
-                                     u * 64 + (lane & 7) * 8);
+      for (int j = 0; j < 4; ++j) {
+        const int64_t off = (int64_t)min(8 * j + (lane >> 3), M - 1) * K + u * 64 + (lane & 7) * 8;
+        craw[i][j] = *(const u32x4*)(act + off);
+        crawl[i][j] = *(const u32x4*)(act_lo + off);
+      }
     }
     // through LDS into the q4 fragment order: lane l takes row l & 31, 16-byte
     // chunks 4(l >> 5) + t, i.e. k = 32(l >> 5) + 8t .. +8 (one wave's LDS
     // operations run in order: no barrier)
+    constexpr int PLANE = UW * 32 * 144;
 #pragma unroll
     for (int i = 0; i < UW; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        *(u32x4*)(stg + (i * 32 + 8 * j + (lane >> 3)) * 144 + (lane & 7) * 16) = craw[i][j];
+      for (int j = 0; j < 4; ++j) {
+        char* d = stg + (i * 32 + 8 * j + (lane >> 3)) * 144 + (lane & 7) * 16;
+        *(u32x4*)d = craw[i][j];
+        *(u32x4*)(d + PLANE) = crawl[i][j];
+      }
 #pragma unroll
     for (int i = 0; i < UW; ++i)
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        af[i][t] = *(const u32x4*)(stg + (i * 32 + (lane & 31)) * 144 + (4 * (lane >> 5) + t) * 16);
+      for (int t = 0; t < 4; ++t) {
+        const char* sp = stg + (i * 32 + (lane & 31)) * 144 + (4 * (lane >> 5) + t) * 16;
+        af[i][t] = *(const u32x4*)sp;
+        afl[i][t] = *(const u32x4*)(sp + PLANE);
+      }
     float xsr[UW][16];
-    row_sums_lane<UW>(af, red + wave * 32 * 33, lane, xsr);
+    row_sums_lane<UW>(af, afl, red + wave * 32 * 33, lane, xsr);
 #pragma unroll
     for (int i = 0; i < UW; ++i) {
-      f16x8 ah[4];
+      f16x8 ah[4], alh[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) ah[t] = __builtin_bit_cast(f16x8, af[i][t]);
-      q4_group_mma1(acc, ah, xsr[i], wq[i], wsb[i]);
+      for (int t = 0; t < 4; ++t) {
+        ah[t] = __builtin_bit_cast(f16x8, af[i][t]);
+        alh[t] = __builtin_bit_cast(f16x8, afl[i][t]);
+      }
+      q4_group_mma1(acc, ah, alh, xsr[i], wq[i], wsb[i]);
     }
     if (ub + UW >= u_hi) break;
   }
@@ -432,26 +467,24 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
 
 #define DRT_WIDE(E, U) template __global__ void skinny_wide_kernel<E, U>(const FusedArgs, int);
 DRT_WIDE(EPI_QKV, 1) DRT_WIDE(EPI_QKV, 2) DRT_WIDE(EPI_QKV, 4) DRT_WIDE(EPI_QKV, 8)
-DRT_WIDE(EPI_QKV, 14) DRT_WIDE(EPI_QKV, 16)
 DRT_WIDE(EPI_SWIGLU, 1) DRT_WIDE(EPI_SWIGLU, 2) DRT_WIDE(EPI_SWIGLU, 4) DRT_WIDE(EPI_SWIGLU, 8)
-DRT_WIDE(EPI_SWIGLU, 14) DRT_WIDE(EPI_SWIGLU, 16)
 #undef DRT_WIDE
 #define DRT_NARROW(E, UW) template __global__ void skinny_narrow_kernel<E, UW>(const FusedArgs, int);
-DRT_NARROW(EPI_RESID, 1) DRT_NARROW(EPI_RESID, 2) DRT_NARROW(EPI_RESID, 4)
-DRT_NARROW(EPI_STORE, 1) DRT_NARROW(EPI_STORE, 2) DRT_NARROW(EPI_STORE, 4)
+DRT_NARROW(EPI_RESID, 1) DRT_NARROW(EPI_RESID, 2)
+DRT_NARROW(EPI_STORE, 1) DRT_NARROW(EPI_STORE, 2)
 #undef DRT_NARROW
 
 namespace drt {
 namespace {
 
-constexpr int WIDE_U[] = {4, 8, 2, 14, 16, 1};  // preference order
 
 // Wide: units per work-group U (instantiated values) with G % U == 0, the largest
 // U whose split still gives >= 128 work-groups; else the smallest U available.
+// (U <= 8: the hi and lo activation of more units would not fit the registers.)
 int wide_units(int N, int K) {
   const int G = K / 64, NG = N / 128;
   int best = 0;
-  for (int u : {16, 14, 8, 4, 2, 1}) {
+  for (int u : {8, 4, 2, 1}) {
     if (G % u) continue;
     if (best == 0) best = u;
     if (NG * (G / u) >= 128) return u;
@@ -518,9 +551,7 @@ bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
     case 1: DRT_SW(E, 1) break;                      \
     case 2: DRT_SW(E, 2) break;                      \
     case 4: DRT_SW(E, 4) break;                      \
-    case 8: DRT_SW(E, 8) break;                      \
-    case 14: DRT_SW(E, 14) break;                    \
-    default: DRT_SW(E, 16) break;                    \
+    default: DRT_SW(E, 8) break;                     \
   }
     if (kind == FL_QKV) {
       DRT_SW_U(EPI_QKV)
@@ -542,10 +573,12 @@ bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
     grant_lds((const void*)fn, SK_NARROW_LDS(UW), granted);                        \
     DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(256), SK_NARROW_LDS(UW), s, a, KS); \
   }
+    // (more than two units per wave: loops of two, the hi and lo fragments of
+    // a larger batch would not fit the registers)
     if (kind == FL_RESID) {
-      if (per_wave <= 1) DRT_SN(EPI_RESID, 1) else if (per_wave <= 2) DRT_SN(EPI_RESID, 2) else DRT_SN(EPI_RESID, 4)
+      if (per_wave <= 1) DRT_SN(EPI_RESID, 1) else DRT_SN(EPI_RESID, 2)
     } else {
-      if (per_wave <= 1) DRT_SN(EPI_STORE, 1) else if (per_wave <= 2) DRT_SN(EPI_STORE, 2) else DRT_SN(EPI_STORE, 4)
+      if (per_wave <= 1) DRT_SN(EPI_STORE, 1) else DRT_SN(EPI_STORE, 2)
     }
 #undef DRT_SN
   } else {

@@ -29,7 +29,8 @@ def _keep(x):
     return x
 
 
-def layer_forward(weights, cfg, i, hidden, cos, sin, visible, kv_hook=None, operand_round=None):
+def layer_forward(weights, cfg, i, hidden, cos, sin, visible, kv_hook=None, operand_round=None,
+                  kv_round=None):
     """One decoder layer over all rows of ``hidden`` (fp32 ``[S, d]``).
 
     ``h += o(attn(rope(qnorm(q(n))), rope(knorm(k(n))), v(n)))`` with
@@ -40,9 +41,12 @@ def layer_forward(weights, cfg, i, hidden, cos, sin, visible, kv_hook=None, oper
     ``operand_round`` (a precision model, not reference semantics) is applied to
     every tensor that a lower-precision device path stores in its operand type:
     the linears' inputs (n, attention output, n2, swiglu output), Q, and the
-    cached K/V. ``None`` is the reference computation.
+    cached K/V. ``kv_round`` (also a precision model) rounds only the K and V
+    that a prefix cache stores (e.g. to fp16): the reference computation with
+    the cache's storage type. ``None`` for both is the reference computation.
     """
     rnd = operand_round or _keep
+    kv_rnd = kv_round or rnd
     kind = cfg["weight_kind"]
     eps = cfg["eps"]
     hq, hkv, hd = cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"]
@@ -54,10 +58,10 @@ def layer_forward(weights, cfg, i, hidden, cos, sin, visible, kv_hook=None, oper
         q = ops.rms_norm(q, weights[p + "self_attn.q_norm.weight"], eps)
     q = rnd(ops.apply_split_half_rope(q, cos, sin))
     k = _lin(weights, p + "self_attn.k_proj", n, kind).reshape(s, hkv, hd)
-    v = rnd(_lin(weights, p + "self_attn.v_proj", n, kind).reshape(s, hkv, hd))
+    v = kv_rnd(_lin(weights, p + "self_attn.v_proj", n, kind).reshape(s, hkv, hd))
     if cfg["qk_norm"]:
         k = ops.rms_norm(k, weights[p + "self_attn.k_norm.weight"], eps)
-    k = rnd(ops.apply_split_half_rope(k, cos, sin))
+    k = kv_rnd(ops.apply_split_half_rope(k, cos, sin))
     if kv_hook is not None:
         kv_hook(i, k, v)
     attn = rnd(ops.attention(q, k, v, visible=visible, dtype=np.float32).astype(np.float32))
@@ -70,14 +74,15 @@ def layer_forward(weights, cfg, i, hidden, cos, sin, visible, kv_hook=None, oper
 
 
 def forward_full(weights, cfg, token_ids, *, mask_kind, mask_geometry=None,
-                 output_rows=None, n_layers=None, kv_hook=None, operand_round=None):
+                 output_rows=None, n_layers=None, kv_hook=None, operand_round=None,
+                 kv_round=None):
     """Raw fp32 logits for ``output_rows`` (default: every row) of ``token_ids``.
 
     ``mask_kind`` is ``"d2f_hybrid"`` (``mask_geometry = (prompt_len,
     block_size)``; BD3 uses origin 0) or ``"bidirectional"`` (Dream, no mask).
     ``n_layers`` limits the layer count (the CPU baseline's bounded sample).
     ``operand_round``: see :func:`layer_forward`; also applied to the final
-    norm's output (the LM head's input).
+    norm's output (the LM head's input). ``kv_round``: see :func:`layer_forward`.
     """
     ids = np.asarray(token_ids, dtype=np.int64)
     s = ids.shape[0]
@@ -94,7 +99,8 @@ def forward_full(weights, cfg, token_ids, *, mask_kind, mask_geometry=None,
         raise ValueError(f"unsupported mask kind {mask_kind!r}")
     layers = cfg["n_layers"] if n_layers is None else n_layers
     for i in range(layers):
-        hidden = layer_forward(weights, cfg, i, hidden, cos, sin, visible, kv_hook, operand_round)
+        hidden = layer_forward(weights, cfg, i, hidden, cos, sin, visible, kv_hook, operand_round,
+                               kv_round)
     rows = list(range(s)) if output_rows is None else [int(r) for r in output_rows]
     h = hidden[rows]
     h = (operand_round or _keep)(ops.rms_norm(h, weights["model.norm.weight"], cfg["eps"]))
@@ -103,7 +109,7 @@ def forward_full(weights, cfg, token_ids, *, mask_kind, mask_geometry=None,
 
 
 def window_logits(weights, cfg, token_ids, scope, *, mask_kind, mask_geometry,
-                  logits_convention, operand_round=None):
+                  logits_convention, operand_round=None, kv_round=None):
     """Convention-applied logits for ``scope`` positions (``execute_window``).
 
     Raw row selection per ``_required_raw_row`` (``mlx_d2f_forward.py:74-93``);
@@ -114,6 +120,6 @@ def window_logits(weights, cfg, token_ids, scope, *, mask_kind, mask_geometry,
     uniq = sorted(set(raw_rows))
     logits = forward_full(weights, cfg, token_ids, mask_kind=mask_kind,
                           mask_geometry=mask_geometry, output_rows=uniq,
-                          operand_round=operand_round)
+                          operand_round=operand_round, kv_round=kv_round)
     index = {r: j for j, r in enumerate(uniq)}
     return logits[[index[r] for r in raw_rows]]

@@ -8,7 +8,8 @@
    selected rows (staircase mask, block 32, absolute blocks) on a small seeded
    model with the real BD3 vocabulary, summarised per row (float64 max-prob
    score, first argmax, second-largest logit, log-sum-exp, row sum / sum of squares, and the logits
-   at fixed probe ids). The GPU tests compare the device path with these.
+   at fixed probe ids; for q4 also the score, argmax and top two logits of the same rows with
+   the cached K/V rounded to fp16). The GPU tests compare the device path with these.
 
 Usage: python tests/golden/make_golden.py [--reference-root PATH]
 """
@@ -59,13 +60,29 @@ def summarise(logits: np.ndarray) -> list:
     return out
 
 
-def oracle_case_logits(model, kind: str, case: dict) -> np.ndarray:
+def kv_round_f16(a):
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+def oracle_case_logits(model, kind: str, case: dict, kv_round=None) -> np.ndarray:
     weights = {}
     for k, v in syn.to_oracle_weights(model).items():
         weights[k] = O.Q4Weight(*v) if isinstance(v, tuple) else v
     cfg = syn.oracle_config(model.geometry, kind)
     return F.forward_full(weights, cfg, case["input_ids"], mask_kind="d2f_hybrid",
-                          mask_geometry=(0, 32), output_rows=case["selected_rows"])
+                          mask_geometry=(0, 32), output_rows=case["selected_rows"],
+                          kv_round=kv_round)
+
+
+def add_kv_summary(rows: list, logits: np.ndarray) -> list:
+    """The same rows with the cached K/V rounded to fp16 (the device cache's
+    storage type): score, argmax, top two logits."""
+    scores, tokens = O.raw_max_prob(logits)
+    for r, row in enumerate(rows):
+        lr = logits[r].astype(np.float64)
+        row.update(kv_score=float(scores[r]), kv_argmax=int(tokens[r]), kv_max=float(lr.max()),
+                   kv_second=float(np.partition(lr, -2)[-2]))
+    return rows
 
 
 def main():
@@ -85,8 +102,12 @@ def main():
            "kinds": {}}
     for kind in ("q4", "bf16"):
         model = syn.build_model(g, kind, seed=SEED)
-        out["kinds"][kind] = {c["name"]: summarise(oracle_case_logits(model, kind, c))
-                              for c in cases}
+        out["kinds"][kind] = {}
+        for c in cases:
+            rows = summarise(oracle_case_logits(model, kind, c))
+            if kind == "q4":
+                rows = add_kv_summary(rows, oracle_case_logits(model, kind, c, kv_round_f16))
+            out["kinds"][kind][c["name"]] = rows
     with open(os.path.join(HERE, "bd3_real_vocab_logits.json"), "w") as f:
         json.dump(out, f, indent=1)
     print("wrote", len(cases), "cases")

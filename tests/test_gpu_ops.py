@@ -48,8 +48,9 @@ def test_q4_linear_config3(m, n, k):
     xf = x.float().numpy()
     x16 = xf.astype(np.float16).astype(np.float64)
     if m <= 32:
-        # what the weight-streaming kernels multiply: fp16 activations, exact
-        # integer nibbles (scale and bias applied in fp32)
+        # what the weight-streaming kernels multiply: the activation as fp16 hi +
+        # lo (a bf16 input is exact in the hi part), exact integer nibbles (scale
+        # and bias applied in fp32)
         ref16 = O.q4_linear64(x16, W)
     else:
         # the large-M kernels dequantize each weight once to fp16: s * q + b with
@@ -86,13 +87,18 @@ def test_q4_linear_large_m_ragged_with_bias(k):
     W = O.Q4Weight(q.w_q.numpy().view(np.uint32), q.scales.float().numpy(),
                    q.biases.float().numpy())
     w16 = O.q4_dequant(W.w_q, W.scales, W.biases, dtype=np.float64).astype(np.float16)
-    x16 = x.numpy().astype(np.float16).astype(np.float64)
-    ref = x16 @ w16.astype(np.float64).T + bias.float().numpy()
+    # the fp32 activation enters as fp16 hi + lo: ~22 significant bits
+    x64 = x.numpy().astype(np.float64)
+    ref = x64 @ w16.astype(np.float64).T + bias.float().numpy()
     assert np.abs(y - ref).max() / np.abs(ref).max() < 2e-5
-    # the bound separates fp16-rounded weights from exact ones: a kernel that
-    # skipped or misplaced the rounding would not pass it
-    exact = O.q4_linear64(x16, W) + bias.float().numpy()
+    # the bound separates fp16-rounded weights from exact ones, and an fp16
+    # activation from the hi + lo pair: a kernel that skipped or misplaced either
+    # would not pass it
+    exact = O.q4_linear64(x64, W) + bias.float().numpy()
     assert np.abs(exact - ref).max() / np.abs(ref).max() > 2e-5
+    x16 = x.numpy().astype(np.float16).astype(np.float64)
+    act16 = x16 @ w16.astype(np.float64).T + bias.float().numpy()
+    assert np.abs(act16 - ref).max() / np.abs(ref).max() > 2e-5
 
 
 def test_q4_linear_fp32_input_and_bias():
@@ -107,8 +113,11 @@ def test_q4_linear_fp32_input_and_bias():
     y = kernels.linear(x.cuda(), w, bias.cuda()).cpu().numpy().astype(np.float64)
     W = O.Q4Weight(q.w_q.numpy().view(np.uint32), q.scales.float().numpy(),
                    q.biases.float().numpy())
-    ref = O.q4_linear64(x.numpy().astype(np.float16).astype(np.float64), W) + bias.float().numpy()
-    assert np.abs(y - ref).max() / np.abs(ref).max() < 2e-5
+    # fp32 activation as fp16 hi + lo, exact nibbles: the reference's fp32 linear
+    ref = O.q4_linear64(x.numpy().astype(np.float64), W) + bias.float().numpy()
+    err = np.abs(y - ref).max() / np.abs(ref).max()
+    _say(f"  err_vs_fp32_input={err:.2e}")
+    assert err < 2e-5
 
 
 @pytest.mark.parametrize("m,n,k", [(32, 1024, 1024), (128, 3072, 1024), (3, 64, 2048)])
@@ -239,7 +248,7 @@ def test_lm_head_scores_tokens(kind):
         args = (C.c_void_p(w.qw.data_ptr()), C.c_void_p(w.sb.data_ptr()), None)
         W = O.Q4Weight(q.w_q.numpy().view(np.uint32), q.scales.float().numpy(),
                        q.biases.float().numpy())
-        ref_logits = O.q4_linear64(x.numpy().astype(np.float16).astype(np.float64), W)
+        ref_logits = O.q4_linear64(x.numpy().astype(np.float64), W)  # hi + lo activation
     else:
         wt = (torch.randn((n, k), generator=gen) * 0.02).to(torch.bfloat16)
         w = kernels.DeviceBF16Weight(wt.cuda())

@@ -171,15 +171,23 @@ def test_kv_hook_sees_roped_keys():
 
 
 @pytest.mark.parametrize("seed", [21, 22])
-def test_fp16_operand_margin_perturbation(seed):
-    """The operand-precision tie band (helpers.OPERAND_TIE_REL) is measured, not
-    chosen: rounding the tensors the device path keeps in fp16 (linear inputs, Q,
-    K/V) moves the margins between the top token and the next seven by less than
-    0.8x the band at the BD3 layer shapes (2 layers, all 128 rows of a 96-token
-    prompt + one masked block)."""
+def test_operand_precision_sites(seed):
+    """Per-site attribution of the device path's operand precision at the BD3
+    layer shapes (2 layers, all 128 rows of a 96-token prompt + one masked
+    block), measured as the largest shift of the margins between the top token
+    and the next seven:
+      * fp16 rounding of every operand site (the linears' inputs, Q, K/V and the
+        LM head's input) shifts them by more than the 1e-3 tie bar: a device
+        path with plain fp16 operands could not meet it;
+      * the fp16 hi + lo pairs the device carries for those sites (x as fp16(x)
+        + fp16(x - fp16(x))) shift them by < 2e-5, far inside the bar;
+      * fp16 storage of the cached K/V alone, the one site that stays, shifts
+        them by < 2e-3 but > 1e-4: the GPU tests hold the device to the 1e-3
+        bar against the oracle run with that rounding (``kv_round``) and
+        attribute the remaining disagreements with the exact oracle to it."""
     import dataclasses
 
-    from helpers import OPERAND_TIE_REL
+    from helpers import NEAR_TIE_REL, kv_round_f16
 
     geom = dataclasses.replace(syn.BD3_QWEN3_06B, layer_count=2, vocab_size=4096,
                                mask_token_id=4000, eos_token_id=4001)
@@ -190,24 +198,30 @@ def test_fp16_operand_margin_perturbation(seed):
     def r16(a):
         return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
 
-    ref = F.forward_full(W, cfg, x, mask_kind="d2f_hybrid", mask_geometry=(0, 32))
-    got = F.forward_full(W, cfg, x, mask_kind="d2f_hybrid", mask_geometry=(0, 32),
-                         operand_round=r16)
-    ref, got = ref.astype(np.float64), got.astype(np.float64)
+    def hilo(a):
+        a = np.asarray(a, np.float32)
+        hi = a.astype(np.float16).astype(np.float32)
+        return hi + (a - hi).astype(np.float16).astype(np.float32)
+
+    def run(**kw):
+        return F.forward_full(W, cfg, x, mask_kind="d2f_hybrid", mask_geometry=(0, 32),
+                              **kw).astype(np.float64)
+
+    ref = run()
     order = np.argsort(-ref, axis=-1)[:, :8]
     rows = np.arange(ref.shape[0])
     top = order[:, 0]
-    shift = max(np.abs((got[rows, order[:, j]] - got[rows, top]) -
-                       (ref[rows, order[:, j]] - ref[rows, top])).max() for j in range(1, 8))
-    assert 0 < shift < 0.8 * OPERAND_TIE_REL, shift
-    # the rounding does reach the margins (the band is not vacuous) ...
-    assert shift > 0.2 * OPERAND_TIE_REL
-    # ... and a planted fp16 -> bf16 operand precision breaks the bound
-    def r_bf16(a):
-        return O.bf16_round(np.asarray(a, np.float32))
 
-    coarse = F.forward_full(W, cfg, x, mask_kind="d2f_hybrid", mask_geometry=(0, 32),
-                            operand_round=r_bf16).astype(np.float64)
-    shift_bf16 = max(np.abs((coarse[rows, order[:, j]] - coarse[rows, top]) -
-                            (ref[rows, order[:, j]] - ref[rows, top])).max() for j in range(1, 8))
-    assert shift_bf16 > OPERAND_TIE_REL
+    def shift(got):
+        return max(np.abs((got[rows, order[:, j]] - got[rows, top]) -
+                          (ref[rows, order[:, j]] - ref[rows, top])).max() for j in range(1, 8))
+
+    all_f16 = shift(run(operand_round=r16))
+    pairs = shift(run(operand_round=hilo, kv_round=lambda a: a))
+    kv_only = shift(run(kv_round=kv_round_f16))
+    assert all_f16 > NEAR_TIE_REL, all_f16
+    assert 0 < pairs < 2e-5, pairs
+    assert 1e-4 < kv_only < 2e-3, kv_only
+    # a planted coarser cache (bf16 storage) is not what the bar is measured on
+    bf16_kv = shift(run(kv_round=lambda a: O.bf16_round(np.asarray(a, np.float32))))
+    assert bf16_kv > 2 * kv_only
