@@ -346,9 +346,8 @@ def main():
     sess = rt.session(bd3_session_config(BLOCK, steps_budget, PREFIX + max_tokens))
     state = decode.MaskState(x=list(prefix) + [g.mask_token_id] * max_tokens, prompt_len=PREFIX,
                              mask_token_id=g.mask_token_id, eos_token_id=g.eos_token_id)
-    layout = decode.BlockLayout(start=PREFIX, length=max_tokens, block_size=BLOCK, origin=0)
-    policy = decode.BD3FixedQuotaCommit(block_size=BLOCK, requested_steps=steps_budget,
-                                        generated_token_count=max_tokens, block_layout=layout)
+    policy = decode.QuotaSchedule(prompt_len=PREFIX, generated=max_tokens, block_size=BLOCK,
+                                  steps=steps_budget, absolute=True)
     sess.start_device(state.x, prompt_len=0, block_size=BLOCK, mask_token_id=g.mask_token_id,
                       exact_kv=False, steps=steps_budget)
     step_iter = iter(range(policy.iteration_limit))

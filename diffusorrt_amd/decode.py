@@ -1,10 +1,11 @@
 """Host control plane of the denoise loop for the strategies the device session
 runs: the two fixed-quota policies and Dream's block threshold.
 
-Mirrors the reference's ``backends/diffusion_runtime.py`` (``MaskState``
-:387-558, ``BlockThresholdCommit`` :1023-1098, ``BlockLayout`` :1099-1141,
-``FixedQuotaCommit`` :1145-1196, ``BD3FixedQuotaCommit`` :1200-1346,
-``run_decode_loop`` :1829-1991),
+Behaviour follows the reference's ``backends/diffusion_runtime.py`` (the masked
+canvas :387-558, block threshold :1023-1098, block grid :1099-1141, fixed
+quota :1145-1196, BD3 fixed quota :1200-1346, the decode loop :1829-1991);
+the two fixed-quota policies are one precomputed schedule here
+(``QuotaSchedule``), the shape the library's native loop also takes;
 ``backends/decode_session.py`` (``DecodeRequest.prepare`` :113-210) and
 ``backends/device_runtime.py`` (``_run_device_state`` :108-183,
 ``generate_device_tokens`` :186-274), limited to what the device route needs:
@@ -61,46 +62,6 @@ class MaskState:
             visible = answer
         return {"visible_token_ids": list(visible), "hit_eos": hit_eos,
                 "remaining_mask_count": remaining, "finish_reason": reason}
-
-
-@dataclass(frozen=True)
-class BlockLayout:
-    """A generated interval on a fixed block grid (``diffusion_runtime.py:1099-1141``).
-    ``origin=0`` gives BD3's absolute blocks."""
-
-    start: int
-    length: int
-    block_size: int
-    origin: int = 0
-
-    def __post_init__(self):
-        for name in ("start", "length", "origin"):
-            v = getattr(self, name)
-            if type(v) is not int or v < 0:
-                raise ValueError(f"block layout {name} must be a nonnegative integer")
-        if type(self.block_size) is not int or self.block_size <= 0:
-            raise ValueError("block layout block_size must be a positive integer")
-        if self.origin > self.start:
-            raise ValueError("block layout origin must not exceed start")
-
-    @property
-    def count(self) -> int:
-        if self.length == 0:
-            return 0
-        first = (self.start - self.origin) // self.block_size
-        last = (self.start + self.length - 1 - self.origin) // self.block_size
-        return last - first + 1
-
-    def span(self, index: int) -> tuple:
-        if not 0 <= index < self.count:
-            raise IndexError(f"block index {index} outside layout with {self.count} blocks")
-        first = (self.start - self.origin) // self.block_size
-        grid = self.origin + (first + index) * self.block_size
-        return max(self.start, grid), min(self.start + self.length, grid + self.block_size)
-
-    @property
-    def mask_geometry(self) -> dict:
-        return {"prompt_len": self.origin, "block_size": self.block_size}
 
 
 @dataclass
@@ -171,122 +132,101 @@ class BlockThresholdCommit:
 
 
 
-@dataclass
-class FixedQuotaCommit:
-    """Prompt-relative logical blocks, full bidirectional canvas
-    (``diffusion_runtime.py:1145-1196``)."""
+def block_spans(start: int, length: int, block_size: int, origin: int = 0) -> list:
+    """Cut the interval ``[start, start + length)`` at the multiples of
+    ``block_size`` counted from ``origin``; returns the ``(lo, hi)`` pieces in
+    order. ``origin = 0`` gives BD3's absolute blocks, ``origin = start`` the
+    prompt-relative blocks of the full-canvas policy (the block geometry of
+    ``backends/diffusion_runtime.py:1099-1141``)."""
+    for label, v, least in (("start", start, 0), ("length", length, 0), ("origin", origin, 0),
+                            ("block_size", block_size, 1)):
+        if isinstance(v, bool) or not isinstance(v, int) or v < least:
+            raise ValueError(f"block grid: {label} must be an int >= {least}, got {v!r}")
+    if origin > start:
+        raise ValueError(f"block grid: origin {origin} lies after the interval start {start}")
+    spans, lo, end = [], start, start + length
+    while lo < end:
+        hi = min(end, origin + ((lo - origin) // block_size + 1) * block_size)
+        spans.append((lo, hi))
+        lo = hi
+    return spans
 
-    block_size: int
-    requested_steps: int
-    generated_token_count: int
-    name: str = field(default="fixed_quota", init=False)
-    _active_block: int | None = field(default=None, init=False)
-    _quota: int = field(default=0, init=False)
-    _base: int = field(default=0, init=False)
-    _remainder: int = field(default=0, init=False)
 
-    def __post_init__(self):
-        if self.block_size <= 0 or self.requested_steps <= 0:
-            raise ValueError("fixed quota requires positive block_size and steps")
+def round_quotas(masked: int, rounds: int) -> list:
+    """Rows committed by each of a block's ``rounds`` rounds: ``masked`` spread
+    evenly, the remainder going to the earliest rounds (the divmod rule of
+    ``diffusion_runtime.py:1145-1196, 1320-1330``)."""
+    base, extra = divmod(masked, rounds)
+    return [base + 1] * extra + [base] * (rounds - extra)
 
-    @property
-    def block_count(self) -> int:
-        return (self.generated_token_count + self.block_size - 1) // self.block_size
 
-    @property
-    def steps_per_block(self) -> int:
-        if not self.block_count:
-            return 0
-        return (self.requested_steps + self.block_count - 1) // self.block_count
+class QuotaSchedule:
+    """The two fixed-quota policies as one precomputed schedule.
+
+    The generated region is cut into block spans (``block_spans``); every span
+    gets ``rounds`` steps, ``rounds = ceil(steps / ceil(generated / block))``,
+    so the step budget is ``len(spans) * rounds``. When step ``k`` enters span
+    ``k // rounds`` the span's masked rows fix that span's per-round quotas
+    (``round_quotas``); step ``k`` proposes the span's still-masked rows and
+    commits the ``quota[k % rounds]`` most confident ones (``argsort(-score)``);
+    a step with no masked row or a zero quota is skipped.
+
+    ``absolute=True`` is BD3 (``diffusion_runtime.py:1200-1346,
+    2223-2264``): blocks on the absolute grid, the proposal's window ends at the
+    span's end, an end token ends the decode at a block boundary, and so does a
+    canvas with no mask left. ``absolute=False`` is the full-canvas policy
+    (``:1145-1196, 2199-2219``): prompt-relative blocks, no window, no early
+    stop."""
+
+    def __init__(self, *, prompt_len: int, generated: int, block_size: int, steps: int,
+                 absolute: bool, requires_prompt_block_alignment: bool = True):
+        for label, v, least in (("block_size", block_size, 1), ("steps", steps, 1),
+                                ("generated", generated, 0), ("prompt_len", prompt_len, 0)):
+            if isinstance(v, bool) or not isinstance(v, int) or v < least:
+                raise ValueError(f"fixed-quota schedule: {label} must be an int >= {least}")
+        self.prompt_len = prompt_len
+        self.generated = generated
+        self.block_size = block_size
+        self.absolute = absolute
+        self.aligned = requires_prompt_block_alignment
+        self.spans = block_spans(prompt_len, generated, block_size,
+                                 0 if absolute else prompt_len)
+        sched_blocks = -(-generated // block_size)
+        self.rounds = -(-steps // sched_blocks) if self.spans else 0
+        self.name = "bd3_fixed_quota" if absolute else "fixed_quota"
+        self._span = -1       # span whose quotas are in _quotas
+        self._quotas: list = []
+        self._quota = 0       # quota of the step last planned
 
     @property
     def iteration_limit(self) -> int:
-        return self.block_count * self.steps_per_block
+        return len(self.spans) * self.rounds
 
     def plan(self, *, state: MaskState, step: int) -> StepPlan:
+        if self.absolute and (state.prompt_len, len(state.x) - state.prompt_len) != (
+                self.prompt_len, self.generated):
+            raise ValueError("the canvas no longer matches the schedule's generated region")
         if step >= self.iteration_limit:
             return StepPlan(frontier=[], stop=True)
-        block = step // self.steps_per_block
-        start = block * self.block_size
-        positions = state.all_fillable_positions()[start:start + self.block_size]
-        frontier = [p for p in positions if state.x[p] == state.mask_token_id]
-        if block != self._active_block:
-            self._active_block = block
-            self._base, self._remainder = divmod(len(frontier), self.steps_per_block)
-        self._quota = self._base + int(step % self.steps_per_block < self._remainder)
-        return StepPlan(frontier=frontier, skip=not frontier or self._quota == 0)
+        if self.absolute and self.aligned and self.prompt_len % self.block_size:
+            raise ValueError(f"prompt of {self.prompt_len} tokens is not aligned to "
+                             f"{self.block_size}-token blocks")
+        span, rnd = divmod(step, self.rounds)
+        if self.absolute:
+            region = state.x[self.prompt_len:]
+            if (rnd == 0 and state.eos_token_id in region) or state.mask_token_id not in region:
+                return StepPlan(frontier=[], stop=True)
+        lo, hi = self.spans[span]
+        frontier = [p for p in range(lo, hi) if state.x[p] == state.mask_token_id]
+        if span != self._span:
+            self._span, self._quotas = span, round_quotas(len(frontier), self.rounds)
+        self._quota = self._quotas[rnd]
+        if not frontier or self._quota == 0:
+            return StepPlan(frontier=[], skip=True)
+        return StepPlan(frontier=frontier, window_end=hi if self.absolute else None)
 
     def select(self, *, scores, step: int) -> list:
         return topk_count_choices(scores, self._quota)
-
-
-@dataclass
-class BD3FixedQuotaCommit:
-    """BD3LM absolute blocks + fixed per-round transfer (``diffusion_runtime.py:1200-1346``)."""
-
-    block_size: int
-    requested_steps: int
-    generated_token_count: int
-    block_layout: BlockLayout
-    requires_prompt_block_alignment: bool = True
-    name: str = field(default="bd3_fixed_quota", init=False)
-    _active_block_id: int | None = field(default=None, init=False)
-    _round: int = field(default=0, init=False)
-    _base: int = field(default=0, init=False)
-    _remainder: int = field(default=0, init=False)
-
-    def __post_init__(self):
-        if type(self.block_size) is not int or self.block_size <= 0:
-            raise ValueError("block_size must be a positive integer")
-        if type(self.requested_steps) is not int or self.requested_steps <= 0:
-            raise ValueError("requested_steps must be a positive integer")
-
-    @property
-    def steps_per_block(self) -> int:
-        if self.block_layout.count == 0:
-            return 0
-        sched = (self.block_layout.length + self.block_size - 1) // self.block_size
-        return (self.requested_steps + sched - 1) // sched
-
-    @property
-    def iteration_limit(self) -> int:
-        return self.block_layout.count * self.steps_per_block
-
-    def plan(self, *, state: MaskState, step: int) -> StepPlan:
-        x, prompt_len = state.x, state.prompt_len
-        if len(x) - prompt_len != self.generated_token_count:
-            raise ValueError("BD3LM generated-token count changed during decode")
-        if (self.block_layout.start, self.block_layout.length) != (prompt_len,
-                                                                   self.generated_token_count):
-            raise ValueError("BD3LM block layout does not cover the generated region")
-        if step >= self.iteration_limit:
-            return StepPlan(frontier=[], stop=True)
-        if self.requires_prompt_block_alignment and prompt_len % self.block_size:
-            raise ValueError("BD3LM Candidate prompt length must be a multiple of block_size")
-        spb = self.steps_per_block
-        generated = x[prompt_len:]
-        # EOS ends the decode only at a block boundary (:1305-1309).
-        if step % spb == 0 and state.eos_token_id in generated:
-            return StepPlan(frontier=[], stop=True)
-        mask = state.mask_token_id
-        if mask not in generated:  # no masked position left
-            return StepPlan(frontier=[], stop=True)
-        block_id = step // spb
-        # the block's span lies inside the generated region (the layout covers
-        # exactly [prompt_len, len(x)), checked above), so its masked positions
-        # are the masked positions of the canvas that fall in the span
-        start, end = self.block_layout.span(block_id)
-        frontier = [p for p in range(start, end) if x[p] == mask]
-        if self._active_block_id != block_id:
-            self._active_block_id = block_id
-            self._base, self._remainder = divmod(len(frontier), spb)
-        self._round = step % spb
-        if not frontier or self._base + int(self._round < self._remainder) == 0:
-            return StepPlan(frontier=[], skip=True)
-        return StepPlan(frontier=frontier, window_end=end)
-
-    def select(self, *, scores, step: int) -> list:
-        return topk_count_choices(scores, self._base + int(self._round < self._remainder))
 
 
 # --------------------------------------------------------------------------- loop
@@ -347,6 +287,35 @@ def run_decode_loop(state: MaskState, *, commit_policy, iteration_limit: int, pr
     return forwards, committed, iterations
 
 
+_DEVICE_STRATEGIES = ("bd3_fixed_quota", "fixed_quota", "block_threshold")
+
+
+def _count(name: str, value, least: int) -> None:
+    if type(value) is not int or value < least:  # bools are refused too
+        raise ValueError(f"{name} must be an integer >= {least}")
+
+
+def _check_request(strategy: str, *, max_tokens, steps, block_size, memory_budget_bytes,
+                   temperature, prompt, mask_token_id) -> None:
+    """The device route's request rules (``backends/device_runtime.py:80-92,
+    186-247``), checked before the session is touched."""
+    if strategy not in _DEVICE_STRATEGIES:
+        raise ValueError(f"decode strategy {strategy!r} has no rocm device session "
+                         f"(available: {', '.join(_DEVICE_STRATEGIES)})")
+    _count("max_tokens", max_tokens, 0)
+    _count("steps", steps, 1)
+    _count("block_size", block_size, 1)
+    _count("memory_budget_bytes", memory_budget_bytes, 0)
+    if not (math.isfinite(temperature) and temperature >= 0):
+        raise ValueError("temperature must be a finite number >= 0")
+    if strategy == "block_threshold" and temperature != 0:
+        raise ValueError("block_threshold scores greedily: temperature must be 0")
+    if len(prompt) == 0:
+        raise ValueError("a device decode needs at least one prompt token")
+    if strategy == "bd3_fixed_quota" and mask_token_id in prompt:
+        raise ValueError("a bd3_fixed_quota prompt on the device may not contain the mask token")
+
+
 def generate_device_tokens(session, prompt_token_ids: list, *, max_tokens: int,
                            mask_token_id: int, eos_token_id: int, steps: int, block_size: int,
                            decode_strategy: str = "bd3_fixed_quota",
@@ -362,22 +331,9 @@ def generate_device_tokens(session, prompt_token_ids: list, *, max_tokens: int,
     prompt and the frozen blocks. With ``native`` (and no trace or cancellation
     hook) ``bd3_fixed_quota`` runs the same loop inside the library
     (``drt_session_bd3_decode``)."""
-    if decode_strategy not in {"fixed_quota", "bd3_fixed_quota", "block_threshold"}:
-        raise ValueError("the rocm device session runs block_threshold, fixed_quota and "
-                         f"bd3_fixed_quota, not {decode_strategy!r}")
-    if decode_strategy == "block_threshold" and temperature != 0:
-        raise ValueError("block_threshold decodes greedily; temperature must be 0")
-    for name, value, minimum in (("max_tokens", max_tokens, 0), ("steps", steps, 1),
-                                 ("block_size", block_size, 1),
-                                 ("memory_budget_bytes", memory_budget_bytes, 0)):
-        if isinstance(value, bool) or not isinstance(value, int) or value < minimum:
-            raise ValueError(f"{name} must be an integer >= {minimum}")
-    if not math.isfinite(temperature) or temperature < 0:
-        raise ValueError("temperature must be finite and >= 0")
-    if not prompt_token_ids:
-        raise ValueError("device generation requires a non-empty prompt")
-    if decode_strategy == "bd3_fixed_quota" and mask_token_id in prompt_token_ids:
-        raise ValueError("device bd3_fixed_quota cannot carry MASK in its prompt")
+    _check_request(decode_strategy, max_tokens=max_tokens, steps=steps, block_size=block_size,
+                   memory_budget_bytes=memory_budget_bytes, temperature=temperature,
+                   prompt=prompt_token_ids, mask_token_id=mask_token_id)
     prompt_len = len(prompt_token_ids)
     state = MaskState(x=[*prompt_token_ids, *([mask_token_id] * max_tokens)],
                       prompt_len=prompt_len, mask_token_id=mask_token_id,
@@ -387,43 +343,32 @@ def generate_device_tokens(session, prompt_token_ids: list, *, max_tokens: int,
         # D2F over the exact prompt + frozen-block K/V: blocks count from the
         # prompt, each proposal forwards the active block (and the Dream shift's
         # feeder row) over the cached prefix (backends/device_runtime.py:108-183)
-        layout = None
         policy = BlockThresholdCommit(confidence_threshold=confidence_threshold,
                                       block_size=block_size, requested_steps=steps)
         origin = prompt_len
         exact_kv = True
         loop_kind = "rocm_dream_block_threshold"
-    elif decode_strategy == "bd3_fixed_quota":
-        layout = BlockLayout(start=prompt_len, length=max_tokens, block_size=block_size, origin=0)
-        policy = BD3FixedQuotaCommit(block_size=block_size, requested_steps=steps,
-                                     generated_token_count=max_tokens, block_layout=layout,
-                                     requires_prompt_block_alignment=requires_prompt_block_alignment)
-        origin = 0
-        loop_kind = "rocm_qwen3_bd3_fixed_quota"
     else:
-        layout = None
-        policy = FixedQuotaCommit(block_size=block_size, requested_steps=steps,
-                                  generated_token_count=max_tokens)
-        origin = prompt_len
-        loop_kind = "rocm_bidirectional_fixed_quota"
+        bd3 = decode_strategy == "bd3_fixed_quota"
+        policy = QuotaSchedule(prompt_len=prompt_len, generated=max_tokens,
+                               block_size=block_size, steps=steps, absolute=bd3,
+                               requires_prompt_block_alignment=requires_prompt_block_alignment)
+        origin = 0 if bd3 else prompt_len
+        loop_kind = "rocm_qwen3_bd3_fixed_quota" if bd3 else "rocm_bidirectional_fixed_quota"
     session.start_device(state.x, prompt_len=origin, block_size=block_size,
                          mask_token_id=mask_token_id, exact_kv=exact_kv, steps=steps,
                          memory_budget_bytes=memory_budget_bytes,
                          temperature=float(temperature), seed=int(seed))
 
     def propose(plan):
-        if decode_strategy == "block_threshold":
-            block = (min(plan.frontier) - origin) // block_size
-            frozen = origin + block * block_size
-            return session.propose_device(plan.frontier,
-                                          window_end=min(len(state.x), frozen + block_size),
-                                          frozen_prefix=frozen)
-        if layout is None:
+        # rows before the active block's grid start are frozen (served from the
+        # cache on a d2f session); the full canvas freezes only its prompt
+        if decode_strategy == "fixed_quota":
             return session.propose_device(plan.frontier, window_end=len(state.x),
                                           frozen_prefix=state.prompt_len)
-        block = (min(plan.frontier) - origin) // block_size
-        frozen = origin + block * block_size
-        return session.propose_device(plan.frontier, window_end=plan.window_end,
+        frozen = origin + (min(plan.frontier) - origin) // block_size * block_size
+        window_end = plan.window_end or min(len(state.x), frozen + block_size)
+        return session.propose_device(plan.frontier, window_end=window_end,
                                       frozen_prefix=frozen)
 
     if (native and decode_strategy == "bd3_fixed_quota" and trace is None and cancelled is None

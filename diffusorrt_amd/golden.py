@@ -45,40 +45,52 @@ def digest(array) -> str:
     return hashlib.sha256(a.tobytes()).hexdigest()
 
 
+def _result(tier: int, problem: str | None, ok: str) -> ParityResult:
+    return ParityResult(tier, problem is None, ok if problem is None else problem)
+
+
 def compare_control_plane(a: dict, b: dict) -> ParityResult:
-    """Bit-exact; names the first differing key in sorted order."""
+    """Bit-exact: the result names the first key, in sorted order, that one side
+    lacks or whose values differ."""
+    missing = object()
     for key in sorted(set(a) | set(b)):
-        if key not in a or key not in b:
-            return ParityResult(ParityTier.CONTROL_PLANE, False,
-                                f"{key}: present on one side only")
-        if a[key] != b[key]:
-            return ParityResult(ParityTier.CONTROL_PLANE, False,
-                                f"{key}: {a[key]!r} != {b[key]!r}")
-    return ParityResult(ParityTier.CONTROL_PLANE, True, "identical")
+        va, vb = a.get(key, missing), b.get(key, missing)
+        if va is missing or vb is missing:
+            return _result(ParityTier.CONTROL_PLANE, f"{key}: present on one side only", "")
+        if va != vb:
+            return _result(ParityTier.CONTROL_PLANE, f"{key}: {va!r} != {vb!r}", "")
+    return _result(ParityTier.CONTROL_PLANE, None, "identical")
 
 
 def compare_tensor_tolerant(a, b, *, rtol: float, atol: float) -> ParityResult:
-    a_arr, b_arr = np.asarray(a), np.asarray(b)
-    if a_arr.shape != b_arr.shape:
-        return ParityResult(ParityTier.CROSS_BACKEND, False, f"shape {a_arr.shape} != {b_arr.shape}")
-    if np.allclose(a_arr, b_arr, rtol=rtol, atol=atol):
-        return ParityResult(ParityTier.CROSS_BACKEND, True, "within tolerance")
-    diff = np.max(np.abs(a_arr.astype(np.float64) - b_arr.astype(np.float64)))
-    return ParityResult(ParityTier.CROSS_BACKEND, False,
-                        f"max abs diff {diff:.3e} exceeds rtol={rtol} atol={atol}")
+    """Elementwise |a - b| <= atol + rtol * |b|; a failure reports how many
+    elements miss the bound and the largest difference."""
+    x = np.asarray(a, dtype=np.float64)
+    y = np.asarray(b, dtype=np.float64)
+    if x.shape != y.shape:
+        return _result(ParityTier.CROSS_BACKEND, f"shape {x.shape} != {y.shape}", "")
+    miss = ~np.isclose(x, y, rtol=rtol, atol=atol)
+    if not miss.any():
+        return _result(ParityTier.CROSS_BACKEND, None, "within tolerance")
+    worst = float(np.max(np.abs(x - y)))
+    return _result(ParityTier.CROSS_BACKEND,
+                   f"{int(miss.sum())} elements beyond rtol={rtol} atol={atol} "
+                   f"(max abs diff {worst:.3e})", "")
 
 
 def compare_tokens(a, b) -> ParityResult:
-    a_arr, b_arr = np.asarray(a), np.asarray(b)
-    if a_arr.shape != b_arr.shape:
-        return ParityResult(ParityTier.CROSS_BACKEND, False,
-                            f"token shape {a_arr.shape} != {b_arr.shape}")
-    bad = np.nonzero(a_arr != b_arr)[0]
-    if bad.size == 0:
-        return ParityResult(ParityTier.CROSS_BACKEND, True, "tokens identical")
-    i = int(bad[0])
-    return ParityResult(ParityTier.CROSS_BACKEND, False,
-                        f"first token divergence at index {i}: {a_arr.flat[i]} != {b_arr.flat[i]}")
+    """Committed-token equality, the promise that holds across backends; a
+    failure names the first index where the two sequences part."""
+    x, y = np.asarray(a), np.asarray(b)
+    if x.shape != y.shape:
+        return _result(ParityTier.CROSS_BACKEND, f"token shape {x.shape} != {y.shape}", "")
+    where = np.flatnonzero(x.ravel() != y.ravel())
+    if where.size == 0:
+        return _result(ParityTier.CROSS_BACKEND, None, "tokens identical")
+    i = int(where[0])
+    return _result(ParityTier.CROSS_BACKEND,
+                   f"tokens differ from index {i} on ({x.flat[i]} != {y.flat[i]}; "
+                   f"{where.size} positions in all)", "")
 
 
 def _jsonable(v):

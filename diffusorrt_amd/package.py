@@ -80,7 +80,7 @@ def _err(scope: str, artifact: str, reason: str) -> ValueError:
     return ValueError("_".join(p for p in (scope, artifact, reason) if p))
 
 
-def safe_relative_ref(ref, *, scope: str, artifact: str) -> tuple[str, ...]:
+def package_ref_parts(ref, *, scope: str, artifact: str) -> tuple[str, ...]:
     """The components of a package-relative reference, or ``<scope>_<artifact>_ref_unsafe``
     for an empty, absolute, NUL-bearing or ``.``/``..``/empty-component reference
     (``package_artifacts.py:21-45``)."""
@@ -98,7 +98,7 @@ def open_artifact(package_dir, ref, *, scope: str, artifact: str,
     """Open a regular file of the package for reading, walking the reference one
     component at a time from the package directory with ``O_NOFOLLOW``: a symbolic
     link anywhere below the package directory is refused."""
-    parts = safe_relative_ref(ref, scope=scope, artifact=artifact)
+    parts = package_ref_parts(ref, scope=scope, artifact=artifact)
     try:
         root = Path(package_dir).resolve(strict=True)
     except (OSError, TypeError, ValueError) as exc:
@@ -153,7 +153,7 @@ def _same_file(a: os.stat_result, b: os.stat_result) -> bool:
                                                               b.st_mtime_ns)
 
 
-def _strict_json(payload: bytes, *, scope: str, artifact: str):
+def _load_json_unique_keys(payload: bytes, *, scope: str, artifact: str):
     """JSON with duplicate keys and non-finite numbers refused
     (``weight_store.py:61-82``)."""
     def pairs(items):
@@ -178,7 +178,7 @@ def read_manifest(package_dir) -> dict:
     with open_artifact(package_dir, MANIFEST_REF, scope="package", artifact="manifest",
                        max_bytes=MAX_MANIFEST_BYTES) as (handle, _):
         payload = handle.read(MAX_MANIFEST_BYTES + 1)
-    manifest = _strict_json(payload, scope="package", artifact="manifest")
+    manifest = _load_json_unique_keys(payload, scope="package", artifact="manifest")
     if not isinstance(manifest, dict):
         raise _err("package", "manifest", "malformed")
     return manifest
@@ -203,16 +203,16 @@ class WeightArtifactSpec:
             raise ValueError(f"weight_artifact_format_unknown: {self.format!r}")
         if not isinstance(self.primary_ref, str) or not self.primary_ref:
             raise ValueError("weight_artifact_primary_ref_invalid")
-        safe_relative_ref(self.primary_ref, scope="weight_store", artifact="primary")
+        package_ref_parts(self.primary_ref, scope="weight_store", artifact="primary")
         if self.format == NPZ_V1 and self.storage_dtype != "fp32":
             raise ValueError("npz_v1 requires weight_storage_dtype='fp32'")
         if self.format == SAFETENSORS_SHARDED_V1 and self.storage_dtype != PRESERVED_DTYPE:
             raise ValueError("safetensors_sharded_v1 requires weight_storage_dtype='preserved'")
-        if self.digest and not _is_sha256(self.digest):
+        if self.digest and not _hex_sha256(self.digest):
             raise ValueError("weight_artifact_digest_invalid")
 
 
-def _is_sha256(value) -> bool:
+def _hex_sha256(value) -> bool:
     return (isinstance(value, str) and len(value) == 64
             and all(c in "0123456789abcdef" for c in value))
 
@@ -265,68 +265,88 @@ class WeightStoreIndex:
         return frozenset(t.name for s in self.shards for t in s.tensors)
 
 
+def _require(ok: bool, error_id: str) -> None:
+    if not ok:
+        raise ValueError(error_id)
+
+
+def _text(v) -> bool:
+    return isinstance(v, str) and v != ""
+
+
+def _int_at_least(least: int):
+    return lambda v: type(v) is int and v >= least
+
+
+def _record(obj, fields: frozenset, error_id: str, checks) -> dict:
+    """``obj`` must be a JSON object with exactly ``fields``; each ``(key,
+    predicate, error id)`` of ``checks`` is then tried in order."""
+    _require(isinstance(obj, dict) and set(obj) == fields, error_id)
+    for key, ok, err in checks:
+        _require(ok(obj[key]), err)
+    return obj
+
+
+# The weight-store index contract (weight_store.py:201-296) as check tables; the
+# error identifiers are the reference's, so a caller sees the same failures.
+_TENSOR_CHECKS = (
+    ("name", _text, "weight_store_tensor_name_invalid"),
+    ("dtype", _text, "weight_store_tensor_dtype_invalid"),
+    ("shape", lambda v: isinstance(v, list) and all(type(d) is int and d >= 0 for d in v),
+     "weight_store_tensor_shape_invalid"),
+    ("byte_length", _int_at_least(0), "weight_store_tensor_bytes_invalid"),
+)
+_INDEX_CHECKS = (
+    ("schema_version", lambda v: type(v) is int and v == WEIGHT_STORE_INDEX_VERSION,
+     "weight_store_index_version_unsupported"),
+    ("format", lambda v: v == "safetensors", "weight_store_index_format_unsupported"),
+    ("storage_dtype", lambda v: v == PRESERVED_DTYPE, "weight_store_index_storage_dtype_invalid"),
+    ("tensor_count", _int_at_least(1), "weight_store_index_tensor_count_invalid"),
+    ("total_tensor_bytes", _int_at_least(1), "weight_store_index_tensor_bytes_invalid"),
+    ("shards", lambda v: isinstance(v, list) and len(v) > 0, "weight_store_index_shards_invalid"),
+)
+
+
 def _tensor_record(p) -> TensorRecord:
-    if not isinstance(p, dict) or set(p) != _TENSOR_FIELDS:
-        raise ValueError("weight_store_tensor_record_invalid")
-    name, dtype, shape, nbytes = p["name"], p["dtype"], p["shape"], p["byte_length"]
-    if not isinstance(name, str) or not name:
-        raise ValueError("weight_store_tensor_name_invalid")
-    if not isinstance(dtype, str) or not dtype:
-        raise ValueError("weight_store_tensor_dtype_invalid")
-    if not isinstance(shape, list) or any(type(d) is not int or d < 0 for d in shape):
-        raise ValueError("weight_store_tensor_shape_invalid")
-    if type(nbytes) is not int or nbytes < 0:
-        raise ValueError("weight_store_tensor_bytes_invalid")
-    return TensorRecord(name, dtype, tuple(shape), nbytes)
+    r = _record(p, _TENSOR_FIELDS, "weight_store_tensor_record_invalid", _TENSOR_CHECKS)
+    return TensorRecord(r["name"], r["dtype"], tuple(r["shape"]), r["byte_length"])
+
+
+def _shard_record(sp, seen_refs: set) -> ShardRecord:
+    def fresh_ref(ref) -> bool:
+        package_ref_parts(ref, scope="weight_store", artifact="shard")
+        _require(ref not in seen_refs, "weight_store_shard_ref_duplicated")
+        seen_refs.add(ref)
+        return True
+
+    r = _record(sp, _SHARD_FIELDS, "weight_store_shard_record_invalid", (
+        ("ref", _text, "weight_store_shard_ref_invalid"),
+        ("ref", fresh_ref, "weight_store_shard_ref_invalid"),
+        ("sha256", _hex_sha256, "weight_store_shard_digest_invalid"),
+        ("byte_length", _int_at_least(1), "weight_store_shard_bytes_invalid"),
+        ("tensors", lambda v: isinstance(v, list) and len(v) > 0,
+         "weight_store_shard_tensors_invalid"),
+    ))
+    return ShardRecord(r["ref"], r["sha256"], r["byte_length"],
+                       tuple(_tensor_record(t) for t in r["tensors"]))
 
 
 def parse_weight_store_index(payload: bytes) -> WeightStoreIndex:
-    """Validate the index contract (``weight_store.py:211-296``)."""
-    idx = _strict_json(payload, scope="weight_store", artifact="index")
-    if not isinstance(idx, dict) or set(idx) != _INDEX_FIELDS:
-        raise ValueError("weight_store_index_contract_invalid")
-    if type(idx["schema_version"]) is not int or idx["schema_version"] != WEIGHT_STORE_INDEX_VERSION:
-        raise ValueError("weight_store_index_version_unsupported")
-    if idx["format"] != "safetensors":
-        raise ValueError("weight_store_index_format_unsupported")
-    if idx["storage_dtype"] != PRESERVED_DTYPE:
-        raise ValueError("weight_store_index_storage_dtype_invalid")
-    count, total, shards_p = idx["tensor_count"], idx["total_tensor_bytes"], idx["shards"]
-    if type(count) is not int or count <= 0:
-        raise ValueError("weight_store_index_tensor_count_invalid")
-    if type(total) is not int or total <= 0:
-        raise ValueError("weight_store_index_tensor_bytes_invalid")
-    if not isinstance(shards_p, list) or not shards_p:
-        raise ValueError("weight_store_index_shards_invalid")
-    shards, refs, names, nbytes = [], set(), set(), 0
-    for sp in shards_p:
-        if not isinstance(sp, dict) or set(sp) != _SHARD_FIELDS:
-            raise ValueError("weight_store_shard_record_invalid")
-        ref, digest, blen, tp = sp["ref"], sp["sha256"], sp["byte_length"], sp["tensors"]
-        if not isinstance(ref, str) or not ref:
-            raise ValueError("weight_store_shard_ref_invalid")
-        safe_relative_ref(ref, scope="weight_store", artifact="shard")
-        if ref in refs:
-            raise ValueError("weight_store_shard_ref_duplicated")
-        refs.add(ref)
-        if not _is_sha256(digest):
-            raise ValueError("weight_store_shard_digest_invalid")
-        if type(blen) is not int or blen <= 0:
-            raise ValueError("weight_store_shard_bytes_invalid")
-        if not isinstance(tp, list) or not tp:
-            raise ValueError("weight_store_shard_tensors_invalid")
-        tensors = tuple(_tensor_record(t) for t in tp)
-        for t in tensors:
-            if t.name in names:
-                raise ValueError("weight_store_tensor_name_duplicated")
-            names.add(t.name)
-            nbytes += t.byte_length
-        shards.append(ShardRecord(ref, digest, blen, tensors))
-    if len(names) != count:
-        raise ValueError("weight_store_index_tensor_count_mismatch")
-    if nbytes != total:
-        raise ValueError("weight_store_index_tensor_bytes_mismatch")
-    return WeightStoreIndex(tuple(shards), count, total, hashlib.sha256(payload).hexdigest())
+    """Validate the index contract (``weight_store.py:211-296``): the record's
+    fields, each shard and tensor record, unique shard refs and tensor names,
+    and the declared tensor count and byte total."""
+    idx = _record(_load_json_unique_keys(payload, scope="weight_store", artifact="index"), _INDEX_FIELDS,
+                  "weight_store_index_contract_invalid", _INDEX_CHECKS)
+    refs: set = set()
+    shards = tuple(_shard_record(sp, refs) for sp in idx["shards"])
+    records = [t for sh in shards for t in sh.tensors]
+    names = {t.name for t in records}
+    _require(len(names) == len(records), "weight_store_tensor_name_duplicated")
+    _require(len(names) == idx["tensor_count"], "weight_store_index_tensor_count_mismatch")
+    _require(sum(t.byte_length for t in records) == idx["total_tensor_bytes"],
+             "weight_store_index_tensor_bytes_mismatch")
+    return WeightStoreIndex(shards, idx["tensor_count"], idx["total_tensor_bytes"],
+                            hashlib.sha256(payload).hexdigest())
 
 
 def read_weight_store_index(package_dir, spec: WeightArtifactSpec) -> WeightStoreIndex:

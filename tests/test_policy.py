@@ -124,12 +124,8 @@ def test_product_loop_matches_oracle_loop(strategy, prompt_len, gen, bs, steps):
                                    frontier_logits_fn=fn, trace=trace_o)
     state = D.MaskState(x=[*prompt, *([MASK] * gen)], prompt_len=prompt_len,
                         mask_token_id=MASK, eos_token_id=EOS)
-    if strategy == "bd3_fixed_quota":
-        layout = D.BlockLayout(start=prompt_len, length=gen, block_size=bs, origin=0)
-        pol = D.BD3FixedQuotaCommit(block_size=bs, requested_steps=steps,
-                                    generated_token_count=gen, block_layout=layout)
-    else:
-        pol = D.FixedQuotaCommit(block_size=bs, requested_steps=steps, generated_token_count=gen)
+    pol = D.QuotaSchedule(prompt_len=prompt_len, generated=gen, block_size=bs, steps=steps,
+                          absolute=strategy == "bd3_fixed_quota")
 
     def propose(plan):
         scores, toks = O.raw_max_prob(fn(list(state.x), plan.frontier, plan.window_end))
@@ -164,9 +160,7 @@ def test_product_bd3_eos_boundary_matches_oracle():
                                    frontier_logits_fn=fn)
     state = D.MaskState(x=[3] * 32 + [MASK] * 96, prompt_len=32, mask_token_id=MASK,
                         eos_token_id=EOS)
-    layout = D.BlockLayout(start=32, length=96, block_size=32, origin=0)
-    pol = D.BD3FixedQuotaCommit(block_size=32, requested_steps=24, generated_token_count=96,
-                                block_layout=layout)
+    pol = D.QuotaSchedule(prompt_len=32, generated=96, block_size=32, steps=24, absolute=True)
 
     def propose(plan):
         s, t = O.raw_max_prob(fn(list(state.x), plan.frontier, plan.window_end))
@@ -178,17 +172,35 @@ def test_product_bd3_eos_boundary_matches_oracle():
     assert ref["hit_eos"] and MASK in ref["x"]   # stopped with later blocks still masked
 
 
+def test_block_spans_match_the_oracle_grid():
+    """block_spans against the oracle's block_span / block_count on absolute and
+    prompt-relative grids, aligned and ragged."""
+    for start, length, bs, origin in [(40, 64, 32, 0), (64, 128, 32, 0), (0, 5, 2, 0),
+                                      (17, 33, 8, 17), (256, 256, 256, 256), (9, 0, 4, 0),
+                                      (5, 40, 64, 0)]:
+        spans = D.block_spans(start, length, bs, origin)
+        assert len(spans) == P.block_count(start, length, bs, origin)
+        assert spans == [P.block_span(start, length, bs, origin, i) for i in range(len(spans))]
+    assert D.round_quotas(32, 8) == [4] * 8
+    assert D.round_quotas(32, 3) == [11, 11, 10]
+    assert D.round_quotas(2, 4) == [1, 1, 0, 0]
+
+
 def test_product_policy_validation():
     with pytest.raises(ValueError):
-        D.BlockLayout(start=-1, length=4, block_size=2)
+        D.block_spans(-1, 4, 2)
     with pytest.raises(ValueError):
-        D.BlockLayout(start=4, length=4, block_size=2, origin=5)
+        D.block_spans(4, 4, 2, 5)
     with pytest.raises(ValueError):
-        D.BD3FixedQuotaCommit(block_size=0, requested_steps=1, generated_token_count=1,
-                              block_layout=D.BlockLayout(start=0, length=1, block_size=1))
+        D.QuotaSchedule(prompt_len=0, generated=1, block_size=0, steps=1, absolute=True)
+    with pytest.raises(ValueError):  # a misaligned BD3 prompt
+        st = D.MaskState(x=[1] * 40 + [MASK] * 64, prompt_len=40, mask_token_id=MASK,
+                         eos_token_id=EOS)
+        D.QuotaSchedule(prompt_len=40, generated=64, block_size=32, steps=4,
+                        absolute=True).plan(state=st, step=0)
     with pytest.raises(D.GenerationCancelled):
         state = D.MaskState(x=[1, MASK], prompt_len=1, mask_token_id=MASK, eos_token_id=EOS)
-        pol = D.FixedQuotaCommit(block_size=1, requested_steps=1, generated_token_count=1)
+        pol = D.QuotaSchedule(prompt_len=1, generated=1, block_size=1, steps=1, absolute=False)
         D.run_decode_loop(state, commit_policy=pol, iteration_limit=1,
                           propose_fn=lambda p: ([1.0], [5], 1),
                           commit_device_fn=lambda p, t: None, cancelled=lambda: True)
