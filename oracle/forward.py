@@ -30,7 +30,7 @@ def _keep(x):
 
 
 def layer_forward(weights, cfg, i, hidden, cos, sin, visible, kv_hook=None, operand_round=None,
-                  kv_round=None):
+                  kv_round=None, query_rows=None):
     """One decoder layer over all rows of ``hidden`` (fp32 ``[S, d]``).
 
     ``h += o(attn(rope(qnorm(q(n))), rope(knorm(k(n))), v(n)))`` with
@@ -44,6 +44,11 @@ def layer_forward(weights, cfg, i, hidden, cos, sin, visible, kv_hook=None, oper
     cached K/V. ``kv_round`` (also a precision model) rounds only the K and V
     that a prefix cache stores (e.g. to fp16): the reference computation with
     the cache's storage type. ``None`` for both is the reference computation.
+
+    ``query_rows`` (optional, sorted row indices): only these rows' outputs are
+    computed and returned; the K/V still come from every row. Row outputs are
+    independent, so this gives the same values for those rows as a full layer
+    (up to float32 summation order in the row-subset matmuls).
     """
     rnd = operand_round or _keep
     kv_rnd = kv_round or rnd
@@ -53,10 +58,11 @@ def layer_forward(weights, cfg, i, hidden, cos, sin, visible, kv_hook=None, oper
     p = f"model.layers.{i}."
     s = hidden.shape[0]
     n = rnd(ops.rms_norm(hidden, weights[p + "input_layernorm.weight"], eps))
-    q = _lin(weights, p + "self_attn.q_proj", n, kind).reshape(s, hq, hd)
+    qr = slice(None) if query_rows is None else np.asarray(query_rows, dtype=np.int64)
+    q = _lin(weights, p + "self_attn.q_proj", n[qr], kind).reshape(-1, hq, hd)
     if cfg["qk_norm"]:
         q = ops.rms_norm(q, weights[p + "self_attn.q_norm.weight"], eps)
-    q = rnd(ops.apply_split_half_rope(q, cos, sin))
+    q = rnd(ops.apply_split_half_rope(q, cos[qr], sin[qr]))
     k = _lin(weights, p + "self_attn.k_proj", n, kind).reshape(s, hkv, hd)
     v = kv_rnd(_lin(weights, p + "self_attn.v_proj", n, kind).reshape(s, hkv, hd))
     if cfg["qk_norm"]:
@@ -64,8 +70,9 @@ def layer_forward(weights, cfg, i, hidden, cos, sin, visible, kv_hook=None, oper
     k = kv_rnd(ops.apply_split_half_rope(k, cos, sin))
     if kv_hook is not None:
         kv_hook(i, k, v)
-    attn = rnd(ops.attention(q, k, v, visible=visible, dtype=np.float32).astype(np.float32))
-    hidden = (hidden + _lin(weights, p + "self_attn.o_proj", attn, kind)).astype(np.float32)
+    vis = None if visible is None else visible[qr]
+    attn = rnd(ops.attention(q, k, v, visible=vis, dtype=np.float32).astype(np.float32))
+    hidden = (hidden[qr] + _lin(weights, p + "self_attn.o_proj", attn, kind)).astype(np.float32)
     n2 = rnd(ops.rms_norm(hidden, weights[p + "post_attention_layernorm.weight"], eps))
     gate = _lin(weights, p + "mlp.gate_proj", n2, kind)
     up = _lin(weights, p + "mlp.up_proj", n2, kind)
@@ -75,7 +82,7 @@ def layer_forward(weights, cfg, i, hidden, cos, sin, visible, kv_hook=None, oper
 
 def forward_full(weights, cfg, token_ids, *, mask_kind, mask_geometry=None,
                  output_rows=None, n_layers=None, kv_hook=None, operand_round=None,
-                 kv_round=None):
+                 kv_round=None, last_layer_output_rows_only=False):
     """Raw fp32 logits for ``output_rows`` (default: every row) of ``token_ids``.
 
     ``mask_kind`` is ``"d2f_hybrid"`` (``mask_geometry = (prompt_len,
@@ -83,6 +90,8 @@ def forward_full(weights, cfg, token_ids, *, mask_kind, mask_geometry=None,
     ``n_layers`` limits the layer count (the CPU baseline's bounded sample).
     ``operand_round``: see :func:`layer_forward`; also applied to the final
     norm's output (the LM head's input). ``kv_round``: see :func:`layer_forward`.
+    ``last_layer_output_rows_only``: the last layer computes only the rows the LM
+    head reads (a shortcut for long canvases; see ``query_rows``).
     """
     ids = np.asarray(token_ids, dtype=np.int64)
     s = ids.shape[0]
@@ -98,18 +107,24 @@ def forward_full(weights, cfg, token_ids, *, mask_kind, mask_geometry=None,
     else:
         raise ValueError(f"unsupported mask kind {mask_kind!r}")
     layers = cfg["n_layers"] if n_layers is None else n_layers
-    for i in range(layers):
-        hidden = layer_forward(weights, cfg, i, hidden, cos, sin, visible, kv_hook, operand_round,
-                               kv_round)
     rows = list(range(s)) if output_rows is None else [int(r) for r in output_rows]
-    h = hidden[rows]
+    kept = sorted(set(rows))
+    for i in range(layers):
+        only = last_layer_output_rows_only and i == layers - 1
+        hidden = layer_forward(weights, cfg, i, hidden, cos, sin, visible, kv_hook, operand_round,
+                               kv_round, query_rows=kept if only else None)
+    if last_layer_output_rows_only and layers > 0:
+        h = hidden[[kept.index(r) for r in rows]]
+    else:
+        h = hidden[rows]
     h = (operand_round or _keep)(ops.rms_norm(h, weights["model.norm.weight"], cfg["eps"]))
     logits = ops.linear(h, weights["lm_head.weight"], None, weight_kind=cfg["weight_kind"])
     return logits.astype(np.float32)
 
 
 def window_logits(weights, cfg, token_ids, scope, *, mask_kind, mask_geometry,
-                  logits_convention, operand_round=None, kv_round=None):
+                  logits_convention, operand_round=None, kv_round=None,
+                  last_layer_output_rows_only=False):
     """Convention-applied logits for ``scope`` positions (``execute_window``).
 
     Raw row selection per ``_required_raw_row`` (``mlx_d2f_forward.py:74-93``);
@@ -120,6 +135,7 @@ def window_logits(weights, cfg, token_ids, scope, *, mask_kind, mask_geometry,
     uniq = sorted(set(raw_rows))
     logits = forward_full(weights, cfg, token_ids, mask_kind=mask_kind,
                           mask_geometry=mask_geometry, output_rows=uniq,
-                          operand_round=operand_round, kv_round=kv_round)
+                          operand_round=operand_round, kv_round=kv_round,
+                          last_layer_output_rows_only=last_layer_output_rows_only)
     index = {r: j for j, r in enumerate(uniq)}
     return logits[[index[r] for r in raw_rows]]

@@ -225,3 +225,19 @@ def test_operand_precision_sites(seed):
     # a planted coarser cache (bf16 storage) is not what the bar is measured on
     bf16_kv = shift(run(kv_round=lambda a: O.bf16_round(np.asarray(a, np.float32))))
     assert bf16_kv > 2 * kv_only
+
+
+@pytest.mark.parametrize("kind,mask", [("q4", "d2f_hybrid"), ("bf16", "bidirectional")])
+def test_last_layer_output_rows_shortcut(kind, mask):
+    """The long-canvas shortcut (the last layer computes only the LM rows) gives
+    the full forward's logits for those rows, in the requested order."""
+    g = tiny_geometry(layer_count=2)
+    model = syn.build_model(g, kind, seed=31)
+    W, cfg = oracle_weights(model), syn.oracle_config(g, kind)
+    ids = syn.prompt_ids(31, 70, high=1000)
+    rows = [69, 3, 40, 3]
+    geom = (0, 32) if mask == "d2f_hybrid" else None
+    full = F.forward_full(W, cfg, ids, mask_kind=mask, mask_geometry=geom, output_rows=rows)
+    fast = F.forward_full(W, cfg, ids, mask_kind=mask, mask_geometry=geom, output_rows=rows,
+                          last_layer_output_rows_only=True)
+    np.testing.assert_allclose(fast, full, rtol=1e-5, atol=1e-5)
