@@ -112,6 +112,7 @@ SIGNATURES = {
     "drt_op_q4_linear_workspace_bytes": (_SZ, [_I32, _I32, _I32]),
     "drt_op_q4_linear": (_I32, [_VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _VP, _VP, _SZ,
                                 _VP]),
+    "drt_op_q4_linear_noalloc": (_I32, [_VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _VP, _VP]),
     "drt_op_bf16_repack": (_I32, [_VP, _I32, _I32, _VP, _VP]),
     "drt_op_bf16_linear_workspace_bytes": (_SZ, [_I32, _I32, _I32]),
     "drt_op_bf16_linear": (_I32, [_VP, _VP, _I32, _I32, _I32, _VP, _VP, _VP, _SZ, _VP]),

@@ -1544,10 +1544,10 @@ int32_t drt_op_cast_bf16(const float* x, void* y, int64_t n, void* stream) {
   });
 }
 
-int32_t drt_op_q4_linear(const void* qw, const void* sb, const void* x, int32_t x_dtype,
-                         int32_t m, int32_t n, int32_t k, const void* bias, float* y,
-                         void* workspace, size_t workspace_bytes, void* stream) {
-  return guarded([&] {
+static void q4_linear_into(const void* qw, const void* sb, const void* x, int32_t x_dtype,
+                           int32_t m, int32_t n, int32_t k, const void* bias, float* y,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  {
     require(qw && sb && x && y && m > 0 && n > 0 && k > 0, "bad q4_linear arguments");
     require(n % 32 == 0 && k % 64 == 0, "q4_linear needs n % 32 == 0 and k % 64 == 0");
     require(x_dtype == DRT_F32 || x_dtype == DRT_BF16, "q4_linear x must be F32 or BF16");
@@ -1580,6 +1580,58 @@ int32_t drt_op_q4_linear(const void* qw, const void* sb, const void* x, int32_t 
     } else {
       fused_linear(f, FL_STORE, st);
     }
+  }
+}
+
+int32_t drt_op_q4_linear(const void* qw, const void* sb, const void* x, int32_t x_dtype,
+                         int32_t m, int32_t n, int32_t k, const void* bias, float* y,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  return guarded([&] {
+    q4_linear_into(qw, sb, x, x_dtype, m, n, k, bias, y, workspace, workspace_bytes, stream);
+  });
+}
+
+// ---- the allocation-free variant: its workspace is a file-scope device array
+
+// The workspace of drt_op_q4_linear_noalloc: one copy per GPU the library runs
+// on (each device holds its own, at its own address, until the process ends).
+// In host code `scratch` only names the symbol; its device address comes from
+// hipGetSymbolAddress, once per device (scratch_on_current_device).
+constexpr size_t DRT_NOALLOC_SCRATCH_BYTES = (size_t)64 << 20;
+static __device__ __align__(256) unsigned char scratch[DRT_NOALLOC_SCRATCH_BYTES];
+
+static std::mutex g_scratch_mu;
+static std::map<int, void*> g_scratch_ptr;  // device ordinal -> address of its scratch
+
+static void* scratch_on_current_device() {
+  int dev = -1;
+  DRT_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  auto it = g_scratch_ptr.find(dev);
+  if (it != g_scratch_ptr.end()) return it->second;
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || ptr == nullptr)
+    fail(INTERNAL_ERROR, std::string("hipGetSymbolAddress of the q4 linear scratch failed on "
+                                     "device ") + std::to_string(dev) + ": " +
+                             hipGetErrorString(e));
+  g_scratch_ptr[dev] = ptr;
+  return ptr;
+}
+
+int32_t drt_op_q4_linear_noalloc(const void* qw, const void* sb, const void* x, int32_t x_dtype,
+                                 int32_t m, int32_t n, int32_t k, const void* bias, float* y,
+                                 void* stream) {
+  return guarded([&] {
+    require(m > 0 && n > 0 && k > 0, "bad q4_linear_noalloc arguments");
+    const size_t need = drt_op_q4_linear_workspace_bytes(m, n, k);
+    if (need > DRT_NOALLOC_SCRATCH_BYTES)
+      fail(INVALID_ARGUMENT, "q4_linear_noalloc: m=" + std::to_string(m) + ", n=" +
+                                 std::to_string(n) + ", k=" + std::to_string(k) + " needs " +
+                                 std::to_string(need) + " bytes of workspace, above its " +
+                                 std::to_string(DRT_NOALLOC_SCRATCH_BYTES) + "-byte scratch");
+    q4_linear_into(qw, sb, x, x_dtype, m, n, k, bias, y, scratch_on_current_device(),
+                   DRT_NOALLOC_SCRATCH_BYTES, stream);
   });
 }
 

@@ -223,6 +223,17 @@ size_t drt_op_q4_linear_workspace_bytes(int32_t m, int32_t n, int32_t k);
 int32_t drt_op_q4_linear(const void* qw, const void* sb, const void* x, int32_t x_dtype,
                          int32_t m, int32_t n, int32_t k, const void* bias, float* y,
                          void* workspace, size_t workspace_bytes, void* stream);
+/* drt_op_q4_linear without a workspace argument and without any device allocation: for
+ * callers that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. Its workspace is a
+ * 64 MiB device array of the library, one per GPU (held until the process ends, its
+ * address looked up once per device); shapes whose drt_op_q4_linear_workspace_bytes
+ * exceed 64 MiB are refused with DRT_INVALID_ARGUMENT. The launch uses the calling
+ * thread's current device. Calls that overlap on one GPU share that array and race:
+ * serialize them (one stream, or events). Nothing in the array needs to start at zero. */
+int32_t drt_op_q4_linear_noalloc(const void* qw, const void* sb, const void* x, int32_t x_dtype,
+                                 int32_t m, int32_t n, int32_t k, const void* bias, float* y,
+                                 void* stream);
 /* bf16 weight W [n, k] -> device tile layout wb (same size). */
 int32_t drt_op_bf16_repack(const void* w, int32_t n, int32_t k, void* wb, void* stream);
 /* linear(x, bf16 W): y = bf16(bf16(x) @ W^T) as fp32 [m, n]; x bf16 [m, k]. */
