@@ -19,6 +19,9 @@ struct FusedArgs {
   // work-group sets if it finds itself on another XCD (next to M, N, K: the
   // skinny kernels fetch these first, in one scalar load)
   int n_xcc = 1;
+  // 1: the placement above is not assumed; split-K slices meet through
+  // device-scope fences and atomics instead of one XCD's L2
+  int fenced = 0;
   int* placement_err = nullptr;
   // PRO_ACT: activation [M][K] (ACT_F16P + xsum[M][K/64], or ACT_BF16)
   const void* act = nullptr;
@@ -64,6 +67,8 @@ void fused_linear(const FusedArgs& a, int kind, hipStream_t s);
 bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s);
 // Workspace the skinny kernels need for a linear of N outputs and K inputs.
 size_t skinny_part_floats(int N, int K);
+// One probe launch: does work-group i run on XCD i % n_xcc? (scratch_dev: >= 256 ints)
+bool probe_round_robin(int n_xcc, int* scratch_dev, hipStream_t s);
 int skinny_counters(int N);
 // The large-M q4 kernels (M > 32): ACT_F16P activation in, kinds FL_QKV,
 // FL_SWIGLU (ACT_F16P out) and FL_STORE (KS > 1: fp32 partial slices

@@ -141,6 +141,7 @@ struct Runtime {
   bool sk_all = true;
   int sk_n_counters = 0;
   int n_xcc = 1;
+  bool fenced = false;           // split-K exchange through device-scope fences (no placement assumed)
   DevBuf placement_err;          // int, set by a kernel that finds itself on an unexpected XCD
   int* placement_host = nullptr; // pinned copy, read after each synchronized forward
   // pinned landing area of a forward's scores and tokens, written by the LM head's
@@ -451,6 +452,19 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
     if (hipDeviceGetAttribute(&nx, hipDeviceAttributeNumberOfXccs, rt->device) != hipSuccess)
       nx = 1;
     rt->n_xcc = std::max(1, nx);
+    // DRT_N_XCC overrides the XCD count the split-K grids are laid out for (a
+    // test hook: a wrong count must surface as the placement error); otherwise
+    // one probe launch checks the round-robin placement, and where it does not
+    // hold the split-K exchange runs fenced (DRT_SPLITK_FENCED=1 forces that).
+    const char* nx_env = getenv("DRT_N_XCC");
+    if (nx_env && atoi(nx_env) >= 1) {
+      rt->n_xcc = atoi(nx_env);
+    } else {
+      DevBuf probe;
+      probe.alloc(256 * sizeof(int));
+      rt->fenced = !probe_round_robin(rt->n_xcc, probe.as<int>(), s);
+    }
+    if (getenv("DRT_SPLITK_FENCED") != nullptr) rt->fenced = true;
     rt->placement_err.alloc(4);
     DRT_HIP(hipMemsetAsync(rt->placement_err.p, 0, 4, s));
     DRT_HIP(hipHostMalloc((void**)&rt->placement_host, 4, hipHostMallocCoherent));
@@ -646,6 +660,7 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
       f.counters = rt.sk_counters.as<int>();
       f.n_counters = rt.sk_n_counters;
       f.n_xcc = rt.n_xcc;
+      f.fenced = rt.fenced ? 1 : 0;
       f.placement_err = rt.placement_err.as<int>();
       return f;
     };

@@ -16,7 +16,10 @@
 // then coherent with each other, with no device-wide fence (an L2 writeback and
 // invalidate per work-group costs tens of microseconds). Each work-group checks
 // the XCD it runs on and raises `placement_err` if the layout assumption fails,
-// which the host turns into an error.
+// which the host turns into an error. The runtime probes the placement once at
+// creation; where it does not hold, the kernels run `fenced`: each slice's
+// stores are released at device scope before a device-scope arrival atomic,
+// and the last work-group acquires before reading the slices.
 //
 //   skinny_wide_kernel  : 128 columns (4 n-tiles, one per wave), RMSNorm
 //                         prologue (row statistics from the producer's
@@ -35,6 +38,7 @@
 #include "linear_dev.h"
 
 #include <cstdlib>
+#include <vector>
 
 namespace {
 
@@ -66,11 +70,12 @@ constexpr int SK_SS_PER_THREAD = 14; // K / 32 <= 8 * 14 = 112 partial sums (d <
 // loads: an early return would let the compiler sink the loads, and the kernel
 // argument fetches they need, behind the branch - one more round trip for
 // every work-group.) n_xcc and perr are the pinned a.n_xcc, a.placement_err.
-DRT_DEV bool sk_place(int n_xcc, int* perr, int n_blocks, int KS, int& blk, int& ks) {
+DRT_DEV bool sk_place(int n_xcc, int fenced, int* perr, int n_blocks, int KS, int& blk,
+                      int& ks) {
   const int i = blockIdx.x, x = i % n_xcc, j = i / n_xcc;
   blk = x + n_xcc * (j / KS);
   ks = j - (j / KS) * KS;
-  if (n_xcc > 1 && threadIdx.x == 0 && perr) {
+  if (n_xcc > 1 && !fenced && threadIdx.x == 0 && perr) {
     const int xcc = (int)(__builtin_amdgcn_s_getreg((31 << 11) | 20) & 0xf);  // HW_REG_XCC_ID
     if (xcc != x) __hip_atomic_fetch_or(perr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -82,15 +87,35 @@ DRT_DEV bool sk_place(int n_xcc, int* perr, int n_blocks, int KS, int& blk, int&
 // Called after this work-group stored its partial: returns true in the last
 // work-group of the block to arrive (which then adds the partials up), false
 // elsewhere. The stores complete (in this XCD's L2) before the barrier, and the
-// counter is bumped by an L2 atomic after it.
-DRT_DEV bool last_to_arrive(int* counter, int arrivals, int* flag) {
+// counter is bumped by an L2 atomic after it. Fenced (placement not assumed):
+// the stores are released at device scope and the arrival is a device-scope
+// acquire-release, so the last work-group sees every slice wherever it ran.
+DRT_DEV bool last_to_arrive(int* counter, int arrivals, int* flag, int fenced) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0)
-    *flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) ==
-            arrivals - 1;
+  if (threadIdx.x == 0) {
+    if (fenced)
+      *flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
+              arrivals - 1;
+    else
+      *flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_WORKGROUP) == arrivals - 1;
+  }
   __syncthreads();
   return *flag != 0;
+}
+
+// The arrival counter back to zero for the next launch (fenced: at device scope,
+// where the next launch's arrivals count).
+DRT_DEV void reset_counter(int* counter, int fenced) {
+  if (fenced) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else *counter = 0;
+}
+
+// XCD of every work-group of a 1-D launch (the placement probe).
+__global__ void xcc_probe_kernel(int* __restrict__ xcc) {
+  if (threadIdx.x == 0)
+    xcc[blockIdx.x] = (int)(__builtin_amdgcn_s_getreg((31 << 11) | 20) & 0xf);  // HW_REG_XCC_ID
 }
 
 // The last work-group's sum of the KS <= KSC partial tiles of a wide block into
@@ -144,7 +169,7 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
   int* perr = (int*)gerr;
   const int G = K >> 6;
   int grp, ks;
-  const bool live = sk_place(n_xcc, perr, N / 128, KS, grp, ks);
+  const bool live = sk_place(n_xcc, a.fenced, perr, N / 128, KS, grp, ks);
   const int nt = grp * 4 + wave;
   const int u0 = ks * U, kc0 = u0 * 64;
   constexpr int KCN = U * 64;
@@ -270,7 +295,7 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj)
       *(f32x4*)(pw + 256 * jj) = f32x4{acc[4 * jj], acc[4 * jj + 1], acc[4 * jj + 2], acc[4 * jj + 3]};
-    if (!last_to_arrive(&a.counters[grp], KS, flag)) return;
+    if (!last_to_arrive(&a.counters[grp], KS, flag, a.fenced)) return;
     const float* pbase = a.part + (size_t)grp * KS * 4096;
     auto tables = [&]() {
       if (EPI == EPI_QKV) qt = qkv_tables(a, grp, row0, M);
@@ -278,7 +303,7 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
     if (KS <= 2) sk_wide_sum_slices<2>(pbase, KS, red, tables);
     else if (KS <= 4) sk_wide_sum_slices<4>(pbase, KS, red, tables);
     else sk_wide_sum_slices<SK_KS_MAX>(pbase, KS, red, tables);
-    if (threadIdx.x == 0) a.counters[grp] = 0;
+    if (threadIdx.x == 0) reset_counter(&a.counters[grp], a.fenced);
   } else {
     if (EPI == EPI_QKV) qt = qkv_tables(a, grp, row0, M);
 #pragma unroll
@@ -352,7 +377,7 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
   const int G = K >> 6;
   const int U = G / KS;
   int nt, ks;
-  const bool live = sk_place(n_xcc, perr, N / 32, KS, nt, ks);
+  const bool live = sk_place(n_xcc, a.fenced, perr, N / 32, KS, nt, ks);
   const int u_lo = ks * U + (U * wave) / 4, u_hi = ks * U + (U * (wave + 1)) / 4;
   extern __shared__ __align__(16) char smem[];
   float* red = (float*)smem;  // [4][32][33]
@@ -433,7 +458,7 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
            red[(96 + m) * 33 + c0 + e];
   if (KS > 1) {
     *(f32x4*)(a.part + (size_t)(nt * KS + ks) * 1024 + m * 32 + c0) = v;
-    if (!last_to_arrive(&a.counters[nt], KS, flag)) return;
+    if (!last_to_arrive(&a.counters[nt], KS, flag, a.fenced)) return;
     const float* pp = a.part + (size_t)nt * KS * 1024 + m * 32 + c0;
     f32x4 pv[SK_KS_MAX];
 #pragma unroll
@@ -441,7 +466,7 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
     v = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int k2 = 0; k2 < SK_KS_MAX; ++k2) v += pv[k2] * (k2 < KS ? 1.f : 0.f);  // unconditional loads
-    if (threadIdx.x == 0) a.counters[nt] = 0;
+    if (threadIdx.x == 0) reset_counter(&a.counters[nt], a.fenced);
   }
   if (a.bias) {
     const uint2 bb = *(const uint2*)(a.bias + n);
@@ -506,6 +531,21 @@ int narrow_slices(int N, int K) {
 }
 
 }  // namespace
+
+// Whether work-group i of a launch runs on XCD i % n_xcc (the layout the
+// split-K exchange assumes), from one probe launch of 4 * 64 work-groups.
+bool probe_round_robin(int n_xcc, int* scratch_dev, hipStream_t s) {
+  if (n_xcc <= 1) return true;
+  constexpr int WGS = 256;
+  hipLaunchKernelGGL(xcc_probe_kernel, dim3(WGS), dim3(64), 0, s, scratch_dev);
+  DRT_HIP(hipGetLastError());
+  std::vector<int> xcc(WGS);
+  DRT_HIP(hipMemcpyAsync(xcc.data(), scratch_dev, WGS * sizeof(int), hipMemcpyDeviceToHost, s));
+  DRT_HIP(hipStreamSynchronize(s));
+  for (int i = 0; i < WGS; ++i)
+    if (xcc[i] != i % n_xcc) return false;
+  return true;
+}
 
 size_t skinny_part_floats(int N, int K) {
   if (K % 64 || N % 32) return 0;
