@@ -753,7 +753,13 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
 // Bit 2 of the same flag: a wave of the decode attention gave up waiting for a K/V
 // tile (its bounded wait ran out), so that forward's attention is not valid.
 void check_placement(const Runtime& rt) {
+  // the placement first: a split-K exchange across XCDs produces garbage, which
+  // may also trip the other two checks
   const int e = *rt.placement_host;
+  if (e & 1)
+    fail(INTERNAL_ERROR,
+         "a split-K linear ran on an unexpected XCD (work-group placement is not the "
+         "round-robin the kernels assume); results of this runtime are not valid");
   if (e & 2)
     fail(INTERNAL_ERROR,
          "decode attention: a bounded wait for a K/V tile expired; results of this runtime "
@@ -762,10 +768,7 @@ void check_placement(const Runtime& rt) {
     fail(INTERNAL_ERROR,
          "an activation, Q, K or V value exceeded the fp16 range (|x| >= 65504); results of "
          "this forward are not valid");
-  if (e != 0)
-    fail(INTERNAL_ERROR,
-         "a split-K linear ran on an unexpected XCD (work-group placement is not the "
-         "round-robin the kernels assume); results of this runtime are not valid");
+  if (e != 0) fail(INTERNAL_ERROR, "a kernel reported an unknown error word");
 }
 
 void run_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_stride,
