@@ -10,6 +10,9 @@
   masked tokens: window logits of every masked row, then two fixed-quota steps
   (4 rows each) teacher-forced against the oracle.
 
+* Dream's <= 32-row forwards at the 7B layer shapes (its block-threshold decode
+  runs them): a 32-row window through the split-K linears at those shapes.
+
 One decoder layer and a 4096-token vocabulary keep the oracle to seconds; every
 kernel runs at its real shape. The bar is the one of every session test: strict
 (1e-3 tie band, scores within SCORE_REL_TOL) against the oracle with the cached
@@ -148,5 +151,32 @@ def test_dream_512_row_canvas_window_and_fixed_quota_steps():
         _say(f"  steps score rel max {worst:.2e}; reported: {ties}")
         assert not problems, problems
         assert state.x == xx
+    finally:
+        rt.close()
+
+
+def test_dream_7b_shapes_32_row_window():
+    from diffusorrt_amd import synthetic as syn
+    from diffusorrt_amd.runtime import Runtime, fixed_quota_session_config
+
+    _say("dream 7B shapes, 32-row window (split-K linears)")
+    geom = _geometry(syn.DREAM_QWEN25_7B)
+    model = syn.build_model(geom, "q4", seed=5)
+    W, cfg = oracle_weights(model), syn.oracle_config(geom, "q4")
+    x = np.random.default_rng(5).integers(0, 3900, 24).tolist() + [geom.mask_token_id] * 8
+    scope = list(range(24, 32))
+    rt = Runtime(model, max_forward_rows=64, max_positions=256)
+    try:
+        with rt.session(fixed_quota_session_config(8, 8, len(x))) as s:
+            win = s.execute_window(x, scope)
+        assert win.forwarded_rows == len(x)
+        ref, kv = [F.window_logits(W, cfg, x, scope, mask_kind="bidirectional",
+                                   mask_geometry=None, logits_convention="dream_ar_shift",
+                                   kv_round=kr) for kr in (None, kv_round_f16)]
+        got = win.array()
+        err, err_kv = rel_err_rows(got, ref), rel_err_rows(got, kv)
+        _say(f"  window rel err max={err.max():.2e} (vs fp16-K/V oracle {err_kv.max():.2e})")
+        assert err.max() < LOGITS_REL_TOL
+        assert err_kv.max() < 2e-3  # every operand but the K/V cache carries ~22 bits
     finally:
         rt.close()
