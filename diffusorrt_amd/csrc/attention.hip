@@ -242,7 +242,10 @@ __global__ __launch_bounds__(64 * QW) void attn_split_kernel(
 // m = -inf, l = 0; the combine then skips their O.
 // n_keys comes from `desc` when it is set (graph replays), else from the argument.
 constexpr int DEC_QROW = 136;  // 16-bit elements per Q row in LDS (+16 B pad)
-constexpr int DEC_QLO = 64 * DEC_QROW;  // elements from the Q hi plane to the lo plane in LDS
+// elements from the Q hi plane to the lo plane in LDS (64 rows of hi plane up to
+// two query tiles, 128 for four)
+template <int QT> constexpr int dec_qlo() { return (QT <= 2 ? 64 : 32 * QT) * DEC_QROW; }
+constexpr int DEC_QLO = dec_qlo<2>();
 constexpr int DEC_TILES_UP_FRONT = 3;
 
 // K/V fragments of tile t. With real == false every lane reads the first 16
@@ -283,7 +286,7 @@ DRT_DEV float max_xor32(float v) {
 // (the kernel is instantiated with QT = ceil(n_qv / 32)); rows beyond n_qv hold
 // Q = 0. c = scale * log2(e); m_run is the base in scaled units (-inf before
 // any key). key0 / nk are wave-uniform.
-template <typename T, int QT, int NG>
+template <typename T, int QT, int NG, int QLO = DEC_QLO>
 DRT_DEV void attend_group(const typename MfmaT<T>::vec (&kc)[NG][8],
                           const typename MfmaT<T>::vec (&vc)[NG][8], const T* __restrict__ qs,
                           const int (&key0)[NG], const int (&nk)[NG], float c, int lane,
@@ -298,15 +301,15 @@ DRT_DEV void attend_group(const typename MfmaT<T>::vec (&kc)[NG][8],
   // (inline asm, so the compiler does not sink them to their use) before step
   // i's MFMAs, and waited for after them; the wait takes the registers as
   // operands, so nothing reads them earlier.
-  // The lo plane of Q sits DEC_QLO elements after the hi plane: every score
-  // MFMA has a twin on the lo fragments (Q carried to ~22 bits, K exact).
+  // The lo plane of Q sits QLO elements after the hi plane: every score MFMA
+  // has a twin on the lo fragments (Q carried to ~22 bits, K exact).
   const T* qrow = qs + (lane & 31) * DEC_QROW + 8 * (lane >> 5);
   const uint32_t qaddr = (uint32_t)(uintptr_t)qrow;
   vec qf[QT], qfl[QT];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     qf[qt] = *(const vec*)(qrow + qt * 32 * DEC_QROW);
-    qfl[qt] = *(const vec*)(qrow + DEC_QLO + qt * 32 * DEC_QROW);
+    qfl[qt] = *(const vec*)(qrow + QLO + qt * 32 * DEC_QROW);
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -319,7 +322,7 @@ DRT_DEV void attend_group(const typename MfmaT<T>::vec (&kc)[NG][8],
                      : "v"(qaddr), "i"((qt * 32 * DEC_QROW + 16 * (i + 1)) * 2));
         asm volatile("ds_read_b128 %0, %1 offset:%2"
                      : "=v"(qnl[qt])
-                     : "v"(qaddr), "i"((DEC_QLO + qt * 32 * DEC_QROW + 16 * (i + 1)) * 2));
+                     : "v"(qaddr), "i"((QLO + qt * 32 * DEC_QROW + 16 * (i + 1)) * 2));
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -564,9 +567,9 @@ __global__ __launch_bounds__(256) void attn_decode_reg_kernel(
 // the rest of the range is still streaming, and release each slot (freed flag)
 // after reading it into registers. Every wait on a flag is bounded: a wait that
 // runs out sets *err (the host reports it) and the kernel still finishes.
-// Tile slots of the ring: 8, or 7 when the Q planes of 64 query vectors leave
-// no room for an eighth (160 KiB of LDS per work-group).
-template <int QT> constexpr int decr_slots() { return QT == 1 ? 8 : 7; }
+// Tile slots of the ring: as many as the LDS left by the Q planes holds (160
+// KiB per work-group): 8 for 32 query vectors, 7 for 64, 5 for 128.
+template <int QT> constexpr int decr_slots() { return QT == 1 ? 8 : (QT == 2 ? 7 : 5); }
 constexpr int DECR_SPIN = 1 << 22;
 // s_waitcnt immediates (gfx9: vmcnt bits 3:0 + 15:14, expcnt 6:4, lgkmcnt 11:8)
 constexpr int DECR_VM48 = 0xCF70, DECR_VM32 = 0x8F70, DECR_VM16 = 0x4F70, DECR_VM0 = 0x0F70;
@@ -618,6 +621,7 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
     float* __restrict__ o_part, float* __restrict__ ml_part, float scale, int* err) {
   typedef typename MfmaT<T>::vec vec;
   constexpr int DECR_SLOTS = decr_slots<QT>();
+  constexpr int QLO = dec_qlo<QT>();
   constexpr int SLOTS = QT * 4096;
   constexpr int SLOT = SLOTS + QT * 64 * 2;
   const int lane = threadIdx.x & 63;
@@ -635,8 +639,8 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
   extern __shared__ __align__(16) char smem[];
   int* ready = (int*)smem;                               // [DECR_SLOTS]
   int* freed = ready + DECR_SLOTS;                       // [DECR_SLOTS]
-  T* qs = (T*)(smem + 128);  // [QT*32][DEC_QROW] hi, lo plane at + DEC_QLO
-  char* tiles = smem + 128 + (DEC_QLO + QT * 32 * DEC_QROW) * 2;  // [DECR_SLOTS][16 KiB]
+  T* qs = (T*)(smem + 128);  // [QT*32][DEC_QROW] hi, lo plane at + QLO
+  char* tiles = smem + 128 + (QLO + QT * 32 * DEC_QROW) * 2;  // [DECR_SLOTS][16 KiB]
   float* mrg = (float*)(smem + 128);                     // [4][SLOT], over Q and the tiles
 
   if (n <= 0) {
@@ -685,7 +689,7 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
       const bool ok = (ch >> 4) < n_qv;
       T* d = qs + (ch >> 4) * DEC_QROW + (ch & 15) * 8;
       *(u32x4*)d = ok ? qraw[i] : u32x4{0u, 0u, 0u, 0u};
-      *(u32x4*)(d + DEC_QLO) = ok ? qrawl[i] : u32x4{0u, 0u, 0u, 0u};
+      *(u32x4*)(d + QLO) = ok ? qrawl[i] : u32x4{0u, 0u, 0u, 0u};
     }
     decr_waitcnt<DECR_LGKM0>();  // Q and the flags are written
   }
@@ -702,6 +706,10 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
   constexpr int TSTRIDE = 4 / QT;
   constexpr int SLOT1 = 4096 + 64 * 2;  // one wave's merge slot: O of one query tile + (m, l)
   const int my_qt = wave % QT, phase = wave / QT;
+  // a first mask segment (desc->seg_rows rows, a whole number of query tiles)
+  // sees only the keys before its end
+  const int seg = desc ? desc->seg_rows : 0;
+  const int nk_mine = seg > 0 && my_qt * 32 < seg * G ? desc->row0 + seg : n_keys;
   float m_run[1] = {-INFINITY}, l_run[1] = {0.f};
   f32x16 o[1][4];
 #pragma unroll
@@ -755,8 +763,8 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
                        : "v"((uint32_t)(uintptr_t)&freed[t % DECR_SLOTS]), "v"(1)
                        : "memory");
       }
-      const int key0[1] = {(t_begin + t) * 32}, nk[1] = {n_keys};
-      attend_group<T, 1, 1>(kc, vc, my_q, key0, nk, c, lane, m_run, l_run, o);
+      const int key0[1] = {(t_begin + t) * 32}, nk[1] = {nk_mine};
+      attend_group<T, 1, 1, QLO>(kc, vc, my_q, key0, nk, c, lane, m_run, l_run, o);
     }
     l_run[0] += __shfl_xor(l_run[0], 32, 64);
   }
@@ -1094,6 +1102,13 @@ template __global__ void attn_decode_kernel<_Float16, 2>(const _Float16*, const 
 template __global__ void attn_decode_kernel<__bf16, 1>(const __bf16*, const __bf16*, int64_t, int,
                                                         int, int, int, const StepDesc*, float*,
                                                         float*, float, int*);
+template __global__ void attn_decode_kernel<_Float16, 4>(const _Float16*, const _Float16*,
+                                                       int64_t, int, int, int, int,
+                                                       const StepDesc*, float*, float*, float,
+                                                       int*);
+template __global__ void attn_decode_kernel<__bf16, 4>(const __bf16*, const __bf16*, int64_t, int,
+                                                     int, int, int, const StepDesc*, float*,
+                                                     float*, float, int*);
 template __global__ void attn_decode_kernel<__bf16, 2>(const __bf16*, const __bf16*, int64_t, int,
                                                         int, int, int, const StepDesc*, float*,
                                                         float*, float, int*);
@@ -1163,7 +1178,7 @@ void attention(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_s
 }
 
 size_t attention_decode_part_bytes(int ranges, int Hkv, int n_qv) {
-  const int qt = (n_qv + 31) / 32;
+  const int qt = n_qv <= 64 ? (n_qv + 31) / 32 : 4;
   return (size_t)ranges * Hkv * ((size_t)qt * 4096 + (size_t)qt * 32 * 2) * 4;
 }
 
@@ -1176,15 +1191,17 @@ int attention_decode_ranges(int n_keys, int Hkv) {
   return std::max(1, std::min(std::min(per_cu, 128), (tiles + 3) / 4));
 }
 
-// Decode attention (one mask segment, <= 64 query vectors per KV head) + combine.
+// Decode attention (one mask segment, or two whose split desc->seg_rows falls on
+// a query-tile boundary; <= 128 query vectors per KV head) + combine.
 // `part` holds attention_decode_part_bytes(ranges, Hkv, n_rows * Hq / Hkv).
 void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_stride,
                       int n_rows, int Hq, int Hkv, int n_keys, const StepDesc* desc, int ranges,
                       float* part, void* out, float* xsum, int out_fmt, hipStream_t s, int* err) {
   const int G = Hq / Hkv;
-  require(Hq % Hkv == 0 && n_rows * G <= 64, "decode attention needs <= 64 query vectors per head");
+  require(Hq % Hkv == 0 && n_rows * G <= 128,
+          "decode attention needs <= 128 query vectors per head");
   require(ranges >= 1 && ranges <= 128, "decode attention takes 1..128 key ranges");
-  const int qt = (n_rows * G + 31) / 32;
+  const int qt = n_rows * G <= 64 ? (n_rows * G + 31) / 32 : 4;
   const float scale = 1.0f / sqrtf(128.0f);
   const size_t lds = std::max((size_t)(DEC_QLO + qt * 32 * DEC_QROW) * 2,
                               (size_t)4 * (qt * 4096 + qt * 128) * 4);
@@ -1210,14 +1227,17 @@ void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv
                (const T*)kv_layer, kv_head_stride, n_rows, Hq, Hkv, n_keys, desc, o_part,   \
                ml_part, scale, err);                                                        \
   }
+  // (the per-wave register form serves up to 64 query vectors)
   static const bool reg_tiles = getenv("DRT_ATTN_NO_DMA") != nullptr;
-  const size_t ldsr = 128 + (size_t)(DEC_QLO + qt * 32 * DEC_QROW) * 2 +
-                      (size_t)(qt == 1 ? decr_slots<1>() : decr_slots<2>()) * 16384;
-  if (!reg_tiles) {
+  const size_t ldsr =
+      qt == 4 ? 128 + (size_t)(dec_qlo<4>() + 4 * 32 * DEC_QROW) * 2 + (size_t)decr_slots<4>() * 16384
+              : 128 + (size_t)(DEC_QLO + qt * 32 * DEC_QROW) * 2 +
+                    (size_t)(qt == 1 ? decr_slots<1>() : decr_slots<2>()) * 16384;
+  if (!reg_tiles || qt == 4) {
     if (bf16) {
-      if (qt == 1) DRT_DECR(__bf16, 1) else DRT_DECR(__bf16, 2)
+      if (qt == 1) DRT_DECR(__bf16, 1) else if (qt == 2) DRT_DECR(__bf16, 2) else DRT_DECR(__bf16, 4)
     } else {
-      if (qt == 1) DRT_DECR(_Float16, 1) else DRT_DECR(_Float16, 2)
+      if (qt == 1) DRT_DECR(_Float16, 1) else if (qt == 2) DRT_DECR(_Float16, 2) else DRT_DECR(_Float16, 4)
     }
   } else if (bf16) {
     if (qt == 1) DRT_DEC(__bf16, 1) else DRT_DEC(__bf16, 2)
@@ -1233,8 +1253,11 @@ void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv
   if (qt == 1)
     hipLaunchKernelGGL(attn_decode_combine_kernel<1>, cgrid, dim3(256), clds, s, o_part, ml_part,
                        ranges, n_rows, Hq, Hkv, out, out_fmt, err);
-  else
+  else if (qt == 2)
     hipLaunchKernelGGL(attn_decode_combine_kernel<2>, cgrid, dim3(256), clds, s, o_part, ml_part,
+                       ranges, n_rows, Hq, Hkv, out, out_fmt, err);
+  else
+    hipLaunchKernelGGL(attn_decode_combine_kernel<4>, cgrid, dim3(256), clds, s, o_part, ml_part,
                        ranges, n_rows, Hq, Hkv, out, out_fmt, err);
   DRT_HIP(hipGetLastError());
 }

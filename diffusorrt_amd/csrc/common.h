@@ -120,4 +120,7 @@ struct StepDesc {
   uint64_t seed;
   float temperature;
   int32_t exclude_col;      // vocabulary column left out of the scoring (-1: none)
+  // rows [row0, row0 + seg_rows) form a first mask segment that sees only keys
+  // [0, row0 + seg_rows); the rest see [0, n_keys) (0: one segment)
+  int32_t seg_rows;
 };

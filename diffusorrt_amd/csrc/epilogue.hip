@@ -39,16 +39,18 @@ DRT_DEV float block_sum_256(float v, float* red) {
 // tokens[M] -> hidden fp32 [M][d] (bf16 embedding rows cast to fp32,
 // backends/mlx_forward.py:1538-1557).
 // Also writes, when ss_out is set, the rows' partial sums of squares per 32
-// columns (ss_out[c*32 + m], c = column / 32) for the next RMSNorm; grid rows
-// M .. 31 (when launched) write zero partials.
+// columns for the next RMSNorm, one [d/32][32] block per 32-row tile
+// (ss_out[(m / 32) * d + c * 32 + m % 32], c = column / 32); grid rows M .. up to
+// the end of the last tile (when launched) write zero partials.
 extern "C" __global__ void embed_kernel(const int32_t* __restrict__ tokens,
                                         const uint16_t* __restrict__ table,
                                         float* __restrict__ hidden, int M, int d,
                                         float* __restrict__ ss_out) {
   const int m = blockIdx.x;
+  float* ss_row = ss_out ? ss_out + (int64_t)(m >> 5) * d + (m & 31) : nullptr;
   if (m >= M) {
     if (ss_out)
-      for (int c = threadIdx.x; c < d / 32; c += blockDim.x) ss_out[c * 32 + m] = 0.f;
+      for (int c = threadIdx.x; c < d / 32; c += blockDim.x) ss_row[c * 32] = 0.f;
     return;
   }
   const int64_t tok = tokens[m];
@@ -61,7 +63,7 @@ extern "C" __global__ void embed_kernel(const int32_t* __restrict__ tokens,
         const float v = bf16_bits_to_float(table[tok * d + c * 32 + k]);
         q += v * v;
       }
-      ss_out[c * 32 + m] = q;
+      ss_row[c * 32] = q;
     }
   }
 }
@@ -242,8 +244,8 @@ namespace drt {
 
 void embed(const int32_t* tokens, const uint16_t* table, float* hidden, int M, int d,
            float* ss_out, hipStream_t s) {
-  // with ss_out, rows up to 32 are launched so unused rows get zero partials
-  const int grid = ss_out ? std::max(M, 32) : M;
+  // with ss_out, whole 32-row tiles are launched so unused rows get zero partials
+  const int grid = ss_out ? (M + 31) / 32 * 32 : M;
   hipLaunchKernelGGL(embed_kernel, dim3(grid), dim3(256), 0, s, tokens, table, hidden, M, d,
                      ss_out);
   DRT_HIP(hipGetLastError());

@@ -49,16 +49,26 @@ struct FusedArgs {
   int64_t kv_head_stride = 0;
   int Hq = 0, Hkv = 0, kv_bf16 = 0;
   const StepDesc* desc = nullptr;  // row0: absolute position of row 0
-  // Skinny (M <= 32, q4) path: split-K partial tiles, arrival counters (zero on
-  // entry, left zero on exit) and the RMSNorm row statistics carried between
-  // kernels as per-32-column partial sums of squares ([K/32][32] floats).
+  // Skinny (M <= 32 per row tile, q4) path: split-K partial tiles, arrival
+  // counters (zero on entry, left zero on exit) and the RMSNorm row statistics
+  // carried between kernels as per-32-column partial sums of squares ([K/32][32]
+  // floats per row tile).
   float* part = nullptr;
   size_t part_floats = 0;
   int* counters = nullptr;
   int n_counters = 0;
   const float* ss_in = nullptr;  // PRO_NORM: partial sums of squares of `hidden` rows
   float* ss_out = nullptr;       // EPI_RESID: partial sums of squares of the new rows
+  // 32-row tiles the skinny workspaces hold (part, counters and the sums of
+  // squares, one block each per tile: part_floats and n_counters per tile, the
+  // sums of squares [K/32][32] at + tile * K): M <= 32 * sk_row_tiles
+  int sk_row_tiles = 1;
 };
+
+// Row tiles of the runtime's split-K workspaces: forwards of up to 64 rows (a
+// block-diffusion step together with the commit of the block before it) run
+// on the split-K linears.
+constexpr int SK_ROW_TILES = 2;
 
 namespace drt {
 void fused_linear(const FusedArgs& a, int kind, hipStream_t s);

@@ -151,18 +151,19 @@ struct Runtime {
   double* scores_host() const { return (double*)out_host; }
   int32_t* tokens_host() const { return (int32_t*)(out_host + (size_t)lm_cap * 8); }
   // Per-forward inputs: one pinned host slot + its device copy per forward, moved
-  // by a single async copy. Slot 0 belongs to the commit graph, slot 1 to the
-  // step graph; eager forwards rotate through the rest.
+  // by a single async copy. Slots 0-2 belong to the session graphs (commit, step,
+  // commit + step); eager forwards rotate through the rest.
   struct StepUpload {
     StepDesc desc;
     int32_t lm_rows[32];
     int32_t lm_pos[32];
-    int32_t tokens[32];
+    int32_t tokens[64];
   };
   static constexpr int UPLOAD_SLOTS = 64;
+  static constexpr int EAGER_SLOT0 = 3;
   StepUpload* up_host = nullptr;
   DevBuf up_dev;
-  int up_next = 2;
+  int up_next = EAGER_SLOT0;
   size_t attn_part_budget = 0;
   int logits_rows_cap = 0;
 
@@ -429,10 +430,11 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
 
     rt->sk_part_floats = pf;
     rt->sk_n_counters = nc;
-    rt->sk_part.alloc(std::max<size_t>(pf, 1) * 4);
-    rt->sk_counters.alloc((size_t)std::max(nc, 1) * 4);
+    // one block per 32-row tile of a <= SK_ROW_TILES * 32-row forward
+    rt->sk_part.alloc(std::max<size_t>(pf, 1) * 4 * SK_ROW_TILES);
+    rt->sk_counters.alloc((size_t)std::max(nc, 1) * 4 * SK_ROW_TILES);
     DRT_HIP(hipMemsetAsync(rt->sk_counters.p, 0, rt->sk_counters.bytes, s));
-    rt->sk_ss.alloc((size_t)d * 4);  // [d/32][32]
+    rt->sk_ss.alloc((size_t)d * 4 * SK_ROW_TILES);  // [tile][d/32][32]
     if (rt->q4 && M > 32) {
       rt->act2.alloc((size_t)2 * M * widest * 2);
       size_t bf = 0;
@@ -498,6 +500,9 @@ struct ForwardArgs {
   uint64_t seed = 0;
   int step = 0;
   int exclude_col = -1;  // vocabulary column left out of the scores (-1: none)
+  // rows [row0, row0 + seg_rows) form a first mask segment that sees only keys
+  // [0, row0 + seg_rows) (a block committed with the next block's step; 0: none)
+  int seg_rows = 0;
 };
 
 // Rows [row0, row0 + n_rows) sit in one mask segment and see every key in
@@ -509,6 +514,26 @@ bool one_segment(const ForwardArgs& a) {
   if (s0 != s1) return false;
   const int seg_end = s0 < 0 ? a.mask_prompt_len : a.mask_prompt_len + (s0 + 1) * a.mask_block;
   return a.n_keys <= seg_end;
+}
+
+// Rows [row0, row0 + seg_rows) and the rest each sit in one mask segment, the
+// first seeing keys up to its own end and the second every key in [0, n_keys),
+// with the split on a query-tile boundary of the decode attention.
+bool two_segments(const ForwardArgs& a, int G) {
+  if (a.seg_rows <= 0 || a.seg_rows >= a.n_rows || (a.seg_rows * G) % 32) return false;
+  ForwardArgs first, second;
+  first.row0 = a.row0;
+  first.n_rows = a.seg_rows;
+  first.n_keys = a.row0 + a.seg_rows;
+  second.row0 = a.row0 + a.seg_rows;
+  second.n_rows = a.n_rows - a.seg_rows;
+  second.n_keys = a.n_keys;
+  for (ForwardArgs* f : {&first, &second}) {
+    f->mask_kind = a.mask_kind;
+    f->mask_prompt_len = a.mask_prompt_len;
+    f->mask_block = a.mask_block;
+  }
+  return one_segment(first) && one_segment(second);
 }
 
 
@@ -531,7 +556,7 @@ ForwardPtrs stage_forward(Runtime& rt, const ForwardArgs& a, int slot, bool grap
   if (slot < 0) {
     if (rt.up_next >= Runtime::UPLOAD_SLOTS) {  // every slot in flight: drain first
       DRT_HIP(hipStreamSynchronize(s));
-      rt.up_next = 2;
+      rt.up_next = Runtime::EAGER_SLOT0;
     }
     slot = rt.up_next++;
   }
@@ -550,6 +575,7 @@ ForwardPtrs stage_forward(Runtime& rt, const ForwardArgs& a, int slot, bool grap
   hd.seed = a.seed;
   hd.temperature = a.temperature;
   hd.exclude_col = a.exclude_col;
+  hd.seg_rows = a.seg_rows;
   ForwardPtrs p;
   p.desc = &d->desc;
   if (a.n_lm <= 32) {
@@ -571,7 +597,7 @@ ForwardPtrs stage_forward(Runtime& rt, const ForwardArgs& a, int slot, bool grap
     p.n_lm_launch = a.n_lm;
   }
   if (graph_mode) {
-    require(a.n_rows <= 32 && tokens_host, "graph forwards take at most 32 rows");
+    require(a.n_rows <= 64 && tokens_host, "graph forwards take at most 64 rows");
     for (int i = 0; i < a.n_rows; ++i) u->tokens[i] = tokens_host[a.row0 + i];
     p.tokens_rel = d->tokens;
   } else {
@@ -599,7 +625,8 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
   auto kv_layer = [&](int l) { return (void*)((char*)kv + (size_t)l * layer_stride * 2); };
   const StepDesc* desc = p.desc;
 
-  const bool decode_attn = M * G <= 64 && one_segment(a);
+  const bool decode_attn = a.seg_rows > 0 ? M * G <= 128 && two_segments(a, G)
+                                           : M * G <= 64 && one_segment(a);
   AttnPlan ap;
   int ranges = 1;
   size_t apb;
@@ -615,13 +642,13 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
   float* o_part = rt.attn_part.as<float>();
   float* ml_part = o_part + (size_t)splits * Hkv * M * G * 128;
 
-  // <= 32-row forwards use the split-K linears, which carry the RMSNorm row
-  // statistics from each residual update to the next norm
-  float* ss = M <= 32 ? rt.sk_ss.as<float>() : nullptr;
-  // > 32-row q4 forwards use the large-M kernels: each linear reads an ACT_F16P
+  // forwards of up to SK_ROW_TILES 32-row tiles use the split-K linears, which
+  // carry the RMSNorm row statistics from each residual update to the next norm
+  float* ss = M <= 32 * SK_ROW_TILES ? rt.sk_ss.as<float>() : nullptr;
+  // longer q4 forwards use the large-M kernels: each linear reads an ACT_F16P
   // activation, the RMSNorms run as their own passes, fused with the split-K
   // reduce and residual add of the projection before them
-  const bool big = rt.q4 && M > 32;
+  const bool big = rt.q4 && M > 32 * SK_ROW_TILES;
   float* bpart = big ? rt.big_part.as<float>() : nullptr;
   embed(p.tokens_rel, rt.embed.as<uint16_t>(), hidden, M, d, ss, s);
   const int L = (int)rt.layers.size();
@@ -657,6 +684,7 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
       f.part_floats = rt.sk_part_floats;
       f.counters = rt.sk_counters.as<int>();
       f.n_counters = rt.sk_n_counters;
+      f.sk_row_tiles = SK_ROW_TILES;
       f.n_xcc = rt.n_xcc;
       f.fenced = rt.fenced ? 1 : 0;
       f.placement_err = rt.placement_err.as<int>();
@@ -810,32 +838,38 @@ struct Session {
   std::vector<int32_t> win_tokens;
   drt_metrics m{};
   Profiler prof;
-  // HIP graphs of the two fixed-shape forwards of a block-diffusion decode: the
-  // commit of one finished block and the denoise step of the active block.
-  hipGraphExec_t g_commit = nullptr, g_step = nullptr;
-  bool g_commit_warm = false, g_step_warm = false;
+  // HIP graphs of the fixed-shape forwards of a block-diffusion decode: the
+  // commit of one finished block, the denoise step of the active block, and the
+  // two together (a block's first step after the block before it finished).
+  enum GraphKind { G_COMMIT = 0, G_STEP = 1, G_PAIR = 2, G_KINDS = 3 };
+  hipGraphExec_t g_exec[G_KINDS] = {nullptr, nullptr, nullptr};
+  bool g_warm[G_KINDS] = {false, false, false};
   int g_ranges = 0;
   bool use_graphs = getenv("DRT_DISABLE_GRAPHS") == nullptr;
+  // DRT_SEPARATE_COMMIT=1 keeps the commit forward of a finished block apart
+  // from the next step (an A/B switch for parity and timing comparisons)
+  bool pair_commit = getenv("DRT_SEPARATE_COMMIT") == nullptr;
 
   void drop_graphs() {
-    if (g_commit) (void)hipGraphExecDestroy(g_commit);
-    if (g_step) (void)hipGraphExecDestroy(g_step);
-    g_commit = g_step = nullptr;
-    g_commit_warm = g_step_warm = false;
+    for (int k = 0; k < G_KINDS; ++k) {
+      if (g_exec[k]) (void)hipGraphExecDestroy(g_exec[k]);
+      g_exec[k] = nullptr;
+      g_warm[k] = false;
+    }
   }
   ~Session() {
     if (rt && rt->stream) (void)hipStreamSynchronize(rt->stream);
     drop_graphs();
   }
 
-  // Run a <= 32-row forward whose inputs live in a fixed upload slot: eager the
+  // Run a <= 64-row forward whose inputs live in a fixed upload slot: eager the
   // first time (grants kernel attributes), captured into a graph the second
   // time, replayed afterwards.
-  void graph_forward(bool commit, const ForwardArgs& a) {
+  void graph_forward(GraphKind kind, const ForwardArgs& a) {
     Runtime& r = *rt;
-    hipGraphExec_t& exec = commit ? g_commit : g_step;
-    bool& warm = commit ? g_commit_warm : g_step_warm;
-    ForwardPtrs p = stage_forward(r, a, commit ? 0 : 1, true, canvas.data());
+    hipGraphExec_t& exec = g_exec[kind];
+    bool& warm = g_warm[kind];
+    ForwardPtrs p = stage_forward(r, a, (int)kind, true, canvas.data());
     p.ranges = g_ranges;
     if (!warm) {
       launch_forward(r, kv.p, head_stride, layer_stride, a, p);
@@ -866,6 +900,16 @@ struct Session {
     const Runtime& r = *rt;
     return use_graphs && !prof.on && rows == block && rows <= 32 &&
            rows * (r.Hq() / r.Hkv()) <= 64;
+  }
+
+  // A block's commit can run with the next block's step as one forward when
+  // both blocks fit the decode attention's 128 query vectors, the split falls
+  // on a query tile, and the rows fit the split-K linears' row tiles.
+  bool pairable() const {
+    const Runtime& r = *rt;
+    const int G = r.Hq() / r.Hkv();
+    return pair_commit && origin == 0 && 2 * block <= std::min(r.max_rows, 32 * SK_ROW_TILES) &&
+           2 * block * G <= 128 && (block * G) % 32 == 0;
   }
 
   void publish_profile() {
@@ -1119,6 +1163,7 @@ static void propose_impl(uint64_t session, const int32_t* frontier, int32_t n_fr
     a.seed = s->seed;
     a.step = s->proposals;
     int forwarded = 0;
+    bool graph = false;  // the forward is a session graph's (D2F block forwards)
     if (s->cfg.attention_mask_kind == DRT_MASK_D2F_HYBRID) {
       require(window_end >= 1 && window_end <= n, "window_end outside the canvas");
       require(frozen_prefix >= 0 && frozen_prefix < window_end, "frozen_prefix outside the window");
@@ -1148,6 +1193,18 @@ static void propose_impl(uint64_t session, const int32_t* frontier, int32_t n_fr
         s->feeder_pos = -1;
       }
       DRT_HIP(hipEventRecord(r.ev0, r.stream));
+      // One block left to commit right before this forward's block: both run as
+      // one forward, the committed block a first mask segment (its rows see keys
+      // up to their block's end, exactly what the commit forward computes).
+      const bool pair = s->pairable() && s->cache_len + s->block == frozen_prefix &&
+                        s->cache_len % s->block == 0 && window_end - frozen_prefix == s->block &&
+                        feeder_i < 0 && n_frontier <= 32;
+      const int row0 = pair ? s->cache_len : frozen_prefix;
+      if (pair) {
+        forwarded += s->block;
+        s->m.commit_rows += s->block;
+        s->cache_len = frozen_prefix;
+      }
       if (s->cache_len < frozen_prefix) {
         const int todo = frozen_prefix - s->cache_len;
         const bool by_block = s->graphable(s->block) && s->origin == 0 &&
@@ -1163,7 +1220,7 @@ static void propose_impl(uint64_t session, const int32_t* frontier, int32_t n_fr
             c.mask_kind = 1;
             c.mask_prompt_len = s->origin;
             c.mask_block = s->block;
-            s->graph_forward(true, c);
+            s->graph_forward(Session::G_COMMIT, c);
             if (b + s->block < frozen_prefix) DRT_HIP(hipStreamSynchronize(r.stream));  // slot reuse
             s->m.commit_rows += s->block;
           }
@@ -1195,20 +1252,23 @@ static void propose_impl(uint64_t session, const int32_t* frontier, int32_t n_fr
         s->upload_tokens(frozen_prefix - 1, frozen_prefix);
         run_forward(r, s->kv.p, s->head_stride, s->layer_stride, f);
         DRT_HIP(hipStreamSynchronize(r.stream));
-        r.up_next = 2;
+        r.up_next = Runtime::EAGER_SLOT0;
         check_placement(r);
         s->feeder_pos = frozen_prefix;
         s->feeder_score = r.scores_host()[0];
         s->feeder_token = r.tokens_host()[0];
         forwarded += 1;
       }
-      a.row0 = frozen_prefix;
-      a.n_rows = window_end - frozen_prefix;
+      a.row0 = row0;
+      a.n_rows = window_end - row0;
       a.n_keys = window_end;
       a.mask_kind = 1;
       a.mask_prompt_len = s->origin;
       a.mask_block = s->block;
-      if (!(s->graphable(a.n_rows) && n_frontier <= 32)) s->upload_tokens(frozen_prefix, window_end);
+      a.seg_rows = pair ? s->block : 0;
+      graph = n_frontier <= 32 && (pair ? s->use_graphs && !s->prof.on
+                                        : s->graphable(a.n_rows));
+      if (!graph) s->upload_tokens(row0, window_end);
     } else {
       // Full bidirectional canvas, no cache (Dream / MDLM fixed_quota).
       for (int i = 0; i < n_frontier; ++i)
@@ -1229,13 +1289,13 @@ static void propose_impl(uint64_t session, const int32_t* frontier, int32_t n_fr
     }
     a.n_lm = (int)a.lm_rows.size();
     if (a.n_lm > 0) {
-      if (a.mask_kind == 1 && s->graphable(a.n_rows) && a.n_lm <= 32)
-        s->graph_forward(false, a);
+      if (graph)
+        s->graph_forward(a.seg_rows > 0 ? Session::G_PAIR : Session::G_STEP, a);
       else
         run_forward(r, s->kv.p, s->head_stride, s->layer_stride, a);
-      forwarded += a.n_rows;
+      forwarded += a.n_rows - a.seg_rows;
     }
-    r.up_next = 2;  // the stream is drained below before any slot is reused
+    r.up_next = Runtime::EAGER_SLOT0;  // the stream is drained below before any slot is reused
     DRT_HIP(hipEventRecord(r.ev1, r.stream));
     // the LM head's last kernel wrote scores, tokens and the placement flags
     // into pinned host memory: nothing to copy once the stream has drained
@@ -1255,7 +1315,7 @@ static void propose_impl(uint64_t session, const int32_t* frontier, int32_t n_fr
     s->publish_profile();
     s->proposals += 1;
     s->m.forward_count += 1;
-    s->m.active_rows += a.n_rows;
+    s->m.active_rows += a.n_rows - a.seg_rows;  // a committed block's rows are commit rows
     s->m.lm_rows += n_frontier;
     s->m.kv_cache_len = s->cache_len;
     if (out_forwarded_rows) *out_forwarded_rows = forwarded;

@@ -1,4 +1,5 @@
-// Split-K linears for decode-sized activations (M <= 32 rows) and q4 weights.
+// Split-K linears for decode-sized activations (M <= 32 rows per row tile, up to
+// sk_row_tiles tiles) and q4 weights.
 //
 // A decode step's linears read only 1-4 MB of weights; what bounds them is how
 // much each CU must pull (about 64 GB/s per CU) and how many dependent memory
@@ -9,6 +10,9 @@
 // writes its partial tile, bumps the block's arrival counter, and the last to
 // arrive adds the partials in slice order (deterministic) and runs the
 // epilogue. Nothing waits on another work-group, so no launch order is assumed.
+// A forward of more than 32 rows runs its 32-row tiles as the grid's y
+// dimension: each tile's work-groups repeat the weight slices (the second read
+// mostly from L2) and keep partials, counters and row statistics of their own.
 //
 // The exchange stays inside one XCD's L2: work-group i runs on XCD i % n_xcc
 // (the dispatcher's round-robin), so the grid is laid out to give every slice
@@ -165,8 +169,14 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
   const uint32_t* sbp = (const uint32_t*)gsb;
   const float* hidden = (const float*)ghid;
   const uint16_t* norm_w = (const uint16_t*)gnw;
-  const float* ss_in = (const float*)gss;
   int* perr = (int*)gerr;
+  // 32-row tile of this work-group: rows m0 .. m0 + M - 1 of the forward
+  const int mt = blockIdx.y, m0 = 32 * mt, M_all = M;
+  M = min(32, M_all - m0);
+  hidden += (int64_t)m0 * K;
+  const float* ss_in = (const float*)gss + (int64_t)mt * K;
+  float* part = a.part + (size_t)mt * a.part_floats;
+  int* counters = a.counters + (size_t)mt * a.n_counters;
   const int G = K >> 6;
   int grp, ks;
   const bool live = sk_place(n_xcc, a.fenced, perr, N / 128, KS, grp, ks);
@@ -291,21 +301,21 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
     // partial tile of this wave in accumulator order: chunk jj*64 + lane holds
     // rows 8jj + 4(lane >> 5) .. +3 of column lane & 31, so each store
     // instruction writes 1 KiB of whole cache lines
-    float* pw = a.part + ((size_t)(grp * KS + ks) * 4 + wave) * 1024 + 4 * lane;
+    float* pw = part + ((size_t)(grp * KS + ks) * 4 + wave) * 1024 + 4 * lane;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj)
       *(f32x4*)(pw + 256 * jj) = f32x4{acc[4 * jj], acc[4 * jj + 1], acc[4 * jj + 2], acc[4 * jj + 3]};
-    if (!last_to_arrive(&a.counters[grp], KS, flag, a.fenced)) return;
-    const float* pbase = a.part + (size_t)grp * KS * 4096;
+    if (!last_to_arrive(&counters[grp], KS, flag, a.fenced)) return;
+    const float* pbase = part + (size_t)grp * KS * 4096;
     auto tables = [&]() {
-      if (EPI == EPI_QKV) qt = qkv_tables(a, grp, row0, M);
+      if (EPI == EPI_QKV) qt = qkv_tables(a, grp, row0 + m0, M);
     };
     if (KS <= 2) sk_wide_sum_slices<2>(pbase, KS, red, tables);
     else if (KS <= 4) sk_wide_sum_slices<4>(pbase, KS, red, tables);
     else sk_wide_sum_slices<SK_KS_MAX>(pbase, KS, red, tables);
-    if (threadIdx.x == 0) reset_counter(&a.counters[grp], a.fenced);
+    if (threadIdx.x == 0) reset_counter(&counters[grp], a.fenced);
   } else {
-    if (EPI == EPI_QKV) qt = qkv_tables(a, grp, row0, M);
+    if (EPI == EPI_QKV) qt = qkv_tables(a, grp, row0 + m0, M);
 #pragma unroll
     for (int r = 0; r < 16; ++r) red[(wave * 32 + mfma_row(r, lane)) * 33 + (lane & 31)] = acc[r];
   }
@@ -326,7 +336,7 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
         const float g = TT(m, 8 * c + e), u = TT(m, 64 + 8 * c + e);
         y[e] = g * (1.f / (1.f + expf(-g))) * u;
       }
-      uint16_t* dst = (uint16_t*)a.act_out + (int64_t)m * F + f0 + 8 * c;
+      uint16_t* dst = (uint16_t*)a.act_out + (int64_t)(m0 + m) * F + f0 + 8 * c;
       u32x4 pk;
       if (a.act_fmt == ACT_F16P) {
         u32x4 pl;
@@ -339,7 +349,7 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
                   ((uint32_t)half_bits(f16_lo(y[e + 4], h1)) << 16);
           over = over || f16_overflows(y[e]) || f16_overflows(y[e + 4]);
         }
-        *(u32x4*)(dst + (int64_t)M * F) = pl;
+        *(u32x4*)(dst + (int64_t)M_all * F) = pl;
         if (over) raise_range(a);
       } else {
 #pragma unroll
@@ -351,8 +361,8 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
     }
   } else if (EPI == EPI_QKV) {
     auto get = [&](int m, int d) { return red[((d >> 5) * 32 + m) * 33 + (d & 31)]; };
-    if (a.kv_bf16) qkv_epilogue<__bf16>(a, qt, grp, 0, row0, M, get, vbuf);
-    else qkv_epilogue<_Float16>(a, qt, grp, 0, row0, M, get, vbuf);
+    if (a.kv_bf16) qkv_epilogue<__bf16>(a, qt, grp, m0, row0 + m0, M, get, vbuf);
+    else qkv_epilogue<_Float16>(a, qt, grp, m0, row0 + m0, M, get, vbuf);
   }
 #undef TT
 }
@@ -374,6 +384,11 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
   const uint32_t* sbp = (const uint32_t*)gsb;
   const uint16_t* act = (const uint16_t*)gact;
   int* perr = (int*)gerr;
+  // 32-row tile of this work-group: rows m0 .. m0 + M - 1 of the forward
+  const int mt = blockIdx.y, m0 = 32 * mt, M_all = M;
+  M = min(32, M_all - m0);
+  float* part = a.part + (size_t)mt * a.part_floats;
+  int* counters = a.counters + (size_t)mt * a.n_counters;
   const int G = K >> 6;
   const int U = G / KS;
   int nt, ks;
@@ -386,7 +401,8 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
   f32x16 acc = f32x16{};
   // this wave's A staging: [2 planes][UW][32 rows][144 B] (128 B of a unit's row + pad)
   char* stg = smem + SK_NARROW_STG + wave * (2 * UW * 32 * 144);
-  const uint16_t* act_lo = act + (int64_t)M * K;  // ACT_F16P lo plane
+  const uint16_t* act_lo = act + (int64_t)M_all * K + (int64_t)m0 * K;  // ACT_F16P lo plane
+  act += (int64_t)m0 * K;
   for (int ub = u_lo; ub < u_hi || ub == u_lo; ub += UW) {
     u32x4 wq[UW], craw[UW][4], crawl[UW][4], af[UW][4], afl[UW][4];
     uint32_t wsb[UW];
@@ -450,23 +466,23 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
   const int n = nt * 32 + c0;
   // the epilogue's input, loaded before the exchange so its latency overlaps it
   f32x4 h_old = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (EPI == EPI_RESID && m < M) h_old = *(const f32x4*)(a.hidden_out + (int64_t)m * N + n);
+  if (EPI == EPI_RESID && m < M) h_old = *(const f32x4*)(a.hidden_out + (int64_t)(m0 + m) * N + n);
   f32x4 v;
 #pragma unroll
   for (int e = 0; e < 4; ++e)
     v[e] = red[m * 33 + c0 + e] + red[(32 + m) * 33 + c0 + e] + red[(64 + m) * 33 + c0 + e] +
            red[(96 + m) * 33 + c0 + e];
   if (KS > 1) {
-    *(f32x4*)(a.part + (size_t)(nt * KS + ks) * 1024 + m * 32 + c0) = v;
-    if (!last_to_arrive(&a.counters[nt], KS, flag, a.fenced)) return;
-    const float* pp = a.part + (size_t)nt * KS * 1024 + m * 32 + c0;
+    *(f32x4*)(part + (size_t)(nt * KS + ks) * 1024 + m * 32 + c0) = v;
+    if (!last_to_arrive(&counters[nt], KS, flag, a.fenced)) return;
+    const float* pp = part + (size_t)nt * KS * 1024 + m * 32 + c0;
     f32x4 pv[SK_KS_MAX];
 #pragma unroll
     for (int k2 = 0; k2 < SK_KS_MAX; ++k2) pv[k2] = *(const f32x4*)(pp + (size_t)min(k2, KS - 1) * 1024);
     v = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int k2 = 0; k2 < SK_KS_MAX; ++k2) v += pv[k2] * (k2 < KS ? 1.f : 0.f);  // unconditional loads
-    if (threadIdx.x == 0) reset_counter(&a.counters[nt], a.fenced);
+    if (threadIdx.x == 0) reset_counter(&counters[nt], a.fenced);
   }
   if (a.bias) {
     const uint2 bb = *(const uint2*)(a.bias + n);
@@ -479,14 +495,14 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
     f32x4 h = f32x4{0.f, 0.f, 0.f, 0.f};
     if (m < M) {
       h = h_old + v;
-      *(f32x4*)(a.hidden_out + (int64_t)m * N + n) = h;
+      *(f32x4*)(a.hidden_out + (int64_t)(m0 + m) * N + n) = h;
     }
     if (a.ss_out) {
       const float q = sum8_dpp(h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3]);
-      if ((threadIdx.x & 7) == 0) a.ss_out[nt * 32 + m] = q;
+      if ((threadIdx.x & 7) == 0) a.ss_out[(int64_t)mt * N + nt * 32 + m] = q;
     }
   } else if (m < M) {
-    *(f32x4*)(a.y + (int64_t)m * N + n) = v;
+    *(f32x4*)(a.y + (int64_t)(m0 + m) * N + n) = v;
   }
 }
 
@@ -564,8 +580,9 @@ bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
   // DRT_DISABLE_SKINNY=1 keeps every linear on the single-pass fused kernels
   // (an A/B switch for parity and timing comparisons)
   static const bool disabled = getenv("DRT_DISABLE_SKINNY") != nullptr;
-  if (disabled || !a.qw || a.M < 1 || a.M > 32 || !a.part || !a.counters || a.K % 64 ||
-      a.N % 32 || a.n_xcc < 1)
+  const int MT = (a.M + 31) / 32;
+  if (disabled || !a.qw || a.M < 1 || MT > a.sk_row_tiles || !a.part || !a.counters ||
+      a.K % 64 || a.N % 32 || a.n_xcc < 1)
     return false;
   const int G = a.K / 64;
   const double bytes = (double)a.N * a.K / 2 + (double)a.N * a.K / 16 + 2.0 * a.M * a.K +
@@ -578,7 +595,7 @@ bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
     if (KS > SK_KS_MAX || (size_t)NG * KS * 4096 > a.part_floats || NG > a.n_counters)
       return false;  // (padding work-groups past the last block exit before any access)
     const size_t lds = SK_WIDE_LDS(U);
-    const dim3 grid((unsigned)((NG + a.n_xcc - 1) / a.n_xcc * a.n_xcc * KS));
+    const dim3 grid((unsigned)((NG + a.n_xcc - 1) / a.n_xcc * a.n_xcc * KS), MT);
 #define DRT_SW(E, UU)                                                             \
   {                                                                               \
     auto fn = skinny_wide_kernel<E, UU>;                                          \
@@ -605,7 +622,7 @@ bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
     if (KS > SK_KS_MAX || (size_t)NT * KS * 1024 > a.part_floats || NT > a.n_counters)
       return false;
     const int per_wave = (G / KS + 3) / 4;
-    const dim3 grid((unsigned)((NT + a.n_xcc - 1) / a.n_xcc * a.n_xcc * KS));
+    const dim3 grid((unsigned)((NT + a.n_xcc - 1) / a.n_xcc * a.n_xcc * KS), MT);
 #define DRT_SN(E, UW)                                                              \
   {                                                                                \
     auto fn = skinny_narrow_kernel<E, UW>;                                         \
