@@ -123,4 +123,8 @@ struct StepDesc {
   // rows [row0, row0 + seg_rows) form a first mask segment that sees only keys
   // [0, row0 + seg_rows); the rest see [0, n_keys) (0: one segment)
   int32_t seg_rows;
+  // the fixed-quota choice made on the device after the LM head: this many of
+  // the n_lm LM rows whose canvas token is still the mask take their proposed
+  // token (highest scores first, equal scores lower row first; 0: none)
+  int32_t quota;
 };

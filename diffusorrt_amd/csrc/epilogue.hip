@@ -42,11 +42,15 @@ DRT_DEV float block_sum_256(float v, float* red) {
 // columns for the next RMSNorm, one [d/32][32] block per 32-row tile
 // (ss_out[(m / 32) * d + c * 32 + m % 32], c = column / 32); grid rows M .. up to
 // the end of the last tile (when launched) write zero partials.
+// With row_desc the token of row m is tokens[row_desc->row0 + m] (a canvas on the
+// device that a graph-replayed forward reads at its step's rows).
 extern "C" __global__ void embed_kernel(const int32_t* __restrict__ tokens,
                                         const uint16_t* __restrict__ table,
                                         float* __restrict__ hidden, int M, int d,
-                                        float* __restrict__ ss_out) {
+                                        float* __restrict__ ss_out,
+                                        const StepDesc* __restrict__ row_desc) {
   const int m = blockIdx.x;
+  if (row_desc) tokens += row_desc->row0;
   float* ss_row = ss_out ? ss_out + (int64_t)(m >> 5) * d + (m & 31) : nullptr;
   if (m >= M) {
     if (ss_out)
@@ -243,11 +247,11 @@ extern "C" __global__ void swiglu_rows_kernel(const float* __restrict__ g,
 namespace drt {
 
 void embed(const int32_t* tokens, const uint16_t* table, float* hidden, int M, int d,
-           float* ss_out, hipStream_t s) {
+           float* ss_out, hipStream_t s, const StepDesc* row_desc) {
   // with ss_out, whole 32-row tiles are launched so unused rows get zero partials
   const int grid = ss_out ? (M + 31) / 32 * 32 : M;
   hipLaunchKernelGGL(embed_kernel, dim3(grid), dim3(256), 0, s, tokens, table, hidden, M, d,
-                     ss_out);
+                     ss_out, row_desc);
   DRT_HIP(hipGetLastError());
 }
 

@@ -199,7 +199,7 @@ void kv_pack(bool kv_bf16, const void* k, const void* v, bool src_bf16, int n, i
 // ss_out (optional, M <= 32): per-32-column partial sums of squares of the rows,
 // [d/32][32], the row statistics of the first decoder layer's RMSNorm.
 void embed(const int32_t* tokens, const uint16_t* table, float* hidden, int M, int d,
-           float* ss_out, hipStream_t s);
+           float* ss_out, hipStream_t s, const StepDesc* row_desc = nullptr);
 void residual_norm(float* hidden, const float* part, int splits, int M_part, bool rnd_bf16,
                    const int32_t* src_rows, bool write_hidden, const uint16_t* norm_w, float eps,
                    int d, int fmt, void* act, float* xsum, int n_out_rows, hipStream_t s,
@@ -209,7 +209,13 @@ size_t lmhead_stats_bytes(int M, int N);
 void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* logits_out,
             void* stats, float temperature, uint64_t seed, int step, const int32_t* positions,
             double* scores, int32_t* tokens, hipStream_t s, const StepDesc* desc = nullptr,
-            int exclude_col = -1, const int* err_dev = nullptr, int* err_host = nullptr);
+            int exclude_col = -1, const int* err_dev = nullptr, int* err_host = nullptr,
+            double* scores_d = nullptr, int32_t* tokens_d = nullptr);
+// The device-side fixed-quota commit of a block step (desc->quota of the
+// desc->n_lm LM rows at `positions`, from the LM head's device scores / tokens)
+// into the device canvas.
+void block_commit(const double* scores_d, const int32_t* tokens_d, const int32_t* positions,
+                  int32_t* canvas, int mask_id, const StepDesc* desc, hipStream_t s);
 
 // y = round_bf16(y) (+ bias after rounding); x fp32 -> bf16 bits.
 void round_bf16_inplace(float* y, int64_t n, const uint16_t* bias, int N, hipStream_t s);

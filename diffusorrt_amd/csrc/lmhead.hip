@@ -243,13 +243,16 @@ __global__ __launch_bounds__(64 * WAVES) void lmhead_kernel(
 
 // One 256-thread WG per row: join the N/64 block statistics in float64. scores
 // and tokens may be pinned host memory (the session's landing area: no copy
-// after the forward); err_host, when given, receives the forward's placement
-// and bounded-wait flags (*err_dev, final once the earlier kernels are done).
+// after the forward); scores_d / tokens_d (optional) get the same values in
+// device memory; err_host, when given, receives the forward's placement and
+// bounded-wait flags (*err_dev, final once the earlier kernels are done).
 extern "C" __global__ void lmhead_finalize_kernel(const LmStat* __restrict__ stats, int NB,
                                                   int sampling_arg,
                                                   const StepDesc* __restrict__ desc,
                                                   double* __restrict__ scores,
                                                   int32_t* __restrict__ tokens,
+                                                  double* __restrict__ scores_d,
+                                                  int32_t* __restrict__ tokens_d,
                                                   const int* __restrict__ err_dev,
                                                   int* __restrict__ err_host) {
   const int sampling = desc ? (desc->temperature > 0.f) : sampling_arg;
@@ -302,19 +305,55 @@ extern "C" __global__ void lmhead_finalize_kernel(const LmStat* __restrict__ sta
   if (threadIdx.x == 0) {
     double tot = 0.0;
     for (int w = 0; w < 4; ++w) tot += red_d[w];
+    double sc;
+    int32_t tk;
     if (!sampling) {
-      scores[row] = 1.0 / tot;
-      tokens[row] = st[mb].arg;
+      sc = 1.0 / tot;
+      tk = st[mb].arg;
     } else {
       double k = red_k[0];
       int j = red_j[0];
       for (int w = 1; w < 4; ++w)
         if (red_k[w] > k || (red_k[w] == k && red_j[w] < j)) { k = red_k[w]; j = red_j[w]; }
       if (j < 0 || j >= NB) j = 0;  // all keys NaN: keep the index in bounds
-      tokens[row] = st[j].sarg;
-      scores[row] = exp((double)st[j].sl - M) / tot;
+      tk = st[j].sarg;
+      sc = exp((double)st[j].sl - M) / tot;
+    }
+    scores[row] = sc;
+    tokens[row] = tk;
+    if (scores_d) {
+      scores_d[row] = sc;
+      tokens_d[row] = tk;
     }
   }
+}
+
+// The fixed-quota choice of one block step on the device
+// (backends/diffusion_runtime.py:290-299, the top-k of the confidences, and
+// :1200-1346, its commit): of the desc->n_lm LM rows (positions[r]) whose canvas
+// token is still the mask, the desc->quota with the highest scores take their
+// proposed token; equal scores go to the lower row (the lower position), as the
+// host loop's stable order does. One wave, n_lm <= 64; rows are distinct
+// positions, and every canvas read happens before any write.
+extern "C" __global__ void block_commit_kernel(const double* __restrict__ scores,
+                                               const int32_t* __restrict__ tokens,
+                                               const int32_t* __restrict__ positions,
+                                               int32_t* __restrict__ canvas, int mask_id,
+                                               const StepDesc* __restrict__ desc) {
+  const int quota = desc->quota, n = min(desc->n_lm, 64);
+  if (quota <= 0) return;
+  const int r = threadIdx.x;
+  const bool row = r < n;
+  const int pos = row ? positions[r] : 0;
+  const bool masked = row && canvas[pos] == mask_id;
+  const double sc = row ? scores[r] : 0.0;
+  int rank = 0;
+  for (int j = 0; j < n; ++j) {
+    const double sj = __shfl(sc, j, 64);
+    const int mj = __shfl((int)masked, j, 64);
+    rank += (mj && (sj > sc || (sj == sc && j < r))) ? 1 : 0;
+  }
+  if (masked && rank < quota) canvas[pos] = tokens[r];
 }
 
 template __global__ void lmhead_kernel<0, 4, 4>(const uint32_t*, const uint32_t*, const uint16_t*,
@@ -333,7 +372,8 @@ size_t lmhead_stats_bytes(int M, int N) { return (size_t)M * (N / 64) * sizeof(L
 void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* logits_out,
             void* stats, float temperature, uint64_t seed, int step, const int32_t* positions,
             double* scores, int32_t* tokens, hipStream_t s, const StepDesc* desc,
-            int exclude_col, const int* err_dev, int* err_host) {
+            int exclude_col, const int* err_dev, int* err_host, double* scores_d,
+            int32_t* tokens_d) {
   require(w.N % 64 == 0, "lm head needs vocab % 64 == 0");
   require(M >= 1, "lm head needs at least one row");
   // k per LDS chunk: q4 stages hi and lo rows, so half the k of bf16 keeps the
@@ -367,9 +407,19 @@ void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* 
   DRT_HIP(hipGetLastError());
   if (scores && tokens) {
     hipLaunchKernelGGL(lmhead_finalize_kernel, dim3(M), dim3(256), 0, s, (const LmStat*)stats, NB,
-                       (int)(temperature > 0.f), desc, scores, tokens, err_dev, err_host);
+                       (int)(temperature > 0.f), desc, scores, tokens, scores_d, tokens_d,
+                       err_dev, err_host);
     DRT_HIP(hipGetLastError());
   }
+}
+
+void block_commit(const double* scores_d, const int32_t* tokens_d, const int32_t* positions,
+                  int32_t* canvas, int mask_id, const StepDesc* desc, hipStream_t s) {
+  require(desc && scores_d && tokens_d && positions && canvas,
+          "block_commit needs the step descriptor, device scores, tokens, positions and canvas");
+  hipLaunchKernelGGL(block_commit_kernel, dim3(1), dim3(64), 0, s, scores_d, tokens_d, positions,
+                     canvas, mask_id, desc);
+  DRT_HIP(hipGetLastError());
 }
 
 }  // namespace drt

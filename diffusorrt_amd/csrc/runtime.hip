@@ -149,6 +149,8 @@ struct Runtime {
   char* out_host = nullptr;
   int lm_cap = 0;
   double* scores_host() const { return (double*)out_host; }
+  // the same scores and tokens in device memory (the device-side block commit)
+  DevBuf lm_scores_d, lm_tokens_d;
   int32_t* tokens_host() const { return (int32_t*)(out_host + (size_t)lm_cap * 8); }
   // Per-forward inputs: one pinned host slot + its device copy per forward, moved
   // by a single async copy. Slots 0-2 belong to the session graphs (commit, step,
@@ -416,6 +418,8 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
   // LM head's last kernel: [lm_cap] doubles, then [lm_cap] ints
   rt->lm_cap = lm_cap;
   DRT_HIP(hipHostMalloc((void**)&rt->out_host, (size_t)lm_cap * 12 + 16, hipHostMallocCoherent));
+  rt->lm_scores_d.alloc((size_t)lm_cap * 8);
+  rt->lm_tokens_d.alloc((size_t)lm_cap * 4);
   rt->lm_rows.alloc((size_t)lm_cap * 4);
   rt->lm_pos.alloc((size_t)lm_cap * 4);
   {
@@ -503,6 +507,7 @@ struct ForwardArgs {
   // rows [row0, row0 + seg_rows) form a first mask segment that sees only keys
   // [0, row0 + seg_rows) (a block committed with the next block's step; 0: none)
   int seg_rows = 0;
+  int quota = 0;  // device-side block commit of this many proposals (0: none)
 };
 
 // Rows [row0, row0 + n_rows) sit in one mask segment and see every key in
@@ -542,16 +547,24 @@ bool two_segments(const ForwardArgs& a, int G) {
 struct ForwardPtrs {
   const StepDesc* desc = nullptr;
   const int32_t* tokens_rel = nullptr;  // tokens of rows 0 .. n_rows-1 of this forward
+  bool tokens_at_row0 = false;          // tokens_rel is the whole canvas: rows from desc->row0
+  int32_t* canvas = nullptr;            // device canvas of the block commit (desc->quota)
+  int mask_id = -1;
   const int32_t* lm_rows = nullptr;
   const int32_t* lm_pos = nullptr;
   int n_lm_launch = 0;  // LM rows launched (graph mode pads to 32)
   int ranges = 0;       // decode-attention ranges (0: from n_keys)
 };
 
-// Upload the forward's descriptor, LM rows and (graph mode) tokens with one
-// async copy from a pinned slot. slot < 0 takes the next eager slot.
+// Upload the forward's descriptor and LM rows with one async copy from a pinned
+// slot. slot < 0 takes the next eager slot. Graph forwards read their tokens from
+// the device canvas at desc->row0; the slot's copy of the canvas rows is copied
+// there first unless upload_tokens is false (the canvas rows were written on the
+// device, by a block commit). dev_slot (>= 0) receives the slot's contents
+// instead of the slot's own device copy (a graph's fixed descriptor).
 ForwardPtrs stage_forward(Runtime& rt, const ForwardArgs& a, int slot, bool graph_mode,
-                          const int32_t* tokens_host) {
+                          const int32_t* tokens_host, bool upload_tokens = true,
+                          int dev_slot = -1) {
   hipStream_t s = rt.stream;
   if (slot < 0) {
     if (rt.up_next >= Runtime::UPLOAD_SLOTS) {  // every slot in flight: drain first
@@ -561,7 +574,7 @@ ForwardPtrs stage_forward(Runtime& rt, const ForwardArgs& a, int slot, bool grap
     slot = rt.up_next++;
   }
   Runtime::StepUpload* u = rt.up_host + slot;
-  Runtime::StepUpload* d = rt.up_dev.as<Runtime::StepUpload>() + slot;
+  Runtime::StepUpload* d = rt.up_dev.as<Runtime::StepUpload>() + (dev_slot >= 0 ? dev_slot : slot);
   StepDesc& hd = u->desc;
   hd = StepDesc{};
   hd.row0 = a.row0;
@@ -576,6 +589,7 @@ ForwardPtrs stage_forward(Runtime& rt, const ForwardArgs& a, int slot, bool grap
   hd.temperature = a.temperature;
   hd.exclude_col = a.exclude_col;
   hd.seg_rows = a.seg_rows;
+  hd.quota = a.quota;
   ForwardPtrs p;
   p.desc = &d->desc;
   if (a.n_lm <= 32) {
@@ -596,14 +610,19 @@ ForwardPtrs stage_forward(Runtime& rt, const ForwardArgs& a, int slot, bool grap
     p.lm_pos = rt.lm_pos.as<int32_t>();
     p.n_lm_launch = a.n_lm;
   }
+  DRT_HIP(hipMemcpyAsync(d, u, sizeof(Runtime::StepUpload), hipMemcpyHostToDevice, s));
   if (graph_mode) {
-    require(a.n_rows <= 64 && tokens_host, "graph forwards take at most 64 rows");
-    for (int i = 0; i < a.n_rows; ++i) u->tokens[i] = tokens_host[a.row0 + i];
-    p.tokens_rel = d->tokens;
+    require(a.n_rows <= 64 && tokens_host && a.tokens_dev, "graph forwards take at most 64 rows");
+    if (upload_tokens) {
+      for (int i = 0; i < a.n_rows; ++i) u->tokens[i] = tokens_host[a.row0 + i];
+      DRT_HIP(hipMemcpyAsync(const_cast<int32_t*>(a.tokens_dev) + a.row0, u->tokens,
+                             (size_t)a.n_rows * 4, hipMemcpyHostToDevice, s));
+    }
+    p.tokens_rel = a.tokens_dev;
+    p.tokens_at_row0 = true;
   } else {
     p.tokens_rel = a.tokens_dev + a.row0;
   }
-  DRT_HIP(hipMemcpyAsync(d, u, sizeof(Runtime::StepUpload), hipMemcpyHostToDevice, s));
   return p;
 }
 
@@ -650,7 +669,8 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
   // reduce and residual add of the projection before them
   const bool big = rt.q4 && M > 32 * SK_ROW_TILES;
   float* bpart = big ? rt.big_part.as<float>() : nullptr;
-  embed(p.tokens_rel, rt.embed.as<uint16_t>(), hidden, M, d, ss, s);
+  embed(p.tokens_rel, rt.embed.as<uint16_t>(), hidden, M, d, ss, s,
+        p.tokens_at_row0 ? desc : nullptr);
   const int L = (int)rt.layers.size();
   if (big && L > 0)
     residual_norm(hidden, nullptr, 0, M, false, nullptr, false,
@@ -770,7 +790,11 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
                   rt.placement_err.as<int>());
     lmhead(rt.lm_head, rt.act_lm.p, rt.xsum_lm.as<float>(), p.n_lm_launch, a.logits, rt.stats.p,
            a.temperature, a.seed, a.step, p.lm_pos, rt.scores_host(), rt.tokens_host(), s, desc,
-           a.exclude_col, rt.placement_err.as<int>(), rt.placement_host);
+           a.exclude_col, rt.placement_err.as<int>(), rt.placement_host,
+           rt.lm_scores_d.as<double>(), rt.lm_tokens_d.as<int32_t>());
+    if (p.canvas && desc)
+      block_commit(rt.lm_scores_d.as<double>(), rt.lm_tokens_d.as<int32_t>(), p.lm_pos, p.canvas,
+                   p.mask_id, desc, s);
   }
 }
 
@@ -864,12 +888,21 @@ struct Session {
 
   // Run a <= 64-row forward whose inputs live in a fixed upload slot: eager the
   // first time (grants kernel attributes), captured into a graph the second
-  // time, replayed afterwards.
-  void graph_forward(GraphKind kind, const ForwardArgs& a) {
+  // time, replayed afterwards. The step forwards end with the device-side block
+  // commit (a no-op unless the descriptor carries a quota). host_slot >= 0: the
+  // inputs are staged in that pinned slot (a block's steps queued without a
+  // synchronisation keep one slot each) and copied to the graph's own.
+  void graph_forward(GraphKind kind, const ForwardArgs& a, int host_slot = -1,
+                     bool upload_tokens = true) {
     Runtime& r = *rt;
     hipGraphExec_t& exec = g_exec[kind];
     bool& warm = g_warm[kind];
-    ForwardPtrs p = stage_forward(r, a, (int)kind, true, canvas.data());
+    ForwardPtrs p = stage_forward(r, a, host_slot >= 0 ? host_slot : (int)kind, true,
+                                  canvas.data(), upload_tokens, host_slot >= 0 ? (int)kind : -1);
+    if (kind != G_COMMIT) {
+      p.canvas = tokens_dev.as<int32_t>();
+      p.mask_id = mask_id;
+    }
     p.ranges = g_ranges;
     if (!warm) {
       launch_forward(r, kv.p, head_stride, layer_stride, a, p);
@@ -894,12 +927,108 @@ struct Session {
     DRT_HIP(hipGraphLaunch(exec, r.stream));
   }
 
+  // Commit forwards for the rows [cache_len, frozen_prefix) (exact prefix K/V):
+  // block by block through the commit graph for up to four aligned blocks, else
+  // in max_forward_rows chunks. Returns the rows committed.
+  int commit_to(int frozen_prefix) {
+    Runtime& r = *rt;
+    if (cache_len >= frozen_prefix) return 0;
+    const int todo = frozen_prefix - cache_len;
+    const bool by_block = graphable(block) && origin == 0 && cache_len % block == 0 &&
+                          todo % block == 0 && todo <= 4 * block;
+    if (by_block) {
+      for (int b = cache_len; b < frozen_prefix; b += block) {
+        ForwardArgs c;
+        c.tokens_dev = tokens_dev.as<int32_t>();
+        c.row0 = b;
+        c.n_rows = block;
+        c.n_keys = b + block;
+        c.mask_kind = 1;
+        c.mask_prompt_len = origin;
+        c.mask_block = block;
+        graph_forward(G_COMMIT, c);
+        if (b + block < frozen_prefix) DRT_HIP(hipStreamSynchronize(r.stream));  // slot reuse
+        m.commit_rows += block;
+      }
+    } else {
+      upload_tokens(cache_len, frozen_prefix);
+      commit_rows(cache_len, frozen_prefix, origin, block);
+    }
+    cache_len = frozen_prefix;
+    return todo;
+  }
+
+  // One block [fp, fp + block) of the native BD3 loop with no host
+  // synchronisation between its steps: the commit of what precedes it (merged
+  // into the first step when pairable), then one graph-replayed step forward per
+  // quota, each ending in the device-side choice and commit of its quota into the
+  // device canvas; the stream is drained once, at the end, and the block's
+  // tokens are read back into the host canvas. Every LM row of the block is
+  // scored (graph forwards score 32 rows either way); the rows already committed
+  // are left out of the choice. Returns the forwards run.
+  int run_block(int fp, const std::vector<int>& quotas) {
+    Runtime& r = *rt;
+    const int hi = fp + block, S = (int)quotas.size();
+    require(S >= 1 && Runtime::EAGER_SLOT0 + S <= Runtime::UPLOAD_SLOTS,
+            "a device block takes 1..61 steps");
+    DRT_HIP(hipEventRecord(r.ev0, r.stream));
+    const bool pair = pairable() && cache_len + block == fp && cache_len % block == 0;
+    if (!pair) commit_to(fp);
+    const int row_first = pair ? fp - block : fp;
+    upload_tokens(row_first, hi);  // the device canvas is the forwards' from here on
+    for (int j = 0; j < S; ++j) {
+      ForwardArgs a;
+      a.tokens_dev = tokens_dev.as<int32_t>();
+      a.temperature = (float)temperature;
+      a.seed = seed;
+      a.step = proposals + j;
+      a.row0 = j == 0 ? row_first : fp;
+      a.n_rows = hi - a.row0;
+      a.n_keys = hi;
+      a.mask_kind = 1;
+      a.mask_prompt_len = origin;
+      a.mask_block = block;
+      a.seg_rows = a.row0 < fp ? block : 0;
+      a.quota = quotas[j];
+      for (int p = fp; p < hi; ++p) {
+        a.lm_rows.push_back(p - a.row0);
+        a.lm_pos.push_back(p);
+      }
+      a.n_lm = block;
+      graph_forward(a.seg_rows > 0 ? G_PAIR : G_STEP, a, Runtime::EAGER_SLOT0 + j, false);
+    }
+    if (pair) {
+      m.commit_rows += block;
+      cache_len = fp;
+    }
+    DRT_HIP(hipEventRecord(r.ev1, r.stream));
+    DRT_HIP(hipMemcpyAsync(canvas.data() + fp, tokens_dev.as<int32_t>() + fp, (size_t)block * 4,
+                           hipMemcpyDeviceToHost, r.stream));
+    DRT_HIP(hipStreamSynchronize(r.stream));
+    r.up_next = Runtime::EAGER_SLOT0;
+    check_placement(r);
+    finish_timing();
+    proposals += S;
+    m.forward_count += S;
+    m.active_rows += (int64_t)S * block;
+    m.lm_rows += (int64_t)S * block;
+    m.kv_cache_len = cache_len;
+    return S;
+  }
+
   // Graph forwards apply to block-sized rows of a session whose decode
   // attention covers the whole block (block rows x GQA group <= 64 vectors).
   bool graphable(int rows) const {
     const Runtime& r = *rt;
     return use_graphs && !prof.on && rows == block && rows <= 32 &&
            rows * (r.Hq() / r.Hkv()) <= 64;
+  }
+
+  // The native loop runs whole blocks on the device (graph forwards, no
+  // profiling; DRT_HOST_TOPK=1 keeps the per-step host choice).
+  bool block_on_device() const {
+    static const bool host_topk = getenv("DRT_HOST_TOPK") != nullptr;
+    return !host_topk && graphable(block) && origin == 0;
   }
 
   // A block's commit can run with the next block's step as one forward when
@@ -1114,7 +1243,9 @@ int32_t drt_session_start(uint64_t session, const int32_t* tokens, int32_t n_tok
       require(tokens[i] >= 0 && tokens[i] < r.V(), "token id outside the vocabulary");
     DRT_HIP(hipSetDevice(r.device));
     s->canvas.assign(tokens, tokens + n_tokens);
+    const void* canvas_was = s->tokens_dev.p;
     s->tokens_dev.ensure((size_t)n_tokens * 4);
+    if (s->tokens_dev.p != canvas_was) s->drop_graphs();  // captured forwards read the canvas
     s->ensure_cache(n_tokens);
     s->cache_len = 0;  // a new request: nothing in the cache belongs to it yet
     s->feeder_pos = -1;
@@ -1205,32 +1336,7 @@ static void propose_impl(uint64_t session, const int32_t* frontier, int32_t n_fr
         s->m.commit_rows += s->block;
         s->cache_len = frozen_prefix;
       }
-      if (s->cache_len < frozen_prefix) {
-        const int todo = frozen_prefix - s->cache_len;
-        const bool by_block = s->graphable(s->block) && s->origin == 0 &&
-                              s->cache_len % s->block == 0 && todo % s->block == 0 &&
-                              todo <= 4 * s->block;
-        if (by_block) {
-          for (int b = s->cache_len; b < frozen_prefix; b += s->block) {
-            ForwardArgs c;
-            c.tokens_dev = s->tokens_dev.as<int32_t>();
-            c.row0 = b;
-            c.n_rows = s->block;
-            c.n_keys = b + s->block;
-            c.mask_kind = 1;
-            c.mask_prompt_len = s->origin;
-            c.mask_block = s->block;
-            s->graph_forward(Session::G_COMMIT, c);
-            if (b + s->block < frozen_prefix) DRT_HIP(hipStreamSynchronize(r.stream));  // slot reuse
-            s->m.commit_rows += s->block;
-          }
-        } else {
-          s->upload_tokens(s->cache_len, frozen_prefix);
-          s->commit_rows(s->cache_len, frozen_prefix, s->origin, s->block);
-        }
-        forwarded += todo;
-        s->cache_len = frozen_prefix;
-      }
+      forwarded += s->commit_to(frozen_prefix);
       if (s->cfg.decode_strategy == DRT_DECODE_BLOCK_THRESHOLD) a.exclude_col = s->mask_id;
       if (feeder_i >= 0 && s->feeder_pos != frozen_prefix) {
         // the frozen row's score and token: one row over its own (cached) context
@@ -1393,6 +1499,24 @@ int32_t drt_session_bd3_decode(uint64_t session, int32_t prompt_len, int32_t max
         L.active = block_id;
         L.base = (int)frontier.size() / L.spb;
         L.rem = (int)frontier.size() % L.spb;
+      }
+      // A whole aligned block at its first step: its forwards run back to back,
+      // each step's choice made on the device (the steps with a quota; a step
+      // without one forwards nothing, as below).
+      if (step % L.spb == 0 && lo == grid && hi == grid + B && !frontier.empty() &&
+          s->block_on_device()) {
+        std::vector<int> quotas;
+        for (int j = 0; j < L.spb; ++j) {
+          const int q = L.base + (j < L.rem ? 1 : 0);
+          if (q > 0) quotas.push_back(q);
+        }
+        if ((int)quotas.size() <= max_forwards - forwards &&
+            (int)quotas.size() <= Runtime::UPLOAD_SLOTS - Runtime::EAGER_SLOT0) {
+          forwards += s->run_block(grid, quotas);
+          for (int q : quotas) committed += q;
+          L.step = step + L.spb;
+          continue;
+        }
       }
       const int quota = L.base + (step % L.spb < L.rem ? 1 : 0);
       L.step = step + 1;
