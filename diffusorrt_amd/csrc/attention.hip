@@ -48,6 +48,22 @@ DRT_DEV int eff_block(int p, int prompt_len, int block) {
 
 constexpr int KV_TILE_ELEMS = 8192;  // K block + V block per 32-key tile
 
+// Softmax bookkeeping of both attention kernels runs in base 2 on scaled scores:
+// u = s * scale * log2(e), p = 2^(u - base). The base of a query vector is only
+// raised when a tile's max exceeds it by more than DEC_RESCALE_LOG2 (or on its
+// first visible keys), so p <= 2^DEC_RESCALE_LOG2 (exact in the MFMA operand
+// types' range) and the rescale of O, which moves the accumulators through
+// VGPRs, is rare instead of once per tile. Any base gives the same o / l.
+constexpr float DEC_RESCALE_LOG2 = 8.f;
+
+// max(v[l], v[l ^ 32]) on every lane (gfx950 v_permlane32_swap, no LDS trip).
+DRT_DEV float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+
 template <typename T, int QW>
 __global__ __launch_bounds__(64 * QW) void attn_split_kernel(
     const T* __restrict__ q,       // [n_rows][Hq][128]
@@ -94,7 +110,15 @@ __global__ __launch_bounds__(64 * QW) void attn_split_kernel(
     }
   }
   const int qpos = row_pos0 + qrow;
-  const int q_eff = mask_kind == 1 ? eff_block(qpos, mask_prompt_len, mask_block) : 0;
+  const float c = scale * 1.44269504088896340736f;  // scores to base-2 exponents
+  // d2f_hybrid: a query sees exactly the keys before the end of its own block
+  // (the whole prompt, then whole blocks up to its own), so visibility is one
+  // compare per key against q_key_end
+  int q_key_end = n_keys;
+  if (mask_kind == 1) {
+    const int e = eff_block(qpos, mask_prompt_len, mask_block);
+    q_key_end = min(n_keys, e < 0 ? mask_prompt_len : mask_prompt_len + (e + 1) * mask_block);
+  }
   // Wave-uniform visibility bound: no key beyond the last visible key of the
   // wave's rows needs loading into this wave's math.
   int wave_key_end = n_keys;
@@ -155,27 +179,29 @@ __global__ __launch_bounds__(64 * QW) void attn_split_kernel(
       float tmax = -INFINITY;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int key = key0 + mfma_row(r, lane);
-        bool vis = key < n_keys;
-        if (mask_kind == 1) vis = vis && eff_block(key, mask_prompt_len, mask_block) <= q_eff;
-        s[r] = vis ? s[r] * scale : -INFINITY;
+        s[r] = key0 + mfma_row(r, lane) < q_key_end ? s[r] * c : -INFINITY;
         tmax = fmaxf(tmax, s[r]);
       }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const float m_new = fmaxf(m_run, tmax);
-      const float base = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __expf(m_run - base);
+      tmax = max_xor32(tmax);  // -inf: no visible key in the tile
+      const bool up = tmax > m_run + DEC_RESCALE_LOG2;
+      if (__ballot(up)) {  // some base has to rise (rare after the first tiles)
+        const float alpha = up ? __builtin_amdgcn_exp2f(m_run - tmax) : 1.f;  // 0 from -inf
+        if (__ballot(up && m_run != -INFINITY)) {
+#pragma unroll
+          for (int hb = 0; hb < 4; ++hb) o[hb] *= alpha;
+        }
+        l_run *= alpha;
+        m_run = up ? tmax : m_run;
+      }
+      const float base = m_run == -INFINITY ? 0.f : m_run;  // no key yet: p = 0
       float psum = 0.f;
       float p[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        p[r] = __expf(s[r] - base);
+        p[r] = __builtin_amdgcn_exp2f(s[r] - base);
         psum += p[r];
       }
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
-#pragma unroll
-      for (int hb = 0; hb < 4; ++hb) o[hb] *= alpha;
+      l_run += psum;
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh) {
         vec pf;
@@ -262,21 +288,6 @@ DRT_DEV void load_tile_nt(const T* __restrict__ base, int t, int lane, bool real
     k[i] = __builtin_nontemporal_load(tp + i * step + l);
     v[i] = __builtin_nontemporal_load(tp + (real ? 512 : 0) + i * step + l);
   }
-}
-
-// Softmax bookkeeping of the decode attention runs in base 2 on scaled scores:
-// u = s * scale * log2(e), p = 2^(u - base). The base of a query vector is only
-// raised when a tile's max exceeds it by more than DEC_RESCALE_LOG2 (or on its
-// first visible keys), so p <= 2^DEC_RESCALE_LOG2 (exact in the MFMA operand
-// types' range) and the rescale of O, which moves the accumulators through
-// VGPRs, is rare instead of once per tile. Any base gives the same o / l.
-constexpr float DEC_RESCALE_LOG2 = 8.f;
-
-// max(v[l], v[l ^ 32]) on every lane (gfx950 v_permlane32_swap, no LDS trip).
-DRT_DEV float max_xor32(float v) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
-                                                  false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // NG 32-key tiles for all query tiles at once: S^T = K Q^T for every (tile,
@@ -957,7 +968,8 @@ __global__ __launch_bounds__(256) void attn_decode_combine_kernel(
   }
 }
 
-// Combine key splits. One wave per (row, head); lane holds hd = lane, lane + 64.
+// Combine key splits (statistics in the base-2 units of attn_split_kernel).
+// One wave per (row, head); lane holds hd = lane, lane + 64.
 // The split statistics are loaded across lanes (split s by lane s), the weights
 // broadcast by shuffles, and every partial-O load is independent, so the
 // combine costs one memory latency, not one per split. n_splits <= 64.
@@ -982,7 +994,7 @@ extern "C" __global__ void attn_combine_kernel(const float* __restrict__ o_part,
     ls = ml_part[(idx0 + lane * stride) * 2 + 1];
   }
   const float mmax = wave_max(ms);
-  const float w = (ms == -INFINITY) ? 0.f : __expf(ms - mmax);
+  const float w = (ms == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms - mmax);
   const float lsum = wave_sum(w * ls);
   float a0 = 0.f, a1 = 0.f;
   for (int s0 = 0; s0 < n_splits; s0 += 16) {
