@@ -144,27 +144,22 @@ __global__ __launch_bounds__(64 * QW) void attn_split_kernel(
   const T* kvh_base = kv + (int64_t)kvh * kv_head_stride;
   constexpr int VEC_PER_TILE = KV_TILE_ELEMS / 8;  // 16-byte vectors per tile
   constexpr int PER_THREAD = VEC_PER_TILE / (64 * QW);
-  u32x4 stage[PER_THREAD];
-  auto load_tile = [&](int t) {
+  // K/V tiles go global -> registers -> LDS (double buffered), loaded two tiles
+  // ahead through two register stages (tile t + 2 is in flight while tile t is
+  // computed and tile t + 1 is stored), so a tile's memory latency overlaps two
+  // iterations' work instead of one.
+  u32x4 stage_a[PER_THREAD], stage_b[PER_THREAD];
+  auto load_tile = [&](u32x4 (&st)[PER_THREAD], int t) {
     const u32x4* src = (const u32x4*)(kvh_base + (int64_t)t * KV_TILE_ELEMS);
 #pragma unroll
-    for (int i = 0; i < PER_THREAD; ++i) stage[i] = src[threadIdx.x + i * 64 * QW];
+    for (int i = 0; i < PER_THREAD; ++i) st[i] = src[threadIdx.x + i * 64 * QW];
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](const u32x4 (&st)[PER_THREAD], int buf) {
     u32x4* dst = (u32x4*)(lds + buf * KV_TILE_ELEMS);
 #pragma unroll
-    for (int i = 0; i < PER_THREAD; ++i) dst[threadIdx.x + i * 64 * QW] = stage[i];
+    for (int i = 0; i < PER_THREAD; ++i) dst[threadIdx.x + i * 64 * QW] = st[i];
   };
-
-  if (t_begin < t_stop) {
-    load_tile(t_begin);
-    store_tile(0);
-  }
-  __syncthreads();
-  for (int t = t_begin; t < t_stop; ++t) {
-    const int buf = (t - t_begin) & 1;
-    const bool more = t + 1 < t_stop;
-    if (more) load_tile(t + 1);
+  auto compute = [&](int t, int buf) {
     const int key0 = t * 32;
     if (key0 < wave_key_end) {
       const T* kt = lds + buf * KV_TILE_ELEMS;
@@ -214,11 +209,28 @@ __global__ __launch_bounds__(64 * QW) void attn_split_kernel(
         }
       }
     }
-    if (more) {
-      // The other buffer was last read before the previous iteration's barrier.
-      store_tile(buf ^ 1);
-      __syncthreads();
-    }
+  };
+
+  if (t_begin < t_stop) {
+    load_tile(stage_a, t_begin);
+    store_tile(stage_a, 0);
+  }
+  if (t_begin + 1 < t_stop) load_tile(stage_b, t_begin + 1);
+  __syncthreads();
+  // two tiles per pass: buffer 0 / stage_a for tiles t_begin + 2k, buffer 1 /
+  // stage_b for tiles t_begin + 2k + 1. A buffer is rewritten only after the
+  // barrier that follows its last read.
+  for (int t = t_begin; t < t_stop; t += 2) {
+    if (t + 2 < t_stop) load_tile(stage_a, t + 2);
+    compute(t, 0);
+    if (t + 1 >= t_stop) break;
+    store_tile(stage_b, 1);
+    __syncthreads();
+    if (t + 3 < t_stop) load_tile(stage_b, t + 3);
+    compute(t + 1, 1);
+    if (t + 2 >= t_stop) break;
+    store_tile(stage_a, 0);
+    __syncthreads();
   }
   l_run += __shfl_xor(l_run, 32, 64);
 
