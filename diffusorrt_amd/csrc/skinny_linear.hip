@@ -631,11 +631,14 @@ bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
     DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(256), SK_NARROW_LDS(UW), s, a, KS); \
   }
     // (more than two units per wave: loops of two, the hi and lo fragments of
-    // a larger batch would not fit the registers)
+    // a larger batch would not fit the registers). Two row tiles double the
+    // work-groups: one unit at a time keeps two of them per CU (the LDS of
+    // two-unit staging holds one), so they run in one round instead of two.
+    const bool one_unit = per_wave <= 1 || MT > 1;
     if (kind == FL_RESID) {
-      if (per_wave <= 1) DRT_SN(EPI_RESID, 1) else DRT_SN(EPI_RESID, 2)
+      if (one_unit) DRT_SN(EPI_RESID, 1) else DRT_SN(EPI_RESID, 2)
     } else {
-      if (per_wave <= 1) DRT_SN(EPI_STORE, 1) else DRT_SN(EPI_STORE, 2)
+      if (one_unit) DRT_SN(EPI_STORE, 1) else DRT_SN(EPI_STORE, 2)
     }
 #undef DRT_SN
   } else {
