@@ -74,8 +74,15 @@ class StepPlan:
 
 def topk_count_choices(scores, transfer_count: int) -> list:
     """Top ``transfer_count`` rows by descending score: ``argsort(-score)[:k]``
-    (``diffusion_runtime.py:290-299``)."""
-    chosen = np.argsort(-np.asarray(scores, dtype=np.float64))[:transfer_count]
+    (``diffusion_runtime.py:290-299``).
+
+    Rows with exactly equal scores go lowest index first (a stable sort). The
+    reference's default-quicksort ``np.argsort`` leaves their order to the sort
+    implementation (an introsort, handed to SIMD sorts by numpy 2.x where the
+    CPU has them), so no single order matches it everywhere; this one is what
+    the native loop and the device-side choice use too, so every loop of this
+    build commits the same rows."""
+    chosen = np.argsort(-np.asarray(scores, dtype=np.float64), kind="stable")[:transfer_count]
     return [int(i) for i in chosen]
 
 

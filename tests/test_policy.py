@@ -214,6 +214,23 @@ def test_topk_matches_oracle_and_numpy_quicksort():
         assert D.topk_count_choices(s, k) == O.topk_count_choices(s, k)
 
 
+def test_topk_exact_ties_lowest_index_first():
+    """Exactly equal scores go lowest index first (the native loop and the
+    device-side choice take the same order), and a tie never outranks a higher
+    score; the choices always form a valid top-k of the scores."""
+    assert D.topk_count_choices([0.5, 0.7, 0.5, 0.7, 0.5], 3) == [1, 3, 0]
+    assert D.topk_count_choices([0.25] * 32, 4) == [0, 1, 2, 3]
+    rng = np.random.default_rng(4)
+    for _ in range(200):
+        s = rng.integers(0, 4, int(rng.integers(1, 40))) / 4.0  # many exact ties
+        k = int(rng.integers(0, len(s) + 1))
+        got = D.topk_count_choices(s, k)
+        ref = sorted(range(len(s)), key=lambda i: (-s[i], i))[:k]
+        assert got == ref
+        # the same multiset of scores as numpy's (any) quicksort order takes
+        assert sorted(s[got]) == sorted(s[O.topk_count_choices(s, k)])
+
+
 def test_threshold_choices_closed_forms():
     for pick in (D.threshold_choices, P.threshold_pick):
         assert pick([0.95, 0.5, 0.91], 0.9) == [0, 2]
