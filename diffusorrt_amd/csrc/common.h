@@ -99,6 +99,41 @@ DRT_DEV uint32_t q4_pair_to_f16(uint32_t w) {
   return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, w | 0x64006400u) + k);
 }
 
+// The constants of q4_word_to_f16x8 held in registers (VOP3 forms take no
+// literal operand on gfx9, so literals would cost a separate and + or each).
+struct Q4Consts {
+  uint32_t magic, n1024, sixteenth, n64;
+};
+DRT_DEV Q4Consts q4_consts() {
+  uint32_t m = 0x64006400u, a = 0xE400E400u, s = 0x2C002C00u, b = 0xD400D400u;
+  asm volatile("" : "+v"(m), "+s"(a), "+s"(s), "+v"(b));
+  return Q4Consts{m, a, s, b};
+}
+
+// One q4 weight word (nibbles n0..n7, n0 lowest) as the fp16 B fragment
+// (n0, n4, n1, n5, n2, n6, n3, n7), the element order of four q4_pair_to_f16
+// calls on w, w >> 4, w >> 8, w >> 12, in 9 instructions instead of 15: the
+// nibbles at bits 4-7 / 20-23 are placed one position higher under the
+// exponent of 1024 (fp16 1024 + 16 q), which one packed fma with 1/16 and -64
+// turns into q (exact: (1024 + 16 q) / 16 - 64 = q, one rounding of an exact
+// value).
+DRT_DEV u32x4 q4_word_to_f16x8(uint32_t w, const Q4Consts& k) {
+  const uint32_t w8 = w >> 8;
+  const f16x2 n1024 = __builtin_bit_cast(f16x2, k.n1024);
+  const f16x2 s16 = __builtin_bit_cast(f16x2, k.sixteenth);
+  const f16x2 n64 = __builtin_bit_cast(f16x2, k.n64);
+  u32x4 r;
+  r[0] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, (w & 0x000F000Fu) | k.magic) + n1024);
+  r[1] = __builtin_bit_cast(
+      uint32_t,
+      __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (w & 0x00F000F0u) | k.magic), s16, n64));
+  r[2] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, (w8 & 0x000F000Fu) | k.magic) + n1024);
+  r[3] = __builtin_bit_cast(
+      uint32_t,
+      __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (w8 & 0x00F000F0u) | k.magic), s16, n64));
+  return r;
+}
+
 // Position of element k within an ACT_F16P row: chunk order (0,4,1,5,2,6,3,7).
 DRT_DEV int f16p_index(int k) {
   const int j = k & 7;

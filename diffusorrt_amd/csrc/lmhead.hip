@@ -17,6 +17,9 @@
 #include "gemm_core.h"
 #include "launch.h"
 
+#include <cstdlib>
+#include <type_traits>
+
 struct LmStat {
   float m;       // block max logit
   float s;       // sum exp(l - m) over the block (fp32)
@@ -241,6 +244,312 @@ __global__ __launch_bounds__(64 * WAVES) void lmhead_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// q4 LM head over a persistent grid (K = 1024): one 8-wave work-group per CU
+// owns a contiguous range of 32-column tiles and stages the 32-row activation
+// tile (hi and lo planes, 128 KiB) into LDS once, with direct-to-LDS loads; its
+// waves take the tiles in turn (wave w: tiles w, w + 8, ...), each keeping the
+// next tile's 16 groups of weights in flight while it multiplies the current
+// one. The bias term sum_g b_g * xsum_g goes through three bf16 MFMAs per tile
+// (the group sums split into three bf16 planes, exact), so the per-group VALU
+// work is the dequantisation and one scale fma per result. Statistics are
+// joined per row over the work-group's columns: one LmStat per (row,
+// work-group), in column order, for lmhead_finalize_kernel.
+namespace {
+
+constexpr int LMP_WAVES = 8;
+constexpr int LMP_G = 16;                    // 64-k groups: K = 1024
+constexpr int LMP_PF = 8;                    // weight groups in flight per wave
+constexpr int LMP_ROW = LMP_G * 64 + 8;      // halves per LDS activation row (+16 B)
+constexpr int LMP_TRS = 40;                  // floats per transpose row
+constexpr int LMP_TR = 16 * LMP_TRS;         // floats of a wave's half-tile transpose
+constexpr size_t LMP_ACT_BYTES = (size_t)2 * 32 * LMP_ROW * 2;
+constexpr size_t LMP_XS_OFF = LMP_ACT_BYTES + (size_t)LMP_WAVES * LMP_TR * 4;
+constexpr size_t LMP_LDS = LMP_XS_OFF + 3 * 64 * 16;  // + the bias product's A planes
+constexpr float LMP_L2E = 1.44269504088896340736f;
+
+// Running statistics of one row over the columns seen so far (in increasing
+// column order): max, sum of exp(l - max), first column of the max, and the
+// sampling draw (best l + T g, its column and logit).
+struct RowRun {
+  float m, s;
+  int arg;
+  int sarg;
+  double skey;
+  float sl;
+};
+
+DRT_DEV RowRun rowrun_empty() { return RowRun{-INFINITY, 0.f, 0x7fffffff, 0x7fffffff, -INFINITY, 0.f}; }
+
+// a and b cover disjoint column sets; equal maxima (and equal keys) go to the
+// lower column, so the join does not depend on the order of its operands.
+DRT_DEV RowRun rowrun_join(const RowRun& a, const RowRun& b) {
+  RowRun r;
+  r.m = fmaxf(a.m, b.m);
+  const float ea = a.m == r.m ? 1.f : __builtin_amdgcn_exp2f((a.m - r.m) * LMP_L2E);
+  const float eb = b.m == r.m ? 1.f : __builtin_amdgcn_exp2f((b.m - r.m) * LMP_L2E);
+  r.s = a.s * ea + b.s * eb;
+  r.arg = (a.m > b.m || (a.m == b.m && a.arg < b.arg)) ? a.arg : b.arg;
+  const bool ka = a.skey > b.skey || (a.skey == b.skey && a.sarg < b.sarg);
+  r.skey = ka ? a.skey : b.skey;
+  r.sarg = ka ? a.sarg : b.sarg;
+  r.sl = ka ? a.sl : b.sl;
+  return r;
+}
+
+DRT_DEV RowRun rowrun_shfl_xor(const RowRun& a, int o) {
+  RowRun r;
+  r.m = __shfl_xor(a.m, o, 64);
+  r.s = __shfl_xor(a.s, o, 64);
+  r.arg = __shfl_xor(a.arg, o, 64);
+  r.sarg = __shfl_xor(a.sarg, o, 64);
+  r.skey = __shfl_xor(a.skey, o, 64);
+  r.sl = __shfl_xor(a.sl, o, 64);
+  return r;
+}
+
+}  // namespace
+
+__global__ __launch_bounds__(64 * LMP_WAVES) void lmhead_q4p_kernel(
+    const uint32_t* __restrict__ qw, const uint32_t* __restrict__ sb,
+    const uint16_t* __restrict__ x, const float* __restrict__ xsum, int M, int N,
+    float* __restrict__ logits_out, LmStat* __restrict__ stats, float temperature_arg,
+    uint64_t seed_arg, int step_arg, const int32_t* __restrict__ positions,
+    const StepDesc* __restrict__ desc, int exclude_arg) {
+  constexpr int G = LMP_G, K = G * 64, W = LMP_WAVES;
+  const float temperature = desc ? desc->temperature : temperature_arg;
+  const uint64_t seed = desc ? desc->seed : seed_arg;
+  const int step = desc ? desc->step : step_arg;
+  const int excl = desc ? desc->exclude_col : exclude_arg;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int m0 = blockIdx.z * 32;
+  const int U = N >> 5, nwg = gridDim.x, wg = blockIdx.x;
+  const int ub = (int)((int64_t)U * wg / nwg), ue = (int)((int64_t)U * (wg + 1) / nwg);
+  const int n_mine = ue - ub > wave ? (ue - ub - wave + W - 1) / W : 0;
+  extern __shared__ __align__(16) char smem[];
+  uint16_t* act = (uint16_t*)smem;  // [2 planes][32 rows][LMP_ROW]
+  float* tr = (float*)(smem + LMP_ACT_BYTES) + wave * LMP_TR;
+
+  // 1. the first tile's weights (a wave without tiles loads a valid one, unused)
+  // weights in flight: a ring of LMP_PF groups (group g in slot g % LMP_PF)
+  u32x4 wq[LMP_PF];
+  uint32_t wsb[LMP_PF];
+  {
+    const int nt = min(ub + wave, U - 1);
+#pragma unroll
+    for (int g = 0; g < LMP_PF; ++g) {
+      wq[g] = __builtin_nontemporal_load(q4_tile_words(qw, nt, G, g, lane));
+      wsb[g] = __builtin_nontemporal_load(&sb[((int64_t)nt * G + g) * 32 + (lane & 31)]);
+    }
+  }
+  // 2. the activation tile into LDS: 128 chunks of 1 KiB (plane, row, half row);
+  // rows past M repeat row M - 1 (their results are never stored)
+#pragma unroll
+  for (int i = 0; i < 128 / W; ++i) {
+    const int ch = wave + W * i, p = ch >> 6, r = (ch >> 1) & 31, hf = ch & 1;
+    const int m = min(m0 + r, M - 1);
+    const uint16_t* src = x + ((int64_t)p * M + m) * K + hf * 512 + lane * 8;
+    __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)(
+                                         act + (p * 32 + r) * LMP_ROW + hf * 512),
+                                     16, 0, 0);
+  }
+  // 3. the group sums as three bf16 planes (exact split of the fp32 value) in
+  // the A layout of the bias product: lane l, row l & 31, groups 8 (l >> 5) .. +7
+  u32x4* xsp = (u32x4*)(smem + LMP_XS_OFF);  // [3 planes][64 lanes]
+  if (wave == 0) {
+    const int mr = m0 + (lane & 31);
+    f32x4 xa = f32x4{0.f, 0.f, 0.f, 0.f}, xb = xa;
+    if (mr < M) {
+      const f32x4* xp = (const f32x4*)(xsum + (int64_t)mr * G + 8 * (lane >> 5));
+      xa = xp[0];
+      xb = xp[1];
+    }
+    uint32_t ph[8], pm[8], pl[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = e < 4 ? xa[e] : xb[e - 4];
+      ph[e] = float_to_bf16_bits(v);
+      const float r1 = v - bf16_bits_to_float(ph[e]);
+      pm[e] = float_to_bf16_bits(r1);
+      pl[e] = float_to_bf16_bits(r1 - bf16_bits_to_float(pm[e]));
+    }
+    u32x4 h, md, lo;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      h[j] = ph[2 * j] | (ph[2 * j + 1] << 16);
+      md[j] = pm[2 * j] | (pm[2 * j + 1] << 16);
+      lo[j] = pl[2 * j] | (pl[2 * j + 1] << 16);
+    }
+    xsp[lane] = h;
+    xsp[64 + lane] = md;
+    xsp[128 + lane] = lo;
+  }
+  // sampling: the row keys of this lane's two rows (lane >> 2 and 16 + lane >> 2)
+  const bool sampling = temperature > 0.f;
+  const int rowa = m0 + (lane >> 2), rowb = rowa + 16;
+  const bool va = rowa < M, vb = rowb < M;
+  uint64_t rka = 0, rkb = 0;
+  if (sampling && va) rka = sampling_row_key(seed, step, positions[rowa]);
+  if (sampling && vb) rkb = sampling_row_key(seed, step, positions[rowb]);
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS chunks (and the first weights) landed
+  __builtin_amdgcn_s_barrier();   // ... and every other wave's
+  asm volatile("" ::: "memory");
+
+  const Q4Consts kq = q4_consts();
+  const _Float16* arow = (const _Float16*)act + (lane & 31) * LMP_ROW + 32 * (lane >> 5);
+  RowRun runa = rowrun_empty(), runb = rowrun_empty();
+
+  // statistics of one half tile (rows 16 PH .. +15) through the wave's LDS
+  // area: lane takes row lane >> 2, columns 8 (lane & 3) .. +7 of the tile
+  auto half_tile = [&](const f32x16& acc, int nt, auto ph_c, RowRun& run, uint64_t rk, bool rv) {
+    constexpr int PH = decltype(ph_c)::value;
+    const bool ex = nt * 32 + (lane & 31) == excl;
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr) {
+      const int r = 8 * PH + rr;
+      tr[(mfma_row(r, lane) - 16 * PH) * LMP_TRS + (lane & 31)] = ex ? -INFINITY : acc[r];
+    }
+    const int q = lane >> 2, j4 = lane & 3;
+    const int c0 = nt * 32 + 8 * j4;
+    const f32x4 v0 = *(const f32x4*)(tr + q * LMP_TRS + 8 * j4);
+    const f32x4 v1 = *(const f32x4*)(tr + q * LMP_TRS + 8 * j4 + 4);
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = v0[e];
+      v[e + 4] = v1[e];
+    }
+    RowRun t;
+    t.m = v[0];
+    t.arg = c0;
+#pragma unroll
+    for (int e = 1; e < 8; ++e)
+      if (v[e] > t.m) { t.m = v[e]; t.arg = c0 + e; }
+    const float mb = t.m * LMP_L2E;
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += __builtin_amdgcn_exp2f(fmaf(v[e], LMP_L2E, -mb));
+    t.s = s;
+    t.skey = -INFINITY;
+    t.sarg = 0x7fffffff;
+    t.sl = 0.f;
+    if (sampling && rv) {
+      const double T = (double)temperature;
+      for (int e = 0; e < 8; ++e) {
+        const double key = __dadd_rn((double)v[e], __dmul_rn(T, (double)gumbel(rk, c0 + e)));
+        if (key > t.skey) { t.skey = key; t.sarg = c0 + e; t.sl = v[e]; }
+      }
+    }
+    run = rowrun_join(run, t);
+  };
+
+  // one 32-column tile: 16 groups (each: 8 MFMAs and one scale fma per result),
+  // the next tile's weights loaded into the registers each group frees
+  auto tile = [&](int nt, auto prefetch) {
+    // the activation fragments are the same for every tile: without this
+    // barrier the compiler would hoist their LDS reads out of the tile loop
+    // and hold all 16 groups (512 registers) live
+    asm volatile("" ::: "memory");
+    f32x16 acc = f32x16{};
+    uint32_t bpk[8];
+    const int ntn = nt + W;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      constexpr int PF = LMP_PF;
+      const int sl = g % PF;
+      // keep each group's work in its place: the LDS reads and the
+      // dequantisation would otherwise be hoisted to the tile start for every
+      // group at once (registers for all of them)
+      asm volatile("" ::: "memory");
+      u32x4 wv = wq[sl];
+      asm volatile("" : "+v"(wv));
+      f16x8 a[4], al[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        a[t] = *(const f16x8*)(arow + g * 64 + 8 * t);
+        al[t] = *(const f16x8*)(arow + 32 * LMP_ROW + g * 64 + 8 * t);
+      }
+      f32x16 c = f32x16{};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const f16x8 b = __builtin_bit_cast(f16x8, q4_word_to_f16x8(wv[t], kq));
+        c = mfma_f16(a[t], b, c);
+        c = mfma_f16(al[t], b, c);
+      }
+      const float s = bf16_bits_to_float(wsb[sl] & 0xffffu);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = fmaf(s, c[r], acc[r]);
+      // bias of group g into the bf16 B operand of the bias product
+      if (g & 1) bpk[g >> 1] |= wsb[sl] & 0xffff0000u;
+      else bpk[g >> 1] = wsb[sl] >> 16;
+      // the slot's next group: g + PF of this tile, else g + PF - G of the next
+      if (g + PF < G || decltype(prefetch)::value) {
+        const int tn = g + PF < G ? nt : ntn, gn = g + PF < G ? g + PF : g + PF - G;
+        wq[sl] = __builtin_nontemporal_load(q4_tile_words(qw, tn, G, gn, lane));
+        wsb[sl] = __builtin_nontemporal_load(&sb[((int64_t)tn * G + gn) * 32 + (lane & 31)]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const bool hi_half = lane >= 32;
+    u32x4 bb;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bb[j] = hi_half ? bpk[4 + j] : bpk[j];
+    const bf16x8 bv = __builtin_bit_cast(bf16x8, bb);
+#pragma unroll
+    for (int p = 0; p < 3; ++p) acc = mfma_bf16(__builtin_bit_cast(bf16x8, xsp[64 * p + lane]), bv, acc);
+
+    if (logits_out) {
+      // rows m0 + 4 (lane >> 5) + 8 (r >> 2) + (r & 3): per-r offsets are uniform
+      const int rl = m0 + 4 * (lane >> 5);
+      float* lp = logits_out + (int64_t)rl * N + nt * 32 + (lane & 31);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int dr = 8 * (r >> 2) + (r & 3);
+        if (rl + dr < M) lp[(int64_t)dr * N] = acc[r];
+      }
+    }
+    half_tile(acc, nt, std::integral_constant<int, 0>{}, runa, rka, va);
+    half_tile(acc, nt, std::integral_constant<int, 1>{}, runb, rkb, vb);
+  };
+  for (int i = 0; i < n_mine; ++i) {
+    const int nt = ub + wave + W * i;
+    if (i + 1 < n_mine) tile(nt, std::true_type{});
+    else tile(nt, std::false_type{});
+  }
+
+  // the four column quarters of a row, then the waves, in LDS over the activation
+  runa = rowrun_join(runa, rowrun_shfl_xor(runa, 1));
+  runa = rowrun_join(runa, rowrun_shfl_xor(runa, 2));
+  runb = rowrun_join(runb, rowrun_shfl_xor(runb, 1));
+  runb = rowrun_join(runb, rowrun_shfl_xor(runb, 2));
+  __syncthreads();  // every wave is done with the activation tile
+  RowRun* js = (RowRun*)smem;  // [W][32]
+  if ((lane & 3) == 0) {
+    js[wave * 32 + (lane >> 2)] = runa;
+    js[wave * 32 + 16 + (lane >> 2)] = runb;
+  }
+  __syncthreads();
+  if (threadIdx.x < 32) {
+    const int row = threadIdx.x;
+    RowRun r = js[row];
+#pragma unroll
+    for (int w = 1; w < W; ++w) r = rowrun_join(r, js[w * 32 + row]);
+    if (m0 + row < M) {
+      LmStat st;
+      st.m = r.m;
+      st.s = r.s;
+      st.arg = r.arg;
+      st.sarg = r.sarg;
+      st.skey = r.skey;
+      st.sl = r.sl;
+      st.pad = 0.f;
+      stats[(int64_t)(m0 + row) * nwg + wg] = st;
+    }
+  }
+}
+
 // One 256-thread WG per row: join the N/64 block statistics in float64. scores
 // and tokens may be pinned host memory (the session's landing area: no copy
 // after the forward); scores_d / tokens_d (optional) get the same values in
@@ -380,8 +689,26 @@ void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* 
   // work-group at <= 66 KiB of LDS (two per CU)
   const int chunk_k = std::min(w.q4 ? 256 : 512, w.K);
   require(w.K % chunk_k == 0 || w.K % 64 == 0, "lm head K must be a multiple of 64");
-  const int NB = w.N / 64;
+  int NB = w.N / 64;
   constexpr int WAVES = 4;
+  // K = 1024 q4 heads run on the persistent kernel (DRT_LMHEAD_CHUNKED=1 keeps
+  // them on the chunked one, an A/B switch for parity and timing comparisons)
+  static const bool chunked = getenv("DRT_LMHEAD_CHUNKED") != nullptr;
+  if (w.q4 && w.K == LMP_G * 64 && !chunked) {
+    int dev = 0, n_cu = 0;
+    DRT_HIP(hipGetDevice(&dev));
+    DRT_HIP(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
+    const int U = w.N / 32;
+    NB = std::max(1, std::min(n_cu, U / LMP_WAVES));  // one work-group per CU
+    auto fn = lmhead_q4p_kernel;
+    static size_t granted = 0;
+    grant_lds((const void*)fn, LMP_LDS, granted);
+    const double bytes = (double)w.N * w.K / 2 + (double)w.N * w.K / 16 + 2.0 * M * w.K;
+    DRT_LAUNCH(Profiler::LMHEAD, bytes, fn, dim3(NB, 1, (M + 31) / 32), dim3(64 * LMP_WAVES),
+               LMP_LDS, s, w.qw.as<uint32_t>(), w.sb.as<uint32_t>(), (const uint16_t*)act, xsum,
+               M, w.N, logits_out, (LmStat*)stats, temperature, seed, step, positions, desc,
+               exclude_col);
+  } else {
   const size_t lds = (size_t)(w.q4 ? 2 : 1) * 32 * (chunk_k + 8) * 2 +
                      (size_t)32 * (chunk_k / 64) * 4 + (size_t)WAVES * 32 * 65 * 4;
   const dim3 grid((NB + WAVES - 1) / WAVES, 1, (M + 31) / 32);
@@ -403,6 +730,7 @@ void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* 
                (const uint32_t*)nullptr, (const uint32_t*)nullptr, w.wb.as<uint16_t>(), act, xsum,
                M, w.N, w.K, chunk_k, logits_out, (LmStat*)stats, temperature, seed, step,
                positions, desc, exclude_col);
+  }
   }
   DRT_HIP(hipGetLastError());
   if (scores && tokens) {

@@ -225,13 +225,16 @@ def test_rms_norm_rope_swiglu():
 
 # ---------------------------------------------------------------- LM head + scoring
 
-@pytest.mark.parametrize("kind", ["q4", "bf16"])
-def test_lm_head_scores_tokens(kind):
+@pytest.mark.parametrize("kind,rows,n", [("q4", 32, 151936), ("q4", 20, 8256), ("q4", 45, 8256),
+                                          ("bf16", 32, 151936)])
+def test_lm_head_scores_tokens(kind, rows, n):
+    """The full 151936-column head and a 129-block one (ragged column ranges per
+    work-group), one 32-row tile, a partial tile and two tiles."""
     from diffusorrt_amd import _lib, kernels
     from diffusorrt_amd import synthetic as syn
     import ctypes as C
 
-    rows, n, k = 32, 151936, 1024
+    k = 1024
     _say("lm_head", kind, rows, n, k)
     gen = torch.Generator().manual_seed(9)
     x = torch.randn((rows, k), generator=gen)
@@ -272,16 +275,24 @@ def test_lm_head_scores_tokens(kind):
     np.testing.assert_allclose(scores.cpu().numpy(), s_own, rtol=1e-6)
 
 
-def test_lm_head_sampling_matches_oracle_rule():
+@pytest.mark.parametrize("kind", ["bf16", "q4"])
+def test_lm_head_sampling_matches_oracle_rule(kind):
     from diffusorrt_amd import _lib, kernels
+    from diffusorrt_amd import synthetic as syn
     import ctypes as C
 
-    rows, n, k = 4, 2048, 256
-    _say("lm_head sampling", rows, n, k)
+    rows, n, k = (4, 2048, 256) if kind == "bf16" else (4, 8256, 1024)
+    _say("lm_head sampling", kind, rows, n, k)
     gen = torch.Generator().manual_seed(21)
     x = torch.randn((rows, k), generator=gen)
-    wt = (torch.randn((n, k), generator=gen) * 0.05).to(torch.bfloat16)
-    w = kernels.DeviceBF16Weight(wt.cuda())
+    if kind == "bf16":
+        wt = (torch.randn((n, k), generator=gen) * 0.05).to(torch.bfloat16)
+        w = kernels.DeviceBF16Weight(wt.cuda())
+        wargs = (None, None, C.c_void_p(w.wb.data_ptr()))
+    else:
+        q = syn.random_q4(gen, n, k)
+        w = kernels.DeviceQ4Weight(q.w_q.cuda(), q.scales.cuda(), q.biases.cuda())
+        wargs = (C.c_void_p(w.qw.data_ptr()), C.c_void_p(w.sb.data_ptr()), None)
     lib = _lib.load()
     positions = torch.tensor([5, 6, 9, 40], dtype=torch.int32, device="cuda")
     scores = torch.empty(rows, dtype=torch.float64, device="cuda")
@@ -291,7 +302,7 @@ def test_lm_head_sampling_matches_oracle_rule():
     ws = torch.empty(ws_b, dtype=torch.uint8, device="cuda")
     xc = x.cuda()
     T, seed, step = 0.7, 1234, 3
-    _lib.check(lib.drt_op_lm_head_score(None, None, C.c_void_p(w.wb.data_ptr()), rows, n, k,
+    _lib.check(lib.drt_op_lm_head_score(*wargs, rows, n, k,
                                         C.c_void_p(xc.data_ptr()), T, seed, step,
                                         C.c_void_p(positions.data_ptr()),
                                         C.c_void_p(scores.data_ptr()),

@@ -341,18 +341,20 @@ def test_dream_real_shapes_window():
     rt.close()
 
 
-def test_dream_block_threshold_exact_kv():
+@pytest.mark.parametrize("hidden", [256, 1024])
+def test_dream_block_threshold_exact_kv(hidden):
     """Dream's block-threshold policy on the device session: prompt-relative
     8-row blocks over the exact K/V of the prompt and the frozen blocks, the
     logits shift's feeder row, the MASK column left out of the scoring. The LM
     head's MASK row is set to 4x the row of the first frontier row's top token,
-    so MASK would win that row if it were scored."""
+    so MASK would win that row if it were scored. (Hidden size 1024 takes the
+    persistent q4 LM head, 256 the chunked one.)"""
     from diffusorrt_amd import decode
     from diffusorrt_amd import synthetic as syn
     from diffusorrt_amd.runtime import Runtime, block_threshold_session_config
 
-    _say("dream block_threshold exact K/V")
-    geom = tiny_dream_geometry()
+    _say("dream block_threshold exact K/V, hidden", hidden)
+    geom = tiny_dream_geometry(hidden_size=hidden)
     model = syn.build_model(geom, "q4", 13)
     W, cfg = _oracle(model)
     P_LEN, GEN, BS = 45, 24, 8
