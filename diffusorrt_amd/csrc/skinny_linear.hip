@@ -1,5 +1,8 @@
 // Split-K linears for decode-sized activations (M <= 32 rows per row tile, up to
-// sk_row_tiles tiles) and q4 weights.
+// sk_row_tiles tiles) and q4 or bf16 weights (WK). With bf16 weights the
+// activation is ACT_BF16 (one plane), each 64-k unit is four bf16 MFMAs, and the
+// summed tile is rounded to bf16 before the epilogue, as the reference's bf16
+// matmul output is (backends/mlx_ops.py:122-125) and as fused_linear_kernel does.
 //
 // A decode step's linears read only 1-4 MB of weights; what bounds them is how
 // much each CU must pull (about 64 GB/s per CU) and how many dependent memory
@@ -129,7 +132,7 @@ __global__ void xcc_probe_kernel(int* __restrict__ xcc) {
 // the last one and are added times 0: a load under a branch makes the compiler
 // wait for it, and for everything issued before it, inside the branch.
 template <int KSC, typename After>
-DRT_DEV void sk_wide_sum_slices(const float* pbase, int KS, float* red, After after) {
+DRT_DEV void sk_wide_sum_slices(const float* pbase, int KS, float* red, bool rnd, After after) {
   f32x4 pv[KSC][4];
 #pragma unroll
   for (int k2 = 0; k2 < KSC; ++k2)
@@ -146,17 +149,18 @@ DRT_DEV void sk_wide_sum_slices(const float* pbase, int KS, float* red, After af
     const int q = threadIdx.x + 256 * i, tn = q >> 8, c4 = q & 255;
     const int ln = c4 & 63, col = ln & 31, r0 = 8 * (c4 >> 6) + 4 * (ln >> 5);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) red[(tn * 32 + r0 + e) * 33 + col] = sum[e];
+    for (int e = 0; e < 4; ++e) red[(tn * 32 + r0 + e) * 33 + col] = rnd ? round_bf16(sum[e]) : sum[e];
   }
 }
 
 }  // namespace
 
-template <int EPI, int U>
+template <int WK, int EPI, int U>
 __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int KS) {
+  constexpr bool BF = WK == W_BF16;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int M = a.M, N = a.N, K = a.K;
-  auto gqw = (SK_GLOBAL(const uint32_t)*)a.qw;
+  auto gqw = (SK_GLOBAL(const uint32_t)*)(BF ? (const uint32_t*)a.wb : a.qw);
   auto gsb = (SK_GLOBAL(const uint32_t)*)a.sb;
   auto ghid = (SK_GLOBAL(const float)*)a.hidden;
   auto gnw = (SK_GLOBAL(const uint16_t)*)a.norm_w;
@@ -193,13 +197,22 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
   int* flag = (int*)(red + SK_RED);
   uint16_t* vbuf = (uint16_t*)(smem + SK_WIDE_V_OFF(U));  // [4096] V tile half (QKV)
 
-  // 1. this wave's weights for the U units, issued first
-  u32x4 wq[U];
+  // 1. this wave's weights for the U units, issued first (bf16: the unit's four
+  // 16-k MFMA fragments)
+  u32x4 wq[U][BF ? 4 : 1];
   uint32_t wsb[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    wq[u] = __builtin_nontemporal_load(q4_tile_words(qw, nt, G, u0 + u, lane));
-    wsb[u] = q4_tile_sb(sbp, nt, G, u0 + u, lane);
+    if (BF) {
+#pragma unroll
+      for (int t = 0; t < (BF ? 4 : 1); ++t)
+        wq[u][t] = __builtin_nontemporal_load(
+            (const u32x4*)bf16_tile_frag((const uint16_t*)qw, nt, K >> 4, 4 * (u0 + u) + t, lane));
+      wsb[u] = 0u;
+    } else {
+      wq[u][0] = __builtin_nontemporal_load(q4_tile_words(qw, nt, G, u0 + u, lane));
+      wsb[u] = q4_tile_sb(sbp, nt, G, u0 + u, lane);
+    }
   }
   // 2. the hidden slice (8-wide items: U per thread) and the matching norm weights.
   // Every load of steps 1-3 is unconditional (rows past M read row M - 1 and are
@@ -254,6 +267,15 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
       x[2 * e] = (hv[j][e >> 1][(2 * e) & 3] * inv) * bf16_bits_to_float(nw[j][e] & 0xffffu);
       x[2 * e + 1] = (hv[j][e >> 1][(2 * e + 1) & 3] * inv) * bf16_bits_to_float(nw[j][e] >> 16);
     }
+    if (BF) {  // ACT_BF16 in natural order, no group sums
+      u32x4 pk;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        pk[e] = (uint32_t)float_to_bf16_bits(x[2 * e]) |
+                ((uint32_t)float_to_bf16_bits(x[2 * e + 1]) << 16);
+      *(u32x4*)(xs + r * ROW_H + c8 * 8) = pk;
+      continue;
+    }
     _Float16 h[8], lo[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -281,6 +303,13 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
   f32x16 acc = f32x16{};
 #pragma unroll
   for (int u = 0; u < U; ++u) {
+    if (BF) {  // k = 16 t + 8 (lane >> 5) + e of the unit, natural order
+      const uint16_t* brow = xs + (lane & 31) * ROW_H + u * 64 + 8 * (lane >> 5);
+#pragma unroll
+      for (int t = 0; t < (BF ? 4 : 1); ++t)
+        acc = mfma_bf16(*(const bf16x8*)(brow + 16 * t), __builtin_bit_cast(bf16x8, wq[u][t]), acc);
+      continue;
+    }
     const _Float16* arow = (const _Float16*)xs + (lane & 31) * ROW_H + u * 64 + 32 * (lane >> 5);
     f16x8 af[4], afl[4];
 #pragma unroll
@@ -290,7 +319,7 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
     }
     float xsr[16];
     load_row_sums(xss + u * 32, lane, xsr);
-    q4_group_mma1(acc, af, afl, xsr, wq[u], wsb[u]);
+    q4_group_mma1(acc, af, afl, xsr, wq[u][0], wsb[u]);
   }
   if (!live) return;  // work-group-uniform, before any global store
   // 6. K slices meet: the last work-group of the column block adds the partials
@@ -310,14 +339,17 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
     auto tables = [&]() {
       if (EPI == EPI_QKV) qt = qkv_tables(a, grp, row0 + m0, M);
     };
-    if (KS <= 2) sk_wide_sum_slices<2>(pbase, KS, red, tables);
-    else if (KS <= 4) sk_wide_sum_slices<4>(pbase, KS, red, tables);
-    else sk_wide_sum_slices<SK_KS_MAX>(pbase, KS, red, tables);
+    const bool rnd = BF && a.rnd_bf16;
+    if (KS <= 2) sk_wide_sum_slices<2>(pbase, KS, red, rnd, tables);
+    else if (KS <= 4) sk_wide_sum_slices<4>(pbase, KS, red, rnd, tables);
+    else sk_wide_sum_slices<SK_KS_MAX>(pbase, KS, red, rnd, tables);
     if (threadIdx.x == 0) reset_counter(&counters[grp], a.fenced);
   } else {
     if (EPI == EPI_QKV) qt = qkv_tables(a, grp, row0 + m0, M);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) red[(wave * 32 + mfma_row(r, lane)) * 33 + (lane & 31)] = acc[r];
+    for (int r = 0; r < 16; ++r)
+      red[(wave * 32 + mfma_row(r, lane)) * 33 + (lane & 31)] =
+          BF && a.rnd_bf16 ? round_bf16(acc[r]) : acc[r];
   }
   __syncthreads();
 #define TT(r, c) red[(((c) >> 5) * 32 + (r)) * 33 + ((c) & 31)]
@@ -369,11 +401,12 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
 
 // UW: units per wave held in registers at once (the wave's units are processed
 // in chunks of UW, each chunk's loads issued together).
-template <int EPI, int UW>
+template <int WK, int EPI, int UW>
 __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, int KS) {
+  constexpr bool BF = WK == W_BF16;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int M = a.M, N = a.N, K = a.K;
-  auto gqw = (SK_GLOBAL(const uint32_t)*)a.qw;
+  auto gqw = (SK_GLOBAL(const uint32_t)*)(BF ? (const uint32_t*)a.wb : a.qw);
   auto gsb = (SK_GLOBAL(const uint32_t)*)a.sb;
   auto gact = (SK_GLOBAL(const uint16_t)*)a.act;
   auto gerr = (SK_GLOBAL(int)*)a.placement_err;
@@ -404,22 +437,31 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
   const uint16_t* act_lo = act + (int64_t)M_all * K + (int64_t)m0 * K;  // ACT_F16P lo plane
   act += (int64_t)m0 * K;
   for (int ub = u_lo; ub < u_hi || ub == u_lo; ub += UW) {
-    u32x4 wq[UW], craw[UW][4], crawl[UW][4], af[UW][4], afl[UW][4];
+    u32x4 wq[UW][BF ? 4 : 1], craw[UW][4], crawl[UW][4], af[UW][4], afl[UW][4];
     uint32_t wsb[UW];
 #pragma unroll
     for (int i = 0; i < UW; ++i) {
       // clamped to a valid unit; a unit beyond the wave's range gets scale and
-      // bias 0, an exact no-op, so every load is used unconditionally
+      // bias 0 (bf16: it is not multiplied), an exact no-op, so every load is
+      // used unconditionally
       const int u = min(ub + i, max(u_hi, u_lo + 1) - 1);
-      wq[i] = __builtin_nontemporal_load(q4_tile_words(qw, nt, G, u, lane));
-      wsb[i] = ub + i < u_hi ? q4_tile_sb(sbp, nt, G, u, lane) : 0u;
+      if (BF) {
+#pragma unroll
+        for (int t = 0; t < (BF ? 4 : 1); ++t)
+          wq[i][t] = __builtin_nontemporal_load(
+              (const u32x4*)bf16_tile_frag((const uint16_t*)qw, nt, K >> 4, 4 * u + t, lane));
+        wsb[i] = 0u;
+      } else {
+        wq[i][0] = __builtin_nontemporal_load(q4_tile_words(qw, nt, G, u, lane));
+        wsb[i] = ub + i < u_hi ? q4_tile_sb(sbp, nt, G, u, lane) : 0u;
+      }
       // the unit's 32 x 64 activation block as four coalesced loads of 8 rows x
       // 128 B (rows past M read row M - 1: their outputs are never stored)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int64_t off = (int64_t)min(8 * j + (lane >> 3), M - 1) * K + u * 64 + (lane & 7) * 8;
         craw[i][j] = *(const u32x4*)(act + off);
-        crawl[i][j] = *(const u32x4*)(act_lo + off);
+        if (!BF) crawl[i][j] = *(const u32x4*)(act_lo + off);
       }
     }
     // through LDS into the q4 fragment order: lane l takes row l & 31, 16-byte
@@ -432,8 +474,22 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
       for (int j = 0; j < 4; ++j) {
         char* d = stg + (i * 32 + 8 * j + (lane >> 3)) * 144 + (lane & 7) * 16;
         *(u32x4*)d = craw[i][j];
-        *(u32x4*)(d + PLANE) = crawl[i][j];
+        if (!BF) *(u32x4*)(d + PLANE) = crawl[i][j];
       }
+    if (BF) {  // bf16: 16-k MFMA chunk t of the unit is 16-byte chunk 2 t + (lane >> 5)
+#pragma unroll
+      for (int i = 0; i < UW; ++i) {
+        if (ub + i >= u_hi) break;  // a clamped repeat of the last unit (wave-uniform)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const bf16x8 ab = *(const bf16x8*)(stg + (i * 32 + (lane & 31)) * 144 +
+                                             (2 * t + (lane >> 5)) * 16);
+          acc = mfma_bf16(ab, __builtin_bit_cast(bf16x8, wq[i][BF ? t : 0]), acc);
+        }
+      }
+      if (ub + UW >= u_hi) break;
+      continue;
+    }
 #pragma unroll
     for (int i = 0; i < UW; ++i)
 #pragma unroll
@@ -452,7 +508,7 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
         ah[t] = __builtin_bit_cast(f16x8, af[i][t]);
         alh[t] = __builtin_bit_cast(f16x8, afl[i][t]);
       }
-      q4_group_mma1(acc, ah, alh, xsr[i], wq[i], wsb[i]);
+      q4_group_mma1(acc, ah, alh, xsr[i], wq[i][0], wsb[i]);
     }
     if (ub + UW >= u_hi) break;
   }
@@ -484,6 +540,10 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
     for (int k2 = 0; k2 < SK_KS_MAX; ++k2) v += pv[k2] * (k2 < KS ? 1.f : 0.f);  // unconditional loads
     if (threadIdx.x == 0) reset_counter(&counters[nt], a.fenced);
   }
+  if (BF && a.rnd_bf16) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = round_bf16(v[e]);
+  }
   if (a.bias) {
     const uint2 bb = *(const uint2*)(a.bias + n);
     v[0] += bf16_bits_to_float(bb.x & 0xffffu);
@@ -506,13 +566,17 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
   }
 }
 
-#define DRT_WIDE(E, U) template __global__ void skinny_wide_kernel<E, U>(const FusedArgs, int);
-DRT_WIDE(EPI_QKV, 1) DRT_WIDE(EPI_QKV, 2) DRT_WIDE(EPI_QKV, 4) DRT_WIDE(EPI_QKV, 8)
-DRT_WIDE(EPI_SWIGLU, 1) DRT_WIDE(EPI_SWIGLU, 2) DRT_WIDE(EPI_SWIGLU, 4) DRT_WIDE(EPI_SWIGLU, 8)
+#define DRT_WIDE(W, E, U) template __global__ void skinny_wide_kernel<W, E, U>(const FusedArgs, int);
+#define DRT_WIDE_U(W, E) DRT_WIDE(W, E, 1) DRT_WIDE(W, E, 2) DRT_WIDE(W, E, 4) DRT_WIDE(W, E, 8)
+DRT_WIDE_U(W_Q4, EPI_QKV) DRT_WIDE_U(W_Q4, EPI_SWIGLU)
+DRT_WIDE_U(W_BF16, EPI_QKV) DRT_WIDE_U(W_BF16, EPI_SWIGLU)
+#undef DRT_WIDE_U
 #undef DRT_WIDE
-#define DRT_NARROW(E, UW) template __global__ void skinny_narrow_kernel<E, UW>(const FusedArgs, int);
-DRT_NARROW(EPI_RESID, 1) DRT_NARROW(EPI_RESID, 2)
-DRT_NARROW(EPI_STORE, 1) DRT_NARROW(EPI_STORE, 2)
+#define DRT_NARROW(W, E, UW) template __global__ void skinny_narrow_kernel<W, E, UW>(const FusedArgs, int);
+DRT_NARROW(W_Q4, EPI_RESID, 1) DRT_NARROW(W_Q4, EPI_RESID, 2)
+DRT_NARROW(W_Q4, EPI_STORE, 1) DRT_NARROW(W_Q4, EPI_STORE, 2)
+DRT_NARROW(W_BF16, EPI_RESID, 1) DRT_NARROW(W_BF16, EPI_RESID, 2)
+DRT_NARROW(W_BF16, EPI_STORE, 1) DRT_NARROW(W_BF16, EPI_STORE, 2)
 #undef DRT_NARROW
 
 namespace drt {
@@ -581,12 +645,13 @@ bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
   // (an A/B switch for parity and timing comparisons)
   static const bool disabled = getenv("DRT_DISABLE_SKINNY") != nullptr;
   const int MT = (a.M + 31) / 32;
-  if (disabled || !a.qw || a.M < 1 || MT > a.sk_row_tiles || !a.part || !a.counters ||
-      a.K % 64 || a.N % 32 || a.n_xcc < 1)
+  if (disabled || (!a.qw && !a.wb) || a.M < 1 || MT > a.sk_row_tiles || !a.part ||
+      !a.counters || a.K % 64 || a.N % 32 || a.n_xcc < 1)
     return false;
+  const bool bf = a.qw == nullptr;
   const int G = a.K / 64;
-  const double bytes = (double)a.N * a.K / 2 + (double)a.N * a.K / 16 + 2.0 * a.M * a.K +
-                       2.0 * a.M * a.N;
+  const double bytes = (bf ? 2.0 * a.N * a.K : (double)a.N * a.K / 2 + (double)a.N * a.K / 16) +
+                       2.0 * a.M * a.K + 2.0 * a.M * a.N;
   if (kind == FL_QKV || kind == FL_SWIGLU) {
     if (!a.ss_in || a.N % 128 || a.K / 32 > 8 * SK_SS_PER_THREAD) return false;
     const int U = wide_units(a.N, a.K);
@@ -596,12 +661,17 @@ bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
       return false;  // (padding work-groups past the last block exit before any access)
     const size_t lds = SK_WIDE_LDS(U);
     const dim3 grid((unsigned)((NG + a.n_xcc - 1) / a.n_xcc * a.n_xcc * KS), MT);
-#define DRT_SW(E, UU)                                                             \
+#define DRT_SW1(W, E, UU)                                                         \
   {                                                                               \
-    auto fn = skinny_wide_kernel<E, UU>;                                          \
+    auto fn = skinny_wide_kernel<W, E, UU>;                                       \
     static size_t granted = 0;                                                    \
     grant_lds((const void*)fn, lds, granted);                                     \
     DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(256), lds, s, a, KS);        \
+  }
+#define DRT_SW(E, UU)                  \
+  {                                    \
+    if (bf) DRT_SW1(W_BF16, E, UU)     \
+    else DRT_SW1(W_Q4, E, UU)          \
   }
 #define DRT_SW_U(E)                                  \
   switch (U) {                                       \
@@ -617,18 +687,24 @@ bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
     }
 #undef DRT_SW_U
 #undef DRT_SW
+#undef DRT_SW1
   } else if (kind == FL_RESID || kind == FL_STORE) {
     const int KS = narrow_slices(a.N, a.K), NT = a.N / 32;
     if (KS > SK_KS_MAX || (size_t)NT * KS * 1024 > a.part_floats || NT > a.n_counters)
       return false;
     const int per_wave = (G / KS + 3) / 4;
     const dim3 grid((unsigned)((NT + a.n_xcc - 1) / a.n_xcc * a.n_xcc * KS), MT);
-#define DRT_SN(E, UW)                                                              \
+#define DRT_SN1(W, E, UW)                                                          \
   {                                                                                \
-    auto fn = skinny_narrow_kernel<E, UW>;                                         \
+    auto fn = skinny_narrow_kernel<W, E, UW>;                                      \
     static size_t granted = 0;                                                     \
     grant_lds((const void*)fn, SK_NARROW_LDS(UW), granted);                        \
     DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(256), SK_NARROW_LDS(UW), s, a, KS); \
+  }
+#define DRT_SN(E, UW)                  \
+  {                                    \
+    if (bf) DRT_SN1(W_BF16, E, UW)     \
+    else DRT_SN1(W_Q4, E, UW)          \
   }
     // (more than two units per wave: loops of two, the hi and lo fragments of
     // a larger batch would not fit the registers). Two row tiles double the
@@ -641,6 +717,7 @@ bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
       if (one_unit) DRT_SN(EPI_STORE, 1) else DRT_SN(EPI_STORE, 2)
     }
 #undef DRT_SN
+#undef DRT_SN1
   } else {
     return false;
   }
