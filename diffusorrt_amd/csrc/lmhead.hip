@@ -310,13 +310,22 @@ DRT_DEV RowRun rowrun_shfl_xor(const RowRun& a, int o) {
 
 }  // namespace
 
+// WK = 0 (q4): x is ACT_F16P (hi + lo planes) with group sums xsum. WK = 1
+// (bf16 tile weights in qw's place, sb unused): x is ACT_BF16 (one plane), four
+// bf16 MFMAs per 64-k group, the logits rounded to bf16 before the statistics
+// (the reference's bf16 matmul output), four groups in flight per wave.
+template <int WK>
 __global__ __launch_bounds__(64 * LMP_WAVES) void lmhead_q4p_kernel(
     const uint32_t* __restrict__ qw, const uint32_t* __restrict__ sb,
     const uint16_t* __restrict__ x, const float* __restrict__ xsum, int M, int N,
     float* __restrict__ logits_out, LmStat* __restrict__ stats, float temperature_arg,
     uint64_t seed_arg, int step_arg, const int32_t* __restrict__ positions,
     const StepDesc* __restrict__ desc, int exclude_arg) {
+  constexpr bool BF = WK == 1;
   constexpr int G = LMP_G, K = G * 64, W = LMP_WAVES;
+  constexpr int PF = BF ? 4 : LMP_PF;  // weight groups in flight per wave
+  constexpr int FR = BF ? 4 : 1;       // 16-byte fragments per group and lane
+  constexpr int PLANES = BF ? 1 : 2;
   const float temperature = desc ? desc->temperature : temperature_arg;
   const uint64_t seed = desc ? desc->seed : seed_arg;
   const int step = desc ? desc->step : step_arg;
@@ -325,6 +334,12 @@ __global__ __launch_bounds__(64 * LMP_WAVES) void lmhead_q4p_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int m0 = blockIdx.z * 32;
   const int U = N >> 5, nwg = gridDim.x, wg = blockIdx.x;
+  const uint16_t* wb = (const uint16_t*)qw;
+  // group g of tile nt, fragment f: q4 words or a bf16 16-k MFMA fragment
+  auto wfrag = [&](int nt, int g, int f) {
+    return BF ? (const u32x4*)bf16_tile_frag(wb, nt, K >> 4, 4 * g + f, lane)
+              : q4_tile_words(qw, nt, G, g, lane);
+  };
   const int ub = (int)((int64_t)U * wg / nwg), ue = (int)((int64_t)U * (wg + 1) / nwg);
   const int n_mine = ue - ub > wave ? (ue - ub - wave + W - 1) / W : 0;
   extern __shared__ __align__(16) char smem[];
@@ -332,21 +347,22 @@ __global__ __launch_bounds__(64 * LMP_WAVES) void lmhead_q4p_kernel(
   float* tr = (float*)(smem + LMP_ACT_BYTES) + wave * LMP_TR;
 
   // 1. the first tile's weights (a wave without tiles loads a valid one, unused)
-  // weights in flight: a ring of LMP_PF groups (group g in slot g % LMP_PF)
-  u32x4 wq[LMP_PF];
-  uint32_t wsb[LMP_PF];
+  // weights in flight: a ring of PF groups (group g in slot g % PF)
+  u32x4 wq[PF][FR];
+  uint32_t wsb[PF];
   {
     const int nt = min(ub + wave, U - 1);
 #pragma unroll
-    for (int g = 0; g < LMP_PF; ++g) {
-      wq[g] = __builtin_nontemporal_load(q4_tile_words(qw, nt, G, g, lane));
-      wsb[g] = __builtin_nontemporal_load(&sb[((int64_t)nt * G + g) * 32 + (lane & 31)]);
+    for (int g = 0; g < PF; ++g) {
+#pragma unroll
+      for (int f = 0; f < FR; ++f) wq[g][f] = __builtin_nontemporal_load(wfrag(nt, g, f));
+      wsb[g] = BF ? 0u : __builtin_nontemporal_load(&sb[((int64_t)nt * G + g) * 32 + (lane & 31)]);
     }
   }
   // 2. the activation tile into LDS: 128 chunks of 1 KiB (plane, row, half row);
   // rows past M repeat row M - 1 (their results are never stored)
 #pragma unroll
-  for (int i = 0; i < 128 / W; ++i) {
+  for (int i = 0; i < 64 * PLANES / W; ++i) {
     const int ch = wave + W * i, p = ch >> 6, r = (ch >> 1) & 31, hf = ch & 1;
     const int m = min(m0 + r, M - 1);
     const uint16_t* src = x + ((int64_t)p * M + m) * K + hf * 512 + lane * 8;
@@ -358,7 +374,7 @@ __global__ __launch_bounds__(64 * LMP_WAVES) void lmhead_q4p_kernel(
   // 3. the group sums as three bf16 planes (exact split of the fp32 value) in
   // the A layout of the bias product: lane l, row l & 31, groups 8 (l >> 5) .. +7
   u32x4* xsp = (u32x4*)(smem + LMP_XS_OFF);  // [3 planes][64 lanes]
-  if (wave == 0) {
+  if (!BF && wave == 0) {
     const int mr = m0 + (lane & 31);
     f32x4 xa = f32x4{0.f, 0.f, 0.f, 0.f}, xb = xa;
     if (mr < M) {
@@ -457,48 +473,65 @@ __global__ __launch_bounds__(64 * LMP_WAVES) void lmhead_q4p_kernel(
     const int ntn = nt + W;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      constexpr int PF = LMP_PF;
       const int sl = g % PF;
       // keep each group's work in its place: the LDS reads and the
       // dequantisation would otherwise be hoisted to the tile start for every
       // group at once (registers for all of them)
       asm volatile("" ::: "memory");
-      u32x4 wv = wq[sl];
-      asm volatile("" : "+v"(wv));
-      f16x8 a[4], al[4];
+      if (BF) {  // k = 64 g + 16 t + 8 (lane >> 5) + e, natural order
+        const uint16_t* brow = (const uint16_t*)arow - 32 * (lane >> 5) + 8 * (lane >> 5);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        a[t] = *(const f16x8*)(arow + g * 64 + 8 * t);
-        al[t] = *(const f16x8*)(arow + 32 * LMP_ROW + g * 64 + 8 * t);
+        for (int t = 0; t < FR; ++t) {
+          u32x4 wv = wq[sl][t];
+          asm volatile("" : "+v"(wv));
+          acc = mfma_bf16(*(const bf16x8*)(brow + g * 64 + 16 * t), __builtin_bit_cast(bf16x8, wv), acc);
+        }
+      } else {
+        u32x4 wv = wq[sl][0];
+        asm volatile("" : "+v"(wv));
+        f16x8 a[4], al[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          a[t] = *(const f16x8*)(arow + g * 64 + 8 * t);
+          al[t] = *(const f16x8*)(arow + 32 * LMP_ROW + g * 64 + 8 * t);
+        }
+        f32x16 c = f32x16{};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const f16x8 b = __builtin_bit_cast(f16x8, q4_word_to_f16x8(wv[t], kq));
+          c = mfma_f16(a[t], b, c);
+          c = mfma_f16(al[t], b, c);
+        }
+        const float s = bf16_bits_to_float(wsb[sl] & 0xffffu);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = fmaf(s, c[r], acc[r]);
+        // bias of group g into the bf16 B operand of the bias product
+        if (g & 1) bpk[g >> 1] |= wsb[sl] & 0xffff0000u;
+        else bpk[g >> 1] = wsb[sl] >> 16;
       }
-      f32x16 c = f32x16{};
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const f16x8 b = __builtin_bit_cast(f16x8, q4_word_to_f16x8(wv[t], kq));
-        c = mfma_f16(a[t], b, c);
-        c = mfma_f16(al[t], b, c);
-      }
-      const float s = bf16_bits_to_float(wsb[sl] & 0xffffu);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] = fmaf(s, c[r], acc[r]);
-      // bias of group g into the bf16 B operand of the bias product
-      if (g & 1) bpk[g >> 1] |= wsb[sl] & 0xffff0000u;
-      else bpk[g >> 1] = wsb[sl] >> 16;
       // the slot's next group: g + PF of this tile, else g + PF - G of the next
       if (g + PF < G || decltype(prefetch)::value) {
         const int tn = g + PF < G ? nt : ntn, gn = g + PF < G ? g + PF : g + PF - G;
-        wq[sl] = __builtin_nontemporal_load(q4_tile_words(qw, tn, G, gn, lane));
-        wsb[sl] = __builtin_nontemporal_load(&sb[((int64_t)tn * G + gn) * 32 + (lane & 31)]);
+#pragma unroll
+        for (int f = 0; f < FR; ++f) wq[sl][f] = __builtin_nontemporal_load(wfrag(tn, gn, f));
+        if (!BF)
+          wsb[sl] = __builtin_nontemporal_load(&sb[((int64_t)tn * G + gn) * 32 + (lane & 31)]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    const bool hi_half = lane >= 32;
-    u32x4 bb;
+    if (BF) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) bb[j] = hi_half ? bpk[4 + j] : bpk[j];
-    const bf16x8 bv = __builtin_bit_cast(bf16x8, bb);
+      for (int r = 0; r < 16; ++r) acc[r] = round_bf16(acc[r]);
+    } else {
+      const bool hi_half = lane >= 32;
+      u32x4 bb;
 #pragma unroll
-    for (int p = 0; p < 3; ++p) acc = mfma_bf16(__builtin_bit_cast(bf16x8, xsp[64 * p + lane]), bv, acc);
+      for (int j = 0; j < 4; ++j) bb[j] = hi_half ? bpk[4 + j] : bpk[j];
+      const bf16x8 bv = __builtin_bit_cast(bf16x8, bb);
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+        acc = mfma_bf16(__builtin_bit_cast(bf16x8, xsp[64 * p + lane]), bv, acc);
+    }
 
     if (logits_out) {
       // rows m0 + 4 (lane >> 5) + 8 (r >> 2) + (r & 3): per-r offsets are uniform
@@ -691,23 +724,34 @@ void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* 
   require(w.K % chunk_k == 0 || w.K % 64 == 0, "lm head K must be a multiple of 64");
   int NB = w.N / 64;
   constexpr int WAVES = 4;
-  // K = 1024 q4 heads run on the persistent kernel (DRT_LMHEAD_CHUNKED=1 keeps
+  // K = 1024 heads (q4 or bf16) run on the persistent kernel (DRT_LMHEAD_CHUNKED=1 keeps
   // them on the chunked one, an A/B switch for parity and timing comparisons)
   static const bool chunked = getenv("DRT_LMHEAD_CHUNKED") != nullptr;
-  if (w.q4 && w.K == LMP_G * 64 && !chunked) {
+  if (w.K == LMP_G * 64 && !chunked) {
     int dev = 0, n_cu = 0;
     DRT_HIP(hipGetDevice(&dev));
     DRT_HIP(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
     const int U = w.N / 32;
     NB = std::max(1, std::min(n_cu, U / LMP_WAVES));  // one work-group per CU
-    auto fn = lmhead_q4p_kernel;
-    static size_t granted = 0;
-    grant_lds((const void*)fn, LMP_LDS, granted);
-    const double bytes = (double)w.N * w.K / 2 + (double)w.N * w.K / 16 + 2.0 * M * w.K;
-    DRT_LAUNCH(Profiler::LMHEAD, bytes, fn, dim3(NB, 1, (M + 31) / 32), dim3(64 * LMP_WAVES),
-               LMP_LDS, s, w.qw.as<uint32_t>(), w.sb.as<uint32_t>(), (const uint16_t*)act, xsum,
-               M, w.N, logits_out, (LmStat*)stats, temperature, seed, step, positions, desc,
-               exclude_col);
+    if (w.q4) {
+      auto fn = lmhead_q4p_kernel<0>;
+      static size_t granted = 0;
+      grant_lds((const void*)fn, LMP_LDS, granted);
+      const double bytes = (double)w.N * w.K / 2 + (double)w.N * w.K / 16 + 2.0 * M * w.K;
+      DRT_LAUNCH(Profiler::LMHEAD, bytes, fn, dim3(NB, 1, (M + 31) / 32), dim3(64 * LMP_WAVES),
+                 LMP_LDS, s, w.qw.as<uint32_t>(), w.sb.as<uint32_t>(), (const uint16_t*)act,
+                 xsum, M, w.N, logits_out, (LmStat*)stats, temperature, seed, step, positions,
+                 desc, exclude_col);
+    } else {
+      auto fn = lmhead_q4p_kernel<1>;
+      static size_t granted = 0;
+      grant_lds((const void*)fn, LMP_LDS, granted);
+      const double bytes = 2.0 * w.N * w.K + 2.0 * M * w.K;
+      DRT_LAUNCH(Profiler::LMHEAD, bytes, fn, dim3(NB, 1, (M + 31) / 32), dim3(64 * LMP_WAVES),
+                 LMP_LDS, s, (const uint32_t*)w.wb.as<uint16_t>(), (const uint32_t*)nullptr,
+                 (const uint16_t*)act, xsum, M, w.N, logits_out, (LmStat*)stats, temperature,
+                 seed, step, positions, desc, exclude_col);
+    }
   } else {
   const size_t lds = (size_t)(w.q4 ? 2 : 1) * 32 * (chunk_k + 8) * 2 +
                      (size_t)32 * (chunk_k / 64) * 4 + (size_t)WAVES * 32 * 65 * 4;
