@@ -22,6 +22,13 @@
 // registers per lane) hide each other's waits.
 // Split-K over blockIdx.z (KS slices) writes fp32 partial slices y + ks * M * N
 // that a reduce pass sums (residual_norm_kernel).
+// Split last round (tail.kt >= 2, one-dimensional grid): when the tiles fill the
+// device's work-group slots (two per CU) once with a few left over, the first
+// tail.full tiles run whole and each of the remaining ones is split into tail.kt
+// K ranges on as many work-groups of one XCD, so the last round takes a fraction
+// of a tile instead of leaving most CUs idle. The slices meet as in the split-K
+// decode linears: each writes its partial tile, counts its arrival in that XCD's
+// L2, and the last to arrive adds the slices in slice order and runs the epilogue.
 // Epilogues run on 32-row pieces of the tile staged through LDS:
 //   EPI_STORE : y (+ bias on slice 0)
 //   EPI_SWIGLU: [gate 64 | up 64] column blocks -> silu(g) * u -> ACT_F16P
@@ -73,11 +80,38 @@ DRT_DEV void lds_read16(f16x8& v, uint32_t addr) {
 
 }  // namespace
 
+struct BgTail {
+  int full = 0;            // whole tiles (tile t = work-group t)
+  int kt = 0;              // K slices per remaining tile (0: the three-dimensional grid)
+  int tx = 0;              // tiles per row of tiles (tile t: column t % tx, row t / tx)
+  float* part = nullptr;   // [remaining tiles][kt][128 * 256] partial tiles
+  int* count = nullptr;    // [remaining tiles] arrival counters, zero on entry and exit
+};
+constexpr int BG_TAIL_KT_MAX = 8;
+
 template <int EPI>
-__global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int KS) {
+__global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int KS, const BgTail tail) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int M = a.M, N = a.N, K = a.K, G = K >> 6;
-  const int n0 = blockIdx.x * BG_WN, m0 = blockIdx.y * BG_WM, ks = blockIdx.z;
+  int tile_x = blockIdx.x, tile_y = blockIdx.y, ks = blockIdx.z, tail_idx = -1;
+  if (EPI == EPI_SWIGLU && tail.kt) {
+    // work-group b: tile b, or K slice of a remaining tile; the slices of one
+    // remaining tile share b % 8, i.e. one XCD (full % 8 == 0)
+    const int b = blockIdx.x;
+    int t = b;
+    ks = 0;
+    KS = 1;
+    if (b >= tail.full) {
+      const int j = b - tail.full, q = j >> 3;
+      tail_idx = (j & 7) + 8 * (q / tail.kt);
+      ks = q % tail.kt;
+      KS = tail.kt;
+      t = tail.full + tail_idx;
+    }
+    tile_x = t % tail.tx;
+    tile_y = t / tail.tx;
+  }
+  const int n0 = tile_x * BG_WN, m0 = tile_y * BG_WM;
   const int g_lo = (int)((int64_t)G * ks / KS), g_hi = (int)((int64_t)G * (ks + 1) / KS);
   const int n_g = g_hi - g_lo;
   const int NT = N >> 5;
@@ -159,6 +193,44 @@ __global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int K
     step(gb, Slot<0>{});
     if (gb + 1 < n_g) step(gb + 1, Slot<1>{});
   }
+  if (EPI == EPI_SWIGLU && tail_idx >= 0) {  // (the split last round is used for gate|up)
+    // a K slice of a remaining tile: store it, lane-major (value i of thread t
+    // at i * 256 + t), and let the last slice to arrive add them all in order
+    float* pt = tail.part + (size_t)tail_idx * tail.kt * (BG_WM * BG_WN);
+    float* mine = pt + (size_t)ks * (BG_WM * BG_WN) + threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mine[((i * 2 + j) * 16 + r) * 256] = acc[i][j][r];
+    __shared__ int last_flag;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // every store of the work-group is in this XCD's L2
+    if (threadIdx.x == 0)
+      last_flag = __hip_atomic_fetch_add(&tail.count[tail_idx], 1, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_WORKGROUP) == tail.kt - 1;
+    __syncthreads();
+    if (!last_flag) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int at = ((i * 2 + j) * 16 + r) * 256 + threadIdx.x;
+          float v[BG_TAIL_KT_MAX];
+#pragma unroll
+          for (int k = 0; k < BG_TAIL_KT_MAX; ++k)  // every slice's value loaded first
+            v[k] = pt[(size_t)min(k, tail.kt - 1) * (BG_WM * BG_WN) + at];
+          float sum = 0.f;
+#pragma unroll
+          for (int k = 0; k < BG_TAIL_KT_MAX; ++k)
+            if (k < tail.kt) sum += k == ks ? acc[i][j][r] : v[k];
+          acc[i][j][r] = sum;
+        }
+    if (threadIdx.x == 0) tail.count[tail_idx] = 0;
+  }
   __syncthreads();  // every wave's last fragment reads are done: the epilogue reuses the LDS
 
   // Epilogue in 32-row pieces (MFMA m-tile p of every wave) through LDS.
@@ -234,9 +306,9 @@ __global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int K
   }
 }
 
-template __global__ void big_q4_kernel<EPI_STORE>(const FusedArgs, int);
-template __global__ void big_q4_kernel<EPI_SWIGLU>(const FusedArgs, int);
-template __global__ void big_q4_kernel<EPI_QKV>(const FusedArgs, int);
+template __global__ void big_q4_kernel<EPI_STORE>(const FusedArgs, int, const BgTail);
+template __global__ void big_q4_kernel<EPI_SWIGLU>(const FusedArgs, int, const BgTail);
+template __global__ void big_q4_kernel<EPI_QKV>(const FusedArgs, int, const BgTail);
 
 // The QKV epilogue of a split-K q|k|v projection: work-group (head, 32-row
 // block) sums the KS fp32 partial slices of its head's 128 columns (bias
@@ -320,11 +392,38 @@ bool big_linear_supported(const FusedArgs& a, int kind) {
   return kind == FL_QKV || kind == FL_SWIGLU || kind == FL_STORE;
 }
 
-void big_linear(const FusedArgs& a, int kind, int KS, hipStream_t s) {
+size_t big_tail_part_floats(int M, int N, int K, int n_cu) {
+  const int tx = (N + BG_WN - 1) / BG_WN, T = tx * ((M + BG_WM - 1) / BG_WM), S = 2 * n_cu;
+  if (n_cu < 1 || T <= S) return 0;
+  const int full = T / S * S, rest = T - full;
+  const int kt = std::min(BG_TAIL_KT_MAX, std::min(S / std::max(rest, 1), K / 64));
+  if (rest % 8 || kt < 2) return 0;
+  return (size_t)rest * kt * BG_WM * BG_WN;
+}
+
+void big_linear(const FusedArgs& a, int kind, int KS, hipStream_t s, float* tail_part,
+                size_t tail_part_floats, int* tail_count, int n_tail_count) {
   require(big_linear_supported(a, kind), "large-M linear: unsupported shape or kind");
   require(KS >= 1 && KS <= a.K / 64 && (KS == 1 || kind == FL_STORE),
           "large-M linear: split-K only for plain stores");
-  const dim3 grid((a.N + BG_WN - 1) / BG_WN, (a.M + BG_WM - 1) / BG_WM, KS);
+  dim3 grid((a.N + BG_WN - 1) / BG_WN, (a.M + BG_WM - 1) / BG_WM, KS);
+  BgTail tail;
+  if (kind == FL_SWIGLU && KS == 1 && tail_part && tail_count && !a.fenced && a.n_xcc == 8) {
+    // the tiles past the last whole round of two work-groups per CU, split by K
+    int dev = 0, n_cu = 0;
+    DRT_HIP(hipGetDevice(&dev));
+    DRT_HIP(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
+    const size_t need = big_tail_part_floats(a.M, a.N, a.K, n_cu);
+    const int T = (int)(grid.x * grid.y), S = 2 * n_cu;
+    if (need && need <= tail_part_floats && T - T / S * S <= n_tail_count) {
+      tail.full = T / S * S;
+      tail.kt = std::min(BG_TAIL_KT_MAX, std::min(S / (T - tail.full), a.K / 64));
+      tail.tx = (int)grid.x;
+      tail.part = tail_part;
+      tail.count = tail_count;
+      grid = dim3((unsigned)(tail.full + (T - tail.full) * tail.kt), 1, 1);
+    }
+  }
   const double bytes = (double)a.N * a.K / 2 + (double)a.N * a.K / 16 + 2.0 * a.M * a.K +
                        (kind == FL_STORE ? 4.0 * KS : 2.0) * a.M * a.N;
 #define DRT_BG(E)                                                                        \
@@ -332,7 +431,7 @@ void big_linear(const FusedArgs& a, int kind, int KS, hipStream_t s) {
     auto fn = big_q4_kernel<E>;                                                          \
     static size_t granted = 0;                                                           \
     grant_lds((const void*)fn, BG_LDS, granted);                                         \
-    DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(256), BG_LDS, s, a, KS);            \
+    DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(256), BG_LDS, s, a, KS, tail);      \
   }
   if (kind == FL_QKV) DRT_BG(EPI_QKV)
   else if (kind == FL_SWIGLU) DRT_BG(EPI_SWIGLU)

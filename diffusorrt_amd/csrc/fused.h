@@ -85,7 +85,13 @@ int skinny_counters(int N);
 // y + ks * M * N for a reduce pass).
 bool big_linear_supported(const FusedArgs& a, int kind);
 int big_linear_splits(int M, int N, int K, int max_ks);
-void big_linear(const FusedArgs& a, int kind, int KS, hipStream_t s);
+// tail_part / tail_count (optional): the workspace of the split last round (see
+// big_linear.hip), big_tail_part_floats() floats and one counter per split tile,
+// zero on entry and left zero.
+void big_linear(const FusedArgs& a, int kind, int KS, hipStream_t s, float* tail_part = nullptr,
+                size_t tail_part_floats = 0, int* tail_count = nullptr, int n_tail_count = 0);
+size_t big_tail_part_floats(int M, int N, int K, int n_cu);
+constexpr int BIG_TAIL_COUNTERS = 512;  // split tiles a runtime's counters cover
 // q|k|v projection + epilogue: split-K into `part` (when the tiles alone would
 // leave CUs idle and part_floats suffices) and a separate epilogue pass.
 void big_qkv(const FusedArgs& a, float* part, size_t part_floats, hipStream_t s);

@@ -132,7 +132,7 @@ struct Runtime {
   DevBuf sk_part, sk_counters, sk_ss;
   // large-M (> 32 rows) q4 forwards: the down projection's input activation and
   // the split-K partial slices of o_proj / down_proj
-  DevBuf act2, big_part;
+  DevBuf act2, big_part, big_tail_count;
   size_t big_part_floats = 0;
   size_t sk_part_floats = 0;
   // The split-K linears serve every <= 32-row q4 linear (their residual
@@ -449,8 +449,16 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
           bf = std::max(bf, (size_t)big_linear_splits(rows, d, K2, BG_RESID_MAX_KS) * rows * d);
         bf = std::max(bf, (size_t)big_linear_splits(rows, n_qkv, d, BG_QKV_MAX_KS) * rows * n_qkv);
       }
+      // the gate|up projection's split last round shares the workspace (it runs
+      // between the q|k|v and down projections, which use it too)
+      int n_cu = 0;
+      DRT_HIP(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, rt->device));
+      for (int mt = 1; mt <= (M + 127) / 128; ++mt)
+        bf = std::max(bf, big_tail_part_floats(std::min(M, mt * 128), 2 * F, d, n_cu));
       rt->big_part_floats = bf;
       rt->big_part.alloc(bf * 4);
+      rt->big_tail_count.alloc((size_t)BIG_TAIL_COUNTERS * 4);
+      DRT_HIP(hipMemsetAsync(rt->big_tail_count.p, 0, rt->big_tail_count.bytes, s));
     }
     int nx = 1;
     if (hipDeviceGetAttribute(&nx, hipDeviceAttributeNumberOfXccs, rt->device) != hipSuccess)
@@ -751,7 +759,8 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
       fg.act = rt.act.p;
       fg.act_out = rt.act2.p;
       fg.act_fmt = ACT_F16P;
-      big_linear(fg, FL_SWIGLU, 1, s);
+      big_linear(fg, FL_SWIGLU, 1, s, bpart, rt.big_part_floats, rt.big_tail_count.as<int>(),
+                 BIG_TAIL_COUNTERS);
       FusedArgs fd = base(w.down);
       fd.act = rt.act2.p;
       big_resid(fd, last ? nullptr : rt.layers[l + 1].in_norm.as<uint16_t>());
