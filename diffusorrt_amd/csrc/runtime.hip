@@ -1528,8 +1528,10 @@ int32_t drt_session_bd3_decode(uint64_t session, int32_t prompt_len, int32_t max
         }
       }
       const int quota = L.base + (step % L.spb < L.rem ? 1 : 0);
-      L.step = step + 1;
-      if (frontier.empty() || quota == 0) continue;
+      if (frontier.empty() || quota == 0) {
+        L.step = step + 1;
+        continue;
+      }
       const int nf = (int)frontier.size();
       sc.assign(nf, 0.0);
       tk.assign(nf, 0);
@@ -1539,8 +1541,10 @@ int32_t drt_session_bd3_decode(uint64_t session, int32_t prompt_len, int32_t max
       ++forwards;
       order.resize(nf);
       for (int i = 0; i < nf; ++i) order[i] = i;
-      std::stable_sort(order.begin(), order.end(),
-                       [&](int a, int b) { return sc[a] > sc[b]; });
+      // highest score first, equal scores in row order; a NaN score ranks as
+      // -inf (a strict weak order for the sort)
+      auto key = [&](int i) { return std::isnan(sc[i]) ? -INFINITY : sc[i]; };
+      std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return key(a) > key(b); });
       const int k = std::min(quota, nf);
       for (int i = 0; i < k; ++i) {
         const int r = order[i];
@@ -1548,6 +1552,7 @@ int32_t drt_session_bd3_decode(uint64_t session, int32_t prompt_len, int32_t max
         s->canvas[frontier[r]] = tk[r];
       }
       committed += k;
+      L.step = step + 1;  // only once the step is committed: a failed call repeats it
     }
     if (out_forwards) *out_forwards = forwards;
     if (out_committed) *out_committed = committed;
