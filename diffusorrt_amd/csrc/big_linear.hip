@@ -459,6 +459,11 @@ void big_qkv(const FusedArgs& a, float* part, size_t part_floats, hipStream_t s)
   g.bias = nullptr;  // the epilogue adds it
   g.y = part;
   big_linear(g, FL_STORE, ks, s);
+  qkv_epilogue_slices(a, part, ks, s);
+}
+
+void qkv_epilogue_slices(const FusedArgs& a, const float* part, int ks, hipStream_t s) {
+  require(ks >= 1 && ks <= BG_QKV_MAX_KS && a.N % 128 == 0, "q|k|v epilogue: 1..4 slices");
   const dim3 grid(a.N / 128, (a.M + 31) / 32);
   if (a.kv_bf16)
     hipLaunchKernelGGL(big_qkv_epilogue_kernel<__bf16>, grid, dim3(256), 0, s, a, part, ks);

@@ -95,9 +95,31 @@ constexpr int BIG_TAIL_COUNTERS = 512;  // split tiles a runtime's counters cove
 // q|k|v projection + epilogue: split-K into `part` (when the tiles alone would
 // leave CUs idle and part_floats suffices) and a separate epilogue pass.
 void big_qkv(const FusedArgs& a, float* part, size_t part_floats, hipStream_t s);
+// The per-head q|k|v epilogue (bias, q/k norm, RoPE, Q out, K/V into the cache)
+// of a projection given as ks <= BG_QKV_MAX_KS fp32 slices [ks][M][N].
+void qkv_epilogue_slices(const FusedArgs& a, const float* part, int ks, hipStream_t s);
 constexpr int BG_QKV_MAX_KS = 4;    // split-K slices of the q|k|v projection
 constexpr int BG_RESID_MAX_KS = 8;  // ... of o_proj / down_proj (reduced with the next norm)
 constexpr int BG_OP_MAX_KS = 8;     // ... of the per-op linear (summed into its output)
+// Weight-streaming q4 linears (stream_linear.hip) for M <= 32 rows and at least
+// STREAM_MIN_WEIGHTS weights: the activation's K slice in LDS, the weights of a
+// range of 128-column blocks streamed past it; fp32 K slices y[ks][M][N] out.
+constexpr int64_t STREAM_MIN_WEIGHTS = (int64_t)8 << 20;
+struct StreamPlan {
+  int KS = 0, R = 0, nblk = 0;  // K slices, block ranges, most blocks per range
+  bool single = true;           // the slice's activation fits LDS whole
+};
+bool stream_supported(int M, int N, int K);
+StreamPlan stream_plan(int M, int N, int K, int max_ks);  // KS == 0: not supported
+size_t stream_part_floats(int M, int N, int K, int max_ks);
+// a.hidden set: the input is the fp32 residual stream, RMSNormed (a.norm_w, the
+// row statistics a.ss_in) while staged; else a.act (ACT_F16P).
+void stream_linear(const FusedArgs& f, const StreamPlan& p, hipStream_t s);
+// SwiGLU of [gate 64 | up 64]-interleaved fp32 slices [KS][M][N] -> ACT_F16P [M][N / 2]
+void swiglu_slices(const float* part, int KS, int M, int N, void* act, int* err, hipStream_t s);
+// hidden[M][N] += the KS slices, and the new rows' partial sums of squares ss[N / 32][32]
+void residual_slices(const float* part, int KS, int M, int N, float* hidden, float* ss,
+                     hipStream_t s);
 // y[i] = sum_k part[k * n + i] (+ bias[i % N]) in slice order (the per-op linear's reduce)
 void sum_slices(const float* part, int KS, int64_t n, const uint16_t* bias, int N, float* y,
                 hipStream_t s);

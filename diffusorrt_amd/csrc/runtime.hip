@@ -135,10 +135,14 @@ struct Runtime {
   DevBuf act2, big_part, big_tail_count;
   size_t big_part_floats = 0;
   size_t sk_part_floats = 0;
-  // The split-K linears serve every <= 32-row q4 linear (their residual
-  // epilogues carry the next norm's row statistics). At the 7B shapes they beat
-  // the single-pass kernels too: q|k|v 21.9 vs 43.7 us (36 work-groups of 128
-  // columns leave most CUs idle), o / down 35 vs 32, gate/up 84 vs 87 us.
+  // The split-K linears serve the <= 32-row q4 linears of small layers (their
+  // residual epilogues carry the next norm's row statistics). Layers whose every
+  // linear holds at least STREAM_MIN_WEIGHTS weights (the 7B shapes) forward
+  // <= 32 rows through the weight-streaming linears instead (`streaming`): fp32 K
+  // slices reduced by small passes (residual add + row statistics, q|k|v
+  // epilogue, SwiGLU). The split-K units re-read the activation for every 128
+  // columns there: gate|up 84 us, o / down 35, q|k|v 22 us per call.
+  bool streaming = false;
   int sk_n_counters = 0;
   int n_xcc = 1;
   bool fenced = false;           // split-K exchange through device-scope fences (no placement assumed)
@@ -439,10 +443,18 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
     rt->sk_counters.alloc((size_t)std::max(nc, 1) * 4 * SK_ROW_TILES);
     DRT_HIP(hipMemsetAsync(rt->sk_counters.p, 0, rt->sk_counters.bytes, s));
     rt->sk_ss.alloc((size_t)d * 4 * SK_ROW_TILES);  // [tile][d/32][32]
-    if (rt->q4 && M > 32) {
+    rt->streaming = rt->q4 && stream_supported(32, n_qkv, d) && stream_supported(32, d, Hq * hd) &&
+                 stream_supported(32, 2 * F, d) && stream_supported(32, d, F);
+    if (rt->q4 && (M > 32 || rt->streaming)) {
       rt->act2.alloc((size_t)2 * M * widest * 2);
       size_t bf = 0;
-      const int n_qkv = (Hq + 2 * Hkv) * hd;
+      if (rt->streaming) {
+        const int rows = std::min(M, 32);
+        bf = std::max({stream_part_floats(rows, n_qkv, d, BG_QKV_MAX_KS),
+                       stream_part_floats(rows, d, Hq * hd, BG_RESID_MAX_KS),
+                       stream_part_floats(rows, 2 * F, d, 8),
+                       stream_part_floats(rows, d, F, BG_RESID_MAX_KS)});
+      }
       for (int mt = 1; mt <= (M + 127) / 128; ++mt) {
         const int rows = std::min(M, mt * 128);
         for (int K2 : {Hq * hd, F})
@@ -676,7 +688,12 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
   // activation, the RMSNorms run as their own passes, fused with the split-K
   // reduce and residual add of the projection before them
   const bool big = rt.q4 && M > 32 * SK_ROW_TILES;
-  float* bpart = big ? rt.big_part.as<float>() : nullptr;
+  // <= 32-row forwards of 7B-class layers: the weight-streaming linears (fp32 K
+  // slices, reduced by small passes: residual add + row statistics, q|k|v
+  // epilogue, SwiGLU; the RMSNorms run inside the next linear's staging)
+  const bool stream = !big && rt.streaming && M <= 32;
+  const bool pipe = big || stream;
+  float* bpart = pipe ? rt.big_part.as<float>() : nullptr;
   embed(p.tokens_rel, rt.embed.as<uint16_t>(), hidden, M, d, ss, s,
         p.tokens_at_row0 ? desc : nullptr);
   const int L = (int)rt.layers.size();
@@ -686,11 +703,26 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
                   rt.placement_err.as<int>());
   // split-K projection (o_proj / down_proj) into partial slices, then
   // hidden += sum of the slices and the next norm's activation
-  auto big_resid = [&](FusedArgs f, const uint16_t* next_norm) {
-    const int ks = big_linear_splits(M, f.N, f.K, BG_RESID_MAX_KS);
-    require((size_t)ks * M * f.N <= rt.big_part_floats, "large-M partials exceed the workspace");
+  // fp32 K slices of a projection into bpart (the streaming or the large-M
+  // kernels); returns the slice count
+  auto slices = [&](FusedArgs f, int max_ks) {
+    f.bias = nullptr;  // added by the reduce pass
     f.y = bpart;
+    if (stream) {
+      const StreamPlan sp = stream_plan(M, f.N, f.K, max_ks);
+      require(sp.KS >= 1 && (size_t)sp.KS * M * f.N <= rt.big_part_floats,
+              "streaming linear: no plan or partials exceed the workspace");
+      stream_linear(f, sp, s);
+      return sp.KS;
+    }
+    const int ks = big_linear_splits(M, f.N, f.K, max_ks);
+    require((size_t)ks * M * f.N <= rt.big_part_floats, "large-M partials exceed the workspace");
     big_linear(f, FL_STORE, ks, s);
+    return ks;
+  };
+  auto big_resid = [&](FusedArgs f, const uint16_t* next_norm) {
+    require(f.bias == nullptr, "o_proj / down_proj bias is not supported on this path");
+    const int ks = slices(f, BG_RESID_MAX_KS);
     residual_norm(hidden, bpart, ks, M, false, nullptr, true, next_norm, eps, d, ACT_F16P,
                   rt.act.p, xs, M, s, rt.placement_err.as<int>());
   };
@@ -736,6 +768,8 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
       if (big) {
         f.act = rt.act.p;
         big_qkv(f, bpart, rt.big_part_floats, s);
+      } else if (stream) {  // normed from the residual stream while staged
+        qkv_epilogue_slices(f, bpart, slices(f, BG_QKV_MAX_KS), s);
       } else {
         fused_linear(f, FL_QKV, s);
       }
@@ -751,6 +785,26 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
       attention(rt.kv_bf16, rt.qbuf.p, kv_layer(l), head_stride, M, Hq, Hkv, a.n_keys, a.row0,
                 a.mask_kind, a.mask_prompt_len, a.mask_block, ap, o_part, ml_part, rt.act.p, xs,
                 fmt, s, rt.placement_err.as<int>());
+    if (stream) {
+      // o_proj slices -> hidden += (+ the row statistics of the next norm)
+      FusedArgs fo = base(w.o);
+      require(fo.bias == nullptr, "o_proj bias is not supported on this path");
+      fo.act = rt.act.p;
+      residual_slices(bpart, slices(fo, BG_RESID_MAX_KS), M, d, hidden, ss, s);
+      // post-attention RMSNorm (while staged) -> gate|up slices -> SwiGLU
+      FusedArgs fg = base(w.gu);
+      require(fg.bias == nullptr, "gate|up bias is not supported on this path");
+      fg.hidden = hidden;
+      fg.norm_w = w.post_norm.as<uint16_t>();
+      fg.ss_in = ss;
+      swiglu_slices(bpart, slices(fg, 8), M, fg.N, rt.act2.p, rt.placement_err.as<int>(), s);
+      // down_proj slices -> hidden +=
+      FusedArgs fd = base(w.down);
+      require(fd.bias == nullptr, "down_proj bias is not supported on this path");
+      fd.act = rt.act2.p;
+      residual_slices(bpart, slices(fd, BG_RESID_MAX_KS), M, d, hidden, ss, s);
+      continue;
+    }
     if (big) {
       FusedArgs fo = base(w.o);
       fo.act = rt.act.p;
@@ -1728,6 +1782,7 @@ size_t drt_op_q4_linear_workspace_bytes(int32_t m, int32_t n, int32_t k) {
   if (m <= 0 || k <= 0) return 0;
   size_t b = q4_op_act_bytes(m, k) + 256;
   if (m > 32 && n > 0) b += (size_t)big_linear_splits(m, n, k, BG_OP_MAX_KS) * m * n * 4;
+  if (m <= 32 && n > 0) b += stream_part_floats(m, n, k, BG_OP_MAX_KS) * 4;
   return b;
 }
 
@@ -1783,7 +1838,16 @@ static void q4_linear_into(const void* qw, const void* sb, const void* x, int32_
     f.act_xsum = xs;
     f.y = y;
     const int ks = m > 32 ? big_linear_splits(m, n, k, BG_OP_MAX_KS) : 1;
-    if (ks > 1 && big_linear_supported(f, FL_STORE)) {
+    const StreamPlan sp = stream_plan(m, n, k, BG_OP_MAX_KS);
+    if (sp.KS >= 1) {
+      // large weights, <= 32 rows: streamed in fp32 K slices, summed (+ bias) into y
+      float* part = (float*)(ws + q4_op_act_bytes(m, k));
+      FusedArgs g = f;
+      g.bias = nullptr;
+      g.y = part;
+      stream_linear(g, sp, st);
+      sum_slices(part, sp.KS, (int64_t)m * n, (const uint16_t*)bias, n, y, st);
+    } else if (ks > 1 && big_linear_supported(f, FL_STORE)) {
       // split-K slices in the workspace, summed (+ bias) into y in a fixed order
       float* part = (float*)(ws + q4_op_act_bytes(m, k));
       FusedArgs g = f;
