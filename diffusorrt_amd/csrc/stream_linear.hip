@@ -255,7 +255,7 @@ __global__ __launch_bounds__(512) void stream_q4_kernel(const StreamArgs a) {
   for (int i = 0; i < LOOK; ++i) fetch(i, g_lo + half + 2 * i);
 
   u32x4 nhi[HS], nlo[HS];
-  NormRaw<NORM ? CH : 2> raw;  // (a stand-in of two registers when unused)
+  NormRaw<CH> raw;  // NORM only (unused registers otherwise)
   auto flag_range = [&](bool over) {
     if (over && a.err)
       __hip_atomic_fetch_or(a.err, DRT_ERR_F16_RANGE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -263,7 +263,7 @@ __global__ __launch_bounds__(512) void stream_q4_kernel(const StreamArgs a) {
   if (NORM) {
     // the first chunk's rows and norm weights, then the row statistics (the K /
     // 32 partial sums of squares of each row), under one memory latency
-    st_norm_load<CH>(a, g_lo, g_hi, reinterpret_cast<NormRaw<CH>&>(raw));
+    st_norm_load<CH>(a, g_lo, g_hi, raw);
     const int np = a.K >> 5, r = threadIdx.x & 31, p0 = threadIdx.x >> 5;
     float sv[ST_SS_MAX];
 #pragma unroll
@@ -281,7 +281,7 @@ __global__ __launch_bounds__(512) void stream_q4_kernel(const StreamArgs a) {
       rinv[threadIdx.x] = 1.f / sqrtf(t / (float)a.K + a.eps);
     }
     __syncthreads();
-    flag_range(st_norm_apply<CH>(a, reinterpret_cast<const NormRaw<CH>&>(raw), rinv, nhi, nlo));
+    flag_range(st_norm_apply<CH>(a, raw, rinv, nhi, nlo));
   } else {
     st_load_act<CH>(a, g_lo, g_hi, nhi, nlo);
   }
@@ -348,12 +348,12 @@ __global__ __launch_bounds__(512) void stream_q4_kernel(const StreamArgs a) {
       __syncthreads();
       const bool more = cg0 + CH < g_hi;
       if (more) {  // the next chunk into registers while this one is consumed
-        if (NORM) st_norm_load<CH>(a, cg0 + CH, g_hi, reinterpret_cast<NormRaw<CH>&>(raw));
+        if (NORM) st_norm_load<CH>(a, cg0 + CH, g_hi, raw);
         else st_load_act<CH>(a, cg0 + CH, g_hi, nhi, nlo);
       }
       consume(cg0);
       if (NORM && more)
-        flag_range(st_norm_apply<CH>(a, reinterpret_cast<const NormRaw<CH>&>(raw), rinv, nhi, nlo));
+        flag_range(st_norm_apply<CH>(a, raw, rinv, nhi, nlo));
       __syncthreads();  // the chunk's LDS is read before the next one overwrites it
     }
   }

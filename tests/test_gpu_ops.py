@@ -101,6 +101,33 @@ def test_q4_linear_large_m_ragged_with_bias(k):
     assert np.abs(act16 - ref).max() / np.abs(ref).max() > 2e-5
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 18944, 3584), (9, 18944, 3584), (17, 3584, 18944)])
+def test_q4_linear_stream_ragged_rows_fp32_with_bias(m, n, k):
+    """The weight-streaming kernels (<= 32 rows, >= 8M weights) on ragged row
+    counts with an fp32 input (a nonzero lo plane) and a bias: 1 and 9 rows over
+    a 3-slice plan with 16-group chunks, 17 rows over 8 slices of 37 groups
+    (8-group chunks), against the exact q4 linear in float64."""
+    from diffusorrt_amd import kernels
+
+    _say("q4_linear stream ragged fp32 + bias", m, n, k)
+    gen, q = _q4_case(n, k, seed=11, centred=False)
+    x = torch.randn((m, k), generator=gen)
+    bias = (torch.randn(n, generator=gen) * 0.1).to(torch.bfloat16)
+    w = kernels.DeviceQ4Weight(q.w_q.cuda(), q.scales.cuda(), q.biases.cuda())
+    y = kernels.linear(x.cuda(), w, bias.cuda()).cpu().numpy().astype(np.float64)
+    W = O.Q4Weight(q.w_q.numpy().view(np.uint32), q.scales.float().numpy(),
+                   q.biases.float().numpy())
+    x64 = x.numpy().astype(np.float64)
+    ref = O.q4_linear64(x64, W) + bias.float().numpy()
+    err = np.abs(y - ref).max() / np.abs(ref).max()
+    # an fp16-only activation (no lo plane) misses the bound by a wide margin
+    x16 = x.numpy().astype(np.float16).astype(np.float64)
+    err16 = np.abs(O.q4_linear64(x16, W) + bias.float().numpy() - ref).max() / np.abs(ref).max()
+    _say(f"  err={err:.2e} (fp16-only activation would be {err16:.2e})")
+    assert err < 2e-5
+    assert err16 > 2e-5
+
+
 def test_q4_linear_fp32_input_and_bias():
     from diffusorrt_amd import kernels
 
