@@ -16,9 +16,9 @@
 // exact fp16 integer, y += s * sum(x q) + b * sum(x) in fp32).
 //
 // Slices of up to 16 groups sit in LDS whole (SINGLE). Longer slices (the
-// down projection: K = 18944) go through LDS 8 groups at a time: while a chunk
+// down projection: K = 18944) go through LDS 16 groups at a time: while a chunk
 // is consumed the next one is already loaded into registers, and written to
-// LDS between the two (PREF).
+// LDS between the two (PREF); the weight ring runs on across the chunks.
 //
 // Output: fp32 K slices y[ks][M][N] (no bias); the consumer reduces them in
 // slice order (residual_norm, the q|k|v epilogue, swiglu_slices_kernel,
@@ -205,16 +205,15 @@ DRT_DEV void st_store(const u32x4 (&hi)[CH / 2], const u32x4 (&lo)[CH / 2], uint
 
 }  // namespace
 
-// NBLK: most blocks a work-group's range holds; CH: groups per LDS chunk (16:
-// the slice fits whole; 8: chunks, the next one held in registers while the
-// current one is consumed); LOOK: steps of weights in flight per wave (divides
+// NBLK: most blocks a work-group's range holds; CH: groups per LDS chunk; PREF:
+// the slice takes several chunks, the next one held in registers while the
+// current one is consumed; LOOK: steps of weights in flight per wave (divides
 // CH / 2); NORM: the input is the fp32 residual stream, RMSNormed while staged.
 // 8 waves: wave w takes n-tile w & 3 of every block and the groups of parity
 // w >> 2 of each chunk (two waves per SIMD, so one's MFMAs run under the
 // other's VALU work); the two halves' sums meet in LDS at the end.
-template <int NBLK, int CH, int LOOK, bool NORM>
+template <int NBLK, int CH, int LOOK, bool NORM, bool PREF>
 __global__ __launch_bounds__(512) void stream_q4_kernel(const StreamArgs a) {
-  constexpr bool PREF = CH == 8;
   constexpr int HS = CH / 2;  // steps of one half per chunk
   static_assert(HS % LOOK == 0, "the weight ring must cycle within a chunk");
   constexpr int UNR = LOOK < 4 ? 4 : LOOK;  // steps unrolled (the bias slots stay static)
@@ -251,8 +250,13 @@ __global__ __launch_bounds__(512) void stream_q4_kernel(const StreamArgs a) {
       wsb[slot][j] = a.sb[u * 32 + (lane & 31)];
     }
   };
+  // the ring's first weights go out after the slice's activation loads: the
+  // vector memory counter retires in order, so the staging (from L2) would
+  // otherwise wait for the weights (from HBM) before it could start
+  auto fill_ring = [&]() {
 #pragma unroll
-  for (int i = 0; i < LOOK; ++i) fetch(i, g_lo + half + 2 * i);
+    for (int i = 0; i < LOOK; ++i) fetch(i, g_lo + half + 2 * i);
+  };
 
   u32x4 nhi[HS], nlo[HS];
   NormRaw<CH> raw;  // NORM only (unused registers otherwise)
@@ -268,6 +272,7 @@ __global__ __launch_bounds__(512) void stream_q4_kernel(const StreamArgs a) {
     float sv[ST_SS_MAX];
 #pragma unroll
     for (int e = 0; e < ST_SS_MAX; ++e) sv[e] = a.ss_in[min(p0 + 16 * e, np - 1) * 32 + r];
+    fill_ring();
     float q = 0.f;
 #pragma unroll
     for (int e = 0; e < ST_SS_MAX; ++e) q += sv[e] * (p0 + 16 * e < np ? 1.f : 0.f);
@@ -284,6 +289,7 @@ __global__ __launch_bounds__(512) void stream_q4_kernel(const StreamArgs a) {
     flag_range(st_norm_apply<CH>(a, raw, rinv, nhi, nlo));
   } else {
     st_load_act<CH>(a, g_lo, g_hi, nhi, nlo);
+    fill_ring();
   }
   f32x16 acc[NBLK];
 #pragma unroll
@@ -466,11 +472,14 @@ __global__ __launch_bounds__(256) void swiglu_slices_kernel(const float* __restr
                                          __HIP_MEMORY_SCOPE_AGENT);
 }
 
-#define DRT_ST(NB, CH, LK)                                                         \
-  template __global__ void stream_q4_kernel<NB, CH, LK, false>(const StreamArgs);   \
-  template __global__ void stream_q4_kernel<NB, CH, LK, true>(const StreamArgs);
+#define DRT_ST(NB, CH, LK)                                                            \
+  template __global__ void stream_q4_kernel<NB, CH, LK, false, false>(const StreamArgs); \
+  template __global__ void stream_q4_kernel<NB, CH, LK, true, false>(const StreamArgs);
 DRT_ST(1, 16, 8) DRT_ST(2, 16, 8) DRT_ST(3, 16, 4) DRT_ST(4, 16, 4) DRT_ST(5, 16, 2)
-DRT_ST(1, 8, 4) DRT_ST(2, 8, 4)
+// slices longer than one chunk take an ACT_F16P input only (a normed input has
+// K = d <= 4096, which the planner always cuts into slices of <= 16 groups)
+template __global__ void stream_q4_kernel<1, 16, 8, false, true>(const StreamArgs);
+template __global__ void stream_q4_kernel<2, 16, 4, false, true>(const StreamArgs);
 #undef DRT_ST
 
 namespace drt {
@@ -550,9 +559,17 @@ void stream_linear(const FusedArgs& f, const StreamPlan& p, hipStream_t s) {
                f.placement_err, f.y, f.M, f.N, f.K, p.KS, p.R};
   const dim3 grid((unsigned)(p.R * p.KS));
   const double bytes = (double)f.N * f.K * 0.5625 + 4.0 * f.M * f.K + 4.0 * p.KS * f.M * f.N;
-#define DRT_STL(NB, CH, LK)                                                              \
+#define DRT_STL(NB, CH, LK)                                                             \
   {                                                                                      \
-    auto fn = norm ? stream_q4_kernel<NB, CH, LK, true> : stream_q4_kernel<NB, CH, LK, false>; \
+    auto fn = norm ? stream_q4_kernel<NB, CH, LK, true, false>                           \
+                   : stream_q4_kernel<NB, CH, LK, false, false>;                         \
+    static size_t granted = 0;                                                           \
+    grant_lds((const void*)fn, st_lds(CH), granted);                                     \
+    DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(512), st_lds(CH), s, a);            \
+  }
+#define DRT_STP(NB, CH, LK)                                                             \
+  {                                                                                      \
+    auto fn = stream_q4_kernel<NB, CH, LK, false, true>;                                 \
     static size_t granted = 0;                                                           \
     grant_lds((const void*)fn, st_lds(CH), granted);                                     \
     DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(512), st_lds(CH), s, a);            \
@@ -568,9 +585,11 @@ void stream_linear(const FusedArgs& f, const StreamPlan& p, hipStream_t s) {
       default: fail(INTERNAL_ERROR, "streaming linear: bad plan");
     }
   } else {
-    if (p.nblk == 1) DRT_STL(1, 8, 4) else if (p.nblk == 2) DRT_STL(2, 8, 4)
+    require(!norm, "streaming linear: a normed input must fit one chunk per slice");
+    if (p.nblk == 1) DRT_STP(1, 16, 8) else if (p.nblk == 2) DRT_STP(2, 16, 4)
     else fail(INTERNAL_ERROR, "streaming linear: bad plan");
   }
+#undef DRT_STP
 #undef DRT_STL
   DRT_HIP(hipGetLastError());
 }
