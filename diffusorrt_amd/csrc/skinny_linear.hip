@@ -197,8 +197,35 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
   int* flag = (int*)(red + SK_RED);
   uint16_t* vbuf = (uint16_t*)(smem + SK_WIDE_V_OFF(U));  // [4096] V tile half (QKV)
 
-  // 1. this wave's weights for the U units, issued first (bf16: the unit's four
-  // 16-k MFMA fragments)
+  // Loads in the order their data is needed: vector memory loads retire in
+  // issue order, so data from L2 issued behind the weights (from HBM) would
+  // wait for them. 1. row statistics: thread (group g = tid / 32, row r = tid %
+  // 32) loads the producer's partial sums of squares g, g + 8, ... at once.
+  // Every load of steps 1-3 is unconditional (rows past M read row M - 1 and are
+  // zeroed by their norm factor, partial sums past the last are clamped and
+  // masked after the wait): a load under a branch makes the compiler wait for it
+  // inside the branch, i.e. for every load issued before it.
+  const int np = K >> 5;  // <= 8 * SK_SS_PER_THREAD
+  float sv[SK_SS_PER_THREAD];
+#pragma unroll
+  for (int e = 0; e < SK_SS_PER_THREAD; ++e)
+    sv[e] = ss_in[min((int)(threadIdx.x >> 5) + 8 * e, np - 1) * 32 + (threadIdx.x & 31)];
+  // 2. the hidden slice (8-wide items: U per thread) and the matching norm weights
+  f32x4 hv[U][2];
+  u32x4 nw[U];
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const int it = threadIdx.x + 256 * j;
+    const int r = it / (8 * U), c8 = it - r * (8 * U);
+    const int k = kc0 + c8 * 8;
+    const f32x4* src = (const f32x4*)(hidden + (int64_t)min(r, M - 1) * K + k);
+    hv[j][0] = src[0];
+    hv[j][1] = src[1];
+    nw[j] = *(const u32x4*)(norm_w + k);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // 3. this wave's weights for the U units (bf16: the unit's four 16-k MFMA
+  // fragments), in flight while the row statistics and the norm are computed
   u32x4 wq[U][BF ? 4 : 1];
   uint32_t wsb[U];
 #pragma unroll
@@ -214,37 +241,14 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
       wsb[u] = q4_tile_sb(sbp, nt, G, u0 + u, lane);
     }
   }
-  // 2. the hidden slice (8-wide items: U per thread) and the matching norm weights.
-  // Every load of steps 1-3 is unconditional (rows past M read row M - 1 and are
-  // zeroed by their norm factor, partial sums past the last are clamped and
-  // masked after the wait): a load under a branch makes the compiler wait for it
-  // inside the branch, i.e. for every load issued before it.
-  f32x4 hv[U][2];
-  u32x4 nw[U];
-#pragma unroll
-  for (int j = 0; j < U; ++j) {
-    const int it = threadIdx.x + 256 * j;
-    const int r = it / (8 * U), c8 = it - r * (8 * U);
-    const int k = kc0 + c8 * 8;
-    const f32x4* src = (const f32x4*)(hidden + (int64_t)min(r, M - 1) * K + k);
-    hv[j][0] = src[0];
-    hv[j][1] = src[1];
-    nw[j] = *(const u32x4*)(norm_w + k);
-  }
-  // 3. row statistics from the producer's partial sums of squares: thread
-  // (group g = tid / 32, row r = tid % 32) loads partials g, g + 8, ... all at
-  // once (one memory round trip); the 8 group sums are added in order.
-  {
-    const int np = K >> 5;  // <= 8 * SK_SS_PER_THREAD
-    const int r = threadIdx.x & 31, g8 = threadIdx.x >> 5;
-    float sv[SK_SS_PER_THREAD];
-#pragma unroll
-    for (int e = 0; e < SK_SS_PER_THREAD; ++e) sv[e] = ss_in[min(g8 + 8 * e, np - 1) * 32 + r];
+  __builtin_amdgcn_sched_barrier(0);
+  {  // the 8 group sums of each row, added in order
+    const int g8 = threadIdx.x >> 5;
     float q = 0.f;
 #pragma unroll
     for (int e = 0; e < SK_SS_PER_THREAD; ++e)  // a product, not a select, so that
       q += sv[e] * (g8 + 8 * e < np ? 1.f : 0.f);  // the load is not sunk into a branch
-    red[g8 * 32 + r] = q;
+    red[g8 * 32 + (threadIdx.x & 31)] = q;
   }
   __syncthreads();
   if (threadIdx.x < 32) {
@@ -439,11 +443,26 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
   for (int ub = u_lo; ub < u_hi || ub == u_lo; ub += UW) {
     u32x4 wq[UW][BF ? 4 : 1], craw[UW][4], crawl[UW][4], af[UW][4], afl[UW][4];
     uint32_t wsb[UW];
+    // the activation (from L2) is issued before the weights (from HBM): loads
+    // retire in issue order, so the LDS transpose below would otherwise wait
+    // for the weights too. Units are clamped to a valid one; a unit beyond the
+    // wave's range gets scale and bias 0 (bf16: it is not multiplied), an exact
+    // no-op, so every load is used unconditionally.
 #pragma unroll
     for (int i = 0; i < UW; ++i) {
-      // clamped to a valid unit; a unit beyond the wave's range gets scale and
-      // bias 0 (bf16: it is not multiplied), an exact no-op, so every load is
-      // used unconditionally
+      const int u = min(ub + i, max(u_hi, u_lo + 1) - 1);
+      // the unit's 32 x 64 activation block as four coalesced loads of 8 rows x
+      // 128 B (rows past M read row M - 1: their outputs are never stored)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t off = (int64_t)min(8 * j + (lane >> 3), M - 1) * K + u * 64 + (lane & 7) * 8;
+        craw[i][j] = *(const u32x4*)(act + off);
+        if (!BF) crawl[i][j] = *(const u32x4*)(act_lo + off);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < UW; ++i) {
       const int u = min(ub + i, max(u_hi, u_lo + 1) - 1);
       if (BF) {
 #pragma unroll
@@ -455,15 +474,8 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
         wq[i][0] = __builtin_nontemporal_load(q4_tile_words(qw, nt, G, u, lane));
         wsb[i] = ub + i < u_hi ? q4_tile_sb(sbp, nt, G, u, lane) : 0u;
       }
-      // the unit's 32 x 64 activation block as four coalesced loads of 8 rows x
-      // 128 B (rows past M read row M - 1: their outputs are never stored)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t off = (int64_t)min(8 * j + (lane >> 3), M - 1) * K + u * 64 + (lane & 7) * 8;
-        craw[i][j] = *(const u32x4*)(act + off);
-        if (!BF) crawl[i][j] = *(const u32x4*)(act_lo + off);
-      }
     }
+    __builtin_amdgcn_sched_barrier(0);
     // through LDS into the q4 fragment order: lane l takes row l & 31, 16-byte
     // chunks 4(l >> 5) + t, i.e. k = 32(l >> 5) + 8t .. +8 (one wave's LDS
     // operations run in order: no barrier)
