@@ -791,51 +791,57 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
     }
     l_run[0] += __shfl_xor(l_run[0], 32, 64);
   }
+  // Merge: the waves of phase p > 0 leave their O (fragment layout) and (m, l)
+  // in LDS; the phase-0 wave of each query tile folds them into its registers
+  // in phase order and stores the range partial itself.
   __syncthreads();  // every tile consumed: Q and the slots become the merge area
-  if (wave < 4) {
+  const int lane_f4 = lane;  // f32x4 (hb * 4 + r4) * 64 + lane of a slot
+  if (wave < 4 && phase > 0) {
     float* mine = mrg + wave * SLOT1;
 #pragma unroll
     for (int hb = 0; hb < 4; ++hb)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4)
-        ((f32x4*)mine)[(hb * 4 + r4) * 64 + lane] =
+        ((f32x4*)mine)[(hb * 4 + r4) * 64 + lane_f4] =
             f32x4{o[0][hb][4 * r4], o[0][hb][4 * r4 + 1], o[0][hb][4 * r4 + 2], o[0][hb][4 * r4 + 3]};
     mine[4096 + lane * 2] = m_run[0];
     mine[4096 + lane * 2 + 1] = l_run[0];
   }
-  __syncthreads();
-  if (wave >= 4) return;
-  // query tile qt: the waves qt + QT * p, p < TSTRIDE
-  f32x4* op = (f32x4*)(o_part + part * SLOTS);
+  __syncthreads();  // the phase-0 waves wait for the others' slots
+  if (wave >= 4 || phase > 0) return;
+  float mw[TSTRIDE], lw[TSTRIDE], wgt[TSTRIDE];
+  mw[0] = m_run[0];
+  lw[0] = l_run[0];
+  float mm = mw[0];
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    float mw[TSTRIDE], lw[TSTRIDE], wgt[TSTRIDE];
-    float mm = -INFINITY;
-#pragma unroll
-    for (int p = 0; p < TSTRIDE; ++p) {
-      mw[p] = mrg[(qt + QT * p) * SLOT1 + 4096 + lane * 2];
-      lw[p] = mrg[(qt + QT * p) * SLOT1 + 4096 + lane * 2 + 1];
-      mm = fmaxf(mm, mw[p]);
-    }
-    float ll = 0.f;
-#pragma unroll
-    for (int p = 0; p < TSTRIDE; ++p) {
-      wgt[p] = mw[p] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw[p] - mm);
-      ll += wgt[p] * lw[p];
-    }
-    if (wave == 0 && lane < 32) {
-      ml_part[(part * (QT * 32) + qt * 32 + lane) * 2] = mm;
-      ml_part[(part * (QT * 32) + qt * 32 + lane) * 2 + 1] = ll;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = threadIdx.x + 256 * i;  // float4 of the query tile (lane = e & 63)
-      f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int p = 0; p < TSTRIDE; ++p) v += wgt[p] * ((const f32x4*)(mrg + (qt + QT * p) * SLOT1))[e];
-      op[qt * 1024 + e] = v;
-    }
+  for (int p = 1; p < TSTRIDE; ++p) {
+    mw[p] = mrg[(my_qt + QT * p) * SLOT1 + 4096 + lane * 2];
+    lw[p] = mrg[(my_qt + QT * p) * SLOT1 + 4096 + lane * 2 + 1];
+    mm = fmaxf(mm, mw[p]);
   }
+  float ll = 0.f;
+#pragma unroll
+  for (int p = 0; p < TSTRIDE; ++p) {
+    wgt[p] = mw[p] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw[p] - mm);
+    ll += wgt[p] * lw[p];
+  }
+  if (lane < 32) {
+    ml_part[(part * (QT * 32) + my_qt * 32 + lane) * 2] = mm;
+    ml_part[(part * (QT * 32) + my_qt * 32 + lane) * 2 + 1] = ll;
+  }
+  f32x4* op = (f32x4*)(o_part + part * SLOTS) + my_qt * 1024;
+#pragma unroll
+  for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int e = (hb * 4 + r4) * 64 + lane_f4;
+      f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+      v += wgt[0] * f32x4{o[0][hb][4 * r4], o[0][hb][4 * r4 + 1], o[0][hb][4 * r4 + 2],
+                          o[0][hb][4 * r4 + 3]};
+#pragma unroll
+      for (int p = 1; p < TSTRIDE; ++p) v += wgt[p] * ((const f32x4*)(mrg + (my_qt + QT * p) * SLOT1))[e];
+      op[e] = v;
+    }
 }
 
 // Combine the ranges of the decode attention. Float ((qt*4 + hb)*4 + r/4)*256 +
