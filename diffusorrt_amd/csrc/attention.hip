@@ -302,6 +302,86 @@ DRT_DEV void load_tile_nt(const T* __restrict__ base, int t, int lane, bool real
   }
 }
 
+// The second half of a key group: keys at or beyond nk[g] masked, one max over
+// the group, softmax weights against the running base, O^T += V^T P^T.
+template <typename T, int QT, int NG>
+DRT_DEV void softmax_pv(f32x16 (&sc)[NG][QT], const typename MfmaT<T>::vec (&vc)[NG][8],
+                        const int (&key0)[NG], const int (&nk)[NG], float c, int lane,
+                        float (&m_run)[QT], float (&l_run)[QT], f32x16 (&o)[QT][4]) {
+  typedef typename MfmaT<T>::vec vec;
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    if (key0[g] + 32 > nk[g]) {  // uniform: a partial (or empty) tile masks its keys
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          sc[g][qt][r] = key0[g] + mfma_row(r, lane) < nk[g] ? sc[g][qt][r] : -INFINITY;
+    }
+  }
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    float tmax = sc[0][qt][0];
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sc[g][qt][r]);
+    const float mc = max_xor32(tmax) * c;  // -inf: no visible key in the group
+    const bool up = mc > m_run[qt] + DEC_RESCALE_LOG2;
+    if (__ballot(up)) {  // uniform: some base has to rise
+      const float alpha = up ? __builtin_amdgcn_exp2f(m_run[qt] - mc) : 1.f;  // 0 from -inf
+      if (__ballot(up && m_run[qt] != -INFINITY)) {  // O is still zero before the first key
+#pragma unroll
+        for (int hb = 0; hb < 4; ++hb) o[qt][hb] *= alpha;
+      }
+      l_run[qt] *= alpha;
+      m_run[qt] = up ? mc : m_run[qt];
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < NG; ++g)
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const float base = m_run[qt] == -INFINITY ? 0.f : m_run[qt];  // no key yet: p = 0
+      float pr[16];
+      float psum = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        pr[r] = __builtin_amdgcn_exp2f(fmaf(sc[g][qt][r], c, -base));
+        psum += pr[r];
+      }
+      l_run[qt] += psum;
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+        vec pf;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pf[j] = MfmaT<T>::from_float(pr[kh * 8 + j]);
+#pragma unroll
+        for (int hb = 0; hb < 4; ++hb)
+          o[qt][hb] = MfmaT<T>::mma(vc[g][hb * 2 + kh], pf, o[qt][hb]);
+      }
+    }
+}
+
+// One 32-key tile for one query tile whose Q fragments the wave holds in
+// registers (qh / ql: hi and lo planes, k-step i = head dims 16 i + 8 (lane >> 5)
+// .. + 8 of query vector lane & 31): the MFMA chain of attend_group.
+template <typename T>
+DRT_DEV void attend_tile_rq(const typename MfmaT<T>::vec (&kc)[1][8],
+                            const typename MfmaT<T>::vec (&vc)[1][8],
+                            const typename MfmaT<T>::vec (&qh)[8],
+                            const typename MfmaT<T>::vec (&ql)[8], int key0, int nk, float c,
+                            int lane, float (&m_run)[1], float (&l_run)[1], f32x16 (&o)[1][4]) {
+  f32x16 sc[1][1] = {{f32x16{}}};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    sc[0][0] = MfmaT<T>::mma(kc[0][i], qh[i], sc[0][0]);
+    sc[0][0] = MfmaT<T>::mma(kc[0][i], ql[i], sc[0][0]);
+  }
+  const int k0[1] = {key0}, nk1[1] = {nk};
+  softmax_pv<T, 1, 1>(sc, vc, k0, nk1, c, lane, m_run, l_run, o);
+}
+
 // NG 32-key tiles for all query tiles at once: S^T = K Q^T for every (tile,
 // query tile) as independent MFMA chains, one max over the group, softmax
 // weights against the running base, O^T += V^T P^T. Keys at or beyond nk[g]
@@ -369,58 +449,7 @@ DRT_DEV void attend_group(const typename MfmaT<T>::vec (&kc)[NG][8],
       }
     }
   }
-#pragma unroll
-  for (int g = 0; g < NG; ++g) {
-    if (key0[g] + 32 > nk[g]) {  // uniform: a partial (or empty) tile masks its keys
-#pragma unroll
-      for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          sc[g][qt][r] = key0[g] + mfma_row(r, lane) < nk[g] ? sc[g][qt][r] : -INFINITY;
-    }
-  }
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    float tmax = sc[0][qt][0];
-#pragma unroll
-    for (int g = 0; g < NG; ++g)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sc[g][qt][r]);
-    const float mc = max_xor32(tmax) * c;  // -inf: no visible key in the group
-    const bool up = mc > m_run[qt] + DEC_RESCALE_LOG2;
-    if (__ballot(up)) {  // uniform: some base has to rise
-      const float alpha = up ? __builtin_amdgcn_exp2f(m_run[qt] - mc) : 1.f;  // 0 from -inf
-      if (__ballot(up && m_run[qt] != -INFINITY)) {  // O is still zero before the first key
-#pragma unroll
-        for (int hb = 0; hb < 4; ++hb) o[qt][hb] *= alpha;
-      }
-      l_run[qt] *= alpha;
-      m_run[qt] = up ? mc : m_run[qt];
-    }
-  }
-#pragma unroll
-  for (int g = 0; g < NG; ++g)
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      const float base = m_run[qt] == -INFINITY ? 0.f : m_run[qt];  // no key yet: p = 0
-      float pr[16];
-      float psum = 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        pr[r] = __builtin_amdgcn_exp2f(fmaf(sc[g][qt][r], c, -base));
-        psum += pr[r];
-      }
-      l_run[qt] += psum;
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
-        vec pf;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) pf[j] = MfmaT<T>::from_float(pr[kh * 8 + j]);
-#pragma unroll
-        for (int hb = 0; hb < 4; ++hb)
-          o[qt][hb] = MfmaT<T>::mma(vc[g][hb * 2 + kh], pf, o[qt][hb]);
-      }
-    }
+  softmax_pv<T, QT, NG>(sc, vc, key0, nk, c, lane, m_run, l_run, o);
 }
 
 template <typename T, int QT>
@@ -768,7 +797,14 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
     decr_waitcnt<DECR_VM0>();
     while (next < n) signal(next++);
   } else {
-    const T* my_q = qs + my_qt * 32 * DEC_QROW;
+    // the query tile's Q fragments, read from LDS once for the whole range
+    typename MfmaT<T>::vec qh[8], ql[8];
+    const T* qrow = qs + (my_qt * 32 + (lane & 31)) * DEC_QROW + 8 * (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      qh[i] = *(const vec*)(qrow + 16 * i);
+      ql[i] = *(const vec*)(qrow + QLO + 16 * i);
+    }
     for (int t = phase; t < n; t += TSTRIDE) {
       decr_wait(&ready[t % DECR_SLOTS], t + 1, err);
       const vec* tp = (const vec*)(tiles + (t % DECR_SLOTS) * 16384);
@@ -786,8 +822,7 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
                        : "v"((uint32_t)(uintptr_t)&freed[t % DECR_SLOTS]), "v"(1)
                        : "memory");
       }
-      const int key0[1] = {(t_begin + t) * 32}, nk[1] = {nk_mine};
-      attend_group<T, 1, 1, QLO>(kc, vc, my_q, key0, nk, c, lane, m_run, l_run, o);
+      attend_tile_rq<T>(kc, vc, qh, ql, (t_begin + t) * 32, nk_mine, c, lane, m_run, l_run, o);
     }
     l_run[0] += __shfl_xor(l_run[0], 32, 64);
   }
