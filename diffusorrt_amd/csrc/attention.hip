@@ -884,13 +884,13 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
 // (qt, hb): query vector qt*32 + (l & 31), head dim hb*32 + 8*(r >> 2) +
 // 4*(l >> 5) + (r & 3). Work-group (kvh, qt, hb*4 + rq) owns the 256 contiguous
 // floats with r in [4rq, 4rq + 4): 32 query vectors x the 8 consecutive head
-// dims hb*32 + 8rq .. +8, one thread per float, so 256 work-groups share the
-// reads. Each query vector's 8 dims are one 8-element
-// chunk of the output row. Empty ranges (m = -inf) are skipped.
+// dims hb*32 + 8rq .. +8, so 256 work-groups share the reads. Each query
+// vector's 8 dims are one 8-element chunk of the output row. Empty ranges
+// (m = -inf) are skipped. MLR: range statistics per thread (R <= 8 MLR).
 // out_fmt: 0 = ACT_F16P (no group sums: its consumer sums the hi + lo values
 // itself), 1 = ACT_BF16, 2 = fp32 plain, 3 = bf16 plain. A value beyond the
 // fp16 range sets DRT_ERR_F16_RANGE in *err.
-template <int QT>
+template <int QT, int MLR>
 __global__ __launch_bounds__(256) void attn_decode_combine_kernel(
     const float* __restrict__ o_part, const float* __restrict__ ml_part, int R, int n_rows,
     int Hq, int Hkv, void* __restrict__ out, int out_fmt, int* __restrict__ err) {
@@ -901,90 +901,101 @@ __global__ __launch_bounds__(256) void attn_decode_combine_kernel(
   const int n_qv = n_rows * G;
   __shared__ float mx[8][32];
   __shared__ float ls[8][32];
+  __shared__ f32x4 red[4][64];
   __shared__ float tile[32][9];
   extern __shared__ float wts[];  // [R][32] unnormalised weights
-  // this thread's float: lane l = j >> 2, r = 4rq + (j & 3)
-  const int l = j >> 2, r = 4 * rq + (j & 3);
-  const int64_t sl = (int64_t)qt * 4096 + (hb * 4 + rq) * 256 + j;
-  // the O values of the first RB ranges are loaded before (and independently
+  // Thread j sums float4 f = j & 63 of the work-group's 256 floats (lane l = f of
+  // the MFMA result: query vector c = f & 31, head dims 4 (f >> 5) .. + 4 of the
+  // 8) over the ranges rgp, rgp + 4, ... (rgp = j >> 6); the four range groups
+  // are added in LDS in a fixed order. One 16-byte load per range and thread
+  // (a load instruction costs the CU about as long whatever its width).
+  const int f = j & 63, rgp = j >> 6, c = f & 31;
+  const int64_t sl4 = ((int64_t)qt * 4096 + (hb * 4 + rq) * 256) / 4 + f;
+  const f32x4* op4 = (const f32x4*)o_part;
+  // the O values of the first 4 RB ranges are loaded before (and independently
   // of) the statistics, so one memory latency covers both
-  constexpr int RB = 32;
-  float v[RB];
+  constexpr int RB = 8;
+  f32x4 v[RB];
 #pragma unroll
-  for (int e = 0; e < RB; ++e)
-    v[e] = o_part[((int64_t)min(e, R - 1) * Hkv + kvh) * SLOTS + sl];  // e >= R: unused
-  // 1. per query vector c: max over ranges, weights, normaliser (8 range groups;
-  // a thread holds ranges pg, pg + 8, ... < R <= 128)
+  for (int e = 0; e < RB; ++e)  // ranges >= R: clamped, unused
+    v[e] = op4[((int64_t)min(rgp + 4 * e, R - 1) * Hkv + kvh) * (SLOTS / 4) + sl4];
+  // 1. per query vector cc: max over ranges, weights, normaliser (8 range
+  // groups; a thread holds ranges pg, pg + 8, ... < R <= 8 MLR)
   {
-    const int c = j & 31, pg = j >> 5;
-    constexpr int MLR = 16;
-    float mr[MLR], lr[MLR];
+    const int cc = j & 31, pg = j >> 5;
+    float2 ml[MLR];
 #pragma unroll
     for (int k = 0; k < MLR; ++k) {
       const int rr = pg + 8 * k;
-      const int64_t mi = (((int64_t)min(rr, R - 1) * Hkv + kvh) * (QT * 32) + qt * 32 + c) * 2;
-      mr[k] = ml_part[mi];
-      lr[k] = ml_part[mi + 1];
+      const int64_t mi = ((int64_t)min(rr, R - 1) * Hkv + kvh) * (QT * 32) + qt * 32 + cc;
+      ml[k] = ((const float2*)ml_part)[mi];
     }
     // every load above is issued before the ranges past R are masked (the
     // compiler would otherwise load under a branch and wait inside it)
     asm volatile("" ::: "memory");
+    float mr[MLR], lr[MLR];
 #pragma unroll
     for (int k = 0; k < MLR; ++k) {
-      mr[k] = pg + 8 * k < R ? mr[k] : -INFINITY;
-      lr[k] = pg + 8 * k < R ? lr[k] : 0.f;
+      mr[k] = pg + 8 * k < R ? ml[k].x : -INFINITY;
+      lr[k] = pg + 8 * k < R ? ml[k].y : 0.f;
     }
     float m_loc = -INFINITY;
 #pragma unroll
     for (int k = 0; k < MLR; ++k) m_loc = fmaxf(m_loc, mr[k]);
-    mx[pg][c] = m_loc;
+    mx[pg][cc] = m_loc;
     __syncthreads();
     float mm = -INFINITY;
 #pragma unroll
-    for (int g = 0; g < 8; ++g) mm = fmaxf(mm, mx[g][c]);
+    for (int g = 0; g < 8; ++g) mm = fmaxf(mm, mx[g][cc]);
     float l_loc = 0.f;
 #pragma unroll
     for (int k = 0; k < MLR; ++k) {
       const int rr = pg + 8 * k;
       const float w = mr[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mr[k] - mm);
-      if (rr < R) wts[rr * 32 + c] = w;
+      if (rr < R) wts[rr * 32 + cc] = w;
       l_loc += w * lr[k];
     }
-    ls[pg][c] = l_loc;
+    ls[pg][cc] = l_loc;
     __syncthreads();
   }
   // 2. weighted sum over the ranges (a zero weight never multiplies its O,
   // which an empty range does not write)
-  const int c = l & 31;
-  float lsum = 0.f;
-#pragma unroll
-  for (int g = 0; g < 8; ++g) lsum += ls[g][c];
-  // all RB weights read before any is used (one LDS latency, no branches)
   float wv[RB];
 #pragma unroll
-  for (int e = 0; e < RB; ++e) wv[e] = wts[min(e, R - 1) * 32 + c];
+  for (int e = 0; e < RB; ++e) wv[e] = wts[min(rgp + 4 * e, R - 1) * 32 + c];
   asm volatile("" ::: "memory");
-  float acc = 0.f;
+  const f32x4 zero4 = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 acc = zero4;
 #pragma unroll
   for (int e = 0; e < RB; ++e) {
-    const float w = e < R ? wv[e] : 0.f;
-    acc = fmaf(w, w == 0.f ? 0.f : v[e], acc);
+    const float w = rgp + 4 * e < R ? wv[e] : 0.f;
+    acc += w * (w == 0.f ? zero4 : v[e]);
   }
-  for (int rr = RB; rr < R; rr += 8) {
-    float u[8];
+  for (int r0 = 4 * RB; r0 < R; r0 += 4 * RB) {
+    f32x4 u[RB];
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      u[e] = o_part[((int64_t)min(rr + e, R - 1) * Hkv + kvh) * SLOTS + sl];  // >= R: unused
+    for (int e = 0; e < RB; ++e)  // >= R: unused
+      u[e] = op4[((int64_t)min(r0 + rgp + 4 * e, R - 1) * Hkv + kvh) * (SLOTS / 4) + sl4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      if (rr + e < R) {
-        const float w = wts[(rr + e) * 32 + c];
-        acc = fmaf(w, w == 0.f ? 0.f : u[e], acc);
+    for (int e = 0; e < RB; ++e) {
+      const int rr = r0 + rgp + 4 * e;
+      if (rr < R) {
+        const float w = wts[rr * 32 + c];
+        acc += w * (w == 0.f ? zero4 : u[e]);
       }
     }
   }
-  // 3. gather each query vector's 8 dims: dim offset 4*(l >> 5) + (r & 3)
-  tile[c][4 * (l >> 5) + (r & 3)] = acc / lsum;
+  red[rgp][f] = acc;
+  __syncthreads();
+  // 3. gather each query vector's 8 dims: dim offset 4 (f >> 5) + e
+  if (j < 64) {
+    float lsum = 0.f;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) lsum += ls[g][c];
+    const f32x4 sum = ((red[0][f] + red[1][f]) + red[2][f]) + red[3][f];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tile[c][4 * (f >> 5) + e] = sum[e] / lsum;
+  }
   __syncthreads();
   if (j >= 32) return;
   const int qv = qt * 32 + j;
@@ -1315,15 +1326,15 @@ void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv
   (void)xsum;  // the F16P output's consumer computes its own group sums
   const dim3 cgrid(Hkv, qt, 16);
   const size_t clds = (size_t)ranges * 32 * 4;
-  if (qt == 1)
-    hipLaunchKernelGGL(attn_decode_combine_kernel<1>, cgrid, dim3(256), clds, s, o_part, ml_part,
-                       ranges, n_rows, Hq, Hkv, out, out_fmt, err);
-  else if (qt == 2)
-    hipLaunchKernelGGL(attn_decode_combine_kernel<2>, cgrid, dim3(256), clds, s, o_part, ml_part,
-                       ranges, n_rows, Hq, Hkv, out, out_fmt, err);
-  else
-    hipLaunchKernelGGL(attn_decode_combine_kernel<4>, cgrid, dim3(256), clds, s, o_part, ml_part,
-                       ranges, n_rows, Hq, Hkv, out, out_fmt, err);
+#define DRT_COMB(QT, MLR)                                                                   \
+  hipLaunchKernelGGL((attn_decode_combine_kernel<QT, MLR>), cgrid, dim3(256), clds, s, o_part, \
+                     ml_part, ranges, n_rows, Hq, Hkv, out, out_fmt, err)
+  if (ranges <= 32) {
+    if (qt == 1) DRT_COMB(1, 4); else if (qt == 2) DRT_COMB(2, 4); else DRT_COMB(4, 4);
+  } else {
+    if (qt == 1) DRT_COMB(1, 16); else if (qt == 2) DRT_COMB(2, 16); else DRT_COMB(4, 16);
+  }
+#undef DRT_COMB
   DRT_HIP(hipGetLastError());
 }
 
