@@ -194,6 +194,29 @@ def test_block_attention_config2_bf16(L):
     assert mean_rel < 6e-3
 
 
+@pytest.mark.parametrize("hq,hkv", [(4, 2), (8, 4)])
+def test_block_attention_many_key_ranges(hq, hkv):
+    """Few KV heads over an 8K prefix: the decode attention splits each head's keys
+    into 64-65 ranges (more than 32, the combine's second statistics form, and
+    range batches past the first with a ragged last one)."""
+    from diffusorrt_amd.kernels import PrefixKVCache
+
+    L = 8192
+    _say("attention bf16 many ranges hq/hkv=", hq, hkv)
+    q, k, v = _attention_inputs(L, seed=3, hq=hq, hkv=hkv)
+    cache = PrefixKVCache(1, hkv, L + 32, dtype="bf16")
+    cache.store(0, k.cuda(), v.cuda(), 0)
+    out = cache.attention(0, q.cuda(), n_keys=L + 32, row_pos0=L, kind="bidirectional",
+                          out_dtype=torch.bfloat16)
+    got = out.float().cpu().numpy().astype(np.float64)
+    ref = O.attention(q.float().numpy(), k.float().numpy(), v.float().numpy())
+    err = np.abs(got - ref).max() / np.abs(ref).max()
+    mean_rel = np.mean(np.abs(got - ref)) / np.mean(np.abs(ref))
+    _say(f"  max_err={err:.2e} mean_rel={mean_rel:.2e}")
+    assert err < 2e-2
+    assert mean_rel < 6e-3
+
+
 @pytest.mark.parametrize("kind,rows,pos0,L", [("d2f_hybrid", 96, 64, 160),
                                               ("d2f_hybrid", 32, 8192, 8224),
                                               ("bidirectional", 100, 0, 100)])
