@@ -260,47 +260,19 @@ __global__ __launch_bounds__(64 * QW) void attn_split_kernel(
 }
 
 // Decode attention: rows of one mask segment (every key in [0, n_keys) is
-// visible to every row) with at most 32*QT query vectors per KV head. Two
-// kernels share the partial layout and the range combine: attn_decode_kernel
-// (below: K/V streamed into LDS by a producer wave) and attn_decode_reg_kernel
-// (this one: every wave loads its own tiles into registers; kept as the
-// DRT_ATTN_NO_DMA alternative).
-//
-// attn_decode_reg_kernel: grid (Hkv, R ranges), 4 waves per work-group, one
-// work-group per CU (the host keeps R * Hkv <= 256). Range r owns the tiles [n_tiles*r/R,
-// n_tiles*(r+1)/R) of its KV head; wave w takes tiles t0 + w, t0 + w + 4 and
-// t0 + w + 8 and issues all three tiles' K/V loads (nontemporal: the cache is
-// streamed once per layer) before anything else, so one memory latency covers
-// a range of up to 12 tiles (longer ranges continue with a load-then-use loop).
-// The head's Q vectors are loaded once per work-group into LDS (fragments are
-// read from LDS at each MFMA). After the tiles all four waves store (m, l, O)
-// to LDS and all 256 threads combine them slot by slot, so every range writes
-// one partial in the MFMA register order ("slot" order, see
-// attn_decode_combine_kernel) with coalesced stores. Empty ranges write only
-// m = -inf, l = 0; the combine then skips their O.
-// n_keys comes from `desc` when it is set (graph replays), else from the argument.
+// visible to every row) with at most 32*QT query vectors per KV head
+// (attn_decode_kernel below). Grid (Hkv, R ranges), one work-group per CU (the
+// host keeps R * Hkv <= 256): range r owns the tiles [n_tiles*r/R,
+// n_tiles*(r+1)/R) of its KV head and writes one partial (m, l, O) in the MFMA
+// register order ("slot" order, see attn_decode_combine_kernel) with coalesced
+// stores; empty ranges write only m = -inf, l = 0, and the combine then skips
+// their O. n_keys comes from `desc` when it is set (graph replays), else from
+// the argument.
 constexpr int DEC_QROW = 136;  // 16-bit elements per Q row in LDS (+16 B pad)
 // elements from the Q hi plane to the lo plane in LDS (64 rows of hi plane up to
 // two query tiles, 128 for four)
 template <int QT> constexpr int dec_qlo() { return (QT <= 2 ? 64 : 32 * QT) * DEC_QROW; }
 constexpr int DEC_QLO = dec_qlo<2>();
-constexpr int DEC_TILES_UP_FRONT = 3;
-
-// K/V fragments of tile t. With real == false every lane reads the first 16
-// bytes of the tile (one cache line per wave: a placeholder that keeps the load
-// count static; the caller gives such a tile no visible key).
-template <typename T>
-DRT_DEV void load_tile_nt(const T* __restrict__ base, int t, int lane, bool real,
-                          typename MfmaT<T>::vec (&k)[8], typename MfmaT<T>::vec (&v)[8]) {
-  typedef typename MfmaT<T>::vec vec;
-  const vec* tp = (const vec*)(base + (int64_t)t * KV_TILE_ELEMS);
-  const int l = real ? lane : 0, step = real ? 64 : 0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    k[i] = __builtin_nontemporal_load(tp + i * step + l);
-    v[i] = __builtin_nontemporal_load(tp + (real ? 512 : 0) + i * step + l);
-  }
-}
 
 // The second half of a key group: keys at or beyond nk[g] masked, one max over
 // the group, softmax weights against the running base, O^T += V^T P^T.
@@ -365,7 +337,8 @@ DRT_DEV void softmax_pv(f32x16 (&sc)[NG][QT], const typename MfmaT<T>::vec (&vc)
 
 // One 32-key tile for one query tile whose Q fragments the wave holds in
 // registers (qh / ql: hi and lo planes, k-step i = head dims 16 i + 8 (lane >> 5)
-// .. + 8 of query vector lane & 31): the MFMA chain of attend_group.
+// .. + 8 of query vector lane & 31): S^T = K Q^T as one MFMA chain per plane,
+// then softmax_pv.
 template <typename T>
 DRT_DEV void attend_tile_rq(const typename MfmaT<T>::vec (&kc)[1][8],
                             const typename MfmaT<T>::vec (&vc)[1][8],
@@ -382,236 +355,10 @@ DRT_DEV void attend_tile_rq(const typename MfmaT<T>::vec (&kc)[1][8],
   softmax_pv<T, 1, 1>(sc, vc, k0, nk1, c, lane, m_run, l_run, o);
 }
 
-// NG 32-key tiles for all query tiles at once: S^T = K Q^T for every (tile,
-// query tile) as independent MFMA chains, one max over the group, softmax
-// weights against the running base, O^T += V^T P^T. Keys at or beyond nk[g]
-// get zero weight (nk[g] <= key0[g] makes tile g a no-op). Every query tile runs
-// (the kernel is instantiated with QT = ceil(n_qv / 32)); rows beyond n_qv hold
-// Q = 0. c = scale * log2(e); m_run is the base in scaled units (-inf before
-// any key). key0 / nk are wave-uniform.
-template <typename T, int QT, int NG, int QLO = DEC_QLO>
-DRT_DEV void attend_group(const typename MfmaT<T>::vec (&kc)[NG][8],
-                          const typename MfmaT<T>::vec (&vc)[NG][8], const T* __restrict__ qs,
-                          const int (&key0)[NG], const int (&nk)[NG], float c, int lane,
-                          float (&m_run)[QT], float (&l_run)[QT], f32x16 (&o)[QT][4]) {
-  typedef typename MfmaT<T>::vec vec;
-  f32x16 sc[NG][QT];
-#pragma unroll
-  for (int g = 0; g < NG; ++g)
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) sc[g][qt] = f32x16{};
-  // Q fragments are read one k-step ahead: step i + 1's ds_reads are issued
-  // (inline asm, so the compiler does not sink them to their use) before step
-  // i's MFMAs, and waited for after them; the wait takes the registers as
-  // operands, so nothing reads them earlier.
-  // The lo plane of Q sits QLO elements after the hi plane: every score MFMA
-  // has a twin on the lo fragments (Q carried to ~22 bits, K exact).
-  const T* qrow = qs + (lane & 31) * DEC_QROW + 8 * (lane >> 5);
-  const uint32_t qaddr = (uint32_t)(uintptr_t)qrow;
-  vec qf[QT], qfl[QT];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    qf[qt] = *(const vec*)(qrow + qt * 32 * DEC_QROW);
-    qfl[qt] = *(const vec*)(qrow + QLO + qt * 32 * DEC_QROW);
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    vec qn[QT], qnl[QT];
-    if (i < 7) {
-#pragma unroll
-      for (int qt = 0; qt < QT; ++qt) {
-        asm volatile("ds_read_b128 %0, %1 offset:%2"
-                     : "=v"(qn[qt])
-                     : "v"(qaddr), "i"((qt * 32 * DEC_QROW + 16 * (i + 1)) * 2));
-        asm volatile("ds_read_b128 %0, %1 offset:%2"
-                     : "=v"(qnl[qt])
-                     : "v"(qaddr), "i"((QLO + qt * 32 * DEC_QROW + 16 * (i + 1)) * 2));
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        sc[g][qt] = MfmaT<T>::mma(kc[g][i], qf[qt], sc[g][qt]);
-        sc[g][qt] = MfmaT<T>::mma(kc[g][i], qfl[qt], sc[g][qt]);
-      }
-    __builtin_amdgcn_sched_barrier(0);
-    if (i < 7) {
-      if constexpr (QT == 1) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(qn[0]), "+v"(qnl[0]));
-      else
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(qn[0]), "+v"(qn[1]), "+v"(qnl[0]), "+v"(qnl[1]));
-#pragma unroll
-      for (int qt = 0; qt < QT; ++qt) {
-        qf[qt] = qn[qt];
-        qfl[qt] = qnl[qt];
-      }
-    }
-  }
-  softmax_pv<T, QT, NG>(sc, vc, key0, nk, c, lane, m_run, l_run, o);
-}
-
-template <typename T, int QT>
-__global__ __launch_bounds__(256) void attn_decode_reg_kernel(
-    const T* __restrict__ q, const T* __restrict__ kv, int64_t kv_head_stride, int n_rows,
-    int Hq, int Hkv, int n_keys_arg, const StepDesc* __restrict__ desc,
-    float* __restrict__ o_part, float* __restrict__ ml_part, float scale) {
-  typedef typename MfmaT<T>::vec vec;
-  constexpr int SLOTS = QT * 4096;              // O slots of one partial
-  constexpr int SLOT = SLOTS + QT * 64 * 2;     // + (m, l) per lane, one wave's LDS share
-  constexpr int UP = DEC_TILES_UP_FRONT;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform tile choices
-  const int G = Hq / Hkv;
-  const int n_qv = n_rows * G;
-  // grid (Hkv, R): with Hkv = 8 every range of a head runs on one XCD (work-group
-  // i runs on XCD i % 8), where the range combine of that head reads the partials
-  const int R = gridDim.y, rg = blockIdx.y, kvh = blockIdx.x;
-  const int n_keys = desc ? desc->n_keys : n_keys_arg;
-  const float c = scale * 1.44269504088896340736f;  // scores to base-2 exponents
-  const int n_tiles = (n_keys + 31) >> 5;
-  const int t_begin = (int)((int64_t)n_tiles * rg / R);
-  const int t_end = (int)((int64_t)n_tiles * (rg + 1) / R);
-  const int64_t part = (int64_t)rg * Hkv + kvh;
-  extern __shared__ __align__(16) char smem[];
-  T* qs = (T*)smem;    // [QT*32][DEC_QROW] hi, lo plane at + DEC_QLO
-  float* mrg = (float*)smem;  // [4][SLOT], over the Q planes once every wave is done
-
-  if (t_begin >= t_end) {  // no keys in this range
-    if (threadIdx.x < QT * 32) {
-      ml_part[(part * (QT * 32) + threadIdx.x) * 2] = -INFINITY;
-      ml_part[(part * (QT * 32) + threadIdx.x) * 2 + 1] = 0.f;
-    }
-    return;
-  }
-  // Q of the head's query vectors (qv = row*G + g) as 16-byte chunks; loads are
-  // unconditional (clamped rows) so the wait for Q below does not also wait for
-  // the K/V loads issued after it.
-  constexpr int QCH = QT * 2;  // QT*32 rows x 16 chunks / 256 threads
-  const T* q_lo = q + (int64_t)n_rows * Hq * 128;  // the Q lo plane
-  u32x4 qraw[QCH], qrawl[QCH];
-#pragma unroll
-  for (int i = 0; i < QCH; ++i) {
-    const int c = threadIdx.x + 256 * i;
-    const int qvc = min(c >> 4, n_qv - 1);
-    const int row = qvc / G, head = kvh * G + (qvc - row * G);
-    const int64_t off = ((int64_t)row * Hq + head) * 128 + (c & 15) * 8;
-    qraw[i] = *(const u32x4*)(q + off);
-    qrawl[i] = *(const u32x4*)(q_lo + off);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  const T* base = kv + (int64_t)kvh * kv_head_stride;
-  const int t0 = t_begin + wave;
-  vec kt[UP][8], vt[UP][8];
-  // a wave short of tiles loads a placeholder (one line of the range's last
-  // tile) and processes it with no visible key, which changes nothing
-#pragma unroll
-  for (int u = 0; u < UP; ++u)
-    load_tile_nt<T>(base, min(t0 + 4 * u, t_end - 1), lane, t0 + 4 * u < t_end, kt[u], vt[u]);
-  // every load is issued before any wait: a compiler-level memory barrier keeps
-  // the loads from being moved past the work-group barrier below
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int i = 0; i < QCH; ++i) {
-    const int c = threadIdx.x + 256 * i;
-    const bool ok = (c >> 4) < n_qv;
-    T* d = qs + (c >> 4) * DEC_QROW + (c & 15) * 8;
-    *(u32x4*)d = ok ? qraw[i] : u32x4{0u, 0u, 0u, 0u};
-    *(u32x4*)(d + DEC_QLO) = ok ? qrawl[i] : u32x4{0u, 0u, 0u, 0u};
-  }
-  __syncthreads();
-
-  float m_run[QT], l_run[QT];
-  f32x16 o[QT][4];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    m_run[qt] = -INFINITY;
-    l_run[qt] = 0.f;
-#pragma unroll
-    for (int hb = 0; hb < 4; ++hb) o[qt][hb] = f32x16{};
-  }
-  {
-    int key0[UP], nk[UP];
-#pragma unroll
-    for (int u = 0; u < UP; ++u) {
-      key0[u] = (t0 + 4 * u) * 32;
-      nk[u] = t0 + 4 * u < t_end ? n_keys : 0;
-    }
-    attend_group<T, QT, UP>(kt, vt, qs, key0, nk, c, lane, m_run, l_run, o);
-  }
-  for (int t = t0 + 4 * UP; t < t_end; t += 4) {  // ranges longer than 4*UP tiles
-    vec k1[1][8], v1[1][8];
-    load_tile_nt<T>(base, t, lane, true, k1[0], v1[0]);
-    const int key0[1] = {t * 32}, nk[1] = {n_keys};
-    attend_group<T, QT, 1>(k1, v1, qs, key0, nk, c, lane, m_run, l_run, o);
-  }
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) l_run[qt] += __shfl_xor(l_run[qt], 32, 64);
-
-  // every wave stores its (O, m, l); O as 16-byte units of 4 accumulator rows,
-  // unit ((qt*4 + hb)*4 + r/4)*64 + lane (the merge area overlays Q: every
-  // wave has read its last Q fragment first)
-  __syncthreads();
-  float* mine = mrg + wave * SLOT;
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-#pragma unroll
-    for (int hb = 0; hb < 4; ++hb)
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4)
-        ((f32x4*)mine)[((qt * 4 + hb) * 4 + r4) * 64 + lane] =
-            f32x4{o[qt][hb][4 * r4], o[qt][hb][4 * r4 + 1], o[qt][hb][4 * r4 + 2],
-                  o[qt][hb][4 * r4 + 3]};
-    mine[SLOTS + (qt * 64 + lane) * 2] = m_run[qt];
-    mine[SLOTS + (qt * 64 + lane) * 2 + 1] = l_run[qt];
-  }
-  __syncthreads();
-  // combine the four waves; unit e = threadIdx.x + 256*i has lane (e & 63) = lane
-  // and query tile i / 4. A wave without keys holds O = 0 and weight 0 (its O is
-  // finite: the cache tiles are zero-initialised and invisible keys get p = 0).
-  float wgt[QT][4];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    float mw[4], lw[4];
-    float mm = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      mw[w] = mrg[w * SLOT + SLOTS + (qt * 64 + lane) * 2];
-      lw[w] = mrg[w * SLOT + SLOTS + (qt * 64 + lane) * 2 + 1];
-      mm = fmaxf(mm, mw[w]);
-    }
-    float ll = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      wgt[qt][w] = mw[w] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw[w] - mm);
-      ll += wgt[qt][w] * lw[w];
-    }
-    if (wave == 0 && lane < 32) {
-      ml_part[(part * (QT * 32) + qt * 32 + lane) * 2] = mm;
-      ml_part[(part * (QT * 32) + qt * 32 + lane) * 2 + 1] = ll;
-    }
-  }
-  f32x4* op = (f32x4*)(o_part + part * SLOTS);
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = qt * 1024 + threadIdx.x + 256 * i;
-      f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int w = 0; w < 4; ++w) v += wgt[qt][w] * ((const f32x4*)(mrg + w * SLOT))[e];
-      op[e] = v;
-    }
-  }
-}
-
-// attn_decode_kernel, the producer / consumer form (same grid, partial layout
-// and combine as attn_decode_reg_kernel). With every wave loading its own tiles
-// a wave cannot compute while its loads wait to issue (the memory system paces
-// them), so the compute started only once the range had nearly streamed.
-// Here five waves split the roles: wave 4 streams the range's 16 KiB K/V tiles
+// attn_decode_kernel, the producer / consumer form. With every wave loading its
+// own tiles a wave cannot compute while its loads wait to issue (the memory
+// system paces them), so the compute would start only once the range had nearly
+// streamed. Here five waves split the roles: wave 4 streams the range's 16 KiB K/V tiles
 // with direct-to-LDS loads (global_load_lds, no registers held) into a ring of
 // DECR_SLOTS tile slots, and after each s_waitcnt that proves a tile complete
 // writes the tile's number (+1) into the slot's ready flag; waves 0-3 take tiles
@@ -1155,18 +902,6 @@ template __global__ void attn_split_kernel<__bf16, 2>(const __bf16*, const __bf1
 template __global__ void attn_split_kernel<__bf16, 4>(const __bf16*, const __bf16*, int64_t, int,
                                                       int, int, int, int, int, int, int, int,
                                                       float*, float*, float);
-template __global__ void attn_decode_reg_kernel<_Float16, 1>(const _Float16*, const _Float16*,
-                                                         int64_t, int, int, int, int,
-                                                         const StepDesc*, float*, float*, float);
-template __global__ void attn_decode_reg_kernel<_Float16, 2>(const _Float16*, const _Float16*,
-                                                         int64_t, int, int, int, int,
-                                                         const StepDesc*, float*, float*, float);
-template __global__ void attn_decode_reg_kernel<__bf16, 1>(const __bf16*, const __bf16*, int64_t, int,
-                                                       int, int, int, const StepDesc*, float*,
-                                                       float*, float);
-template __global__ void attn_decode_reg_kernel<__bf16, 2>(const __bf16*, const __bf16*, int64_t, int,
-                                                       int, int, int, const StepDesc*, float*,
-                                                       float*, float);
 template __global__ void attn_decode_kernel<_Float16, 1>(const _Float16*, const _Float16*,
                                                           int64_t, int, int, int, int,
                                                           const StepDesc*, float*, float*, float,
@@ -1279,21 +1014,10 @@ void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv
   require(ranges >= 1 && ranges <= 128, "decode attention takes 1..128 key ranges");
   const int qt = n_rows * G <= 64 ? (n_rows * G + 31) / 32 : 4;
   const float scale = 1.0f / sqrtf(128.0f);
-  const size_t lds = std::max((size_t)(DEC_QLO + qt * 32 * DEC_QROW) * 2,
-                              (size_t)4 * (qt * 4096 + qt * 128) * 4);
   const dim3 grid(Hkv, ranges);
   const double bytes = 2.0 * n_rows * Hq * 128 + 4.0 * n_keys * Hkv * 128;
   float* o_part = part;
   float* ml_part = part + (size_t)ranges * Hkv * qt * 4096;
-#define DRT_DEC(T, QT)                                                                      \
-  {                                                                                         \
-    auto fn = attn_decode_reg_kernel<T, QT>;                                                    \
-    static size_t granted = 0;                                                              \
-    grant_lds((const void*)fn, lds, granted);                                               \
-    DRT_LAUNCH(Profiler::ATTN, bytes, fn, grid, dim3(256), lds, s, (const T*)q,             \
-               (const T*)kv_layer, kv_head_stride, n_rows, Hq, Hkv, n_keys, desc, o_part,   \
-               ml_part, scale);                                                             \
-  }
 #define DRT_DECR(T, QT)                                                                     \
   {                                                                                         \
     auto fn = attn_decode_kernel<T, QT>;                                                   \
@@ -1303,25 +1027,16 @@ void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv
                (const T*)kv_layer, kv_head_stride, n_rows, Hq, Hkv, n_keys, desc, o_part,   \
                ml_part, scale, err);                                                        \
   }
-  // (the per-wave register form serves up to 64 query vectors)
-  static const bool reg_tiles = getenv("DRT_ATTN_NO_DMA") != nullptr;
   const size_t ldsr =
       qt == 4 ? 128 + (size_t)(dec_qlo<4>() + 4 * 32 * DEC_QROW) * 2 + (size_t)decr_slots<4>() * 16384
               : 128 + (size_t)(DEC_QLO + qt * 32 * DEC_QROW) * 2 +
                     (size_t)(qt == 1 ? decr_slots<1>() : decr_slots<2>()) * 16384;
-  if (!reg_tiles || qt == 4) {
-    if (bf16) {
-      if (qt == 1) DRT_DECR(__bf16, 1) else if (qt == 2) DRT_DECR(__bf16, 2) else DRT_DECR(__bf16, 4)
-    } else {
-      if (qt == 1) DRT_DECR(_Float16, 1) else if (qt == 2) DRT_DECR(_Float16, 2) else DRT_DECR(_Float16, 4)
-    }
-  } else if (bf16) {
-    if (qt == 1) DRT_DEC(__bf16, 1) else DRT_DEC(__bf16, 2)
+  if (bf16) {
+    if (qt == 1) DRT_DECR(__bf16, 1) else if (qt == 2) DRT_DECR(__bf16, 2) else DRT_DECR(__bf16, 4)
   } else {
-    if (qt == 1) DRT_DEC(_Float16, 1) else DRT_DEC(_Float16, 2)
+    if (qt == 1) DRT_DECR(_Float16, 1) else if (qt == 2) DRT_DECR(_Float16, 2) else DRT_DECR(_Float16, 4)
   }
 #undef DRT_DECR
-#undef DRT_DEC
   DRT_HIP(hipGetLastError());
   (void)xsum;  // the F16P output's consumer computes its own group sums
   const dim3 cgrid(Hkv, qt, 16);

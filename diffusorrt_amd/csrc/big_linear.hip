@@ -107,6 +107,13 @@ __global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int K
       ks = q % tail.kt;
       KS = tail.kt;
       t = tail.full + tail_idx;
+      // the slices meet through this XCD's L2: a work-group found elsewhere
+      // raises the placement error (the host then fails the forward)
+      if (threadIdx.x == 0 && a.placement_err) {
+        const int xcc = (int)(__builtin_amdgcn_s_getreg((31 << 11) | 20) & 0xf);  // HW_REG_XCC_ID
+        if (xcc != (b & 7))
+          __hip_atomic_fetch_or(a.placement_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
     tile_x = t % tail.tx;
     tile_y = t / tail.tx;

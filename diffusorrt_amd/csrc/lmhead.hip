@@ -676,7 +676,8 @@ extern "C" __global__ void lmhead_finalize_kernel(const LmStat* __restrict__ sta
 // token is still the mask, the desc->quota with the highest scores take their
 // proposed token; equal scores go to the lower row (the lower position), as the
 // host loop's stable order does. One wave, n_lm <= 64; rows are distinct
-// positions, and every canvas read happens before any write.
+// positions, and every canvas read happens before any write. A NaN score ranks
+// below every number.
 extern "C" __global__ void block_commit_kernel(const double* __restrict__ scores,
                                                const int32_t* __restrict__ tokens,
                                                const int32_t* __restrict__ positions,
@@ -688,7 +689,10 @@ extern "C" __global__ void block_commit_kernel(const double* __restrict__ scores
   const bool row = r < n;
   const int pos = row ? positions[r] : 0;
   const bool masked = row && canvas[pos] == mask_id;
-  const double sc = row ? scores[r] : 0.0;
+  // a NaN score ranks as -inf, as in the library's host loop (the comparisons
+  // below then stay a strict order: score descending, row ascending)
+  const double s0 = row ? scores[r] : 0.0;
+  const double sc = s0 != s0 ? -INFINITY : s0;
   int rank = 0;
   for (int j = 0; j < n; ++j) {
     const double sj = __shfl(sc, j, 64);
@@ -724,10 +728,8 @@ void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* 
   require(w.K % chunk_k == 0 || w.K % 64 == 0, "lm head K must be a multiple of 64");
   int NB = w.N / 64;
   constexpr int WAVES = 4;
-  // K = 1024 heads (q4 or bf16) run on the persistent kernel (DRT_LMHEAD_CHUNKED=1 keeps
-  // them on the chunked one, an A/B switch for parity and timing comparisons)
-  static const bool chunked = getenv("DRT_LMHEAD_CHUNKED") != nullptr;
-  if (w.K == LMP_G * 64 && !chunked) {
+  // K = 1024 heads (q4 or bf16) run on the persistent kernel, other K on the chunked one
+  if (w.K == LMP_G * 64) {
     int dev = 0, n_cu = 0;
     DRT_HIP(hipGetDevice(&dev));
     DRT_HIP(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));

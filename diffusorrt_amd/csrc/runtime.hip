@@ -1036,7 +1036,16 @@ struct Session {
             "a device block takes 1..61 steps");
     DRT_HIP(hipEventRecord(r.ev0, r.stream));
     const bool pair = pairable() && cache_len + block == fp && cache_len % block == 0;
-    if (!pair) commit_to(fp);
+    if (!pair) {
+      commit_to(fp);
+      // commit forwards run eagerly (a prefix longer than four blocks) staged their
+      // descriptors in the eager slots that the steps below rewrite: their copies
+      // must have left those slots first
+      if (r.up_next != Runtime::EAGER_SLOT0) {
+        DRT_HIP(hipStreamSynchronize(r.stream));
+        r.up_next = Runtime::EAGER_SLOT0;
+      }
+    }
     const int row_first = pair ? fp - block : fp;
     upload_tokens(row_first, hi);  // the device canvas is the forwards' from here on
     for (int j = 0; j < S; ++j) {
@@ -1088,10 +1097,9 @@ struct Session {
   }
 
   // The native loop runs whole blocks on the device (graph forwards, no
-  // profiling; DRT_HOST_TOPK=1 keeps the per-step host choice).
+  // profiling); other blocks take the per-step host choice.
   bool block_on_device() const {
-    static const bool host_topk = getenv("DRT_HOST_TOPK") != nullptr;
-    return !host_topk && graphable(block) && origin == 0;
+    return graphable(block) && origin == 0;
   }
 
   // A block's commit can run with the next block's step as one forward when

@@ -653,11 +653,8 @@ size_t skinny_part_floats(int N, int K) {
 int skinny_counters(int N) { return N / 32; }
 
 bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
-  // DRT_DISABLE_SKINNY=1 keeps every linear on the single-pass fused kernels
-  // (an A/B switch for parity and timing comparisons)
-  static const bool disabled = getenv("DRT_DISABLE_SKINNY") != nullptr;
   const int MT = (a.M + 31) / 32;
-  if (disabled || (!a.qw && !a.wb) || a.M < 1 || MT > a.sk_row_tiles || !a.part ||
+  if ((!a.qw && !a.wb) || a.M < 1 || MT > a.sk_row_tiles || !a.part ||
       !a.counters || a.K % 64 || a.N % 32 || a.n_xcc < 1)
     return false;
   const bool bf = a.qw == nullptr;

@@ -511,8 +511,7 @@ int n_cu_of_current_device() {
 }  // namespace
 
 bool stream_supported(int M, int N, int K) {
-  static const bool disabled = getenv("DRT_DISABLE_STREAM") != nullptr;
-  return !disabled && M >= 1 && M <= 32 && N % 128 == 0 && K % 64 == 0 &&
+  return M >= 1 && M <= 32 && N % 128 == 0 && K % 64 == 0 &&
          (int64_t)N * K >= STREAM_MIN_WEIGHTS;
 }
 

@@ -21,6 +21,24 @@ def _gpu_available() -> bool:
         return False
 
 
+@pytest.fixture(autouse=True)
+def _parity_log_test_id(request):
+    """Names the running test in the parity exemption log (tests/helpers.py)."""
+    import helpers
+
+    helpers.CURRENT_TEST[0] = request.node.nodeid
+    yield
+    helpers.CURRENT_TEST[0] = ""
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    """One line with every reported parity exemption of the run (count, kind,
+    bound, largest gap and its test), so that a -q run's tail carries it."""
+    import helpers
+
+    terminalreporter.write_line(helpers.parity_summary())
+
+
 def pytest_collection_modifyitems(config, items):
     if _gpu_available():
         return

@@ -14,6 +14,38 @@ NEAR_TIE_REL = 1e-3        # confidences within this relative gap are reported t
 # of the device path carries ~22 significant bits (fp16 hi + lo), so what is left
 # is the fp16 softmax weights of P.V and fp32 summation order.
 SCORE_REL_TOL = 1e-3
+# A disagreement with the exact oracle that the oracle run with fp16-rounded K/V
+# reproduces ("token~kv" / "chosen~kv") is attributed to the cache's fp16
+# storage only while its relative gap stays within the bound that storage was
+# measured to move the margins by (test_oracle_forward.py's per-site
+# attribution: < 2e-3); a larger gap fails.
+KV_EXEMPT_REL = 2e-3
+
+# Every reported exemption of the session (near-ties, fp16-K/V disagreements):
+# (test id, kind, relative gap). conftest.py sets CURRENT_TEST per test and
+# prints one summary line of this list at the end of the run.
+PARITY_LOG: list = []
+CURRENT_TEST = [""]
+
+
+def note_exemption(kind: str, gap: float) -> None:
+    PARITY_LOG.append((CURRENT_TEST[0], kind, float(gap)))
+
+
+def parity_summary() -> str:
+    if not PARITY_LOG:
+        return "parity exemptions: none (every token and chosen row equal to the oracle's)"
+    parts = []
+    for kind, bound in (("near-tie", f"relative gap <= {NEAR_TIE_REL:g}"),
+                        ("fp16-kv", f"relative gap <= {KV_EXEMPT_REL:g}"),
+                        ("bf16-tie", "logit margin <= 2 bf16 ulps")):
+        rows = [r for r in PARITY_LOG if r[1] == kind]
+        if rows:
+            worst = max(rows, key=lambda r: r[2])
+            parts.append(f"{len(rows)} {kind} ({bound}; largest {worst[2]:.3g} in "
+                         f"{worst[0] or '?'})")
+    tests = sorted({r[0] for r in PARITY_LOG})
+    return "parity exemptions: " + "; ".join(parts) + f"; {len(tests)} test(s)"
 
 
 def kv_round_f16(a):
@@ -95,7 +127,9 @@ def compare_proposals(gpu_scores, gpu_tokens, ref_logits, *, kv_logits=None, quo
         and every score is within SCORE_REL_TOL;
       * against the exact reference a disagreement is a reported near-tie (gap
         <= 1e-3) or, when ``kv_logits`` makes the device's choice, a reported
-        "token~kv" / "chosen~kv": attributed to the cache's fp16 storage alone.
+        "token~kv" / "chosen~kv" (attributed to the cache's fp16 storage alone)
+        while its gap is within KV_EXEMPT_REL; a larger gap is a problem.
+    Every reported entry is logged for the session's summary line.
     Without ``kv_logits`` the strict rule applies to ``ref_logits`` itself.
     bf16 logits (bf16 weights; the reference rounds its logits to bf16): margins
     within 2 bf16 ulps of the row's max logit, the resolution at which the
@@ -121,8 +155,9 @@ def compare_proposals(gpu_scores, gpu_tokens, ref_logits, *, kv_logits=None, quo
                 ("token", r, gt, kv_tokens[r], float(gap)))
         elif gt != ref_tokens[r]:
             gap, _ = _gap(ref_logits[r])
-            report.append(("token" if gap <= NEAR_TIE_REL else "token~kv", r, gt, ref_tokens[r],
-                           float(gap)))
+            kind = "token" if gap <= NEAR_TIE_REL else "token~kv"
+            (report if gap <= KV_EXEMPT_REL else problems).append(
+                (kind, r, gt, ref_tokens[r], float(gap)))
     rel = np.abs(gpu_scores - (ref_scores if bf16_logits else kv_scores)) / \
         (ref_scores if bf16_logits else kv_scores)
     if not bf16_logits and rel.max() > SCORE_REL_TOL:
@@ -149,6 +184,10 @@ def compare_proposals(gpu_scores, gpu_tokens, ref_logits, *, kv_logits=None, quo
                                                                       float(gap)))
             elif got != ref_chosen:
                 gap = _chosen_gap(ref_scores, quota)
-                report.append(("chosen" if gap <= NEAR_TIE_REL else "chosen~kv", got, ref_chosen,
-                               float(gap)))
+                kind = "chosen" if gap <= NEAR_TIE_REL else "chosen~kv"
+                (report if gap <= KV_EXEMPT_REL else problems).append(
+                    (kind, got, ref_chosen, float(gap)))
+    for entry in report:
+        note_exemption("bf16-tie" if bf16_logits else
+                       "fp16-kv" if entry[0].endswith("~kv") else "near-tie", entry[-1])
     return {"score_rel_max": float(rel.max()), "report": report}, problems

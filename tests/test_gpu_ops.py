@@ -325,6 +325,94 @@ def test_lm_head_scores_tokens(kind, rows, n):
     np.testing.assert_allclose(scores.cpu().numpy(), s_own, rtol=1e-6)
 
 
+def _q4_dequant64_cuda(w_q, scales, biases):
+    """float64 dense weights of q4 rows on the device: nibble i of word j is
+    k = 8j + i (low nibble first), w = q * scale + bias per 64-wide group."""
+    n, words = w_q.shape
+    shifts = torch.arange(8, device=w_q.device, dtype=torch.int32) * 4
+    nib = (w_q.unsqueeze(-1) >> shifts) & 15
+    q = nib.reshape(n, words * 8 // 64, 64).double()
+    return (q * scales.double().unsqueeze(-1) + biases.double().unsqueeze(-1)).reshape(n, -1)
+
+
+@pytest.mark.parametrize("kind,rows", [("q4", 256), ("bf16", 64)])
+def test_lm_head_full_vocab_chunked_k3584(kind, rows):
+    """Dream's LM head at its real size (vocabulary 152064, K = 3584: the
+    chunked kernel, every K other than 1024): 256 rows (8 row tiles) for q4,
+    64 for bf16. Logits against float64 truth computed in column chunks (the
+    chunk dequantisation pinned to the oracle's on the first chunk), greedy
+    scores and tokens equal to the float64 scoring of the device's own logits,
+    and, for q4, the T > 0 sampling rule against the oracle on 24 rows spread
+    over the 8 row tiles."""
+    from diffusorrt_amd import _lib, kernels
+    from diffusorrt_amd import synthetic as syn
+    import ctypes as C
+
+    n, k = 152064, 3584
+    _say("lm_head full vocab", kind, rows, n, k)
+    gen = torch.Generator().manual_seed(31)
+    x = torch.randn((rows, k), generator=gen)
+    xc = x.cuda()
+    if kind == "q4":
+        q = syn.random_q4(gen, n, k)
+        w = kernels.DeviceQ4Weight(q.w_q.cuda(), q.scales.cuda(), q.biases.cuda())
+        wargs = (C.c_void_p(w.qw.data_ptr()), C.c_void_p(w.sb.data_ptr()), None)
+        wq_d, sc_d, bi_d = q.w_q.cuda(), q.scales.cuda(), q.biases.cuda()
+        c = 512
+        W0 = O.Q4Weight(q.w_q[:c].numpy().view(np.uint32), q.scales[:c].float().numpy(),
+                        q.biases[:c].float().numpy())
+        dense0 = O.q4_dequant(W0.w_q, W0.scales, W0.biases, dtype=np.float64)
+        assert np.array_equal(_q4_dequant64_cuda(wq_d[:c], sc_d[:c], bi_d[:c]).cpu().numpy(),
+                              dense0)
+        dense = lambda c0, c1: _q4_dequant64_cuda(wq_d[c0:c1], sc_d[c0:c1], bi_d[c0:c1])
+    else:
+        wt = (torch.randn((n, k), generator=gen) * 0.02).to(torch.bfloat16)
+        w = kernels.DeviceBF16Weight(wt.cuda())
+        wargs = (None, None, C.c_void_p(w.wb.data_ptr()))
+        wt_d = wt.cuda()
+        dense = lambda c0, c1: wt_d[c0:c1].double()
+    x64 = xc.double()
+    ref = torch.empty((rows, n), dtype=torch.float64, device="cuda")
+    for c0 in range(0, n, 8192):
+        c1 = min(n, c0 + 8192)
+        ref[:, c0:c1] = x64 @ dense(c0, c1).T
+    if kind == "bf16":  # the reference rounds bf16-weight logits to bf16
+        ref = ref.float().to(torch.bfloat16).double()
+    lib = _lib.load()
+    ws_b = lib.drt_op_lm_head_workspace_bytes(rows, n, k)
+    ws = torch.empty(ws_b, dtype=torch.uint8, device="cuda")
+    positions = torch.arange(1000, 1000 + rows, dtype=torch.int32, device="cuda")
+    for T in ((0.0, 0.7) if kind == "q4" else (0.0,)):
+        scores = torch.empty(rows, dtype=torch.float64, device="cuda")
+        tokens = torch.empty(rows, dtype=torch.int32, device="cuda")
+        logits = torch.empty((rows, n), dtype=torch.float32, device="cuda")
+        seed, step = 77, 5
+        _lib.check(lib.drt_op_lm_head_score(*wargs, rows, n, k, C.c_void_p(xc.data_ptr()), T,
+                                            seed, step, C.c_void_p(positions.data_ptr()),
+                                            C.c_void_p(scores.data_ptr()),
+                                            C.c_void_p(tokens.data_ptr()),
+                                            C.c_void_p(logits.data_ptr()),
+                                            C.c_void_p(ws.data_ptr()), ws_b, None))
+        torch.cuda.synchronize()
+        err = ((logits.double() - ref).abs().amax(dim=1) / ref.abs().amax(dim=1)).max().item()
+        _say(f"  T={T} logits rel err max over rows={err:.2e}")
+        # q4: fp32 sums of the exact-nibble products (hi + lo activation);
+        # bf16: compared at the bf16 resolution of the reference's logits
+        assert err < (1e-4 if kind == "q4" else 1e-2)
+        got = logits.cpu().numpy()
+        if T == 0.0:
+            s_own, t_own = O.raw_max_prob(got)
+            assert tokens.cpu().tolist() == t_own
+            np.testing.assert_allclose(scores.cpu().numpy(), s_own, rtol=1e-6)
+        else:
+            sel = [32 * t + o for t in range(rows // 32) for o in (0, 13, 31)]
+            pos = positions.cpu().tolist()
+            s_ref, t_ref = O.sampled_max_prob(got[sel], temperature=T, seed=seed, step=step,
+                                              positions=[pos[i] for i in sel])
+            assert [tokens.cpu().tolist()[i] for i in sel] == t_ref
+            np.testing.assert_allclose(scores.cpu().numpy()[sel], s_ref, rtol=1e-6)
+
+
 @pytest.mark.parametrize("kind,n,k", [("bf16", 2048, 256), ("bf16", 8256, 1024),
                                       ("q4", 8256, 1024)])
 def test_lm_head_sampling_matches_oracle_rule(kind, n, k):

@@ -204,13 +204,45 @@ def test_engine_dream_block_threshold_from_package(tmp_path):
         assert res.token_ids == direct.visible_generated_token_ids
 
 
-@pytest.mark.parametrize("dream", [False])
+def _device_bundles_as_oracle(root, host: dict, sample_rows: int = 96) -> dict:
+    """The device-prepared weights of a package as oracle weights, each q4 linear
+    first checked bit-exact against the oracle's quantizer on its first and last
+    ``sample_rows`` rows (and every other tensor in full): quantizing whole 7B
+    layers in numpy would take minutes, the device does it in milliseconds."""
+    from diffusorrt_amd import synthetic as syn
+    from diffusorrt_amd.package import load_package
+
+    pm = load_package(root, linear_quant_bits=4)
+    W = {}
+    for name, v in pm.weights.items():
+        a = host[name].float().numpy()
+        if isinstance(v, syn.Q4Tensor):
+            got = (v.w_q.cpu().numpy().view(np.uint32), v.scales.float().cpu().numpy(),
+                   v.biases.float().cpu().numpy())
+            n = a.shape[0]
+            for rows in (slice(0, min(sample_rows, n)), slice(max(0, n - sample_rows), n)):
+                ref = O.q4_quantize(a[rows])
+                for g_, r_ in zip(got, ref):
+                    assert np.array_equal(g_[rows], r_), name
+            W[name] = O.Q4Weight(*got)
+        else:
+            got = v.float().cpu().numpy()
+            assert np.array_equal(got, O.bf16_round(a)), name
+            W[name] = got
+    del pm
+    return W
+
+
+@pytest.mark.timeout(400)
+@pytest.mark.parametrize("dream", [False, True])
 def test_real_shape_package_matches_oracle(tmp_path, dream):
-    """A package with the real BD3 layer shapes (two layers, 4096-token vocabulary),
-    bf16 safetensors quantized on the device, against the oracle's forward on the
-    oracle-quantized weights. (Dream's 7B shapes go through the same quantizer,
-    checked bit-exact at its largest linear above; the oracle quantization of
-    whole 7B layers would dominate the suite's time.)"""
+    """A package with the real BD3 (Qwen3-0.6B) or Dream (Qwen2.5-7B: q/k/v
+    biases, untied head, 28 / 4 heads) layer shapes, two layers and a 4096-token
+    vocabulary, written as bf16 safetensors and quantized on the device, against
+    the oracle's forward. BD3: the oracle quantizes every weight itself. Dream:
+    the oracle takes the device-quantized weights after checking them bit-exact
+    against its quantizer on a row sample of every linear (the whole 7B layers
+    would take minutes in numpy)."""
     import dataclasses
 
     from diffusorrt_amd import synthetic as syn
@@ -222,7 +254,8 @@ def test_real_shape_package_matches_oracle(tmp_path, dream):
                             eos_token_id=4001, max_position_embeddings=4096)
     host = random_weights(g, seed=31, dtype=torch.bfloat16)
     root = write_package(tmp_path / "pkg", g, host, max_shard_bytes=64 << 20)
-    W = _oracle_weights(host, q4=True)
+    W = _device_bundles_as_oracle(root, host) if dream else _oracle_weights(host, q4=True)
+    del host
     cfg = syn.oracle_config(g, "q4")
     rt = Runtime(str(root), engine_config={"linear_quant_bits": 4}, max_forward_rows=512,
                  max_positions=1024)

@@ -8,9 +8,9 @@ from oracle import forward as F
 from oracle import ops as O
 from oracle import policy as P
 
-from helpers import (LOGITS_REL_TOL, NEAR_TIE_REL, SCORE_REL_TOL, compare_proposals,
-                     kv_round_f16, oracle_logits, oracle_weights, rel_err_rows,
-                     tiny_dream_geometry, tiny_geometry)
+from helpers import (KV_EXEMPT_REL, LOGITS_REL_TOL, NEAR_TIE_REL, SCORE_REL_TOL,
+                     compare_proposals, kv_round_f16, note_exemption, oracle_logits,
+                     oracle_weights, rel_err_rows, tiny_dream_geometry, tiny_geometry)
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -252,6 +252,7 @@ def test_reference_mask_cases_against_golden(kind):
                         margin = w["max"] - w["second"]
                         band = 2 * 2.0 ** (np.floor(np.log2(scale)) - 7)
                         assert margin <= band, (c["name"], r, tokens[r], w["argmax"], margin)
+                        note_exemption("bf16-tie", margin)
                         _say(f"  near-tie row {r}: {tokens[r]} vs {w['argmax']} margin {margin:.3g}")
                     else:
                         assert abs(scores[r] - w["score"]) / w["score"] < 1e-2
@@ -261,11 +262,17 @@ def test_reference_mask_cases_against_golden(kind):
                 kv_gap = 1.0 - np.exp(-(w["kv_max"] - w["kv_second"]))
                 if tokens[r] != w["kv_argmax"]:
                     assert kv_gap <= NEAR_TIE_REL, (c["name"], r, tokens[r], w["kv_argmax"], kv_gap)
+                    note_exemption("near-tie", kv_gap)
                     _say(f"  near-tie row {r}: {tokens[r]} vs {w['kv_argmax']} gap {kv_gap:.3g}")
                 else:
                     assert abs(scores[r] - w["kv_score"]) / w["kv_score"] < SCORE_REL_TOL
                     if tokens[r] != w["argmax"]:
-                        _say(f"  row {r}: {tokens[r]} vs exact {w['argmax']} (fp16 K/V storage)")
+                        # attributed to the cache's fp16 storage only within its bound
+                        gap = 1.0 - np.exp(-(w["max"] - w["second"]))
+                        assert gap <= KV_EXEMPT_REL, (c["name"], r, tokens[r], w["argmax"], gap)
+                        note_exemption("near-tie" if gap <= NEAR_TIE_REL else "fp16-kv", gap)
+                        _say(f"  row {r}: {tokens[r]} vs exact {w['argmax']} gap {gap:.3g} "
+                             "(fp16 K/V storage)")
     finally:
         rt.close()
 
@@ -502,6 +509,41 @@ def test_bd3_native_loop_matches_host_loop(kind):
                                       eos_token_id=geom.eos_token_id, max_forwards=5)
             total += f
         assert total == host.forward_count and s.canvas() == host.full_token_ids
+    rt.close()
+
+
+def test_bd3_native_loop_long_prompt_warm_session():
+    """A prompt longer than four blocks is committed by eager forwards before the
+    first device block, and those forwards' descriptors sit in the staging slots
+    that the block's steps then rewrite. One session decodes two prompts of six
+    blocks back to back (the second with its graphs warm, so that the steps are
+    queued within microseconds of the commits); both canvases equal the host
+    loop's."""
+    from diffusorrt_amd import decode
+    from diffusorrt_amd.runtime import bd3_session_config
+
+    _say("bd3 native loop, 192-token prompts, one warm session")
+    geom = tiny_geometry()
+    _, rt = _build(geom, "q4", seed=16)
+    rng = np.random.default_rng(11)
+    prompts = [rng.integers(0, 900, 192).tolist() for _ in range(2)]
+    GEN, STEPS = 64, 16
+    cfg = bd3_session_config(32, STEPS, 192 + GEN)
+
+    def run(s, prompt, native):
+        return decode.generate_device_tokens(
+            s, prompt, max_tokens=GEN, mask_token_id=geom.mask_token_id,
+            eos_token_id=geom.eos_token_id, steps=STEPS, block_size=32, native=native)
+
+    host = []
+    for prompt in prompts:
+        with rt.session(cfg) as s:
+            host.append(run(s, prompt, False))
+    with rt.session(cfg) as s:
+        nat = [run(s, prompt, True) for prompt in prompts]
+    for h, n in zip(host, nat):
+        assert n.full_token_ids == h.full_token_ids
+        assert n.forward_count == h.forward_count
     rt.close()
 
 

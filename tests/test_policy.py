@@ -231,6 +231,20 @@ def test_topk_exact_ties_lowest_index_first():
         assert sorted(s[got]) == sorted(s[O.topk_count_choices(s, k)])
 
 
+def test_topk_nan_scores_rank_last():
+    """A NaN score ranks below every number, NaN rows among themselves in index
+    order: numpy's stable argsort of -score puts NaN last, and the native loop
+    (``std::isnan`` -> -inf) and the device-side choice (``block_commit_kernel``)
+    rank it as -inf, which probabilities in [0, 1] never reach."""
+    nan = float("nan")
+    s = [0.3, nan, 0.7, nan, 0.1]
+    assert D.topk_count_choices(s, 5) == [2, 0, 4, 1, 3]
+    assert D.topk_count_choices(s, 2) == [2, 0]
+    assert D.topk_count_choices([nan, nan, 0.0], 2) == [2, 0]
+    as_neg_inf = [-math.inf if v != v else v for v in s]
+    assert D.topk_count_choices(as_neg_inf, 5) == D.topk_count_choices(s, 5)
+
+
 def test_threshold_choices_closed_forms():
     for pick in (D.threshold_choices, P.threshold_pick):
         assert pick([0.95, 0.5, 0.91], 0.9) == [0, 2]

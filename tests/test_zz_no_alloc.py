@@ -1,8 +1,9 @@
 """drt_op_q4_linear_noalloc (no workspace argument, no device allocation) against
-drt_op_q4_linear with a caller workspace, through the C-ABI: two calls in a
-row, the second with a smaller input (the shared scratch keeps the first call's
-contents), each bit-exact with the workspace entry point (same kernels, same
-workspace layout); a shape beyond the scratch is refused before any launch."""
+drt_op_q4_linear with a caller workspace, through the C-ABI: three calls in a
+row, each with a smaller input than the one before (the shared scratch keeps
+the previous call's contents), each bit-exact with the workspace entry point (same kernels, same
+workspace layout), on the weight-streaming, large-M and decode-sized paths; a
+shape beyond the scratch is refused before any launch."""
 from __future__ import annotations
 
 import ctypes as C
@@ -28,8 +29,10 @@ def test_q4_linear_noalloc_matches_the_workspace_entry_point():
 
     lib = _lib.load()
     stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
-    # large-M (split-K partials in the scratch) first, then a smaller decode-sized call
-    for m, n, k, seed in [(128, 3072, 1024, 41), (8, 1024, 2048, 42)]:
+    # the weight-streaming path (m <= 32, n * k >= 8M weights: fp32 K slices in the
+    # scratch, summed with the bias by the slice pass), then large-M (split-K
+    # partials in the scratch), then a smaller decode-sized call
+    for m, n, k, seed in [(32, 3584, 18944, 40), (128, 3072, 1024, 41), (8, 1024, 2048, 42)]:
         _say("q4_linear_noalloc", m, n, k)
         gen = torch.Generator().manual_seed(seed)
         q = syn.random_q4(gen, n, k, scale_lo=0.005, scale_hi=0.02, centred=False)
