@@ -28,6 +28,10 @@ HIPCC_FLAGS = [
     # MFMA results in ordinary VGPRs: no accumulator-register copies before the
     # VALU epilogues read them (about 0.4 % of a decode step).
     "-mllvm", "-amdgpu-mfma-vgpr-form",
+    # The first 16 dwords of kernel arguments arrive in scalar registers at wave
+    # start (gfx950 kernel-argument preloading): no argument fetch before the
+    # first loads can issue.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 
 
