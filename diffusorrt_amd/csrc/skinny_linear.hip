@@ -155,35 +155,41 @@ DRT_DEV void sk_wide_sum_slices(const float* pbase, int KS, float* red, bool rnd
 
 }  // namespace
 
+// Everything the first loads need is in the leading scalar arguments, which
+// arrive in scalar registers at wave start (kernel-argument preloading, 16
+// dwords): the sizes packed as dims0 = N | K << 16 and dims1 = M | KS << 8 |
+// n_xcc << 16 | fenced << 24. The rest of the arguments (`a`) are fetched
+// while the first loads are in flight.
+DRT_DEV void sk_dims(uint32_t dims0, uint32_t dims1, int& M, int& N, int& K, int& KS, int& n_xcc,
+                     int& fenced) {
+  N = (int)(dims0 & 0xffffu);
+  K = (int)(dims0 >> 16);
+  M = (int)(dims1 & 0xffu);
+  KS = (int)((dims1 >> 8) & 0xffu);
+  n_xcc = (int)((dims1 >> 16) & 0xffu);
+  fenced = (int)(dims1 >> 24);
+}
+
 template <int WK, int EPI, int U>
-__global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int KS) {
+__global__ __launch_bounds__(256) void skinny_wide_kernel(
+    const uint32_t* __restrict__ qw, const uint32_t* __restrict__ sbp,
+    const float* __restrict__ hidden, const uint16_t* __restrict__ norm_w,
+    const float* __restrict__ ss_arg, int* perr, uint32_t dims0, uint32_t dims1,
+    const FusedArgs a) {
   constexpr bool BF = WK == W_BF16;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int M = a.M, N = a.N, K = a.K;
-  auto gqw = (SK_GLOBAL(const uint32_t)*)(BF ? (const uint32_t*)a.wb : a.qw);
-  auto gsb = (SK_GLOBAL(const uint32_t)*)a.sb;
-  auto ghid = (SK_GLOBAL(const float)*)a.hidden;
-  auto gnw = (SK_GLOBAL(const uint16_t)*)a.norm_w;
-  auto gss = (SK_GLOBAL(const float)*)a.ss_in;
-  auto gerr = (SK_GLOBAL(int)*)a.placement_err;
-  int n_xcc = a.n_xcc;
-  asm volatile("" : "+s"(gqw), "+s"(gsb), "+s"(ghid), "+s"(gnw), "+s"(gss), "+s"(gerr), "+s"(M),
-               "+s"(N), "+s"(K), "+s"(n_xcc), "+s"(KS));
-  const uint32_t* qw = (const uint32_t*)gqw;
-  const uint32_t* sbp = (const uint32_t*)gsb;
-  const float* hidden = (const float*)ghid;
-  const uint16_t* norm_w = (const uint16_t*)gnw;
-  int* perr = (int*)gerr;
+  int M, N, K, KS, n_xcc, fenced;
+  sk_dims(dims0, dims1, M, N, K, KS, n_xcc, fenced);
   // 32-row tile of this work-group: rows m0 .. m0 + M - 1 of the forward
   const int mt = blockIdx.y, m0 = 32 * mt, M_all = M;
   M = min(32, M_all - m0);
   hidden += (int64_t)m0 * K;
-  const float* ss_in = (const float*)gss + (int64_t)mt * K;
+  const float* ss_in = ss_arg + (int64_t)mt * K;
   float* part = a.part + (size_t)mt * a.part_floats;
   int* counters = a.counters + (size_t)mt * a.n_counters;
   const int G = K >> 6;
   int grp, ks;
-  const bool live = sk_place(n_xcc, a.fenced, perr, N / 128, KS, grp, ks);
+  const bool live = sk_place(n_xcc, fenced, perr, N / 128, KS, grp, ks);
   const int nt = grp * 4 + wave;
   const int u0 = ks * U, kc0 = u0 * 64;
   constexpr int KCN = U * 64;
@@ -406,21 +412,14 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(const FusedArgs a, int
 // UW: units per wave held in registers at once (the wave's units are processed
 // in chunks of UW, each chunk's loads issued together).
 template <int WK, int EPI, int UW>
-__global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, int KS) {
+__global__ __launch_bounds__(256) void skinny_narrow_kernel(
+    const uint32_t* __restrict__ qw, const uint32_t* __restrict__ sbp,
+    const uint16_t* __restrict__ act, int* perr, uint32_t dims0, uint32_t dims1,
+    const FusedArgs a) {
   constexpr bool BF = WK == W_BF16;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int M = a.M, N = a.N, K = a.K;
-  auto gqw = (SK_GLOBAL(const uint32_t)*)(BF ? (const uint32_t*)a.wb : a.qw);
-  auto gsb = (SK_GLOBAL(const uint32_t)*)a.sb;
-  auto gact = (SK_GLOBAL(const uint16_t)*)a.act;
-  auto gerr = (SK_GLOBAL(int)*)a.placement_err;
-  int n_xcc = a.n_xcc;
-  asm volatile("" : "+s"(gqw), "+s"(gsb), "+s"(gact), "+s"(gerr), "+s"(M), "+s"(N), "+s"(K),
-               "+s"(n_xcc), "+s"(KS));
-  const uint32_t* qw = (const uint32_t*)gqw;
-  const uint32_t* sbp = (const uint32_t*)gsb;
-  const uint16_t* act = (const uint16_t*)gact;
-  int* perr = (int*)gerr;
+  int M, N, K, KS, n_xcc, fenced;
+  sk_dims(dims0, dims1, M, N, K, KS, n_xcc, fenced);
   // 32-row tile of this work-group: rows m0 .. m0 + M - 1 of the forward
   const int mt = blockIdx.y, m0 = 32 * mt, M_all = M;
   M = min(32, M_all - m0);
@@ -429,7 +428,7 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
   const int G = K >> 6;
   const int U = G / KS;
   int nt, ks;
-  const bool live = sk_place(n_xcc, a.fenced, perr, N / 32, KS, nt, ks);
+  const bool live = sk_place(n_xcc, fenced, perr, N / 32, KS, nt, ks);
   const int u_lo = ks * U + (U * wave) / 4, u_hi = ks * U + (U * (wave + 1)) / 4;
   extern __shared__ __align__(16) char smem[];
   float* red = (float*)smem;  // [4][32][33]
@@ -578,13 +577,20 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(const FusedArgs a, i
   }
 }
 
-#define DRT_WIDE(W, E, U) template __global__ void skinny_wide_kernel<W, E, U>(const FusedArgs, int);
+#define DRT_WIDE(W, E, U)                                                                   \
+  template __global__ void skinny_wide_kernel<W, E, U>(const uint32_t*, const uint32_t*,       \
+                                                       const float*, const uint16_t*,          \
+                                                       const float*, int*, uint32_t, uint32_t, \
+                                                       const FusedArgs);
 #define DRT_WIDE_U(W, E) DRT_WIDE(W, E, 1) DRT_WIDE(W, E, 2) DRT_WIDE(W, E, 4) DRT_WIDE(W, E, 8)
 DRT_WIDE_U(W_Q4, EPI_QKV) DRT_WIDE_U(W_Q4, EPI_SWIGLU)
 DRT_WIDE_U(W_BF16, EPI_QKV) DRT_WIDE_U(W_BF16, EPI_SWIGLU)
 #undef DRT_WIDE_U
 #undef DRT_WIDE
-#define DRT_NARROW(W, E, UW) template __global__ void skinny_narrow_kernel<W, E, UW>(const FusedArgs, int);
+#define DRT_NARROW(W, E, UW)                                                                \
+  template __global__ void skinny_narrow_kernel<W, E, UW>(const uint32_t*, const uint32_t*,    \
+                                                          const uint16_t*, int*, uint32_t,      \
+                                                          uint32_t, const FusedArgs);
 DRT_NARROW(W_Q4, EPI_RESID, 1) DRT_NARROW(W_Q4, EPI_RESID, 2)
 DRT_NARROW(W_Q4, EPI_STORE, 1) DRT_NARROW(W_Q4, EPI_STORE, 2)
 DRT_NARROW(W_BF16, EPI_RESID, 1) DRT_NARROW(W_BF16, EPI_RESID, 2)
@@ -652,12 +658,24 @@ size_t skinny_part_floats(int N, int K) {
 
 int skinny_counters(int N) { return N / 32; }
 
+namespace {
+uint32_t sk_dims1(const FusedArgs& a, int KS) {
+  return (uint32_t)a.M | ((uint32_t)KS << 8) | ((uint32_t)a.n_xcc << 16) |
+         ((uint32_t)(a.fenced ? 1 : 0) << 24);
+}
+}  // namespace
+
 bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
   const int MT = (a.M + 31) / 32;
   if ((!a.qw && !a.wb) || a.M < 1 || MT > a.sk_row_tiles || !a.part ||
       !a.counters || a.K % 64 || a.N % 32 || a.n_xcc < 1)
     return false;
   const bool bf = a.qw == nullptr;
+  const uint32_t* wq = bf ? (const uint32_t*)a.wb : a.qw;
+  // the packed sizes of the kernels' leading arguments (see sk_dims)
+  require(a.N < 65536 && a.K < 65536 && a.M < 256 && a.n_xcc < 256,
+          "split-K linear sizes exceed the packed argument fields");
+  const uint32_t dims0 = (uint32_t)a.N | ((uint32_t)a.K << 16);
   const int G = a.K / 64;
   const double bytes = (bf ? 2.0 * a.N * a.K : (double)a.N * a.K / 2 + (double)a.N * a.K / 16) +
                        2.0 * a.M * a.K + 2.0 * a.M * a.N;
@@ -675,7 +693,8 @@ bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
     auto fn = skinny_wide_kernel<W, E, UU>;                                       \
     static size_t granted = 0;                                                    \
     grant_lds((const void*)fn, lds, granted);                                     \
-    DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(256), lds, s, a, KS);        \
+    DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(256), lds, s, wq, a.sb, a.hidden, \
+               a.norm_w, a.ss_in, a.placement_err, dims0, sk_dims1(a, KS), a);    \
   }
 #define DRT_SW(E, UU)                  \
   {                                    \
@@ -708,7 +727,8 @@ bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
     auto fn = skinny_narrow_kernel<W, E, UW>;                                      \
     static size_t granted = 0;                                                     \
     grant_lds((const void*)fn, SK_NARROW_LDS(UW), granted);                        \
-    DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(256), SK_NARROW_LDS(UW), s, a, KS); \
+    DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(256), SK_NARROW_LDS(UW), s, wq, a.sb, \
+               (const uint16_t*)a.act, a.placement_err, dims0, sk_dims1(a, KS), a);      \
   }
 #define DRT_SN(E, UW)                  \
   {                                    \
