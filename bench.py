@@ -176,11 +176,37 @@ def _event_time_us(fn, reps: int) -> float:
     return e0.elapsed_time(e1) / reps * 1e3
 
 
+def _graph_time_us(fn, reps: int) -> float:
+    """Per-call device time of `reps` calls captured in one HIP graph and replayed
+    (no host work between the calls: what a graph-capturing caller sees)."""
+    import torch
+
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(5):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (5 * reps) * 1e3
+
+
 def bench_attention() -> None:
     """Isolated block-over-prefix attention: 32 query rows x 16 heads x 128, bf16,
     K/V of L prefix + 32 block keys x 8 heads, N(0, 1) from seed 1, prefix fully
     visible and the block bidirectional; fp32 accumulate, bf16 output. Timed per
-    call (decode attention + range combine) on the torch stream."""
+    call (Q planes, decode attention, range combine) on the torch stream: 50 calls
+    captured in a HIP graph and replayed, and 50 eager calls."""
     import ctypes as C
 
     import torch
@@ -200,18 +226,20 @@ def bench_attention() -> None:
         out = torch.empty((rows, hq * 128), dtype=torch.bfloat16, device="cuda")
         ws_b = lib.drt_op_attention_workspace_bytes(rows, hq, hkv, n)
         ws = torch.empty(ws_b, dtype=torch.uint8, device="cuda")
-        st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
-
         def run():
+            st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
             _lib.check(lib.drt_op_attention(
                 C.c_void_p(q.data_ptr()), C.c_void_p(cache.data.data_ptr()), cache.head_stride,
                 _lib.BF16, rows, hq, hkv, n, L, 0, 0, 1, C.c_void_p(out.data_ptr()), _lib.BF16,
                 C.c_void_p(ws.data_ptr()), ws_b, st))
 
-        us = _event_time_us(run, 50)
+        us_eager = _event_time_us(run, 50)
+        us = _graph_time_us(run, 50)
         byts = 4.0 * rows * hq * 128 + 4096.0 * n
         print(json.dumps({"workload": "attention", "prefix": L, "rows": rows, "heads": [hq, hkv],
                           "dtype": "bf16", "us_per_call": round(us, 2),
+                          "timed": "50 calls in a HIP graph",
+                          "us_per_call_eager": round(us_eager, 2),
                           "algorithmic_bytes": byts,
                           "achieved_GBps": round(byts / us / 1e3, 1),
                           "hbm_frac": round(byts / us / 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
@@ -220,7 +248,8 @@ def bench_attention() -> None:
 def bench_q4_linear() -> None:
     """Isolated q4 g64 linear (MLX packing): nibbles U{0..15}, scales U(0.005, 0.02),
     biases U(-0.1, 0.1) (bf16), x bf16 N(0, 1), seed 2. Timed per call on the
-    per-op entry point (activation preparation + the linear)."""
+    per-op entry point: 30 calls captured in a HIP graph and replayed (device
+    time per call), and 30 eager calls (host launch rate included)."""
     import ctypes as C
 
     import torch
@@ -236,11 +265,14 @@ def bench_q4_linear() -> None:
         w = kernels.DeviceQ4Weight(qt.w_q.cuda(), qt.scales.cuda(), qt.biases.cuda())
         for M in (32, 128):
             x = torch.randn((M, K), generator=gen).bfloat16().cuda()
-            us = _event_time_us(lambda: kernels.linear(x, w), 30)
+            us_eager = _event_time_us(lambda: kernels.linear(x, w), 30)
+            us = _graph_time_us(lambda: kernels.linear(x, w), 30)
             byts = N * K / 2 + N * K / 16 + 2.0 * M * K + 4.0 * M * N
             flops = 2.0 * M * N * K
             print(json.dumps({"workload": "q4_linear", "M": M, "N": N, "K": K,
-                              "us_per_call": round(us, 2), "algorithmic_bytes": byts,
+                              "us_per_call": round(us, 2), "timed": "30 calls in a HIP graph",
+                              "us_per_call_eager": round(us_eager, 2),
+                              "algorithmic_bytes": byts,
                               "achieved_GBps": round(byts / us / 1e3, 1),
                               "hbm_frac": round(byts / us / 1e3 / HBM_PEAK_GBS, 4),
                               "achieved_TFLOPs": round(flops / us / 1e6, 2),

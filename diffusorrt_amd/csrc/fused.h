@@ -23,8 +23,10 @@ struct FusedArgs {
   // device-scope fences and atomics instead of one XCD's L2
   int fenced = 0;
   int* placement_err = nullptr;
-  // PRO_ACT: activation [M][K] (ACT_F16P + xsum[M][K/64], or ACT_BF16)
+  // PRO_ACT: activation [M][K] (ACT_F16P + xsum[M][K/64], or ACT_BF16); for
+  // the split-K q4 store kernel also fp32 (x_in 1) or bf16 (x_in 2) rows
   const void* act = nullptr;
+  int x_in = 0;
   const float* act_xsum = nullptr;
   // PRO_NORM: fp32 residual stream [M][K] and bf16 norm weight [K]
   const float* hidden = nullptr;

@@ -1790,9 +1790,67 @@ size_t drt_op_q4_linear_workspace_bytes(int32_t m, int32_t n, int32_t k) {
   if (m <= 0 || k <= 0) return 0;
   size_t b = q4_op_act_bytes(m, k) + 256;
   if (m > 32 && n > 0) b += (size_t)big_linear_splits(m, n, k, BG_OP_MAX_KS) * m * n * 4;
-  if (m <= 32 && n > 0) b += stream_part_floats(m, n, k, BG_OP_MAX_KS) * 4;
+  if (m <= 32 && n > 0)
+    b += std::max(stream_part_floats(m, n, k, BG_OP_MAX_KS), skinny_part_floats(n, k)) * 4;
   return b;
 }
+
+// The split-K store kernel of the per-op path (<= 32 rows): its arrival counters
+// live in a device array of the library, zero from load and left zero by every
+// launch, one block of OP_COUNTERS per (device, stream) so that calls on
+// different streams never share one; the XCD placement is probed once per
+// device (on a stream of its own, synchronised once).
+constexpr int OP_COUNTER_BLOCKS = 32, OP_COUNTERS = 4096;
+static __device__ int op_counters[OP_COUNTER_BLOCKS * OP_COUNTERS];
+static __device__ int op_probe[256];
+namespace {
+struct OpDevice {
+  int* counters = nullptr;
+  int n_xcc = 1;
+  bool fenced = false;
+  std::map<hipStream_t, int> blocks;
+};
+std::mutex g_op_mu;
+std::map<int, OpDevice> g_op_dev;
+
+// The counter block of (current device, stream) and the device's placement,
+// or nullptr when every block is taken (the caller then takes another path).
+int* op_counters_for(hipStream_t stream, int& n_xcc, bool& fenced) {
+  int dev = -1;
+  DRT_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(g_op_mu);
+  OpDevice& d = g_op_dev[dev];
+  if (!d.counters) {
+    void* c = nullptr;
+    void* pr = nullptr;
+    DRT_HIP(hipGetSymbolAddress(&c, HIP_SYMBOL(op_counters)));
+    DRT_HIP(hipGetSymbolAddress(&pr, HIP_SYMBOL(op_probe)));
+    int nx = 1;
+    if (hipDeviceGetAttribute(&nx, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess) nx = 1;
+    d.n_xcc = std::max(1, nx);
+    hipStream_t ps = nullptr;
+    DRT_HIP(hipStreamCreateWithFlags(&ps, hipStreamNonBlocking));
+    bool rr = false;
+    try {
+      rr = probe_round_robin(d.n_xcc, (int*)pr, ps);
+    } catch (...) {
+      (void)hipStreamDestroy(ps);
+      throw;
+    }
+    DRT_HIP(hipStreamDestroy(ps));
+    d.fenced = !rr;
+    d.counters = (int*)c;
+  }
+  n_xcc = d.n_xcc;
+  fenced = d.fenced;
+  auto it = d.blocks.find(stream);
+  if (it == d.blocks.end()) {
+    if ((int)d.blocks.size() >= OP_COUNTER_BLOCKS) return nullptr;
+    it = d.blocks.emplace(stream, (int)d.blocks.size()).first;
+  }
+  return d.counters + (size_t)it->second * OP_COUNTERS;
+}
+}  // namespace
 
 int32_t drt_op_q4_repack(const void* w_q, const void* scales, const void* biases, int32_t n,
                          int32_t k, void* qw, void* sb, void* stream) {
@@ -1834,6 +1892,28 @@ static void q4_linear_into(const void* qw, const void* sb, const void* x, int32_
     _Float16* xp = (_Float16*)ws;
     float* xs = (float*)(ws + (size_t)2 * m * k * 2);
     hipStream_t st = as_stream(stream);
+    const StreamPlan sp = stream_plan(m, n, k, BG_OP_MAX_KS);
+    if (m <= 32 && sp.KS < 1 && n / 32 <= OP_COUNTERS) {
+      // one launch: the split-K store kernel reads the fp32 / bf16 rows itself
+      FusedArgs g;
+      g.qw = (const uint32_t*)qw;
+      g.sb = (const uint32_t*)sb;
+      g.bias = (const uint16_t*)bias;
+      g.M = m;
+      g.N = n;
+      g.K = k;
+      g.act = x;
+      g.x_in = x_dtype == DRT_BF16 ? 2 : 1;
+      g.y = y;
+      g.part = (float*)(ws + q4_op_act_bytes(m, k));
+      g.part_floats = skinny_part_floats(n, k);
+      g.sk_row_tiles = 1;
+      bool fenced = false;
+      g.counters = op_counters_for(st, g.n_xcc, fenced);
+      g.n_counters = OP_COUNTERS;
+      g.fenced = fenced ? 1 : 0;
+      if (g.counters && skinny_linear(g, FL_STORE, st)) return;
+    }
     q4_act_prep(x, x_dtype == DRT_BF16, m, k, xp, xs, st);
     FusedArgs f;
     f.qw = (const uint32_t*)qw;
@@ -1846,7 +1926,6 @@ static void q4_linear_into(const void* qw, const void* sb, const void* x, int32_
     f.act_xsum = xs;
     f.y = y;
     const int ks = m > 32 ? big_linear_splits(m, n, k, BG_OP_MAX_KS) : 1;
-    const StreamPlan sp = stream_plan(m, n, k, BG_OP_MAX_KS);
     if (sp.KS >= 1) {
       // large weights, <= 32 rows: streamed in fp32 K slices, summed (+ bias) into y
       float* part = (float*)(ws + q4_op_act_bytes(m, k));

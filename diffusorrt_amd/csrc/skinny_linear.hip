@@ -411,11 +411,15 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(
 
 // UW: units per wave held in registers at once (the wave's units are processed
 // in chunks of UW, each chunk's loads issued together).
-template <int WK, int EPI, int UW>
+// XIN: the activation's format. 0: ACT_F16P (hi plane, lo plane at + M * K);
+// 1: fp32 rows [M][K] and 2: bf16 rows (a per-op call's input), split into the
+// hi and lo planes in registers on the way to LDS (no preparation pass).
+template <int WK, int EPI, int UW, int XIN>
 __global__ __launch_bounds__(256) void skinny_narrow_kernel(
     const uint32_t* __restrict__ qw, const uint32_t* __restrict__ sbp,
     const uint16_t* __restrict__ act, int* perr, uint32_t dims0, uint32_t dims1,
     const FusedArgs a) {
+  static_assert(XIN == 0 || WK == W_Q4, "fp32 / bf16 rows feed the q4 kernels only");
   constexpr bool BF = WK == W_BF16;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int M, N, K, KS, n_xcc, fenced;
@@ -438,9 +442,11 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(
   // this wave's A staging: [2 planes][UW][32 rows][144 B] (128 B of a unit's row + pad)
   char* stg = smem + SK_NARROW_STG + wave * (2 * UW * 32 * 144);
   const uint16_t* act_lo = act + (int64_t)M_all * K + (int64_t)m0 * K;  // ACT_F16P lo plane
+  const float* x32 = (const float*)act + (int64_t)m0 * K;                // XIN == 1
   act += (int64_t)m0 * K;
   for (int ub = u_lo; ub < u_hi || ub == u_lo; ub += UW) {
     u32x4 wq[UW][BF ? 4 : 1], craw[UW][4], crawl[UW][4], af[UW][4], afl[UW][4];
+    f32x4 xr[XIN == 1 ? UW : 1][4][2];  // XIN == 1: the lane's 8 fp32 values
     uint32_t wsb[UW];
     // the activation (from L2) is issued before the weights (from HBM): loads
     // retire in issue order, so the LDS transpose below would otherwise wait
@@ -455,8 +461,13 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int64_t off = (int64_t)min(8 * j + (lane >> 3), M - 1) * K + u * 64 + (lane & 7) * 8;
-        craw[i][j] = *(const u32x4*)(act + off);
-        if (!BF) crawl[i][j] = *(const u32x4*)(act_lo + off);
+        if (XIN == 1) {
+          xr[XIN == 1 ? i : 0][j][0] = *(const f32x4*)(x32 + off);
+          xr[XIN == 1 ? i : 0][j][1] = *(const f32x4*)(x32 + off + 4);
+        } else {
+          craw[i][j] = *(const u32x4*)(act + off);  // XIN == 2: 8 bf16 values
+          if (!BF && XIN == 0) crawl[i][j] = *(const u32x4*)(act_lo + off);
+        }
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -475,6 +486,32 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(
       }
     }
     __builtin_amdgcn_sched_barrier(0);
+    if (XIN != 0) {
+      // fp32 / bf16 rows: the 8 values of each piece as fp16 hi and lo, each
+      // 32-bit word holding elements (w, w + 4) (the ACT_F16P chunk order)
+#pragma unroll
+      for (int i = 0; i < UW; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float v[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            if (XIN == 1) v[e] = xr[XIN == 1 ? i : 0][j][e >> 2][e & 3];
+            else v[e] = bf16_bits_to_float(e & 1 ? craw[i][j][e >> 1] >> 16
+                                                  : craw[i][j][e >> 1] & 0xffffu);
+          }
+          u32x4 hp, lp;
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const _Float16 h0 = (_Float16)v[w], h1 = (_Float16)v[w + 4];
+            hp[w] = (uint32_t)half_bits(h0) | ((uint32_t)half_bits(h1) << 16);
+            lp[w] = (uint32_t)half_bits(f16_lo(v[w], h0)) |
+                    ((uint32_t)half_bits(f16_lo(v[w + 4], h1)) << 16);
+          }
+          craw[i][j] = hp;
+          crawl[i][j] = lp;
+        }
+    }
     // through LDS into the q4 fragment order: lane l takes row l & 31, 16-byte
     // chunks 4(l >> 5) + t, i.e. k = 32(l >> 5) + 8t .. +8 (one wave's LDS
     // operations run in order: no barrier)
@@ -587,14 +624,18 @@ DRT_WIDE_U(W_Q4, EPI_QKV) DRT_WIDE_U(W_Q4, EPI_SWIGLU)
 DRT_WIDE_U(W_BF16, EPI_QKV) DRT_WIDE_U(W_BF16, EPI_SWIGLU)
 #undef DRT_WIDE_U
 #undef DRT_WIDE
-#define DRT_NARROW(W, E, UW)                                                                \
-  template __global__ void skinny_narrow_kernel<W, E, UW>(const uint32_t*, const uint32_t*,    \
-                                                          const uint16_t*, int*, uint32_t,      \
-                                                          uint32_t, const FusedArgs);
+#define DRT_NARROW(W, E, UW) DRT_NARROW_X(W, E, UW, 0)
+#define DRT_NARROW_X(W, E, UW, X)                                                             \
+  template __global__ void skinny_narrow_kernel<W, E, UW, X>(const uint32_t*, const uint32_t*, \
+                                                             const uint16_t*, int*, uint32_t,   \
+                                                             uint32_t, const FusedArgs);
 DRT_NARROW(W_Q4, EPI_RESID, 1) DRT_NARROW(W_Q4, EPI_RESID, 2)
 DRT_NARROW(W_Q4, EPI_STORE, 1) DRT_NARROW(W_Q4, EPI_STORE, 2)
 DRT_NARROW(W_BF16, EPI_RESID, 1) DRT_NARROW(W_BF16, EPI_RESID, 2)
 DRT_NARROW(W_BF16, EPI_STORE, 1) DRT_NARROW(W_BF16, EPI_STORE, 2)
+DRT_NARROW_X(W_Q4, EPI_STORE, 1, 1) DRT_NARROW_X(W_Q4, EPI_STORE, 2, 1)
+DRT_NARROW_X(W_Q4, EPI_STORE, 1, 2) DRT_NARROW_X(W_Q4, EPI_STORE, 2, 2)
+#undef DRT_NARROW_X
 #undef DRT_NARROW
 
 namespace drt {
@@ -680,7 +721,7 @@ bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
   const double bytes = (bf ? 2.0 * a.N * a.K : (double)a.N * a.K / 2 + (double)a.N * a.K / 16) +
                        2.0 * a.M * a.K + 2.0 * a.M * a.N;
   if (kind == FL_QKV || kind == FL_SWIGLU) {
-    if (!a.ss_in || a.N % 128 || a.K / 32 > 8 * SK_SS_PER_THREAD) return false;
+    if (a.x_in != 0 || !a.ss_in || a.N % 128 || a.K / 32 > 8 * SK_SS_PER_THREAD) return false;
     const int U = wide_units(a.N, a.K);
     if (!U) return false;
     const int KS = G / U, NG = a.N / 128;
@@ -722,9 +763,10 @@ bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
       return false;
     const int per_wave = (G / KS + 3) / 4;
     const dim3 grid((unsigned)((NT + a.n_xcc - 1) / a.n_xcc * a.n_xcc * KS), MT);
-#define DRT_SN1(W, E, UW)                                                          \
+#define DRT_SN1(W, E, UW) DRT_SN1X(W, E, UW, 0)
+#define DRT_SN1X(W, E, UW, X)                                                      \
   {                                                                                \
-    auto fn = skinny_narrow_kernel<W, E, UW>;                                      \
+    auto fn = skinny_narrow_kernel<W, E, UW, X>;                                   \
     static size_t granted = 0;                                                     \
     grant_lds((const void*)fn, SK_NARROW_LDS(UW), granted);                        \
     DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(256), SK_NARROW_LDS(UW), s, wq, a.sb, \
@@ -740,12 +782,20 @@ bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
     // work-groups: one unit at a time keeps two of them per CU (the LDS of
     // two-unit staging holds one), so they run in one round instead of two.
     const bool one_unit = per_wave <= 1 || MT > 1;
-    if (kind == FL_RESID) {
+    if (a.x_in != 0) {
+      if (kind != FL_STORE || bf) return false;
+      if (a.x_in == 1) {
+        if (one_unit) DRT_SN1X(W_Q4, EPI_STORE, 1, 1) else DRT_SN1X(W_Q4, EPI_STORE, 2, 1)
+      } else {
+        if (one_unit) DRT_SN1X(W_Q4, EPI_STORE, 1, 2) else DRT_SN1X(W_Q4, EPI_STORE, 2, 2)
+      }
+    } else if (kind == FL_RESID) {
       if (one_unit) DRT_SN(EPI_RESID, 1) else DRT_SN(EPI_RESID, 2)
     } else {
       if (one_unit) DRT_SN(EPI_STORE, 1) else DRT_SN(EPI_STORE, 2)
     }
 #undef DRT_SN
+#undef DRT_SN1X
 #undef DRT_SN1
   } else {
     return false;
