@@ -67,6 +67,7 @@ DRT_DEV float max_xor32(float v) {
 template <typename T, int QW>
 __global__ __launch_bounds__(64 * QW) void attn_split_kernel(
     const T* __restrict__ q,       // [n_rows][Hq][128]
+    const T* __restrict__ q_lo,    // its lo plane (the same layout), or null (zero)
     const T* __restrict__ kv,      // this layer: [Hkv][tile_cap][8192]
     int64_t kv_head_stride,        // elements between kv heads
     int n_rows, int Hq, int Hkv, int n_keys, int row_pos0,
@@ -95,15 +96,17 @@ __global__ __launch_bounds__(64 * QW) void attn_split_kernel(
   const bool q_ok = qv < n_qv;
   const int qrow = q_ok ? qv / G : 0;
   const int qhead = kvh * G + (q_ok ? qv - (qv / G) * G : 0);
-  vec qf[8], qfl[8];  // Q hi / lo planes (lo at + n_rows * Hq * 128)
+  vec qf[8], qfl[8];  // Q hi / lo planes
   {
-    const T* qp = q + ((int64_t)qrow * Hq + qhead) * 128 + 8 * (lane >> 5);
-    const T* qpl = qp + (int64_t)n_rows * Hq * 128;
+    const int64_t qo = ((int64_t)qrow * Hq + qhead) * 128 + 8 * (lane >> 5);
+    const T* qp = q + qo;
+    const T* qpl = (q_lo ? q_lo : q) + qo;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       if (q_ok) {
         qf[i] = *(const vec*)(qp + 16 * i);
         qfl[i] = *(const vec*)(qpl + 16 * i);
+        if (!q_lo) qfl[i] = vec{};
       } else {
         qf[i] = qfl[i] = vec{};
       }
@@ -415,7 +418,8 @@ DRT_DEV bool decr_wait(const int* flag, int want, int* err) {
 
 template <typename T, int QT>
 __global__ __launch_bounds__(320) void attn_decode_kernel(
-    const T* __restrict__ q, const T* __restrict__ kv, int64_t kv_head_stride, int n_rows,
+    const T* __restrict__ q, const T* __restrict__ q_lo, const T* __restrict__ kv,
+    int64_t kv_head_stride, int n_rows,
     int Hq, int Hkv, int n_keys_arg, const StepDesc* __restrict__ desc,
     float* __restrict__ o_part, float* __restrict__ ml_part, float scale, int* err) {
   typedef typename MfmaT<T>::vec vec;
@@ -470,7 +474,7 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
     const int n0 = min(n, 2);
     for (int t = 0; t < n0; ++t) dma_tile(t);
   } else {
-    const T* q_lo = q + (int64_t)n_rows * Hq * 128;  // the Q lo plane
+    const T* ql = q_lo ? q_lo : q;  // the Q lo plane (null: zero)
     u32x4 qraw[QCH], qrawl[QCH];
 #pragma unroll
     for (int i = 0; i < QCH; ++i) {
@@ -479,7 +483,7 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
       const int row = qvc / G, head = kvh * G + (qvc - row * G);
       const int64_t off = ((int64_t)row * Hq + head) * 128 + (ch & 15) * 8;
       qraw[i] = *(const u32x4*)(q + off);
-      qrawl[i] = *(const u32x4*)(q_lo + off);
+      qrawl[i] = *(const u32x4*)(ql + off);
     }
     if (threadIdx.x < 2 * DECR_SLOTS) ready[threadIdx.x] = 0;  // ready and freed
 #pragma unroll
@@ -488,7 +492,7 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
       const bool ok = (ch >> 4) < n_qv;
       T* d = qs + (ch >> 4) * DEC_QROW + (ch & 15) * 8;
       *(u32x4*)d = ok ? qraw[i] : u32x4{0u, 0u, 0u, 0u};
-      *(u32x4*)(d + QLO) = ok ? qrawl[i] : u32x4{0u, 0u, 0u, 0u};
+      *(u32x4*)(d + QLO) = ok && q_lo ? qrawl[i] : u32x4{0u, 0u, 0u, 0u};
     }
     decr_waitcnt<DECR_LGKM0>();  // Q and the flags are written
   }
@@ -890,37 +894,37 @@ __global__ void kv_pack_kernel(const void* __restrict__ k_src, const void* __res
   }
 }
 
-template __global__ void attn_split_kernel<_Float16, 2>(const _Float16*, const _Float16*, int64_t,
+template __global__ void attn_split_kernel<_Float16, 2>(const _Float16*, const _Float16*, const _Float16*, int64_t,
                                                         int, int, int, int, int, int, int, int, int,
                                                         float*, float*, float);
-template __global__ void attn_split_kernel<_Float16, 4>(const _Float16*, const _Float16*, int64_t,
+template __global__ void attn_split_kernel<_Float16, 4>(const _Float16*, const _Float16*, const _Float16*, int64_t,
                                                         int, int, int, int, int, int, int, int, int,
                                                         float*, float*, float);
-template __global__ void attn_split_kernel<__bf16, 2>(const __bf16*, const __bf16*, int64_t, int,
+template __global__ void attn_split_kernel<__bf16, 2>(const __bf16*, const __bf16*, const __bf16*, int64_t, int,
                                                       int, int, int, int, int, int, int, int,
                                                       float*, float*, float);
-template __global__ void attn_split_kernel<__bf16, 4>(const __bf16*, const __bf16*, int64_t, int,
+template __global__ void attn_split_kernel<__bf16, 4>(const __bf16*, const __bf16*, const __bf16*, int64_t, int,
                                                       int, int, int, int, int, int, int, int,
                                                       float*, float*, float);
-template __global__ void attn_decode_kernel<_Float16, 1>(const _Float16*, const _Float16*,
+template __global__ void attn_decode_kernel<_Float16, 1>(const _Float16*, const _Float16*, const _Float16*,
                                                           int64_t, int, int, int, int,
                                                           const StepDesc*, float*, float*, float,
                                                           int*);
-template __global__ void attn_decode_kernel<_Float16, 2>(const _Float16*, const _Float16*,
+template __global__ void attn_decode_kernel<_Float16, 2>(const _Float16*, const _Float16*, const _Float16*,
                                                           int64_t, int, int, int, int,
                                                           const StepDesc*, float*, float*, float,
                                                           int*);
-template __global__ void attn_decode_kernel<__bf16, 1>(const __bf16*, const __bf16*, int64_t, int,
+template __global__ void attn_decode_kernel<__bf16, 1>(const __bf16*, const __bf16*, const __bf16*, int64_t, int,
                                                         int, int, int, const StepDesc*, float*,
                                                         float*, float, int*);
-template __global__ void attn_decode_kernel<_Float16, 4>(const _Float16*, const _Float16*,
+template __global__ void attn_decode_kernel<_Float16, 4>(const _Float16*, const _Float16*, const _Float16*,
                                                        int64_t, int, int, int, int,
                                                        const StepDesc*, float*, float*, float,
                                                        int*);
-template __global__ void attn_decode_kernel<__bf16, 4>(const __bf16*, const __bf16*, int64_t, int,
+template __global__ void attn_decode_kernel<__bf16, 4>(const __bf16*, const __bf16*, const __bf16*, int64_t, int,
                                                      int, int, int, const StepDesc*, float*,
                                                      float*, float, int*);
-template __global__ void attn_decode_kernel<__bf16, 2>(const __bf16*, const __bf16*, int64_t, int,
+template __global__ void attn_decode_kernel<__bf16, 2>(const __bf16*, const __bf16*, const __bf16*, int64_t, int,
                                                         int, int, int, const StepDesc*, float*,
                                                         float*, float, int*);
 template __global__ void kv_pack_kernel<_Float16>(const void*, const void*, int, int, int, int,
@@ -956,7 +960,8 @@ size_t attention_part_bytes(const AttnPlan& p, int n_rows, int Hq, int Hkv) {
 void attention(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_stride,
                int n_rows, int Hq, int Hkv, int n_keys, int row_pos0, int mask_kind,
                int mask_prompt_len, int mask_block, const AttnPlan& plan, float* o_part,
-               float* ml_part, void* out, float* xsum, int out_fmt, hipStream_t s, int* err) {
+               float* ml_part, void* out, float* xsum, int out_fmt, hipStream_t s, int* err,
+               bool q_has_lo) {
   require(Hq % Hkv == 0, "attention needs Hq % Hkv == 0");
   require(n_keys >= 1 && n_rows >= 1, "attention needs at least one query row and key");
   const float scale = 1.0f / sqrtf(128.0f);
@@ -971,9 +976,11 @@ void attention(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_s
     auto fn = attn_split_kernel<T, QW>;                                                         \
     static size_t granted = 0;                                                                  \
     grant_lds((const void*)fn, lds, granted);                                                   \
-    DRT_LAUNCH(Profiler::ATTN, bytes, fn, grid, block, lds, s, (const T*)q, (const T*)kv_layer,  \
-               kv_head_stride, n_rows, Hq, Hkv, n_keys, row_pos0, mask_kind, mask_prompt_len,   \
-               mask_block, plan.tiles_per_split, o_part, ml_part, scale);                       \
+    DRT_LAUNCH(Profiler::ATTN, bytes, fn, grid, block, lds, s, (const T*)q,                     \
+               q_has_lo ? (const T*)q + (int64_t)n_rows * Hq * 128 : (const T*)nullptr,         \
+               (const T*)kv_layer, kv_head_stride, n_rows, Hq, Hkv, n_keys, row_pos0,           \
+               mask_kind, mask_prompt_len, mask_block, plan.tiles_per_split, o_part, ml_part,   \
+               scale);                                                                          \
   }
   if (bf16) {
     if (plan.qw == 2) DRT_ATTN(__bf16, 2) else DRT_ATTN(__bf16, 4)
@@ -1007,7 +1014,8 @@ int attention_decode_ranges(int n_keys, int Hkv) {
 // `part` holds attention_decode_part_bytes(ranges, Hkv, n_rows * Hq / Hkv).
 void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_stride,
                       int n_rows, int Hq, int Hkv, int n_keys, const StepDesc* desc, int ranges,
-                      float* part, void* out, float* xsum, int out_fmt, hipStream_t s, int* err) {
+                      float* part, void* out, float* xsum, int out_fmt, hipStream_t s, int* err,
+                      bool q_has_lo) {
   const int G = Hq / Hkv;
   require(Hq % Hkv == 0 && n_rows * G <= 128,
           "decode attention needs <= 128 query vectors per head");
@@ -1024,6 +1032,7 @@ void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv
     static size_t granted = 0;                                                              \
     grant_lds((const void*)fn, ldsr, granted);                                              \
     DRT_LAUNCH(Profiler::ATTN, bytes, fn, grid, dim3(320), ldsr, s, (const T*)q,            \
+               q_has_lo ? (const T*)q + (int64_t)n_rows * Hq * 128 : (const T*)nullptr,     \
                (const T*)kv_layer, kv_head_stride, n_rows, Hq, Hkv, n_keys, desc, o_part,   \
                ml_part, scale, err);                                                        \
   }

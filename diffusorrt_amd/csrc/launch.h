@@ -182,7 +182,9 @@ void attention(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_s
                int n_rows, int Hq, int Hkv, int n_keys, int row_pos0, int mask_kind,
                int mask_prompt_len, int mask_block, const AttnPlan& plan, float* o_part,
                float* ml_part, void* out, float* xsum, int out_fmt, hipStream_t s,
-               int* err = nullptr);
+               int* err = nullptr, bool q_has_lo = true);
+// (Both attention launchers read Q as its hi plane and, when q_has_lo, its lo plane
+// n_rows * Hq * 128 elements after it; without it the lo plane is zero.)
 // Decode attention over `ranges` key ranges (attention_decode_ranges(n_keys, Hkv) when
 // the key count is known at launch) + the range combine; `part` is a workspace of
 // attention_decode_part_bytes(ranges, Hkv, n_rows * Hq / Hkv) bytes.
@@ -191,7 +193,7 @@ int attention_decode_ranges(int n_keys, int Hkv);
 void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_stride,
                       int n_rows, int Hq, int Hkv, int n_keys, const StepDesc* desc, int ranges,
                       float* part, void* out, float* xsum, int out_fmt, hipStream_t s,
-                      int* err = nullptr);
+                      int* err = nullptr, bool q_has_lo = true);
 void kv_pack(bool kv_bf16, const void* k, const void* v, bool src_bf16, int n, int Hkv, int pos0,
              void* kv_layer, int64_t kv_head_stride, hipStream_t s);
 

@@ -2081,26 +2081,22 @@ int32_t drt_op_attention(const void* q, const void* cache, int64_t head_stride, 
     fa.mask_kind = mask_kind == DRT_MASK_D2F_HYBRID ? 1 : 0;
     fa.mask_prompt_len = mask_prompt_len;
     fa.mask_block = std::max(1, mask_block_size);
-    // the kernels read Q as hi and lo planes: the caller's Q (already in the
-    // operand type) is the hi plane, the lo plane is zero
+    // the caller's Q (already in the operand type) is the kernels' hi plane and
+    // their lo plane is zero: read in place, nothing staged
     const size_t q_bytes = (size_t)rows * hq * 128 * 2;
-    char* qp = (char*)workspace;
-    hipStream_t st = as_stream(stream);
-    DRT_HIP(hipMemcpyAsync(qp, q, q_bytes, hipMemcpyDeviceToDevice, st));
-    DRT_HIP(hipMemsetAsync(qp + q_bytes, 0, q_bytes, st));
-    q = qp;
-    float* o_part = (float*)(qp + (2 * q_bytes + 255) / 256 * 256);
+    float* o_part = (float*)((char*)workspace + (2 * q_bytes + 255) / 256 * 256);
     const int ofmt = out_dtype == DRT_F32 ? 2 : 3;
     if (rows * (hq / hkv) <= 64 && one_segment(fa)) {
       const int ranges = attention_decode_ranges(n_keys, hkv);
       attention_decode(kv_dtype == DRT_BF16, q, cache, head_stride, rows, hq, hkv, n_keys,
-                       nullptr, ranges, o_part, out, nullptr, ofmt, as_stream(stream));
+                       nullptr, ranges, o_part, out, nullptr, ofmt, as_stream(stream), nullptr,
+                       false);
     } else {
       const AttnPlan p = plan_attention(rows, hq, hkv, n_keys, (size_t)256 << 20);
       float* ml_part = o_part + (size_t)p.splits * hkv * rows * (hq / hkv) * 128;
       attention(kv_dtype == DRT_BF16, q, cache, head_stride, rows, hq, hkv, n_keys, row_pos0,
                 fa.mask_kind, mask_prompt_len, fa.mask_block, p, o_part, ml_part, out, nullptr,
-                ofmt, as_stream(stream));
+                ofmt, as_stream(stream), nullptr, false);
     }
   });
 }
