@@ -44,6 +44,10 @@ DRT_DEV uint16_t float_to_bf16_bits(float f) {
 DRT_DEV float round_bf16(float f) { return bf16_bits_to_float(float_to_bf16_bits(f)); }
 
 DRT_DEV uint16_t half_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
+// a in bits 0-15, b in bits 16-31
+DRT_DEV uint32_t pack_half2(_Float16 a, _Float16 b) {
+  return (uint32_t)half_bits(a) | ((uint32_t)half_bits(b) << 16);
+}
 
 // Wave-level reductions (64 lanes) via cross-lane shuffles.
 DRT_DEV float wave_sum(float v) {
@@ -89,6 +93,16 @@ template <> DRT_DEV __bf16 lo_part<__bf16>(float x, __bf16 hi) {
 // valid and the host reports it.
 constexpr int DRT_ERR_F16_RANGE = 4;
 DRT_DEV bool f16_overflows(float x) { return !(fabsf(x) < 65504.f); }
+
+// Scale c of a row's pre-scaled norm input (the split-K q4 path: a residual
+// update writes w * h * c as fp16 hi / lo planes for the next RMSNorm, and the
+// linear that reads them multiplies its output rows by rinv / c): the largest
+// power of two <= the row's norm factor rinv (exact to apply and to undo), over
+// 16, so the planes stay 16-32x below the normalised values unless the row's
+// RMS grew more than 16-fold since rinv was measured.
+DRT_DEV float pre_scale_of(float rinv) {
+  return __uint_as_float(__float_as_uint(rinv) & 0x7f800000u) * 0.0625f;
+}
 
 // Two q4 nibbles at bits 0-3 and 16-19 of w as a pair of exact fp16 integers
 // q: the nibble placed under the exponent of 1024 is the fp16 1024 + q, and one

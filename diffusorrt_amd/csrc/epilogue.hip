@@ -42,34 +42,75 @@ DRT_DEV float block_sum_256(float v, float* red) {
 // columns for the next RMSNorm, one [d/32][32] block per 32-row tile
 // (ss_out[(m / 32) * d + c * 32 + m % 32], c = column / 32); grid rows M .. up to
 // the end of the last tile (when launched) write zero partials.
+// With pre (and ss_out), the first layer's pre-scaled norm input as well: the
+// planes of w * h * c (ACT_F16P, [M][d] hi then lo), c from this row's own norm
+// factor (pre_scale_of), c into pre_sc[m], and the planes' per-32-column sums
+// laid out like ss_out (zero rows past M).
 // With row_desc the token of row m is tokens[row_desc->row0 + m] (a canvas on the
 // device that a graph-replayed forward reads at its step's rows).
-extern "C" __global__ void embed_kernel(const int32_t* __restrict__ tokens,
-                                        const uint16_t* __restrict__ table,
-                                        float* __restrict__ hidden, int M, int d,
-                                        float* __restrict__ ss_out,
-                                        const StepDesc* __restrict__ row_desc) {
+extern "C" __global__ __launch_bounds__(256) void embed_kernel(
+    const int32_t* __restrict__ tokens, const uint16_t* __restrict__ table,
+    float* __restrict__ hidden, int M, int d, float* __restrict__ ss_out,
+    const StepDesc* __restrict__ row_desc, const uint16_t* __restrict__ pre_norm, float eps,
+    uint16_t* __restrict__ pre, float* __restrict__ pre_xs, float* __restrict__ pre_sc,
+    int* __restrict__ err) {
   const int m = blockIdx.x;
   if (row_desc) tokens += row_desc->row0;
   float* ss_row = ss_out ? ss_out + (int64_t)(m >> 5) * d + (m & 31) : nullptr;
+  float* xs_row = pre ? pre_xs + (int64_t)(m >> 5) * d + (m & 31) : nullptr;
   if (m >= M) {
     if (ss_out)
-      for (int c = threadIdx.x; c < d / 32; c += blockDim.x) ss_row[c * 32] = 0.f;
+      for (int c = threadIdx.x; c < d / 32; c += blockDim.x) {
+        ss_row[c * 32] = 0.f;
+        if (xs_row) xs_row[c * 32] = 0.f;
+      }
     return;
   }
   const int64_t tok = tokens[m];
+  const uint16_t* trow = table + tok * d;
   for (int k = threadIdx.x; k < d; k += blockDim.x)
-    hidden[(int64_t)m * d + k] = bf16_bits_to_float(table[tok * d + k]);
-  if (ss_out) {
-    for (int c = threadIdx.x; c < d / 32; c += blockDim.x) {
-      float q = 0.f;
-      for (int k = 0; k < 32; ++k) {
-        const float v = bf16_bits_to_float(table[tok * d + c * 32 + k]);
-        q += v * v;
-      }
-      ss_row[c * 32] = q;
+    hidden[(int64_t)m * d + k] = bf16_bits_to_float(trow[k]);
+  if (!ss_out) return;
+  float qsum = 0.f;
+  for (int c = threadIdx.x; c < d / 32; c += blockDim.x) {
+    float q = 0.f;
+    for (int k = 0; k < 32; ++k) {
+      const float v = bf16_bits_to_float(trow[c * 32 + k]);
+      q += v * v;
     }
+    ss_row[c * 32] = q;
+    qsum += q;
   }
+  if (!pre) return;
+  __shared__ float red[4];
+  const float sc = pre_scale_of(1.f / sqrtf(block_sum_256(qsum, red) / (float)d + eps));
+  if (threadIdx.x == 0) pre_sc[m] = sc;
+  bool over = false;
+  for (int c = threadIdx.x; c < d / 32; c += blockDim.x) {
+    float xsum = 0.f;
+    for (int j = 0; j < 4; ++j) {
+      const int k = c * 32 + 8 * j;
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        x[e] = (bf16_bits_to_float(trow[k + e]) * sc) * bf16_bits_to_float(pre_norm[k + e]);
+      u32x4 ph, pl;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {  // word w holds elements (w, w + 4)
+        const _Float16 h0 = (_Float16)x[w], h1 = (_Float16)x[w + 4];
+        const _Float16 l0 = f16_lo(x[w], h0), l1 = f16_lo(x[w + 4], h1);
+        ph[w] = pack_half2(h0, h1);
+        pl[w] = pack_half2(l0, l1);
+        over = over || f16_overflows(x[w]) || f16_overflows(x[w + 4]);
+        xsum += ((float)h0 + (float)l0) + ((float)h1 + (float)l1);
+      }
+      *(u32x4*)(pre + (int64_t)m * d + k) = ph;
+      *(u32x4*)(pre + (int64_t)(M + m) * d + k) = pl;
+    }
+    xs_row[c * 32] = xsum;
+  }
+  if (over && err)
+    __hip_atomic_fetch_or(err, DRT_ERR_F16_RANGE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // One wave per output row (4 rows per 256-thread work-group). Lane l owns the
@@ -247,11 +288,14 @@ extern "C" __global__ void swiglu_rows_kernel(const float* __restrict__ g,
 namespace drt {
 
 void embed(const int32_t* tokens, const uint16_t* table, float* hidden, int M, int d,
-           float* ss_out, hipStream_t s, const StepDesc* row_desc) {
+           float* ss_out, hipStream_t s, const StepDesc* row_desc, const PreOut* pre) {
+  require(!pre || (ss_out && d % 32 == 0), "pre-scaled planes need the row statistics");
   // with ss_out, whole 32-row tiles are launched so unused rows get zero partials
   const int grid = ss_out ? (M + 31) / 32 * 32 : M;
   hipLaunchKernelGGL(embed_kernel, dim3(grid), dim3(256), 0, s, tokens, table, hidden, M, d,
-                     ss_out, row_desc);
+                     ss_out, row_desc, pre ? pre->norm : nullptr, pre ? pre->eps : 0.f,
+                     pre ? pre->planes : nullptr, pre ? pre->xs : nullptr,
+                     pre ? pre->sc : nullptr, pre ? pre->err : nullptr);
   DRT_HIP(hipGetLastError());
 }
 

@@ -65,6 +65,24 @@ struct FusedArgs {
   // squares, one block each per tile: part_floats and n_counters per tile, the
   // sums of squares [K/32][32] at + tile * K): M <= 32 * sk_row_tiles
   int sk_row_tiles = 1;
+  // Pre-scaled norm inputs (q4 skinny path). The residual update that produces
+  // a row also writes w * h * c as ACT_F16P planes ([M][N] hi, lo at + M * N),
+  // with w the next RMSNorm's weight and c a power of two per row, plus the
+  // planes' per-32-column sums (like ss_out); the next q|k|v or gate|up kernel
+  // then stages the planes as they are and multiplies its output rows by
+  // rsqrt(mean h^2 + eps) / c. c = (the largest power of two <= the row's
+  // previous norm factor) / 16: the planes stay ~16x below the normalised
+  // values' magnitude unless the row's RMS grew more than 16-fold.
+  // Producer (EPI_RESID): planes out, their sums, norm weight, c per row.
+  void* pre_out = nullptr;
+  float* pre_xs_out = nullptr;
+  const uint16_t* pre_norm = nullptr;
+  const float* pre_sc = nullptr;
+  // Consumer (q|k|v, gate|up): act / act_xsum are the planes and their sums,
+  // pre_sc_in the producer's c per row; pre_sc_out receives c for the next
+  // producer (from this kernel's norm factors).
+  const float* pre_sc_in = nullptr;
+  float* pre_sc_out = nullptr;
 };
 
 // Row tiles of the runtime's split-K workspaces: forwards of up to 64 rows (a
@@ -82,6 +100,9 @@ size_t skinny_part_floats(int N, int K);
 // One probe launch: does work-group i run on XCD i % n_xcc? (scratch_dev: >= 256 ints)
 bool probe_round_robin(int n_xcc, int* scratch_dev, hipStream_t s);
 int skinny_counters(int N);
+// Whether the split-K kernels take a linear of this kind and shape (given
+// workspaces sized by skinny_part_floats / skinny_counters).
+bool skinny_supported(int kind, int N, int K);
 // The large-M q4 kernels (M > 32): ACT_F16P activation in, kinds FL_QKV,
 // FL_SWIGLU (ACT_F16P out) and FL_STORE (KS > 1: fp32 partial slices
 // y + ks * M * N for a reduce pass).

@@ -200,8 +200,20 @@ void kv_pack(bool kv_bf16, const void* k, const void* v, bool src_bf16, int n, i
 // Epilogues.
 // ss_out (optional, M <= 32): per-32-column partial sums of squares of the rows,
 // [d/32][32], the row statistics of the first decoder layer's RMSNorm.
+// The first layer's pre-scaled norm input that embed() writes with the residual
+// rows (the q4 split-K path): norm weight, eps, planes [M][d] x 2, their
+// per-32-column sums, the scale per row, and the error word (fp16 range).
+struct PreOut {
+  const uint16_t* norm = nullptr;
+  float eps = 0.f;
+  uint16_t* planes = nullptr;
+  float* xs = nullptr;
+  float* sc = nullptr;
+  int* err = nullptr;
+};
 void embed(const int32_t* tokens, const uint16_t* table, float* hidden, int M, int d,
-           float* ss_out, hipStream_t s, const StepDesc* row_desc = nullptr);
+           float* ss_out, hipStream_t s, const StepDesc* row_desc = nullptr,
+           const PreOut* pre = nullptr);
 void residual_norm(float* hidden, const float* part, int splits, int M_part, bool rnd_bf16,
                    const int32_t* src_rows, bool write_hidden, const uint16_t* norm_w, float eps,
                    int d, int fmt, void* act, float* xsum, int n_out_rows, hipStream_t s,

@@ -130,6 +130,12 @@ struct Runtime {
   // (zeroed once; every kernel leaves them zero) and the residual stream's
   // per-32-column partial sums of squares
   DevBuf sk_part, sk_counters, sk_ss;
+  // q4 models on the split-K linears: the next RMSNorm's input, pre-scaled by
+  // the residual updates (two fp16 planes [rows][d], their per-32-column sums
+  // [tile][d/32][32], and two alternating per-row scale vectors: each q|k|v or
+  // gate|up kernel reads one and writes the other)
+  bool sk_pre_on = false;
+  DevBuf sk_pre, sk_pre_xs, sk_pre_sc;
   // large-M (> 32 rows) q4 forwards: the down projection's input activation and
   // the split-K partial slices of o_proj / down_proj
   DevBuf act2, big_part, big_tail_count;
@@ -443,6 +449,14 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
     rt->sk_counters.alloc((size_t)std::max(nc, 1) * 4 * SK_ROW_TILES);
     DRT_HIP(hipMemsetAsync(rt->sk_counters.p, 0, rt->sk_counters.bytes, s));
     rt->sk_ss.alloc((size_t)d * 4 * SK_ROW_TILES);  // [tile][d/32][32]
+    rt->sk_pre_on = rt->q4 && skinny_supported(FL_QKV, n_qkv, d) &&
+                    skinny_supported(FL_RESID, d, Hq * hd) &&
+                    skinny_supported(FL_SWIGLU, 2 * F, d) && skinny_supported(FL_RESID, d, F);
+    if (rt->sk_pre_on) {
+      rt->sk_pre.alloc((size_t)2 * 32 * SK_ROW_TILES * d * 2);
+      rt->sk_pre_xs.alloc((size_t)d * 4 * SK_ROW_TILES);
+      rt->sk_pre_sc.alloc((size_t)2 * 32 * SK_ROW_TILES * 4);
+    }
     rt->streaming = rt->q4 && stream_supported(32, n_qkv, d) && stream_supported(32, d, Hq * hd) &&
                  stream_supported(32, 2 * F, d) && stream_supported(32, d, F);
     if (rt->q4 && (M > 32 || rt->streaming)) {
@@ -694,9 +708,28 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
   const bool stream = !big && rt.streaming && M <= 32;
   const bool pipe = big || stream;
   float* bpart = pipe ? rt.big_part.as<float>() : nullptr;
-  embed(p.tokens_rel, rt.embed.as<uint16_t>(), hidden, M, d, ss, s,
-        p.tokens_at_row0 ? desc : nullptr);
   const int L = (int)rt.layers.size();
+  // q4 on the split-K linears: each residual update (and the embedding) also
+  // writes the next RMSNorm's input pre-scaled (FusedArgs::pre_out), which the
+  // q|k|v and gate|up kernels stage without normalising
+  const bool pre = rt.sk_pre_on && ss && !big && !stream && L > 0;
+  uint16_t* pre_planes = pre ? rt.sk_pre.as<uint16_t>() : nullptr;
+  float* pre_xs = pre ? rt.sk_pre_xs.as<float>() : nullptr;
+  float* sc_a = pre ? rt.sk_pre_sc.as<float>() : nullptr;  // written by q|k|v
+  float* sc_b = pre ? sc_a + 32 * SK_ROW_TILES : nullptr;  // by gate|up and the embedding
+  {
+    PreOut po;
+    if (pre) {
+      po.norm = rt.layers[0].in_norm.as<uint16_t>();
+      po.eps = eps;
+      po.planes = pre_planes;
+      po.xs = pre_xs;
+      po.sc = sc_b;
+      po.err = rt.placement_err.as<int>();
+    }
+    embed(p.tokens_rel, rt.embed.as<uint16_t>(), hidden, M, d, ss, s,
+          p.tokens_at_row0 ? desc : nullptr, pre ? &po : nullptr);
+  }
   if (big && L > 0)
     residual_norm(hidden, nullptr, 0, M, false, nullptr, false,
                   rt.layers[0].in_norm.as<uint16_t>(), eps, d, ACT_F16P, rt.act.p, xs, M, s,
@@ -765,6 +798,12 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
       f.Hkv = Hkv;
       f.kv_bf16 = rt.kv_bf16;
       f.ss_in = ss;
+      if (pre) {
+        f.act = pre_planes;
+        f.act_xsum = pre_xs;
+        f.pre_sc_in = sc_b;
+        f.pre_sc_out = sc_a;
+      }
       if (big) {
         f.act = rt.act.p;
         big_qkv(f, bpart, rt.big_part_floats, s);
@@ -826,6 +865,12 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
       f.act_xsum = xs;
       f.hidden_out = hidden;
       f.ss_out = ss;
+      if (pre) {
+        f.pre_out = pre_planes;
+        f.pre_xs_out = pre_xs;
+        f.pre_norm = w.post_norm.as<uint16_t>();
+        f.pre_sc = sc_a;
+      }
       fused_linear(f, FL_RESID, s);
     }
     {  // post-attention RMSNorm -> [gate | up] -> SwiGLU -> down activation
@@ -836,6 +881,12 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
       f.xsum_out = xs;
       f.act_fmt = fmt;
       f.ss_in = ss;
+      if (pre) {
+        f.act = pre_planes;
+        f.act_xsum = pre_xs;
+        f.pre_sc_in = sc_a;
+        f.pre_sc_out = sc_b;
+      }
       fused_linear(f, FL_SWIGLU, s);
     }
     {  // down_proj + residual
@@ -844,6 +895,12 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
       f.act_xsum = xs;
       f.hidden_out = hidden;
       f.ss_out = ss;
+      if (pre && !last) {
+        f.pre_out = pre_planes;
+        f.pre_xs_out = pre_xs;
+        f.pre_norm = rt.layers[l + 1].in_norm.as<uint16_t>();
+        f.pre_sc = sc_b;
+      }
       fused_linear(f, FL_RESID, s);
     }
   }

@@ -170,19 +170,26 @@ DRT_DEV void sk_dims(uint32_t dims0, uint32_t dims1, int& M, int& N, int& K, int
   fenced = (int)(dims1 >> 24);
 }
 
-template <int WK, int EPI, int U>
+// PRE: the input is pre-scaled ACT_F16P planes (see FusedArgs::pre_out):
+// `hidden` points at the planes, `norm_w` at their per-32-column sums and sc_in
+// at their scale c per row; they are staged as they are and the output rows are
+// multiplied by rinv / c.
+template <int WK, int EPI, int U, bool PRE>
 __global__ __launch_bounds__(256) void skinny_wide_kernel(
     const uint32_t* __restrict__ qw, const uint32_t* __restrict__ sbp,
     const float* __restrict__ hidden, const uint16_t* __restrict__ norm_w,
-    const float* __restrict__ ss_arg, int* perr, uint32_t dims0, uint32_t dims1,
-    const FusedArgs a) {
+    const float* __restrict__ ss_arg, const float* __restrict__ sc_in, int* perr,
+    uint32_t dims0, uint32_t dims1, const FusedArgs a) {
   constexpr bool BF = WK == W_BF16;
+  static_assert(!PRE || !BF, "pre-scaled planes feed the q4 kernels only");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int M, N, K, KS, n_xcc, fenced;
   sk_dims(dims0, dims1, M, N, K, KS, n_xcc, fenced);
   // 32-row tile of this work-group: rows m0 .. m0 + M - 1 of the forward
   const int mt = blockIdx.y, m0 = 32 * mt, M_all = M;
   M = min(32, M_all - m0);
+  const uint16_t* pl_hi = (const uint16_t*)hidden + (int64_t)m0 * K;  // PRE
+  const float* pl_xs = (const float*)norm_w + (int64_t)mt * K;        // PRE
   hidden += (int64_t)m0 * K;
   const float* ss_in = ss_arg + (int64_t)mt * K;
   float* part = a.part + (size_t)mt * a.part_floats;
@@ -198,7 +205,7 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(
   uint16_t* xs = (uint16_t*)smem;                       // [32][ROW_H] ACT_F16P hi
   uint16_t* xsl = xs + 32 * ROW_H;                      // [32][ROW_H] ACT_F16P lo
   float* xss = (float*)(smem + 2 * 32 * ROW_H * 2);     // [U][32] group sums
-  float* rinv = xss + U * 32;                           // [32]
+  float* rinv = xss + U * 32;                           // [32] (PRE: rinv / c)
   float* red = rinv + 32;                               // [4][32][33]
   int* flag = (int*)(red + SK_RED);
   uint16_t* vbuf = (uint16_t*)(smem + SK_WIDE_V_OFF(U));  // [4096] V tile half (QKV)
@@ -216,18 +223,34 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(
 #pragma unroll
   for (int e = 0; e < SK_SS_PER_THREAD; ++e)
     sv[e] = ss_in[min((int)(threadIdx.x >> 5) + 8 * e, np - 1) * 32 + (threadIdx.x & 31)];
-  // 2. the hidden slice (8-wide items: U per thread) and the matching norm weights
+  // PRE: the planes' scale of this thread's row
+  const float c_in = PRE ? sc_in[m0 + min((int)(threadIdx.x & 31), M - 1)] : 1.f;
+  // 2. the hidden slice (8-wide items: U per thread) and the matching norm weights;
+  // PRE: the planes' slice (hi, lo) and the sums of the slice's 32-column halves
   f32x4 hv[U][2];
   u32x4 nw[U];
+  float xp[2];
 #pragma unroll
   for (int j = 0; j < U; ++j) {
     const int it = threadIdx.x + 256 * j;
     const int r = it / (8 * U), c8 = it - r * (8 * U);
     const int k = kc0 + c8 * 8;
-    const f32x4* src = (const f32x4*)(hidden + (int64_t)min(r, M - 1) * K + k);
-    hv[j][0] = src[0];
-    hv[j][1] = src[1];
-    nw[j] = *(const u32x4*)(norm_w + k);
+    if (PRE) {
+      const uint16_t* src = pl_hi + (int64_t)min(r, M - 1) * K + k;
+      hv[j][0] = __builtin_bit_cast(f32x4, *(const u32x4*)src);
+      hv[j][1] = __builtin_bit_cast(f32x4, *(const u32x4*)(src + (int64_t)M_all * K));
+    } else {
+      const f32x4* src = (const f32x4*)(hidden + (int64_t)min(r, M - 1) * K + k);
+      hv[j][0] = src[0];
+      hv[j][1] = src[1];
+      nw[j] = *(const u32x4*)(norm_w + k);
+    }
+  }
+  if (PRE) {  // thread (unit u = tid / 32 clamped, row tid % 32)
+    const int u = min((int)(threadIdx.x >> 5), U - 1), r = min((int)(threadIdx.x & 31), M - 1);
+    const float* src = pl_xs + ((kc0 >> 5) + 2 * u) * 32 + r;
+    xp[0] = src[0];
+    xp[1] = src[32];
   }
   __builtin_amdgcn_sched_barrier(0);
   // 3. this wave's weights for the U units (bf16: the unit's four 16-k MFMA
@@ -257,17 +280,38 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(
     red[g8 * 32 + (threadIdx.x & 31)] = q;
   }
   __syncthreads();
-  if (threadIdx.x < 32) {
-    float ssum = 0.f;
+  if (PRE) {
+    if (threadIdx.x < 32) {
+      float ssum = 0.f;
 #pragma unroll
-    for (int g8 = 0; g8 < 8; ++g8) ssum += red[g8 * 32 + threadIdx.x];
-    rinv[threadIdx.x] = 1.f / sqrtf(ssum / (float)K + a.eps);
+      for (int g8 = 0; g8 < 8; ++g8) ssum += red[g8 * 32 + threadIdx.x];
+      const float ri = 1.f / sqrtf(ssum / (float)K + a.eps);
+      rinv[threadIdx.x] = (int)threadIdx.x < M ? ri / c_in : 0.f;
+      if (a.pre_sc_out && grp == 0 && ks == 0 && live && (int)threadIdx.x < M)
+        a.pre_sc_out[m0 + threadIdx.x] = pre_scale_of(ri);
+    }
+    // 4. the planes into LDS as they are, and the 64-k group sums
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const int it = threadIdx.x + 256 * j;
+      const int r = it / (8 * U), c8 = it - r * (8 * U);
+      *(u32x4*)(xs + r * ROW_H + c8 * 8) = __builtin_bit_cast(u32x4, hv[j][0]);
+      *(u32x4*)(xsl + r * ROW_H + c8 * 8) = __builtin_bit_cast(u32x4, hv[j][1]);
+    }
+    if ((int)threadIdx.x < 32 * U) xss[threadIdx.x] = xp[0] + xp[1];
+  } else {
+    if (threadIdx.x < 32) {
+      float ssum = 0.f;
+#pragma unroll
+      for (int g8 = 0; g8 < 8; ++g8) ssum += red[g8 * 32 + threadIdx.x];
+      rinv[threadIdx.x] = 1.f / sqrtf(ssum / (float)K + a.eps);
+    }
+    __syncthreads();
   }
-  __syncthreads();
   // 4. RMSNorm(h) * w -> ACT_F16P hi / lo (chunk order 0,4,1,5,2,6,3,7) + group sums
   bool over = false;
 #pragma unroll
-  for (int j = 0; j < U; ++j) {
+  for (int j = 0; j < (PRE ? 0 : U); ++j) {
     const int it = threadIdx.x + 256 * j;
     const int r = it / (8 * U), c8 = it - r * (8 * U);
     const float inv = r < M ? rinv[r] : 0.f;
@@ -330,6 +374,12 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(
     float xsr[16];
     load_row_sums(xss + u * 32, lane, xsr);
     q4_group_mma1(acc, af, afl, xsr, wq[u][0], wsb[u]);
+  }
+  if (PRE) {  // the rows' factors rinv / c (0 past M)
+    float fr[16];
+    load_row_sums(rinv, lane, fr);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] *= fr[i];
   }
   if (!live) return;  // work-group-uniform, before any global store
   // 6. K slices meet: the last work-group of the column block adds the partials
@@ -569,8 +619,15 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(
   const int m = threadIdx.x >> 3, c0 = 4 * (threadIdx.x & 7);
   const int n = nt * 32 + c0;
   // the epilogue's input, loaded before the exchange so its latency overlaps it
+  // (with pre-scaled planes out: the next norm's weights and the row's scale)
   f32x4 h_old = f32x4{0.f, 0.f, 0.f, 0.f};
   if (EPI == EPI_RESID && m < M) h_old = *(const f32x4*)(a.hidden_out + (int64_t)(m0 + m) * N + n);
+  uint2 pw = uint2{0u, 0u};
+  float pc = 0.f;
+  if (EPI == EPI_RESID && a.pre_out) {
+    pw = *(const uint2*)(a.pre_norm + n);
+    pc = a.pre_sc[m0 + min(m, M - 1)];
+  }
   f32x4 v;
 #pragma unroll
   for (int e = 0; e < 4; ++e)
@@ -609,19 +666,65 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(
       const float q = sum8_dpp(h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3]);
       if ((threadIdx.x & 7) == 0) a.ss_out[(int64_t)mt * N + nt * 32 + m] = q;
     }
+    if (a.pre_out) {
+      // the next norm's input w * h * c as hi / lo fp16 (rows past M: zeros,
+      // not stored), and the sum of the 32 columns' hi + lo per row
+      const float wv[4] = {bf16_bits_to_float(pw.x & 0xffffu), bf16_bits_to_float(pw.x >> 16),
+                           bf16_bits_to_float(pw.y & 0xffffu), bf16_bits_to_float(pw.y >> 16)};
+      _Float16 hh[4], ll[4];
+      bool over = false;
+      float xsum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x = (h[e] * pc) * wv[e];
+        hh[e] = (_Float16)x;
+        ll[e] = f16_lo(x, hh[e]);
+        over = over || f16_overflows(x);
+        xsum += (float)hh[e] + (float)ll[e];
+      }
+      xsum = sum8_dpp(xsum);
+      if ((threadIdx.x & 7) == 0) a.pre_xs_out[(int64_t)mt * N + nt * 32 + m] = xsum;
+      // ACT_F16P chunk order: word w of an 8-column chunk holds columns (w, w + 4);
+      // the chunk's columns 0-3 are this (even) thread's, 4-7 its odd neighbour's.
+      // The even thread stores words 0-1, the odd one words 2-3.
+      const bool odd = threadIdx.x & 1;
+      const uint32_t sh = odd ? pack_half2(hh[0], hh[1]) : pack_half2(hh[2], hh[3]);
+      const uint32_t sl = odd ? pack_half2(ll[0], ll[1]) : pack_half2(ll[2], ll[3]);
+      const uint32_t rh = (uint32_t)__shfl_xor((int)sh, 1), rl = (uint32_t)__shfl_xor((int)sl, 1);
+      uint2 wh, wl;
+      if (odd) {
+        wh = uint2{(rh & 0xffffu) | ((uint32_t)half_bits(hh[2]) << 16),
+                   (rh >> 16) | ((uint32_t)half_bits(hh[3]) << 16)};
+        wl = uint2{(rl & 0xffffu) | ((uint32_t)half_bits(ll[2]) << 16),
+                   (rl >> 16) | ((uint32_t)half_bits(ll[3]) << 16)};
+      } else {
+        wh = uint2{(uint32_t)half_bits(hh[0]) | (rh << 16),
+                   (uint32_t)half_bits(hh[1]) | (rh & 0xffff0000u)};
+        wl = uint2{(uint32_t)half_bits(ll[0]) | (rl << 16),
+                   (uint32_t)half_bits(ll[1]) | (rl & 0xffff0000u)};
+      }
+      if (m < M) {
+        uint16_t* dst = (uint16_t*)a.pre_out + (int64_t)(m0 + m) * N + n;
+        *(uint2*)dst = wh;
+        *(uint2*)(dst + (int64_t)M_all * N) = wl;
+        if (over) raise_range(a);
+      }
+    }
   } else if (m < M) {
     *(f32x4*)(a.y + (int64_t)(m0 + m) * N + n) = v;
   }
 }
 
-#define DRT_WIDE(W, E, U)                                                                   \
-  template __global__ void skinny_wide_kernel<W, E, U>(const uint32_t*, const uint32_t*,       \
-                                                       const float*, const uint16_t*,          \
-                                                       const float*, int*, uint32_t, uint32_t, \
-                                                       const FusedArgs);
-#define DRT_WIDE_U(W, E) DRT_WIDE(W, E, 1) DRT_WIDE(W, E, 2) DRT_WIDE(W, E, 4) DRT_WIDE(W, E, 8)
-DRT_WIDE_U(W_Q4, EPI_QKV) DRT_WIDE_U(W_Q4, EPI_SWIGLU)
-DRT_WIDE_U(W_BF16, EPI_QKV) DRT_WIDE_U(W_BF16, EPI_SWIGLU)
+#define DRT_WIDE(W, E, U, P)                                                               \
+  template __global__ void skinny_wide_kernel<W, E, U, P>(const uint32_t*, const uint32_t*,   \
+                                                          const float*, const uint16_t*,      \
+                                                          const float*, const float*, int*,   \
+                                                          uint32_t, uint32_t, const FusedArgs);
+#define DRT_WIDE_U(W, E, P) \
+  DRT_WIDE(W, E, 1, P) DRT_WIDE(W, E, 2, P) DRT_WIDE(W, E, 4, P) DRT_WIDE(W, E, 8, P)
+DRT_WIDE_U(W_Q4, EPI_QKV, true) DRT_WIDE_U(W_Q4, EPI_SWIGLU, true)
+DRT_WIDE_U(W_Q4, EPI_QKV, false) DRT_WIDE_U(W_Q4, EPI_SWIGLU, false)
+DRT_WIDE_U(W_BF16, EPI_QKV, false) DRT_WIDE_U(W_BF16, EPI_SWIGLU, false)
 #undef DRT_WIDE_U
 #undef DRT_WIDE
 #define DRT_NARROW(W, E, UW) DRT_NARROW_X(W, E, UW, 0)
@@ -699,6 +802,15 @@ size_t skinny_part_floats(int N, int K) {
 
 int skinny_counters(int N) { return N / 32; }
 
+bool skinny_supported(int kind, int N, int K) {
+  if (K % 64 || N % 32 || N >= 65536 || K >= 65536) return false;
+  if (kind == FL_QKV || kind == FL_SWIGLU) {
+    const int U = wide_units(N, K);
+    return N % 128 == 0 && K / 32 <= 8 * SK_SS_PER_THREAD && U && K / 64 / U <= SK_KS_MAX;
+  }
+  return narrow_slices(N, K) <= SK_KS_MAX;
+}
+
 namespace {
 uint32_t sk_dims1(const FusedArgs& a, int KS) {
   return (uint32_t)a.M | ((uint32_t)KS << 8) | ((uint32_t)a.n_xcc << 16) |
@@ -706,7 +818,22 @@ uint32_t sk_dims1(const FusedArgs& a, int KS) {
 }
 }  // namespace
 
+static bool skinny_launch(const FusedArgs& a, int kind, hipStream_t s);
+
 bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
+  // pre-scaled planes in or out have no other kernel: refusing them is an error
+  const bool pre = a.pre_sc_in || a.pre_out;
+  if (pre) {
+    require(a.qw && (kind == FL_RESID ? a.pre_xs_out && a.pre_norm && a.pre_sc
+                                      : a.act && a.act_xsum && a.x_in == 0),
+            "pre-scaled planes: q4 weights and every plane argument required");
+  }
+  const bool ok = skinny_launch(a, kind, s);
+  require(ok || !pre, "pre-scaled planes: the split-K kernels refused the linear");
+  return ok;
+}
+
+static bool skinny_launch(const FusedArgs& a, int kind, hipStream_t s) {
   const int MT = (a.M + 31) / 32;
   if ((!a.qw && !a.wb) || a.M < 1 || MT > a.sk_row_tiles || !a.part ||
       !a.counters || a.K % 64 || a.N % 32 || a.n_xcc < 1)
@@ -722,6 +849,10 @@ bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
                        2.0 * a.M * a.K + 2.0 * a.M * a.N;
   if (kind == FL_QKV || kind == FL_SWIGLU) {
     if (a.x_in != 0 || !a.ss_in || a.N % 128 || a.K / 32 > 8 * SK_SS_PER_THREAD) return false;
+    const bool pre = a.pre_sc_in != nullptr;  // q4 (checked by the caller)
+    // PRE: the planes and their sums take the places of the rows and the norm weight
+    const float* x0 = pre ? (const float*)a.act : a.hidden;
+    const uint16_t* x1 = pre ? (const uint16_t*)a.act_xsum : a.norm_w;
     const int U = wide_units(a.N, a.K);
     if (!U) return false;
     const int KS = G / U, NG = a.N / 128;
@@ -729,18 +860,19 @@ bool skinny_linear(const FusedArgs& a, int kind, hipStream_t s) {
       return false;  // (padding work-groups past the last block exit before any access)
     const size_t lds = SK_WIDE_LDS(U);
     const dim3 grid((unsigned)((NG + a.n_xcc - 1) / a.n_xcc * a.n_xcc * KS), MT);
-#define DRT_SW1(W, E, UU)                                                         \
-  {                                                                               \
-    auto fn = skinny_wide_kernel<W, E, UU>;                                       \
-    static size_t granted = 0;                                                    \
-    grant_lds((const void*)fn, lds, granted);                                     \
-    DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(256), lds, s, wq, a.sb, a.hidden, \
-               a.norm_w, a.ss_in, a.placement_err, dims0, sk_dims1(a, KS), a);    \
+#define DRT_SW1(W, E, UU, P)                                                         \
+  {                                                                                  \
+    auto fn = skinny_wide_kernel<W, E, UU, P>;                                       \
+    static size_t granted = 0;                                                       \
+    grant_lds((const void*)fn, lds, granted);                                        \
+    DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(256), lds, s, wq, a.sb, x0, x1,   \
+               a.ss_in, a.pre_sc_in, a.placement_err, dims0, sk_dims1(a, KS), a);    \
   }
-#define DRT_SW(E, UU)                  \
-  {                                    \
-    if (bf) DRT_SW1(W_BF16, E, UU)     \
-    else DRT_SW1(W_Q4, E, UU)          \
+#define DRT_SW(E, UU)                          \
+  {                                            \
+    if (bf) DRT_SW1(W_BF16, E, UU, false)      \
+    else if (pre) DRT_SW1(W_Q4, E, UU, true)   \
+    else DRT_SW1(W_Q4, E, UU, false)           \
   }
 #define DRT_SW_U(E)                                  \
   switch (U) {                                       \
