@@ -278,6 +278,10 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(
     for (int e = 0; e < SK_SS_PER_THREAD; ++e)  // a product, not a select, so that
       q += sv[e] * (g8 + 8 * e < np ? 1.f : 0.f);  // the load is not sunk into a branch
     red[g8 * 32 + (threadIdx.x & 31)] = q;
+    // PRE: c of the row through LDS (the V tile's space, used only by the
+    // epilogue), written by every thread of the row: a use in a branch would
+    // let the compiler sink the load behind the weights
+    if (PRE) ((float*)vbuf)[threadIdx.x & 31] = c_in;
   }
   __syncthreads();
   if (PRE) {
@@ -286,7 +290,7 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(
 #pragma unroll
       for (int g8 = 0; g8 < 8; ++g8) ssum += red[g8 * 32 + threadIdx.x];
       const float ri = 1.f / sqrtf(ssum / (float)K + a.eps);
-      rinv[threadIdx.x] = (int)threadIdx.x < M ? ri / c_in : 0.f;
+      rinv[threadIdx.x] = (int)threadIdx.x < M ? ri / ((float*)vbuf)[threadIdx.x] : 0.f;
       if (a.pre_sc_out && grp == 0 && ks == 0 && live && (int)threadIdx.x < M)
         a.pre_sc_out[m0 + threadIdx.x] = pre_scale_of(ri);
     }
@@ -403,7 +407,6 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(
     if (KS <= 2) sk_wide_sum_slices<2>(pbase, KS, red, rnd, tables);
     else if (KS <= 4) sk_wide_sum_slices<4>(pbase, KS, red, rnd, tables);
     else sk_wide_sum_slices<SK_KS_MAX>(pbase, KS, red, rnd, tables);
-    if (threadIdx.x == 0) reset_counter(&counters[grp], a.fenced);
   } else {
     if (EPI == EPI_QKV) qt = qkv_tables(a, grp, row0 + m0, M);
 #pragma unroll
@@ -457,6 +460,9 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(
     else qkv_epilogue<_Float16>(a, qt, grp, m0, row0 + m0, M, get, vbuf);
   }
 #undef TT
+  // the arrival counter back to zero, after the epilogue: on this target a wait
+  // for a load also waits for every store issued before it
+  if (KS > 1 && threadIdx.x == 0) reset_counter(&counters[grp], a.fenced);
 }
 
 // UW: units per wave held in registers at once (the wave's units are processed
@@ -618,15 +624,21 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(
   __syncthreads();
   const int m = threadIdx.x >> 3, c0 = 4 * (threadIdx.x & 7);
   const int n = nt * 32 + c0;
-  // the epilogue's input, loaded before the exchange so its latency overlaps it
-  // (with pre-scaled planes out: the next norm's weights and the row's scale)
+  // the epilogue's inputs, loaded before the exchange so their latency overlaps
+  // it (with pre-scaled planes out: the next norm's weights and the row's
+  // scale). Unconditional (rows past M read row M - 1; without planes out the
+  // two pre loads read the hidden rows): a load under a branch must be waited for
+  // again after it, and on this target a wait also waits for the stores issued
+  // before it. For the same reason every store of the epilogue comes last.
   f32x4 h_old = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (EPI == EPI_RESID && m < M) h_old = *(const f32x4*)(a.hidden_out + (int64_t)(m0 + m) * N + n);
   uint2 pw = uint2{0u, 0u};
   float pc = 0.f;
-  if (EPI == EPI_RESID && a.pre_out) {
-    pw = *(const uint2*)(a.pre_norm + n);
-    pc = a.pre_sc[m0 + min(m, M - 1)];
+  if (EPI == EPI_RESID) {
+    const int64_t row = m0 + min(m, M - 1);
+    h_old = *(const f32x4*)(a.hidden_out + row * N + n);
+    const bool pre = a.pre_out != nullptr;
+    pw = *(const uint2*)(pre ? (const void*)(a.pre_norm + n) : (const void*)(a.hidden_out + n));
+    pc = *(pre ? a.pre_sc + row : (const float*)a.hidden_out);
   }
   f32x4 v;
 #pragma unroll
@@ -643,7 +655,6 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(
     v = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int k2 = 0; k2 < SK_KS_MAX; ++k2) v += pv[k2] * (k2 < KS ? 1.f : 0.f);  // unconditional loads
-    if (threadIdx.x == 0) reset_counter(&counters[nt], a.fenced);
   }
   if (BF && a.rnd_bf16) {
 #pragma unroll
@@ -657,23 +668,19 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(
     v[3] += bf16_bits_to_float(bb.y >> 16);
   }
   if (EPI == EPI_RESID) {
-    f32x4 h = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (m < M) {
-      h = h_old + v;
-      *(f32x4*)(a.hidden_out + (int64_t)(m0 + m) * N + n) = h;
-    }
-    if (a.ss_out) {
-      const float q = sum8_dpp(h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3]);
-      if ((threadIdx.x & 7) == 0) a.ss_out[(int64_t)mt * N + nt * 32 + m] = q;
-    }
-    if (a.pre_out) {
-      // the next norm's input w * h * c as hi / lo fp16 (rows past M: zeros,
-      // not stored), and the sum of the 32 columns' hi + lo per row
+    const f32x4 h = m < M ? h_old + v : f32x4{0.f, 0.f, 0.f, 0.f};
+    const float q = sum8_dpp(h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3]);
+    // pre-scaled planes: the next norm's input w * h * c as hi / lo fp16 (rows
+    // past M: zeros, not stored), and the sum of the 32 columns' hi + lo per row.
+    // Computed whether or not they are stored, so that every load is used (and
+    // waited for) before the first store.
+    uint2 wh, wl;
+    float xsum = 0.f;
+    bool over = false;
+    {
       const float wv[4] = {bf16_bits_to_float(pw.x & 0xffffu), bf16_bits_to_float(pw.x >> 16),
                            bf16_bits_to_float(pw.y & 0xffffu), bf16_bits_to_float(pw.y >> 16)};
       _Float16 hh[4], ll[4];
-      bool over = false;
-      float xsum = 0.f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float x = (h[e] * pc) * wv[e];
@@ -683,7 +690,6 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(
         xsum += (float)hh[e] + (float)ll[e];
       }
       xsum = sum8_dpp(xsum);
-      if ((threadIdx.x & 7) == 0) a.pre_xs_out[(int64_t)mt * N + nt * 32 + m] = xsum;
       // ACT_F16P chunk order: word w of an 8-column chunk holds columns (w, w + 4);
       // the chunk's columns 0-3 are this (even) thread's, 4-7 its odd neighbour's.
       // The even thread stores words 0-1, the odd one words 2-3.
@@ -691,7 +697,6 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(
       const uint32_t sh = odd ? pack_half2(hh[0], hh[1]) : pack_half2(hh[2], hh[3]);
       const uint32_t sl = odd ? pack_half2(ll[0], ll[1]) : pack_half2(ll[2], ll[3]);
       const uint32_t rh = (uint32_t)__shfl_xor((int)sh, 1), rl = (uint32_t)__shfl_xor((int)sl, 1);
-      uint2 wh, wl;
       if (odd) {
         wh = uint2{(rh & 0xffffu) | ((uint32_t)half_bits(hh[2]) << 16),
                    (rh >> 16) | ((uint32_t)half_bits(hh[3]) << 16)};
@@ -703,6 +708,12 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(
         wl = uint2{(uint32_t)half_bits(ll[0]) | (rl << 16),
                    (uint32_t)half_bits(ll[1]) | (rl & 0xffff0000u)};
       }
+    }
+    // the stores
+    if (m < M) *(f32x4*)(a.hidden_out + (int64_t)(m0 + m) * N + n) = h;
+    if (a.ss_out && (threadIdx.x & 7) == 0) a.ss_out[(int64_t)mt * N + nt * 32 + m] = q;
+    if (a.pre_out) {
+      if ((threadIdx.x & 7) == 0) a.pre_xs_out[(int64_t)mt * N + nt * 32 + m] = xsum;
       if (m < M) {
         uint16_t* dst = (uint16_t*)a.pre_out + (int64_t)(m0 + m) * N + n;
         *(uint2*)dst = wh;
@@ -713,6 +724,7 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(
   } else if (m < M) {
     *(f32x4*)(a.y + (int64_t)(m0 + m) * N + n) = v;
   }
+  if (KS > 1 && threadIdx.x == 0) reset_counter(&counters[nt], a.fenced);
 }
 
 #define DRT_WIDE(W, E, U, P)                                                               \
