@@ -54,63 +54,83 @@ extern "C" __global__ __launch_bounds__(256) void embed_kernel(
     const StepDesc* __restrict__ row_desc, const uint16_t* __restrict__ pre_norm, float eps,
     uint16_t* __restrict__ pre, float* __restrict__ pre_xs, float* __restrict__ pre_sc,
     int* __restrict__ err) {
-  const int m = blockIdx.x;
+  // thread c owns columns 32c .. 32c + 31 (d % 32 == 0, d <= 32 * 256); every
+  // load is issued before the first store (a wait for a load also waits for the
+  // stores issued before it)
+  const int m = blockIdx.x, c = threadIdx.x, ng = d >> 5;
+  const bool live = c < ng;
   if (row_desc) tokens += row_desc->row0;
   float* ss_row = ss_out ? ss_out + (int64_t)(m >> 5) * d + (m & 31) : nullptr;
   float* xs_row = pre ? pre_xs + (int64_t)(m >> 5) * d + (m & 31) : nullptr;
   if (m >= M) {
-    if (ss_out)
-      for (int c = threadIdx.x; c < d / 32; c += blockDim.x) {
-        ss_row[c * 32] = 0.f;
-        if (xs_row) xs_row[c * 32] = 0.f;
-      }
+    if (ss_out && live) {
+      ss_row[c * 32] = 0.f;
+      if (xs_row) xs_row[c * 32] = 0.f;
+    }
     return;
   }
   const int64_t tok = tokens[m];
-  const uint16_t* trow = table + tok * d;
-  for (int k = threadIdx.x; k < d; k += blockDim.x)
-    hidden[(int64_t)m * d + k] = bf16_bits_to_float(trow[k]);
-  if (!ss_out) return;
-  float qsum = 0.f;
-  for (int c = threadIdx.x; c < d / 32; c += blockDim.x) {
-    float q = 0.f;
-    for (int k = 0; k < 32; ++k) {
-      const float v = bf16_bits_to_float(trow[c * 32 + k]);
-      q += v * v;
-    }
-    ss_row[c * 32] = q;
-    qsum += q;
+  const int k0 = min(c, ng - 1) * 32;
+  const uint16_t* trow = table + tok * d + k0;
+  u32x4 tv[4], wv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) tv[j] = *(const u32x4*)(trow + 8 * j);
+  if (pre) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wv[j] = *(const u32x4*)(pre_norm + k0 + 8 * j);
   }
-  if (!pre) return;
-  __shared__ float red[4];
-  const float sc = pre_scale_of(1.f / sqrtf(block_sum_256(qsum, red) / (float)d + eps));
-  if (threadIdx.x == 0) pre_sc[m] = sc;
-  bool over = false;
-  for (int c = threadIdx.x; c < d / 32; c += blockDim.x) {
+  float x[32];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[8 * j + 2 * e] = bf16_bits_to_float(tv[j][e] & 0xffffu);
+      x[8 * j + 2 * e + 1] = bf16_bits_to_float(tv[j][e] >> 16);
+    }
+  float q = 0.f;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) q += x[e] * x[e];
+  if (!live) q = 0.f;
+  if (pre) {
+    __shared__ float red[4];
+    const float sc = pre_scale_of(1.f / sqrtf(block_sum_256(q, red) / (float)d + eps));
+    u32x4 ph[4], pl[4];
     float xsum = 0.f;
-    for (int j = 0; j < 4; ++j) {
-      const int k = c * 32 + 8 * j;
-      float x[8];
+    bool over = false;
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        x[e] = (bf16_bits_to_float(trow[k + e]) * sc) * bf16_bits_to_float(pre_norm[k + e]);
-      u32x4 ph, pl;
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {  // word w holds elements (w, w + 4)
-        const _Float16 h0 = (_Float16)x[w], h1 = (_Float16)x[w + 4];
-        const _Float16 l0 = f16_lo(x[w], h0), l1 = f16_lo(x[w + 4], h1);
-        ph[w] = pack_half2(h0, h1);
-        pl[w] = pack_half2(l0, l1);
-        over = over || f16_overflows(x[w]) || f16_overflows(x[w + 4]);
+      for (int w = 0; w < 4; ++w) {  // word w of chunk j holds elements (w, w + 4)
+        const int e0 = 8 * j + w, e1 = e0 + 4;
+        const uint32_t w0 = wv[j][(e0 & 7) >> 1], w1 = wv[j][(e1 & 7) >> 1];
+        const float g0 = bf16_bits_to_float((e0 & 1) ? w0 >> 16 : w0 & 0xffffu);
+        const float g1 = bf16_bits_to_float((e1 & 1) ? w1 >> 16 : w1 & 0xffffu);
+        const float v0 = (x[e0] * sc) * g0, v1 = (x[e1] * sc) * g1;
+        const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
+        const _Float16 l0 = f16_lo(v0, h0), l1 = f16_lo(v1, h1);
+        ph[j][w] = pack_half2(h0, h1);
+        pl[j][w] = pack_half2(l0, l1);
+        over = over || f16_overflows(v0) || f16_overflows(v1);
         xsum += ((float)h0 + (float)l0) + ((float)h1 + (float)l1);
       }
-      *(u32x4*)(pre + (int64_t)m * d + k) = ph;
-      *(u32x4*)(pre + (int64_t)(M + m) * d + k) = pl;
+    if (live) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        *(u32x4*)(pre + (int64_t)m * d + k0 + 8 * j) = ph[j];
+        *(u32x4*)(pre + (int64_t)(M + m) * d + k0 + 8 * j) = pl[j];
+      }
+      xs_row[c * 32] = xsum;
+      if (over && err)
+        __hip_atomic_fetch_or(err, DRT_ERR_F16_RANGE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    xs_row[c * 32] = xsum;
+    if (threadIdx.x == 0) pre_sc[m] = sc;
   }
-  if (over && err)
-    __hip_atomic_fetch_or(err, DRT_ERR_F16_RANGE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (live) {
+    f32x4* hrow = (f32x4*)(hidden + (int64_t)m * d + k0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) hrow[j] = f32x4{x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]};
+    if (ss_out) ss_row[c * 32] = q;
+  }
 }
 
 // One wave per output row (4 rows per 256-thread work-group). Lane l owns the
@@ -134,23 +154,33 @@ extern "C" __global__ __launch_bounds__(256) void residual_norm_kernel(
   const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (i >= n_rows) return;  // whole waves
   const int src = src_rows ? src_rows[i] : i;
+  // Every load is issued before the first store: a wait for a load also waits
+  // for the stores issued before it. Chunk c exists where 512 c < d (uniform
+  // across the wave); within a last, partial chunk the addresses are clamped
+  // and the lanes past d are zeroed.
   f32x4 v[NC][2];
+  u32x4 wv[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    const int k = (lane + 64 * c) * 8;
-    if (k < d) {
+    v[c][0] = v[c][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    wv[c] = u32x4{0u, 0u, 0u, 0u};
+    if (512 * c < d) {
+      const int k = min((lane + 64 * c) * 8, d - 8);
       const f32x4* hp = (const f32x4*)(hidden + (int64_t)src * d + k);
       v[c][0] = hp[0];
       v[c][1] = hp[1];
-    } else {
-      v[c][0] = v[c][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+  }
+  if (norm_w) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      if (512 * c < d) wv[c] = *(const u32x4*)(norm_w + min((lane + 64 * c) * 8, d - 8));
   }
   if (part) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const int k = (lane + 64 * c) * 8;
-      if (k < d) {
+      if (512 * c < d) {
+        const int k = min((lane + 64 * c) * 8, d - 8);
         // every slice's loads are issued before the first add (one latency)
         f32x4 ps[RN_MAX_SPLITS][2];
 #pragma unroll
@@ -177,11 +207,20 @@ extern "C" __global__ __launch_bounds__(256) void residual_norm_kernel(
         }
         v[c][0] += s0;
         v[c][1] += s1;
-        if (write_hidden) {
-          f32x4* hp = (f32x4*)(hidden + (int64_t)src * d + k);
-          hp[0] = v[c][0];
-          hp[1] = v[c][1];
-        }
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+    if ((lane + 64 * c) * 8 >= d) v[c][0] = v[c][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (part && write_hidden) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int k = (lane + 64 * c) * 8;
+      if (k < d) {
+        f32x4* hp = (f32x4*)(hidden + (int64_t)src * d + k);
+        hp[0] = v[c][0];
+        hp[1] = v[c][1];
       }
     }
   }
@@ -196,12 +235,11 @@ extern "C" __global__ __launch_bounds__(256) void residual_norm_kernel(
   for (int c = 0; c < NC; ++c) {
     const int k = (lane + 64 * c) * 8;
     if (k >= d) break;  // uniform across each 8-lane group (d % 64 == 0)
-    const u32x4 wv = *(const u32x4*)(norm_w + k);
     float n[8];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      n[2 * e] = (v[c][e >> 1][(2 * e) & 3] * inv) * bf16_bits_to_float(wv[e] & 0xffffu);
-      n[2 * e + 1] = (v[c][e >> 1][(2 * e + 1) & 3] * inv) * bf16_bits_to_float(wv[e] >> 16);
+      n[2 * e] = (v[c][e >> 1][(2 * e) & 3] * inv) * bf16_bits_to_float(wv[c][e] & 0xffffu);
+      n[2 * e + 1] = (v[c][e >> 1][(2 * e + 1) & 3] * inv) * bf16_bits_to_float(wv[c][e] >> 16);
     }
     if (fmt == ACT_F16P) {  // hi plane, lo plane at + n_rows * d
       _Float16 h[8], lo[8];
@@ -289,7 +327,8 @@ namespace drt {
 
 void embed(const int32_t* tokens, const uint16_t* table, float* hidden, int M, int d,
            float* ss_out, hipStream_t s, const StepDesc* row_desc, const PreOut* pre) {
-  require(!pre || (ss_out && d % 32 == 0), "pre-scaled planes need the row statistics");
+  require(d % 32 == 0 && d <= 32 * 256, "embed needs d % 32 == 0 and d <= 8192");
+  require(!pre || ss_out, "pre-scaled planes need the row statistics");
   // with ss_out, whole 32-row tiles are launched so unused rows get zero partials
   const int grid = ss_out ? (M + 31) / 32 * 32 : M;
   hipLaunchKernelGGL(embed_kernel, dim3(grid), dim3(256), 0, s, tokens, table, hidden, M, d,

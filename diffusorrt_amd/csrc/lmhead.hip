@@ -604,8 +604,6 @@ extern "C" __global__ void lmhead_finalize_kernel(const LmStat* __restrict__ sta
   __shared__ int red_j[4];
   const int row = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (err_host && row == 0 && threadIdx.x == 0)
-    *err_host = __hip_atomic_load(err_dev, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const LmStat* st = stats + (int64_t)row * NB;
   // pass 1: global max and its first block
   float mx = -INFINITY;
@@ -667,6 +665,10 @@ extern "C" __global__ void lmhead_finalize_kernel(const LmStat* __restrict__ sta
       scores_d[row] = sc;
       tokens_d[row] = tk;
     }
+    // last: a wait for a load also waits for the stores before it, and this
+    // one crosses the bus to host memory
+    if (err_host && row == 0)
+      *err_host = __hip_atomic_load(err_dev, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
