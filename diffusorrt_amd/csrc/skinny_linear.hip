@@ -127,19 +127,18 @@ __global__ void xcc_probe_kernel(int* __restrict__ xcc) {
 
 // The last work-group's sum of the KS <= KSC partial tiles of a wide block into
 // the [4][32][33] LDS tile: 1024 16-byte chunks, 4 per thread; every slice's
-// chunks are loaded before any is added (then added in slice order), and the
-// caller's further loads (after()) are issued behind them. Slices past KS reload
-// the last one and are added times 0: a load under a branch makes the compiler
-// wait for it, and for everything issued before it, inside the branch.
-template <int KSC, typename After>
-DRT_DEV void sk_wide_sum_slices(const float* pbase, int KS, float* red, bool rnd, After after) {
+// chunks are loaded before any is added (then added in slice order). Slices
+// past KS reload the last one and are added times 0: a load under a branch makes
+// the compiler wait for it, and for everything issued before it, inside the
+// branch.
+template <int KSC>
+DRT_DEV void sk_wide_sum_slices(const float* pbase, int KS, float* red, bool rnd) {
   f32x4 pv[KSC][4];
 #pragma unroll
   for (int k2 = 0; k2 < KSC; ++k2)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       pv[k2][i] = *(const f32x4*)(pbase + (size_t)min(k2, KS - 1) * 4096 + 4 * (threadIdx.x + 256 * i));
-  after();
   __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the first wait
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -199,6 +198,9 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(
   const bool live = sk_place(n_xcc, fenced, perr, N / 128, KS, grp, ks);
   const int nt = grp * 4 + wave;
   const int u0 = ks * U, kc0 = u0 * 64;
+  // absolute position of row 0 (the q|k|v epilogue's rotary tables), read at
+  // the start: the tables' loads after the MFMAs depend on it
+  const int row0 = EPI == EPI_QKV && a.desc ? a.desc->row0 : 0;
   constexpr int KCN = U * 64;
   constexpr int ROW_H = KCN + 8;  // 16-bit elements per LDS row (+16 B pad)
   extern __shared__ __align__(16) char smem[];
@@ -385,11 +387,12 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] *= fr[i];
   }
+  // the q|k|v epilogue's tables (rotary angles, q/k norm weights, bias), issued
+  // before the exchange so that their latency passes during it
+  QkvTables qt;
+  if (EPI == EPI_QKV) qt = qkv_tables(a, grp, row0 + m0, M);
   if (!live) return;  // work-group-uniform, before any global store
   // 6. K slices meet: the last work-group of the column block adds the partials
-  // (the epilogue's tables are loaded with the partials)
-  const int row0 = a.desc ? a.desc->row0 : 0;
-  QkvTables qt;
   if (KS > 1) {
     // partial tile of this wave in accumulator order: chunk jj*64 + lane holds
     // rows 8jj + 4(lane >> 5) .. +3 of column lane & 31, so each store
@@ -400,15 +403,11 @@ __global__ __launch_bounds__(256) void skinny_wide_kernel(
       *(f32x4*)(pw + 256 * jj) = f32x4{acc[4 * jj], acc[4 * jj + 1], acc[4 * jj + 2], acc[4 * jj + 3]};
     if (!last_to_arrive(&counters[grp], KS, flag, a.fenced)) return;
     const float* pbase = part + (size_t)grp * KS * 4096;
-    auto tables = [&]() {
-      if (EPI == EPI_QKV) qt = qkv_tables(a, grp, row0 + m0, M);
-    };
     const bool rnd = BF && a.rnd_bf16;
-    if (KS <= 2) sk_wide_sum_slices<2>(pbase, KS, red, rnd, tables);
-    else if (KS <= 4) sk_wide_sum_slices<4>(pbase, KS, red, rnd, tables);
-    else sk_wide_sum_slices<SK_KS_MAX>(pbase, KS, red, rnd, tables);
+    if (KS <= 2) sk_wide_sum_slices<2>(pbase, KS, red, rnd);
+    else if (KS <= 4) sk_wide_sum_slices<4>(pbase, KS, red, rnd);
+    else sk_wide_sum_slices<SK_KS_MAX>(pbase, KS, red, rnd);
   } else {
-    if (EPI == EPI_QKV) qt = qkv_tables(a, grp, row0 + m0, M);
 #pragma unroll
     for (int r = 0; r < 16; ++r)
       red[(wave * 32 + mfma_row(r, lane)) * 33 + (lane & 31)] =
@@ -495,6 +494,12 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(
   int* flag = (int*)(red + SK_RED);
 
   f32x16 acc = f32x16{};
+  // epilogue: thread t owns row t >> 3, columns 4*(t & 7) .. +3 of the tile
+  const int m = threadIdx.x >> 3, c0 = 4 * (threadIdx.x & 7);
+  const int n = nt * 32 + c0;
+  f32x4 h_old = f32x4{0.f, 0.f, 0.f, 0.f};
+  uint2 pw = uint2{0u, 0u};
+  float pc = 0.f;
   // this wave's A staging: [2 planes][UW][32 rows][144 B] (128 B of a unit's row + pad)
   char* stg = smem + SK_NARROW_STG + wave * (2 * UW * 32 * 144);
   const uint16_t* act_lo = act + (int64_t)M_all * K + (int64_t)m0 * K;  // ACT_F16P lo plane
@@ -540,6 +545,22 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(
         wq[i][0] = __builtin_nontemporal_load(q4_tile_words(qw, nt, G, u, lane));
         wsb[i] = ub + i < u_hi ? q4_tile_sb(sbp, nt, G, u, lane) : 0u;
       }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // the epilogue's inputs, issued behind the weights so that their latency
+    // (they may come from another XCD's writes or from HBM) passes during the
+    // MFMAs and the exchange, and no wait before those is held up by them (with
+    // pre-scaled planes out: the next norm's weights and the row's scale;
+    // without, the two pre loads read the hidden rows). Unconditional: a load
+    // under a branch must be waited for again after it, and on this target a wait
+    // also waits for the stores issued before it. (Several unit batches: reloaded
+    // each time, from L2.)
+    if (EPI == EPI_RESID) {
+      const int64_t row = m0 + min(m, M - 1);
+      h_old = *(const f32x4*)(a.hidden_out + row * N + n);
+      const bool pre = a.pre_out != nullptr;
+      pw = *(const uint2*)(pre ? (const void*)(a.pre_norm + n) : (const void*)(a.hidden_out + n));
+      pc = *(pre ? a.pre_sc + row : (const float*)a.hidden_out);
     }
     __builtin_amdgcn_sched_barrier(0);
     if (XIN != 0) {
@@ -622,24 +643,7 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(
 #pragma unroll
   for (int r = 0; r < 16; ++r) red[(wave * 32 + mfma_row(r, lane)) * 33 + (lane & 31)] = acc[r];
   __syncthreads();
-  const int m = threadIdx.x >> 3, c0 = 4 * (threadIdx.x & 7);
-  const int n = nt * 32 + c0;
-  // the epilogue's inputs, loaded before the exchange so their latency overlaps
-  // it (with pre-scaled planes out: the next norm's weights and the row's
-  // scale). Unconditional (rows past M read row M - 1; without planes out the
-  // two pre loads read the hidden rows): a load under a branch must be waited for
-  // again after it, and on this target a wait also waits for the stores issued
-  // before it. For the same reason every store of the epilogue comes last.
-  f32x4 h_old = f32x4{0.f, 0.f, 0.f, 0.f};
-  uint2 pw = uint2{0u, 0u};
-  float pc = 0.f;
-  if (EPI == EPI_RESID) {
-    const int64_t row = m0 + min(m, M - 1);
-    h_old = *(const f32x4*)(a.hidden_out + row * N + n);
-    const bool pre = a.pre_out != nullptr;
-    pw = *(const uint2*)(pre ? (const void*)(a.pre_norm + n) : (const void*)(a.hidden_out + n));
-    pc = *(pre ? a.pre_sc + row : (const float*)a.hidden_out);
-  }
+  // every store of the epilogue comes after its last load (see above)
   f32x4 v;
 #pragma unroll
   for (int e = 0; e < 4; ++e)
