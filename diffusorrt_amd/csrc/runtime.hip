@@ -1029,22 +1029,65 @@ struct Session {
       warm = true;
       return;
     }
-    if (!exec) {
-      hipGraph_t g = nullptr;
-      DRT_HIP(hipStreamBeginCapture(r.stream, hipStreamCaptureModeThreadLocal));
-      try {
-        launch_forward(r, kv.p, head_stride, layer_stride, a, p);
-      } catch (...) {
-        (void)hipStreamEndCapture(r.stream, &g);
-        if (g) (void)hipGraphDestroy(g);
-        throw;
-      }
-      DRT_HIP(hipStreamEndCapture(r.stream, &g));
-      const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
-      (void)hipGraphDestroy(g);
-      DRT_HIP(e);
-    }
+    if (!exec) capture_into(exec, a, p);
     DRT_HIP(hipGraphLaunch(exec, r.stream));
+  }
+
+  // Record the kernels of one forward into an instantiated graph (nothing runs).
+  void capture_into(hipGraphExec_t& exec, const ForwardArgs& a, const ForwardPtrs& p) {
+    Runtime& r = *rt;
+    hipGraph_t g = nullptr;
+    DRT_HIP(hipStreamBeginCapture(r.stream, hipStreamCaptureModeThreadLocal));
+    try {
+      launch_forward(r, kv.p, head_stride, layer_stride, a, p);
+    } catch (...) {
+      (void)hipStreamEndCapture(r.stream, &g);
+      if (g) (void)hipGraphDestroy(g);
+      throw;
+    }
+    DRT_HIP(hipStreamEndCapture(r.stream, &g));
+    const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    DRT_HIP(e);
+  }
+
+  // The merged commit + step forward of the block starting at next_fp (its
+  // first step commits [next_fp - block, next_fp)), captured ahead of its first
+  // use while the steps already queued run: a capture records and executes
+  // nothing, so that first use replays it instead of running eagerly and then
+  // capturing on the host's time in the middle of a decode. Its descriptor slot
+  // is its own (written before every replay); the upload here lands after the
+  // queued steps, in stream order.
+  void precapture_pair(int next_fp) {
+    Runtime& r = *rt;
+    const int hi = next_fp + block;
+    if (!use_graphs || prof.on || !pairable() || !graphable(block) || g_exec[G_PAIR] ||
+        next_fp < block || hi > (int)canvas.size() || hi > r.rope_positions)
+      return;
+    ForwardArgs a;
+    a.tokens_dev = tokens_dev.as<int32_t>();
+    a.temperature = (float)temperature;
+    a.seed = seed;
+    a.step = proposals;
+    a.row0 = next_fp - block;
+    a.n_rows = 2 * block;
+    a.n_keys = hi;
+    a.mask_kind = 1;
+    a.mask_prompt_len = origin;
+    a.mask_block = block;
+    a.seg_rows = block;
+    a.quota = 0;
+    for (int q = next_fp; q < hi; ++q) {
+      a.lm_rows.push_back(q - a.row0);
+      a.lm_pos.push_back(q);
+    }
+    a.n_lm = block;
+    ForwardPtrs p = stage_forward(r, a, (int)G_PAIR, true, canvas.data(), false, (int)G_PAIR);
+    p.canvas = tokens_dev.as<int32_t>();
+    p.mask_id = mask_id;
+    p.ranges = g_ranges;
+    capture_into(g_exec[G_PAIR], a, p);
+    g_warm[G_PAIR] = true;
   }
 
   // Commit forwards for the rows [cache_len, frozen_prefix) (exact prefix K/V):
@@ -1126,6 +1169,7 @@ struct Session {
       a.n_lm = block;
       graph_forward(a.seg_rows > 0 ? G_PAIR : G_STEP, a, Runtime::EAGER_SLOT0 + j, false);
     }
+    precapture_pair(hi);  // the next block's first step, while these run
     if (pair) {
       m.commit_rows += block;
       cache_len = fp;
