@@ -218,7 +218,11 @@ int32_t drt_op_q4_quantize(const void* w, int32_t w_dtype, int32_t n, int32_t k,
  * bf16 y [n]. */
 int32_t drt_op_cast_bf16(const float* x, void* y, int64_t n, void* stream);
 /* linear(x, QuantizedWeight, bias) (mlx_ops.py:97-130): y fp32 [m, n] from x fp32 or
- * bf16 [m, k]; bias bf16 [n] or NULL. Needs drt_op_q4_linear_workspace_bytes(m, n, k). */
+ * bf16 [m, k]; bias bf16 [n] or NULL. Needs drt_op_q4_linear_workspace_bytes(m, n, k).
+ * m <= 32: one split-K launch that reads x as it is; its arrival counters are a block of a
+ * library array reserved for (device, stream) on first use (32 per device; a further
+ * stream's calls take a two-launch path), so calls on different streams never share
+ * counters. Calls that overlap must not share a workspace. */
 size_t drt_op_q4_linear_workspace_bytes(int32_t m, int32_t n, int32_t k);
 int32_t drt_op_q4_linear(const void* qw, const void* sb, const void* x, int32_t x_dtype,
                          int32_t m, int32_t n, int32_t k, const void* bias, float* y,
@@ -249,7 +253,8 @@ int32_t drt_op_kv_pack(const void* k, const void* v, int32_t src_dtype, int32_t 
 /* attention(q, k, v, head_dim=128, kind, mask_geometry, q_positions) (mlx_ops.py:347-443)
  * over the tiled cache: q [rows, hq, 128] of kv_dtype, keys [0, n_keys), query row r at
  * absolute position row_pos0 + r. mask_kind: DRT_MASK_BIDIRECTIONAL or DRT_MASK_D2F_HYBRID
- * (with prompt_len / block_size). out [rows, hq*128] of out_dtype (DRT_F32 or DRT_BF16). */
+ * (with prompt_len / block_size). out [rows, hq*128] of out_dtype (DRT_F32 or DRT_BF16).
+ * q is read in place by the kernels (no staging copy). */
 size_t drt_op_attention_workspace_bytes(int32_t rows, int32_t hq, int32_t hkv, int32_t n_keys);
 int32_t drt_op_attention(const void* q, const void* cache, int64_t head_stride, int32_t kv_dtype,
                          int32_t rows, int32_t hq, int32_t hkv, int32_t n_keys, int32_t row_pos0,
