@@ -1086,8 +1086,15 @@ struct Session {
     p.canvas = tokens_dev.as<int32_t>();
     p.mask_id = mask_id;
     p.ranges = g_ranges;
-    capture_into(g_exec[G_PAIR], a, p);
-    g_warm[G_PAIR] = true;
+    // an optimisation only: if the capture fails, the first use takes the usual
+    // path (eager, then captured), which reports an error that persists
+    try {
+      capture_into(g_exec[G_PAIR], a, p);
+      g_warm[G_PAIR] = true;
+    } catch (const std::exception&) {
+      (void)hipGetLastError();
+      g_exec[G_PAIR] = nullptr;
+    }
   }
 
   // Commit forwards for the rows [cache_len, frozen_prefix) (exact prefix K/V):

@@ -155,16 +155,21 @@ def test_dream_512_row_canvas_window_and_fixed_quota_steps():
         rt.close()
 
 
-def test_dream_7b_shapes_32_row_window():
+@pytest.mark.parametrize("rows", [32, 48])
+def test_dream_7b_shapes_window(rows):
+    """A one-layer Dream window at the 7B layer shapes. 32 rows run the
+    weight-streaming linears; 48 rows (two 32-row tiles) run the split-K linears
+    with the pre-scaled norm inputs at K = 3584 (eight 64-k units per q|k|v
+    work-group)."""
     from diffusorrt_amd import synthetic as syn
     from diffusorrt_amd.runtime import Runtime, fixed_quota_session_config
 
-    _say("dream 7B shapes, 32-row window (split-K linears)")
+    _say(f"dream 7B shapes, {rows}-row window")
     geom = _geometry(syn.DREAM_QWEN25_7B)
     model = syn.build_model(geom, "q4", seed=5)
     W, cfg = oracle_weights(model), syn.oracle_config(geom, "q4")
-    x = np.random.default_rng(5).integers(0, 3900, 24).tolist() + [geom.mask_token_id] * 8
-    scope = list(range(24, 32))
+    x = np.random.default_rng(5).integers(0, 3900, rows - 8).tolist() + [geom.mask_token_id] * 8
+    scope = list(range(rows - 8, rows))
     rt = Runtime(model, max_forward_rows=64, max_positions=256)
     try:
         with rt.session(fixed_quota_session_config(8, 8, len(x))) as s:
