@@ -4,11 +4,12 @@
 Workload (one GPU): BD3LM on the Qwen3-0.6B architecture with q4 affine g64
 weights (seed 4), an 8192-token random prefix already committed to the K/V
 cache, then blocks of 32 masked tokens, 8 denoise steps per block, 4 tokens
-unmasked per step (greedy max-probability). A *step* is one denoise step:
-propose on the device (forward of the active block over the cached prefix,
-fused LM head + float64 softmax scoring of the frontier) -> host top-k select
--> commit. The once-per-block forward that writes a finished block's K/V is
-counted in the step that triggers it.
+unmasked per step (greedy max-probability). A *step* is one denoise step: the
+forward of the active block over the cached prefix, the fused LM head with the
+frontier's float64 scoring, and the step's fixed-quota choice and commit, all
+on the device through the library's native loop (``--host-loop``: the choice
+on the host through propose / commit). A finished block's K/V-writing forward
+runs merged into the next block's first step and is counted there.
 
 Prints one JSON line. ``value`` is generated tokens/s over the timed steps,
 which replay the captured HIP graphs of the step and block-commit forwards.
@@ -16,7 +17,8 @@ which replay the captured HIP graphs of the step and block-commit forwards.
 ``attn_decode_kernel``): its dispatches are timed one by one with HIP events
 (hipExtLaunchKernelGGL start/stop events on the launch stream) over a second
 timed region of the same number of steps run eagerly, since a graph replay
-cannot carry per-dispatch events. ``cpu_baseline`` times the oracle's
+cannot carry per-dispatch events; ``roofline.op`` is the same over the kernel
+and its range combine. ``cpu_baseline`` times the oracle's
 reference-semantics CPU path (full prefix recompute) on a bounded sample.
 
 ``--calibrate-copy`` instead times a plain device copy of a known size (the
@@ -467,7 +469,7 @@ def main():
         "committed_tokens": committed,
     }
     if prof_steps > 0:
-        names = ("attention", "linear", "lm_head")
+        names = ("attention", "attention_combine", "linear", "lm_head")
         comp = {}
         for n in names:
             ms = mp[f"rocm_prof_ms_{n}"]
@@ -487,6 +489,13 @@ def main():
                            "algorithmic_bytes_per_launch": round(per_launch),
                            "avg_launch_us": a["avg_launch_us"], "launches": a["launches"],
                            "timed_over": f"{prof_steps} eager steps after the graph-timed region"}
+        # the attention op: the kernel and its range combine, over the same bytes
+        op_ms = mp["rocm_prof_ms_attention"] + mp["rocm_prof_ms_attention_combine"]
+        op_achieved = mp["rocm_prof_bytes_attention"] / max(op_ms, 1e-9) / 1e6
+        out["roofline"]["op"] = {"kernels": "attn_decode_kernel + attn_decode_combine_kernel",
+                                 "achieved": round(op_achieved, 1),
+                                 "frac": round(op_achieved / HBM_PEAK_GBS, 4),
+                                 "avg_op_us": round(op_ms / max(1, a["launches"]) * 1e3, 3)}
     if not args.no_cpu_baseline:
         t = time.perf_counter()
         out["cpu_baseline"] = cpu_baseline(model, prefix, g.mask_token_id, args.cpu_sample_layers)

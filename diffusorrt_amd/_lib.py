@@ -80,8 +80,8 @@ class Metrics(C.Structure):
                 ("commit_rows", C.c_int64), ("lm_rows", C.c_int64),
                 ("kv_cache_len", C.c_int64), ("kv_cache_bytes", C.c_int64),
                 ("last_forward_ms", C.c_double), ("total_forward_ms", C.c_double),
-                ("prof_ms", C.c_double * 3), ("prof_bytes", C.c_double * 3),
-                ("prof_launches", C.c_int64 * 3)]
+                ("prof_ms", C.c_double * 4), ("prof_bytes", C.c_double * 4),
+                ("prof_launches", C.c_int64 * 4)]
 
 
 _VP, _I32, _I64, _U64, _SZ = C.c_void_p, C.c_int32, C.c_int64, C.c_uint64, C.c_size_t

@@ -1051,8 +1051,8 @@ void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv
   const dim3 cgrid(Hkv, qt, 16);
   const size_t clds = (size_t)ranges * 32 * 4;
 #define DRT_COMB(QT, MLR)                                                                   \
-  hipLaunchKernelGGL((attn_decode_combine_kernel<QT, MLR>), cgrid, dim3(256), clds, s, o_part, \
-                     ml_part, ranges, n_rows, Hq, Hkv, out, out_fmt, err)
+  DRT_LAUNCH(Profiler::ATTN_COMBINE, 0.0, (attn_decode_combine_kernel<QT, MLR>), cgrid,      \
+             dim3(256), clds, s, o_part, ml_part, ranges, n_rows, Hq, Hkv, out, out_fmt, err)
   if (ranges <= 32) {
     if (qt == 1) DRT_COMB(1, 4); else if (qt == 2) DRT_COMB(2, 4); else DRT_COMB(4, 4);
   } else {

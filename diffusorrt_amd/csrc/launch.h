@@ -95,7 +95,9 @@ inline void grant_lds(const void* fn, size_t bytes, size_t& granted) {
 // timestamps (no extra packets in the stream); collect() reads them after the
 // stream has drained.
 struct Profiler {
-  enum Class : int { ATTN = 0, GEMM = 1, LMHEAD = 2, NCLASS = 3 };
+  // ATTN_COMBINE: the decode attention's range combine (no algorithmic bytes of
+  // its own: its partials are the attention's intermediate)
+  enum Class : int { ATTN = 0, GEMM = 1, LMHEAD = 2, ATTN_COMBINE = 3, NCLASS = 4 };
   bool on = false;
   std::vector<hipEvent_t> pool;
   struct Rec { int cls; double bytes; };

@@ -318,14 +318,15 @@ class DeviceSession:
         for name, _ in _lib.Metrics._fields_:
             v = getattr(m, name)
             if name.startswith("prof_"):
-                for i, cls in enumerate(("attention", "linear", "lm_head")):
+                for i, cls in enumerate(("attention", "linear", "lm_head", "attention_combine")):
                     out[f"rocm_{name}_{cls}"] = v[i]
             else:
                 out["rocm_" + name] = v
         return out
 
     def set_profiling(self, enable: bool) -> None:
-        """Time each attention / linear / LM-head dispatch (dispatch timestamps)."""
+        """Time each attention / range-combine / linear / LM-head dispatch (dispatch
+        timestamps)."""
         _lib.check(self._lib.drt_session_set_profiling(self.handle, int(bool(enable))))
 
     def close(self) -> None:

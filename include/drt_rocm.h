@@ -129,11 +129,12 @@ typedef struct drt_metrics {
   double last_forward_ms;         /* device time of the last forward (HIP events) */
   double total_forward_ms;
   /* per-dispatch device time while profiling is on (drt_session_set_profiling), by
-   * kernel class 0 = attention split, 1 = linear GEMMs, 2 = LM head: summed ms,
-   * summed algorithmic bytes, launch counts */
-  double prof_ms[3];
-  double prof_bytes[3];
-  int64_t prof_launches[3];
+   * kernel class 0 = attention, 1 = linear GEMMs, 2 = LM head, 3 = the decode
+   * attention's range combine: summed ms, summed algorithmic bytes (none for the
+   * combine, whose reads are the attention's partials), launch counts */
+  double prof_ms[4];
+  double prof_bytes[4];
+  int64_t prof_launches[4];
 } drt_metrics;
 
 /* ---- library / handles ---- */
