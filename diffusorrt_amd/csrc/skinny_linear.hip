@@ -731,6 +731,172 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(
   if (KS > 1 && threadIdx.x == 0) reset_counter(&counters[nt], a.fenced);
 }
 
+// gate|up + SwiGLU of <= 32 rows per row tile over the whole K, without
+// split-K (q4 weights, pre-scaled norm input, K = 64 G with G in {8, 16}).
+// The fused weight interleaves [gate 64 | up 64] per 128 columns, so n-tiles
+// 4b + i (gate) and 4b + 2 + i (up) give SwiGLU outputs 64b + 32i .. + 31:
+// work-group (p = 2b + i, row tile) owns that pair. The whole activation slice
+// (32 rows x K, hi and lo planes) goes into LDS by direct-to-LDS loads; wave w
+// of 8 takes the 64-k units G/8 w .. + G/8 - 1 of both tiles (one read of the A
+// fragments feeds the gate and the up MFMAs); the waves' tiles are added in
+// LDS in wave order and SwiGLU runs on the sums. No partial tiles, arrival
+// counters or last work-group, whose round trips cost more than staging 4x the
+// activation. Leading arguments as in skinny_wide_kernel (planes, their
+// per-32-column sums, sums of squares, the planes' scale c per row).
+template <int G>
+__global__ __launch_bounds__(512) void skinny_gu_kernel(
+    const uint32_t* __restrict__ qw, const uint32_t* __restrict__ sbp,
+    const uint16_t* __restrict__ planes, const float* __restrict__ xs_part,
+    const float* __restrict__ ss_arg, const float* __restrict__ sc_in, int* perr,
+    uint32_t dims0, uint32_t dims1, const FusedArgs a) {
+  static_assert(G == 8 || G == 16, "K = 512 or 1024");
+  constexpr int K = G * 64, ROW = K + 8, CPR = G / 8, UPW = G / 8;
+  constexpr int RS = 36;  // floats per row of a wave's tile in LDS (16-byte rows, padded)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int M, N, Kd, KS, n_xcc, fenced;
+  sk_dims(dims0, dims1, M, N, Kd, KS, n_xcc, fenced);
+  (void)Kd, (void)KS, (void)n_xcc, (void)fenced, (void)perr;
+  const int mt = blockIdx.y, m0 = 32 * mt, M_all = M;
+  M = min(32, M_all - m0);
+  const int blk = blockIdx.x >> 1, half = blockIdx.x & 1;
+  const int nt_g = 4 * blk + half, nt_u = nt_g + 2;
+  extern __shared__ __align__(16) char smem[];
+  uint16_t* act = (uint16_t*)smem;                   // [2 planes][32][ROW] halves
+  float* xss = (float*)(smem + 2 * 32 * ROW * 2);    // [G][32] group sums
+  float* rfac = xss + G * 32;                        // [32] rinv / c
+  float* red = rfac + 32;                            // [16][32] sums of squares
+  float* cl = red + 16 * 32;                         // [32] c
+  float* red2 = (float*)smem;                        // [8 waves][2 tiles][32][RS] after the MFMAs
+
+  // 1. the small L2-resident loads: thread t takes row t % 32, partial sums of
+  // squares t / 32 and t / 32 + 16, the two 32-column sums of group t / 32,
+  // and c (all unconditional, clamped, masked after the wait)
+  const int np = K >> 5;  // 32-column partial sums per row (<= 32)
+  const int r32 = threadIdx.x & 31, q16 = threadIdx.x >> 5;
+  const float* ss_in = ss_arg + (int64_t)mt * K;
+  const float* xsp = xs_part + (int64_t)mt * K;
+  const int rr = min(r32, M - 1), gx = min(q16, G - 1);
+  const float sv0 = ss_in[min(q16, np - 1) * 32 + r32];
+  const float sv1 = ss_in[min(q16 + 16, np - 1) * 32 + r32];
+  const float xp0 = xsp[(2 * gx) * 32 + rr], xp1 = xsp[(2 * gx + 1) * 32 + rr];
+  const float c_in = sc_in[m0 + rr];
+  // 2. this wave's weights (both tiles; issued before the activation so that
+  // their HBM latency starts first)
+  u32x4 wg[UPW], wu[UPW];
+  uint32_t sg[UPW], su[UPW];
+#pragma unroll
+  for (int j = 0; j < UPW; ++j) {
+    const int g = wave * UPW + j;
+    wg[j] = __builtin_nontemporal_load(q4_tile_words(qw, nt_g, G, g, lane));
+    wu[j] = __builtin_nontemporal_load(q4_tile_words(qw, nt_u, G, g, lane));
+    sg[j] = q4_tile_sb(sbp, nt_g, G, g, lane);
+    su[j] = q4_tile_sb(sbp, nt_u, G, g, lane);
+  }
+  // 3. the activation into LDS: 1 KiB chunks (plane, row, piece), 16 B a lane;
+  // rows past M repeat row M - 1 (their results are never stored)
+#pragma unroll
+  for (int i = 0; i < 2 * 32 * CPR / 8; ++i) {
+    const int ch = wave + 8 * i, pl = ch / (32 * CPR), r = (ch / CPR) & 31, q = ch % CPR;
+    const uint16_t* src = planes + ((int64_t)pl * M_all + m0 + min(r, M - 1)) * K + q * 512 + lane * 8;
+    __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)(
+                                         act + (pl * 32 + r) * ROW + q * 512),
+                                     16, 0, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  red[q16 * 32 + r32] = sv0 * (q16 < np ? 1.f : 0.f) + sv1 * (q16 + 16 < np ? 1.f : 0.f);
+  if ((int)threadIdx.x < 32 * G) xss[threadIdx.x] = xp0 + xp1;
+  if (threadIdx.x < 32) cl[threadIdx.x] = c_in;
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's activation chunks landed
+  __syncthreads();                // ... and every other wave's
+  if (threadIdx.x < 32) {
+    float ssum = 0.f;
+#pragma unroll
+    for (int g = 0; g < 16; ++g) ssum += red[g * 32 + threadIdx.x];
+    const float ri = 1.f / sqrtf(ssum / (float)K + a.eps);
+    rfac[threadIdx.x] = (int)threadIdx.x < M ? ri / cl[threadIdx.x] : 0.f;
+    if (a.pre_sc_out && blockIdx.x == 0 && (int)threadIdx.x < M)
+      a.pre_sc_out[m0 + threadIdx.x] = pre_scale_of(ri);
+  }
+  // 4. this wave's units, each A fragment read once for both tiles
+  f32x16 acc_g = f32x16{}, acc_u = f32x16{};
+  const _Float16* arow = (const _Float16*)act + (lane & 31) * ROW + 32 * (lane >> 5);
+#pragma unroll
+  for (int j = 0; j < UPW; ++j) {
+    const int g = wave * UPW + j;
+    f16x8 af[4], afl[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      af[t] = *(const f16x8*)(arow + g * 64 + 8 * t);
+      afl[t] = *(const f16x8*)(arow + 32 * ROW + g * 64 + 8 * t);
+    }
+    float xsr[16];
+    load_row_sums(xss + g * 32, lane, xsr);
+    q4_group_mma1(acc_g, af, afl, xsr, wg[j], sg[j]);
+    q4_group_mma1(acc_u, af, afl, xsr, wu[j], su[j]);
+  }
+  __syncthreads();  // every wave is done with the activation; rfac is written
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int row = mfma_row(r, lane);
+    red2[((wave * 2 + 0) * 32 + row) * RS + (lane & 31)] = acc_g[r];
+    red2[((wave * 2 + 1) * 32 + row) * RS + (lane & 31)] = acc_u[r];
+  }
+  __syncthreads();
+  // 5. SwiGLU: thread t < 256 takes row t / 8, outputs 4 (t % 8) .. + 3 of the
+  // pair, the 8 waves' tiles added in wave order and scaled by the row's
+  // factor; an 8-column ACT_F16P chunk (order 0,4,1,5,2,6,3,7) is two threads'
+  // halves, paired by a lane exchange (the even thread stores words 0-1, the
+  // odd one words 2-3; rows past M compute and exchange, then store nothing)
+  if (threadIdx.x >= 256) return;
+  const int m = threadIdx.x >> 3, q = threadIdx.x & 7;
+  f32x4 gs = *(const f32x4*)(red2 + (0 * 32 + m) * RS + 4 * q);
+  f32x4 us = *(const f32x4*)(red2 + (1 * 32 + m) * RS + 4 * q);
+#pragma unroll
+  for (int w = 1; w < 8; ++w) {
+    gs += *(const f32x4*)(red2 + ((w * 2 + 0) * 32 + m) * RS + 4 * q);
+    us += *(const f32x4*)(red2 + ((w * 2 + 1) * 32 + m) * RS + 4 * q);
+  }
+  const float f = rfac[m];
+  _Float16 hh[4], ll[4];
+  bool over = false;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float gv = gs[e] * f, uv = us[e] * f;
+    const float y = gv * (1.f / (1.f + expf(-gv))) * uv;
+    hh[e] = (_Float16)y;
+    ll[e] = f16_lo(y, hh[e]);
+    over = over || f16_overflows(y);
+  }
+  const bool odd = q & 1;
+  const uint32_t sh = odd ? pack_half2(hh[0], hh[1]) : pack_half2(hh[2], hh[3]);
+  const uint32_t sl = odd ? pack_half2(ll[0], ll[1]) : pack_half2(ll[2], ll[3]);
+  const uint32_t rh = (uint32_t)__shfl_xor((int)sh, 1), rl = (uint32_t)__shfl_xor((int)sl, 1);
+  uint2 wh, wl;
+  if (odd) {
+    wh = uint2{(rh & 0xffffu) | ((uint32_t)half_bits(hh[2]) << 16),
+               (rh >> 16) | ((uint32_t)half_bits(hh[3]) << 16)};
+    wl = uint2{(rl & 0xffffu) | ((uint32_t)half_bits(ll[2]) << 16),
+               (rl >> 16) | ((uint32_t)half_bits(ll[3]) << 16)};
+  } else {
+    wh = uint2{(uint32_t)half_bits(hh[0]) | (rh << 16), (uint32_t)half_bits(hh[1]) | (rh & 0xffff0000u)};
+    wl = uint2{(uint32_t)half_bits(ll[0]) | (rl << 16), (uint32_t)half_bits(ll[1]) | (rl & 0xffff0000u)};
+  }
+  if (m >= M) return;
+  const int F = N >> 1;
+  uint16_t* dst = (uint16_t*)a.act_out + (int64_t)(m0 + m) * F + 64 * blk + 32 * half + 4 * q;
+  *(uint2*)dst = wh;
+  *(uint2*)(dst + (int64_t)M_all * F) = wl;
+  if (over) raise_range(a);
+}
+#define SK_GU_LDS(G) (2 * 32 * ((G) * 64 + 8) * 2 + ((G) * 32 + 32 + 16 * 32 + 32) * 4)
+template __global__ void skinny_gu_kernel<8>(const uint32_t*, const uint32_t*, const uint16_t*,
+                                             const float*, const float*, const float*, int*,
+                                             uint32_t, uint32_t, const FusedArgs);
+template __global__ void skinny_gu_kernel<16>(const uint32_t*, const uint32_t*, const uint16_t*,
+                                              const float*, const float*, const float*, int*,
+                                              uint32_t, uint32_t, const FusedArgs);
+
 #define DRT_WIDE(W, E, U, P)                                                               \
   template __global__ void skinny_wide_kernel<W, E, U, P>(const uint32_t*, const uint32_t*,   \
                                                           const float*, const uint16_t*,      \
@@ -863,6 +1029,24 @@ static bool skinny_launch(const FusedArgs& a, int kind, hipStream_t s) {
   const int G = a.K / 64;
   const double bytes = (bf ? 2.0 * a.N * a.K : (double)a.N * a.K / 2 + (double)a.N * a.K / 16) +
                        2.0 * a.M * a.K + 2.0 * a.M * a.N;
+  if (kind == FL_SWIGLU && a.pre_sc_in && !bf && a.x_in == 0 && a.ss_in && a.N % 128 == 0 &&
+      (a.K == 512 || a.K == 1024)) {
+    // gate|up over the whole K (no split-K): 64-column work-groups of 8 waves
+    const dim3 grid((unsigned)(a.N / 64), MT);
+#define DRT_GU(GG)                                                                         \
+  {                                                                                        \
+    auto fn = skinny_gu_kernel<GG>;                                                        \
+    static size_t granted = 0;                                                             \
+    grant_lds((const void*)fn, SK_GU_LDS(GG), granted);                                    \
+    DRT_LAUNCH(Profiler::GEMM, bytes, fn, grid, dim3(512), SK_GU_LDS(GG), s, wq, a.sb,     \
+               (const uint16_t*)a.act, a.act_xsum, a.ss_in, a.pre_sc_in, a.placement_err,  \
+               dims0, sk_dims1(a, 1), a);                                                  \
+  }
+    if (a.K == 1024) DRT_GU(16) else DRT_GU(8)
+#undef DRT_GU
+    DRT_HIP(hipGetLastError());
+    return true;
+  }
   if (kind == FL_QKV || kind == FL_SWIGLU) {
     if (a.x_in != 0 || !a.ss_in || a.N % 128 || a.K / 32 > 8 * SK_SS_PER_THREAD) return false;
     const bool pre = a.pre_sc_in != nullptr;  // q4 (checked by the caller)
