@@ -735,14 +735,23 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(
 // split-K (q4 weights, pre-scaled norm input, K = 64 G with G in {8, 16}).
 // The fused weight interleaves [gate 64 | up 64] per 128 columns, so n-tiles
 // 4b + i (gate) and 4b + 2 + i (up) give SwiGLU outputs 64b + 32i .. + 31:
-// work-group (p = 2b + i, row tile) owns that pair. The whole activation slice
-// (32 rows x K, hi and lo planes) goes into LDS by direct-to-LDS loads; wave w
-// of 8 takes the 64-k units G/8 w .. + G/8 - 1 of both tiles (one read of the A
-// fragments feeds the gate and the up MFMAs); the waves' tiles are added in
-// LDS in wave order and SwiGLU runs on the sums. No partial tiles, arrival
-// counters or last work-group, whose round trips cost more than staging 4x the
-// activation. Leading arguments as in skinny_wide_kernel (planes, their
+// work-group (p = 2b + i, 16-row half h of a row tile) owns that pair for 16
+// rows. Its activation slice (16 rows x K, hi and lo planes) goes into LDS by
+// direct-to-LDS loads; wave w of 8 takes the 64-k units G/8 w .. + G/8 - 1 of
+// both tiles (one read of the A fragments feeds the gate and the up MFMAs; the
+// MFMA's rows 16-31 repeat rows 0-15 and are dropped); the waves' tiles are
+// added in LDS in wave order and SwiGLU runs on the sums. No partial tiles,
+// arrival counters or last work-group, whose round trips cost more than every
+// work-group staging all of K; 16-row halves halve that staging and keep two
+// work-groups per CU. Leading arguments as in skinny_wide_kernel (planes, their
 // per-32-column sums, sums of squares, the planes' scale c per row).
+constexpr int GU_RH = 16;  // rows per work-group
+constexpr int GU_RS = 36;  // floats per row of a wave's tile in LDS (16-byte rows, padded)
+// bytes of LDS shared by the activation (before the MFMAs) and the waves' tiles (after)
+constexpr int gu_region_bytes(int G) {
+  return 2 * GU_RH * (G * 64 + 8) * 2 > 8 * 2 * GU_RH * GU_RS * 4 ? 2 * GU_RH * (G * 64 + 8) * 2
+                                                                 : 8 * 2 * GU_RH * GU_RS * 4;
+}
 template <int G>
 __global__ __launch_bounds__(512) void skinny_gu_kernel(
     const uint32_t* __restrict__ qw, const uint32_t* __restrict__ sbp,
@@ -750,35 +759,38 @@ __global__ __launch_bounds__(512) void skinny_gu_kernel(
     const float* __restrict__ ss_arg, const float* __restrict__ sc_in, int* perr,
     uint32_t dims0, uint32_t dims1, const FusedArgs a) {
   static_assert(G == 8 || G == 16, "K = 512 or 1024");
-  constexpr int K = G * 64, ROW = K + 8, CPR = G / 8, UPW = G / 8;
-  constexpr int RS = 36;  // floats per row of a wave's tile in LDS (16-byte rows, padded)
+  constexpr int K = G * 64, ROW = K + 8, CPR = G / 8, UPW = G / 8, RH = GU_RH;
+  constexpr int RS = GU_RS;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int M, N, Kd, KS, n_xcc, fenced;
   sk_dims(dims0, dims1, M, N, Kd, KS, n_xcc, fenced);
   (void)Kd, (void)KS, (void)n_xcc, (void)fenced, (void)perr;
-  const int mt = blockIdx.y, m0 = 32 * mt, M_all = M;
-  M = min(32, M_all - m0);
+  // rows m0 .. m0 + M - 1 of the forward: half hr of 32-row tile mt
+  const int mt = blockIdx.y >> 1, hr = blockIdx.y & 1, tr0 = RH * hr;
+  const int m0 = 32 * mt + tr0, M_all = M;
+  M = min(RH, M_all - m0);
+  if (M <= 0) return;  // work-group-uniform: a half with no rows
   const int blk = blockIdx.x >> 1, half = blockIdx.x & 1;
   const int nt_g = 4 * blk + half, nt_u = nt_g + 2;
   extern __shared__ __align__(16) char smem[];
-  uint16_t* act = (uint16_t*)smem;                   // [2 planes][32][ROW] halves
-  float* xss = (float*)(smem + 2 * 32 * ROW * 2);    // [G][32] group sums
+  uint16_t* act = (uint16_t*)smem;                   // [2 planes][RH][ROW] halves
+  float* xss = (float*)(smem + gu_region_bytes(G));  // [G][32] group sums
   float* rfac = xss + G * 32;                        // [32] rinv / c
   float* red = rfac + 32;                            // [16][32] sums of squares
   float* cl = red + 16 * 32;                         // [32] c
-  float* red2 = (float*)smem;                        // [8 waves][2 tiles][32][RS] after the MFMAs
+  float* red2 = (float*)smem;                        // [8 waves][2 tiles][RH][RS] after the MFMAs
 
-  // 1. the small L2-resident loads: thread t takes row t % 32, partial sums of
-  // squares t / 32 and t / 32 + 16, the two 32-column sums of group t / 32,
-  // and c (all unconditional, clamped, masked after the wait)
+  // 1. the small L2-resident loads: thread t takes row t % 32 (clamped to the
+  // work-group's rows), partial sums of squares t / 32 and t / 32 + 16, the two
+  // 32-column sums of group t / 32, and c (unconditional, masked after the wait)
   const int np = K >> 5;  // 32-column partial sums per row (<= 32)
   const int r32 = threadIdx.x & 31, q16 = threadIdx.x >> 5;
   const float* ss_in = ss_arg + (int64_t)mt * K;
   const float* xsp = xs_part + (int64_t)mt * K;
   const int rr = min(r32, M - 1), gx = min(q16, G - 1);
-  const float sv0 = ss_in[min(q16, np - 1) * 32 + r32];
-  const float sv1 = ss_in[min(q16 + 16, np - 1) * 32 + r32];
-  const float xp0 = xsp[(2 * gx) * 32 + rr], xp1 = xsp[(2 * gx + 1) * 32 + rr];
+  const float sv0 = ss_in[min(q16, np - 1) * 32 + tr0 + rr];
+  const float sv1 = ss_in[min(q16 + 16, np - 1) * 32 + tr0 + rr];
+  const float xp0 = xsp[(2 * gx) * 32 + tr0 + rr], xp1 = xsp[(2 * gx + 1) * 32 + tr0 + rr];
   const float c_in = sc_in[m0 + rr];
   // 2. this wave's weights (both tiles; issued before the activation so that
   // their HBM latency starts first)
@@ -795,12 +807,12 @@ __global__ __launch_bounds__(512) void skinny_gu_kernel(
   // 3. the activation into LDS: 1 KiB chunks (plane, row, piece), 16 B a lane;
   // rows past M repeat row M - 1 (their results are never stored)
 #pragma unroll
-  for (int i = 0; i < 2 * 32 * CPR / 8; ++i) {
-    const int ch = wave + 8 * i, pl = ch / (32 * CPR), r = (ch / CPR) & 31, q = ch % CPR;
+  for (int i = 0; i < 2 * RH * CPR / 8; ++i) {
+    const int ch = wave + 8 * i, pl = ch / (RH * CPR), r = (ch / CPR) % RH, q = ch % CPR;
     const uint16_t* src = planes + ((int64_t)pl * M_all + m0 + min(r, M - 1)) * K + q * 512 + lane * 8;
     __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)src,
                                      (__attribute__((address_space(3))) void*)(
-                                         act + (pl * 32 + r) * ROW + q * 512),
+                                         act + (pl * RH + r) * ROW + q * 512),
                                      16, 0, 0);
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -818,9 +830,10 @@ __global__ __launch_bounds__(512) void skinny_gu_kernel(
     if (a.pre_sc_out && blockIdx.x == 0 && (int)threadIdx.x < M)
       a.pre_sc_out[m0 + threadIdx.x] = pre_scale_of(ri);
   }
-  // 4. this wave's units, each A fragment read once for both tiles
+  // 4. this wave's units, each A fragment read once for both tiles (MFMA rows
+  // 16-31 read rows 0-15 again)
   f32x16 acc_g = f32x16{}, acc_u = f32x16{};
-  const _Float16* arow = (const _Float16*)act + (lane & 31) * ROW + 32 * (lane >> 5);
+  const _Float16* arow = (const _Float16*)act + ((lane & 31) % RH) * ROW + 32 * (lane >> 5);
 #pragma unroll
   for (int j = 0; j < UPW; ++j) {
     const int g = wave * UPW + j;
@@ -828,7 +841,7 @@ __global__ __launch_bounds__(512) void skinny_gu_kernel(
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       af[t] = *(const f16x8*)(arow + g * 64 + 8 * t);
-      afl[t] = *(const f16x8*)(arow + 32 * ROW + g * 64 + 8 * t);
+      afl[t] = *(const f16x8*)(arow + RH * ROW + g * 64 + 8 * t);
     }
     float xsr[16];
     load_row_sums(xss + g * 32, lane, xsr);
@@ -836,26 +849,27 @@ __global__ __launch_bounds__(512) void skinny_gu_kernel(
     q4_group_mma1(acc_u, af, afl, xsr, wu[j], su[j]);
   }
   __syncthreads();  // every wave is done with the activation; rfac is written
+  // accumulators 0-7 hold rows 0-15 (mfma_row < 16)
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
+  for (int r = 0; r < 8; ++r) {
     const int row = mfma_row(r, lane);
-    red2[((wave * 2 + 0) * 32 + row) * RS + (lane & 31)] = acc_g[r];
-    red2[((wave * 2 + 1) * 32 + row) * RS + (lane & 31)] = acc_u[r];
+    red2[((wave * 2 + 0) * RH + row) * RS + (lane & 31)] = acc_g[r];
+    red2[((wave * 2 + 1) * RH + row) * RS + (lane & 31)] = acc_u[r];
   }
   __syncthreads();
-  // 5. SwiGLU: thread t < 256 takes row t / 8, outputs 4 (t % 8) .. + 3 of the
+  // 5. SwiGLU: thread t < 128 takes row t / 8, outputs 4 (t % 8) .. + 3 of the
   // pair, the 8 waves' tiles added in wave order and scaled by the row's
   // factor; an 8-column ACT_F16P chunk (order 0,4,1,5,2,6,3,7) is two threads'
   // halves, paired by a lane exchange (the even thread stores words 0-1, the
   // odd one words 2-3; rows past M compute and exchange, then store nothing)
-  if (threadIdx.x >= 256) return;
+  if (threadIdx.x >= 8 * RH) return;
   const int m = threadIdx.x >> 3, q = threadIdx.x & 7;
-  f32x4 gs = *(const f32x4*)(red2 + (0 * 32 + m) * RS + 4 * q);
-  f32x4 us = *(const f32x4*)(red2 + (1 * 32 + m) * RS + 4 * q);
+  f32x4 gs = *(const f32x4*)(red2 + (0 * RH + m) * RS + 4 * q);
+  f32x4 us = *(const f32x4*)(red2 + (1 * RH + m) * RS + 4 * q);
 #pragma unroll
   for (int w = 1; w < 8; ++w) {
-    gs += *(const f32x4*)(red2 + ((w * 2 + 0) * 32 + m) * RS + 4 * q);
-    us += *(const f32x4*)(red2 + ((w * 2 + 1) * 32 + m) * RS + 4 * q);
+    gs += *(const f32x4*)(red2 + ((w * 2 + 0) * RH + m) * RS + 4 * q);
+    us += *(const f32x4*)(red2 + ((w * 2 + 1) * RH + m) * RS + 4 * q);
   }
   const float f = rfac[m];
   _Float16 hh[4], ll[4];
@@ -889,7 +903,7 @@ __global__ __launch_bounds__(512) void skinny_gu_kernel(
   *(uint2*)(dst + (int64_t)M_all * F) = wl;
   if (over) raise_range(a);
 }
-#define SK_GU_LDS(G) (2 * 32 * ((G) * 64 + 8) * 2 + ((G) * 32 + 32 + 16 * 32 + 32) * 4)
+#define SK_GU_LDS(G) (gu_region_bytes(G) + ((G) * 32 + 32 + 16 * 32 + 32) * 4)
 template __global__ void skinny_gu_kernel<8>(const uint32_t*, const uint32_t*, const uint16_t*,
                                              const float*, const float*, const float*, int*,
                                              uint32_t, uint32_t, const FusedArgs);
@@ -1032,7 +1046,7 @@ static bool skinny_launch(const FusedArgs& a, int kind, hipStream_t s) {
   if (kind == FL_SWIGLU && a.pre_sc_in && !bf && a.x_in == 0 && a.ss_in && a.N % 128 == 0 &&
       (a.K == 512 || a.K == 1024)) {
     // gate|up over the whole K (no split-K): 64-column work-groups of 8 waves
-    const dim3 grid((unsigned)(a.N / 64), MT);
+    const dim3 grid((unsigned)(a.N / 64), 2 * MT);  // 16-row halves of the row tiles
 #define DRT_GU(GG)                                                                         \
   {                                                                                        \
     auto fn = skinny_gu_kernel<GG>;                                                        \

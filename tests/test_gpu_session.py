@@ -348,14 +348,15 @@ def test_dream_real_shapes_window():
     rt.close()
 
 
-@pytest.mark.parametrize("hidden", [256, 1024])
+@pytest.mark.parametrize("hidden", [256, 512, 1024])
 def test_dream_block_threshold_exact_kv(hidden):
     """Dream's block-threshold policy on the device session: prompt-relative
     8-row blocks over the exact K/V of the prompt and the frozen blocks, the
     logits shift's feeder row, the MASK column left out of the scoring. The LM
     head's MASK row is set to 4x the row of the first frontier row's top token,
     so MASK would win that row if it were scored. (Hidden size 1024 takes the
-    persistent q4 LM head, 256 the chunked one.)"""
+    persistent q4 LM head, 256 the chunked one; 512 and 1024 take the whole-K
+    gate|up kernel at K = 512 and 1024.)"""
     from diffusorrt_amd import decode
     from diffusorrt_amd import synthetic as syn
     from diffusorrt_amd.runtime import Runtime, block_threshold_session_config
