@@ -30,6 +30,31 @@ DRT_DEV void q4_group_mma1(f32x16& acc, const f16x8 (&a)[4], const f16x8 (&al)[4
   for (int r = 0; r < 16; ++r) acc[r] = fmaf(s, c[r], fmaf(b, xsr[r], acc[r]));
 }
 
+// q4_group_mma1 for at most 16 rows, their hi and lo halves stacked as the 32
+// rows of one MFMA: a holds this lane's fragment of row lane & 31, which is hi
+// row lane & 15 for lanes with bit 4 clear and its lo row otherwise, so result
+// rows r and r + 16 (accumulators i and i + 8) are the hi and lo products of
+// row r and half the MFMAs do the work. acc[i] (i < 8) is row mfma_row(i, lane);
+// xsr the group sums (hi + lo) in accumulator order.
+DRT_DEV void q4_group_mma_hl(float (&acc)[8], const f16x8 (&a)[4], const float (&xsr)[16],
+                             const u32x4 w, const uint32_t sbv) {
+  f32x16 c = f32x16{};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t wt = w[t];
+    u32x4 bw;
+    bw[0] = q4_pair_to_f16((wt >> 0) & 0x000F000Fu);
+    bw[1] = q4_pair_to_f16((wt >> 4) & 0x000F000Fu);
+    bw[2] = q4_pair_to_f16((wt >> 8) & 0x000F000Fu);
+    bw[3] = q4_pair_to_f16((wt >> 12) & 0x000F000Fu);
+    c = mfma_f16(a[t], __builtin_bit_cast(f16x8, bw), c);
+  }
+  const float s = bf16_bits_to_float(sbv & 0xffffu);
+  const float b = bf16_bits_to_float(sbv >> 16);
+#pragma unroll
+  for (int r = 0; r < 8; ++r) acc[r] = fmaf(s, c[r] + c[r + 8], fmaf(b, xsr[r], acc[r]));
+}
+
 // v[l] + v[l ^ 32] on every lane (gfx950 v_permlane32_swap, no LDS trip); both
 // lanes of a pair add the same two operands in the same order.
 DRT_DEV float sum_xor32(float v) {

@@ -738,8 +738,8 @@ __global__ __launch_bounds__(256) void skinny_narrow_kernel(
 // work-group (p = 2b + i, 16-row half h of a row tile) owns that pair for 16
 // rows. Its activation slice (16 rows x K, hi and lo planes) goes into LDS by
 // direct-to-LDS loads; wave w of 8 takes the 64-k units G/8 w .. + G/8 - 1 of
-// both tiles (one read of the A fragments feeds the gate and the up MFMAs; the
-// MFMA's rows 16-31 repeat rows 0-15 and are dropped); the waves' tiles are
+// both tiles (one read of the A fragments feeds the gate and the up MFMAs, the
+// 16 rows' hi and lo planes stacked as the MFMA's 32 rows); the waves' tiles are
 // added in LDS in wave order and SwiGLU runs on the sums. No partial tiles,
 // arrival counters or last work-group, whose round trips cost more than every
 // work-group staging all of K; 16-row halves halve that staging and keep two
@@ -830,26 +830,24 @@ __global__ __launch_bounds__(512) void skinny_gu_kernel(
     if (a.pre_sc_out && blockIdx.x == 0 && (int)threadIdx.x < M)
       a.pre_sc_out[m0 + threadIdx.x] = pre_scale_of(ri);
   }
-  // 4. this wave's units, each A fragment read once for both tiles (MFMA rows
-  // 16-31 read rows 0-15 again)
-  f32x16 acc_g = f32x16{}, acc_u = f32x16{};
-  const _Float16* arow = (const _Float16*)act + ((lane & 31) % RH) * ROW + 32 * (lane >> 5);
+  // 4. this wave's units, each A fragment read once for both tiles: LDS rows
+  // 0-15 are the hi plane and 16-31 the lo plane, the MFMA's 32 rows
+  static_assert(RH == 16, "hi and lo planes of 16 rows fill the MFMA's 32 rows");
+  float acc_g[8] = {}, acc_u[8] = {};
+  const _Float16* arow = (const _Float16*)act + (lane & 31) * ROW + 32 * (lane >> 5);
 #pragma unroll
   for (int j = 0; j < UPW; ++j) {
     const int g = wave * UPW + j;
-    f16x8 af[4], afl[4];
+    f16x8 af[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      af[t] = *(const f16x8*)(arow + g * 64 + 8 * t);
-      afl[t] = *(const f16x8*)(arow + RH * ROW + g * 64 + 8 * t);
-    }
+    for (int t = 0; t < 4; ++t) af[t] = *(const f16x8*)(arow + g * 64 + 8 * t);
     float xsr[16];
     load_row_sums(xss + g * 32, lane, xsr);
-    q4_group_mma1(acc_g, af, afl, xsr, wg[j], sg[j]);
-    q4_group_mma1(acc_u, af, afl, xsr, wu[j], su[j]);
+    q4_group_mma_hl(acc_g, af, xsr, wg[j], sg[j]);
+    q4_group_mma_hl(acc_u, af, xsr, wu[j], su[j]);
   }
   __syncthreads();  // every wave is done with the activation; rfac is written
-  // accumulators 0-7 hold rows 0-15 (mfma_row < 16)
+  // accumulator i < 8 holds row mfma_row(i, lane) < 16
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
     const int row = mfma_row(r, lane);
