@@ -81,9 +81,8 @@ DRT_DEV void lds_read16(f16x8& v, uint32_t addr) {
 }  // namespace
 
 struct BgTail {
-  int full = 0;            // whole tiles (tile t = work-group t)
+  int full = 0;            // whole tiles (the first work-groups, dealt in XCD runs)
   int kt = 0;              // K slices per remaining tile (0: the three-dimensional grid)
-  int tx = 0;              // tiles per row of tiles (tile t: column t % tx, row t / tx)
   float* part = nullptr;   // [remaining tiles][kt][128 * 256] partial tiles
   int* count = nullptr;    // [remaining tiles] arrival counters, zero on entry and exit
 };
@@ -93,12 +92,30 @@ template <int EPI>
 __global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int KS, const BgTail tail) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int M = a.M, N = a.N, K = a.K, G = K >> 6;
-  int tile_x = blockIdx.x, tile_y = blockIdx.y, ks = blockIdx.z, tail_idx = -1;
+  // Tiles t = y + MT (x + NX z) (row tile y fastest), dealt to the XCDs in
+  // contiguous runs: work-group b runs on XCD b % 8 and takes tile
+  // (b % 8) * T8 / 8 + b / 8 (the last T - T8 tiles as they come), so an XCD's
+  // L2 holds whole columns of row tiles: each weight tile is fetched by one XCD,
+  // and a K slice of a split-K grid whose tiles fill an XCD's run stays on it.
+  const int MT = (M + BG_WM - 1) / BG_WM, NX = (N + BG_WN - 1) / BG_WN;
+  auto xcd_run = [](int b, int T) {
+    const int T8 = T & ~7;
+    return b < T8 ? (b & 7) * (T8 >> 3) + (b >> 3) : b;
+  };
+  int tile_x, tile_y, ks, tail_idx = -1;
+  {
+    const int T = (int)(gridDim.x * gridDim.y * gridDim.z);
+    const int t = xcd_run((int)(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)), T);
+    tile_y = t % MT;
+    tile_x = (t / MT) % NX;
+    ks = t / (MT * NX);
+  }
   if (EPI == EPI_SWIGLU && tail.kt) {
-    // work-group b: tile b, or K slice of a remaining tile; the slices of one
-    // remaining tile share b % 8, i.e. one XCD (full % 8 == 0)
+    // work-group b: tile b (the first full tiles in XCD runs), or K slice of a
+    // remaining tile; the slices of one remaining tile share b % 8, i.e. one
+    // XCD (full % 8 == 0)
     const int b = blockIdx.x;
-    int t = b;
+    int t = xcd_run(b, tail.full);
     ks = 0;
     KS = 1;
     if (b >= tail.full) {
@@ -115,8 +132,8 @@ __global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int K
           __hip_atomic_fetch_or(a.placement_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-    tile_x = t % tail.tx;
-    tile_y = t / tail.tx;
+    tile_y = t % MT;
+    tile_x = t / MT;
   }
   const int n0 = tile_x * BG_WN, m0 = tile_y * BG_WM;
   const int g_lo = (int)((int64_t)G * ks / KS), g_hi = (int)((int64_t)G * (ks + 1) / KS);
@@ -425,7 +442,6 @@ void big_linear(const FusedArgs& a, int kind, int KS, hipStream_t s, float* tail
     if (need && need <= tail_part_floats && T - T / S * S <= n_tail_count) {
       tail.full = T / S * S;
       tail.kt = std::min(BG_TAIL_KT_MAX, std::min(S / (T - tail.full), a.K / 64));
-      tail.tx = (int)grid.x;
       tail.part = tail_part;
       tail.count = tail_count;
       grid = dim3((unsigned)(tail.full + (T - tail.full) * tail.kt), 1, 1);
