@@ -404,8 +404,11 @@ namespace drt {
 int big_linear_splits(int M, int N, int K, int max_ks) {
   const int tiles = ((M + BG_WM - 1) / BG_WM) * ((N + BG_WN - 1) / BG_WN);
   if (tiles >= 384) return 1;
-  int ks = std::min(max_ks, (448 + tiles - 1) / tiles);
-  ks = std::min(ks, std::max(1, (K / 64) / 8));
+  // the most slices that keep the grid within one round of two work-groups per
+  // CU (512 slots on 256 CUs: a CU holding two work-groups while others hold one
+  // sets the time), each slice at least 6 groups of 64 k
+  int ks = std::min(max_ks, std::max(1, 512 / tiles));
+  ks = std::min(ks, std::max(1, (K / 64) / 6));
   return std::max(1, ks);
 }
 
@@ -486,7 +489,7 @@ void big_qkv(const FusedArgs& a, float* part, size_t part_floats, hipStream_t s)
 }
 
 void qkv_epilogue_slices(const FusedArgs& a, const float* part, int ks, hipStream_t s) {
-  require(ks >= 1 && ks <= BG_QKV_MAX_KS && a.N % 128 == 0, "q|k|v epilogue: 1..4 slices");
+  require(ks >= 1 && ks <= BG_QKV_MAX_KS && a.N % 128 == 0, "q|k|v epilogue: 1..8 slices");
   const dim3 grid(a.N / 128, (a.M + 31) / 32);
   if (a.kv_bf16)
     hipLaunchKernelGGL(big_qkv_epilogue_kernel<__bf16>, grid, dim3(256), 0, s, a, part, ks);

@@ -133,39 +133,45 @@ extern "C" __global__ __launch_bounds__(256) void embed_kernel(
   }
 }
 
-// One wave per output row (4 rows per 256-thread work-group). Lane l owns the
-// 8-element chunks l, l + 64, ... of the row (d % 64 == 0, d <= 4096), loaded
-// and stored 16 bytes at a time; the 8 chunks of a 64-wide group are 8
-// consecutive lanes.
+// WPR waves per output row (4 / WPR rows per 256-thread work-group). Wave w of
+// a row owns the 8-element chunks of lanes l + 64 (w + WPR j) of the row
+// (d % 64 == 0, d <= 4096), loaded and stored 16 bytes at a time; the 8 chunks
+// of a 64-wide group are 8 consecutive lanes. One wave per row suits d <= 1024
+// (every chunk's loads in flight at once); four waves per row split the chunks
+// of wider rows so that theirs are too, and add the row's sum of squares in LDS.
 //   src row  = src_rows ? src_rows[i] : i
 //   v        = hidden[src] + R(sum_s part[s][src])          (part may be null)
 //   hidden_out[src] = v                                     (if write_hidden)
 //   act[i]   = fmt(v * rsqrt(mean(v^2) + eps) * w)          (if norm_w non-null)
 // (backends/mlx_ops.py:21-35 for the norm; R rounds to bf16 when rnd_bf16.)
-constexpr int RN_MAX_SPLITS = 8;  // partial slices a reduce takes
+constexpr int RN_MAX_SPLITS = 9;  // partial slices a reduce takes
 
-extern "C" __global__ __launch_bounds__(256) void residual_norm_kernel(
-    float* __restrict__ hidden, const float* __restrict__ part, int splits, int M_part,
-    int rnd_bf16, const int32_t* __restrict__ src_rows, int write_hidden,
-    const uint16_t* __restrict__ norm_w, float eps, int d, int fmt, void* __restrict__ act,
-    float* __restrict__ xsum, int n_rows, int* __restrict__ err) {
-  constexpr int NC = 8;  // chunks per lane for d <= 4096
-  const int lane = threadIdx.x & 63;
-  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (i >= n_rows) return;  // whole waves
+template <int WPR>
+DRT_DEV void residual_norm_rows(float* __restrict__ hidden, const float* __restrict__ part,
+                                int splits, int M_part, int rnd_bf16,
+                                const int32_t* __restrict__ src_rows, int write_hidden,
+                                const uint16_t* __restrict__ norm_w, float eps, int d, int fmt,
+                                void* __restrict__ act, float* __restrict__ xsum, int n_rows,
+                                int* __restrict__ err) {
+  constexpr int NC = 8 / WPR;  // chunks per lane for d <= 4096
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, w = wave % WPR;
+  const int i = blockIdx.x * (4 / WPR) + wave / WPR;
+  if (i >= n_rows) return;  // whole rows (with WPR = 4, the whole work-group)
   const int src = src_rows ? src_rows[i] : i;
+  // chunk j of this wave: lanes' 8-element chunks lane + 64 (w + WPR j)
+  auto kof = [&](int j) { return (lane + 64 * (w + WPR * j)) * 8; };
+  auto has = [&](int j) { return 512 * (w + WPR * j) < d; };  // uniform across the wave
   // Every load is issued before the first store: a wait for a load also waits
-  // for the stores issued before it. Chunk c exists where 512 c < d (uniform
-  // across the wave); within a last, partial chunk the addresses are clamped
-  // and the lanes past d are zeroed.
+  // for the stores issued before it. Within a last, partial chunk the
+  // addresses are clamped and the lanes past d are zeroed.
   f32x4 v[NC][2];
   u32x4 wv[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     v[c][0] = v[c][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     wv[c] = u32x4{0u, 0u, 0u, 0u};
-    if (512 * c < d) {
-      const int k = min((lane + 64 * c) * 8, d - 8);
+    if (has(c)) {
+      const int k = min(kof(c), d - 8);
       const f32x4* hp = (const f32x4*)(hidden + (int64_t)src * d + k);
       v[c][0] = hp[0];
       v[c][1] = hp[1];
@@ -174,13 +180,13 @@ extern "C" __global__ __launch_bounds__(256) void residual_norm_kernel(
   if (norm_w) {
 #pragma unroll
     for (int c = 0; c < NC; ++c)
-      if (512 * c < d) wv[c] = *(const u32x4*)(norm_w + min((lane + 64 * c) * 8, d - 8));
+      if (has(c)) wv[c] = *(const u32x4*)(norm_w + min(kof(c), d - 8));
   }
   if (part) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      if (512 * c < d) {
-        const int k = min((lane + 64 * c) * 8, d - 8);
+      if (has(c)) {
+        const int k = min(kof(c), d - 8);
         // every slice's loads are issued before the first add (one latency)
         f32x4 ps[RN_MAX_SPLITS][2];
 #pragma unroll
@@ -212,11 +218,11 @@ extern "C" __global__ __launch_bounds__(256) void residual_norm_kernel(
   }
 #pragma unroll
   for (int c = 0; c < NC; ++c)
-    if ((lane + 64 * c) * 8 >= d) v[c][0] = v[c][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (kof(c) >= d) v[c][0] = v[c][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   if (part && write_hidden) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const int k = (lane + 64 * c) * 8;
+      const int k = kof(c);
       if (k < d) {
         f32x4* hp = (f32x4*)(hidden + (int64_t)src * d + k);
         hp[0] = v[c][0];
@@ -224,16 +230,25 @@ extern "C" __global__ __launch_bounds__(256) void residual_norm_kernel(
       }
     }
   }
-  if (!norm_w) return;
+  if (!norm_w) return;  // (uniform across the work-group)
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < NC; ++c)
 #pragma unroll
     for (int e = 0; e < 4; ++e) ss += v[c][0][e] * v[c][0][e] + v[c][1][e] * v[c][1][e];
-  const float inv = 1.f / sqrtf(wave_sum(ss) / (float)d + eps);
+  ss = wave_sum(ss);
+  if (WPR > 1) {  // the row's waves in wave order
+    __shared__ float rsum[4];
+    if (lane == 0) rsum[wave] = ss;
+    __syncthreads();
+    ss = rsum[0];
+#pragma unroll
+    for (int q = 1; q < WPR; ++q) ss += rsum[q];
+  }
+  const float inv = 1.f / sqrtf(ss / (float)d + eps);
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    const int k = (lane + 64 * c) * 8;
+    const int k = kof(c);
     if (k >= d) break;  // uniform across each 8-lane group (d % 64 == 0)
     float n[8];
 #pragma unroll
@@ -275,6 +290,21 @@ extern "C" __global__ __launch_bounds__(256) void residual_norm_kernel(
     }
   }
 }
+
+#define DRT_RN_ARGS                                                                            \
+  float *__restrict__ hidden, const float *__restrict__ part, int splits, int M_part,            \
+      int rnd_bf16, const int32_t *__restrict__ src_rows, int write_hidden,                     \
+      const uint16_t *__restrict__ norm_w, float eps, int d, int fmt, void *__restrict__ act,   \
+      float *__restrict__ xsum, int n_rows, int *__restrict__ err
+extern "C" __global__ __launch_bounds__(256) void residual_norm_kernel(DRT_RN_ARGS) {
+  residual_norm_rows<1>(hidden, part, splits, M_part, rnd_bf16, src_rows, write_hidden, norm_w,
+                        eps, d, fmt, act, xsum, n_rows, err);
+}
+extern "C" __global__ __launch_bounds__(256) void residual_norm_wide_kernel(DRT_RN_ARGS) {
+  residual_norm_rows<4>(hidden, part, splits, M_part, rnd_bf16, src_rows, write_hidden, norm_w,
+                        eps, d, fmt, act, xsum, n_rows, err);
+}
+#undef DRT_RN_ARGS
 
 // ---- per-op kernels for the KernelTable seam (fp32 tensors) ----
 
@@ -343,11 +373,16 @@ void residual_norm(float* hidden, const float* part, int splits, int M_part, boo
                    int d, int fmt, void* act, float* xsum, int n_out_rows, hipStream_t s,
                    int* err) {
   require(d % 64 == 0 && d <= 4096, "residual_norm needs d % 64 == 0 and d <= 4096");
-  require(!part || (splits >= 1 && splits <= RN_MAX_SPLITS), "residual_norm takes 1..8 slices");
+  require(!part || (splits >= 1 && splits <= RN_MAX_SPLITS), "residual_norm takes 1..9 slices");
   if (n_out_rows <= 0) return;
-  hipLaunchKernelGGL(residual_norm_kernel, dim3((n_out_rows + 3) / 4), dim3(256), 0, s, hidden,
-                     part, splits, M_part, (int)rnd_bf16, src_rows, (int)write_hidden, norm_w, eps,
-                     d, fmt, act, xsum, n_out_rows, err);
+  if (d > 1024)  // one row per work-group, its chunks over four waves
+    hipLaunchKernelGGL(residual_norm_wide_kernel, dim3(n_out_rows), dim3(256), 0, s, hidden, part,
+                       splits, M_part, (int)rnd_bf16, src_rows, (int)write_hidden, norm_w, eps, d,
+                       fmt, act, xsum, n_out_rows, err);
+  else
+    hipLaunchKernelGGL(residual_norm_kernel, dim3((n_out_rows + 3) / 4), dim3(256), 0, s, hidden,
+                       part, splits, M_part, (int)rnd_bf16, src_rows, (int)write_hidden, norm_w,
+                       eps, d, fmt, act, xsum, n_out_rows, err);
   DRT_HIP(hipGetLastError());
 }
 

@@ -121,8 +121,9 @@ void big_qkv(const FusedArgs& a, float* part, size_t part_floats, hipStream_t s)
 // The per-head q|k|v epilogue (bias, q/k norm, RoPE, Q out, K/V into the cache)
 // of a projection given as ks <= BG_QKV_MAX_KS fp32 slices [ks][M][N].
 void qkv_epilogue_slices(const FusedArgs& a, const float* part, int ks, hipStream_t s);
-constexpr int BG_QKV_MAX_KS = 4;    // split-K slices of the q|k|v projection
-constexpr int BG_RESID_MAX_KS = 8;  // ... of o_proj / down_proj (reduced with the next norm)
+constexpr int BG_QKV_MAX_KS = 8;    // split-K slices of the q|k|v projection
+constexpr int BG_RESID_MAX_KS = 9;  // ... of o_proj / down_proj (reduced with the next norm)
+constexpr int ST_QKV_MAX_KS = 4;    // ... of the weight-streaming q|k|v projection
 constexpr int BG_OP_MAX_KS = 8;     // ... of the per-op linear (summed into its output)
 // Weight-streaming q4 linears (stream_linear.hip) for M <= 32 rows and at least
 // STREAM_MIN_WEIGHTS weights: the activation's K slice in LDS, the weights of a

@@ -464,7 +464,7 @@ std::shared_ptr<Runtime> create_runtime(const drt_engine_config& e, const drt_mo
       size_t bf = 0;
       if (rt->streaming) {
         const int rows = std::min(M, 32);
-        bf = std::max({stream_part_floats(rows, n_qkv, d, BG_QKV_MAX_KS),
+        bf = std::max({stream_part_floats(rows, n_qkv, d, ST_QKV_MAX_KS),
                        stream_part_floats(rows, d, Hq * hd, BG_RESID_MAX_KS),
                        stream_part_floats(rows, 2 * F, d, 8),
                        stream_part_floats(rows, d, F, BG_RESID_MAX_KS)});
@@ -808,7 +808,7 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
         f.act = rt.act.p;
         big_qkv(f, bpart, rt.big_part_floats, s);
       } else if (stream) {  // normed from the residual stream while staged
-        qkv_epilogue_slices(f, bpart, slices(f, BG_QKV_MAX_KS), s);
+        qkv_epilogue_slices(f, bpart, slices(f, ST_QKV_MAX_KS), s);
       } else {
         fused_linear(f, FL_QKV, s);
       }

@@ -486,6 +486,7 @@ namespace drt {
 
 namespace {
 constexpr int ST_SINGLE_MAX_NBLK = 5, ST_PREF_MAX_NBLK = 2;
+constexpr int ST_MAX_KS = 8;  // K slices the slice reductions take
 // activation chunk (hi, lo), group sums and row factors; the halves' final sums
 // (NBLK x 16 KiB) reuse it
 size_t st_lds(int ch) {
@@ -524,7 +525,7 @@ StreamPlan stream_plan(int M, int N, int K, int max_ks) {
   if (!stream_supported(M, N, K)) return best;
   const int G = K / 64, NB = N / 128, n_cu = n_cu_of_current_device();
   int64_t best_cost = -1;
-  for (int ks = 1; ks <= std::min(max_ks, G); ++ks) {
+  for (int ks = 1; ks <= std::min({max_ks, G, ST_MAX_KS}); ++ks) {
     const int ng = (G + ks - 1) / ks;
     const bool single = ng <= 16;
     const int max_nblk = single ? ST_SINGLE_MAX_NBLK : ST_PREF_MAX_NBLK;
