@@ -784,80 +784,97 @@ __global__ __launch_bounds__(256) void attn_decode_combine_kernel(
 }
 
 // Combine key splits (statistics in the base-2 units of attn_split_kernel).
-// One wave per (row, head); lane holds hd = lane, lane + 64.
-// The split statistics are loaded across lanes (split s by lane s), the weights
-// broadcast by shuffles, and every partial-O load is independent, so the
-// combine costs one memory latency, not one per split. n_splits <= 64.
+// Sixteen threads per (row, head), thread c holding head dims 8c .. 8c + 7: it
+// loads the (m, l) pair and its 32 bytes of O of up to 8 splits at once (one
+// memory latency per 8 splits; their partial O are added against the batch's
+// running maximum) and stores its 8 outputs as 16-byte chunks.
 // out_fmt: 0 = ACT_F16P (+ xsum), 1 = ACT_BF16, 2 = fp32 plain, 3 = bf16 plain.
-extern "C" __global__ void attn_combine_kernel(const float* __restrict__ o_part,
-                                               const float* __restrict__ ml_part, int n_splits,
-                                               int n_rows, int Hq, int Hkv, void* __restrict__ out,
-                                               float* __restrict__ xsum, int out_fmt,
-                                               int* __restrict__ err) {
-  const int lane = threadIdx.x & 63;
-  const int64_t wid = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
-  if (wid >= (int64_t)n_rows * Hq) return;
+extern "C" __global__ __launch_bounds__(256) void attn_combine_kernel(
+    const float* __restrict__ o_part, const float* __restrict__ ml_part, int n_splits, int n_rows,
+    int Hq, int Hkv, void* __restrict__ out, float* __restrict__ xsum, int out_fmt,
+    int* __restrict__ err) {
+  constexpr int SB = 8;  // splits per batch of loads
+  const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  const int64_t n_wid = (int64_t)n_rows * Hq;
+  if ((t >> 4) >= n_wid) return;  // whole groups of 16 (n_wid * 16 threads)
+  const int64_t wid = t >> 4;
+  const int ch = (int)(t & 15);
   const int row = (int)(wid / Hq), head = (int)(wid % Hq);
   const int G = Hq / Hkv;
   const int kvh = head / G, qv = row * G + (head - kvh * G);
   const int n_qv = n_rows * G;
   const int64_t stride = (int64_t)Hkv * n_qv;  // between splits
   const int64_t idx0 = (int64_t)kvh * n_qv + qv;
-  float ms = -INFINITY, ls = 0.f;
-  if (lane < n_splits) {
-    ms = ml_part[(idx0 + lane * stride) * 2];
-    ls = ml_part[(idx0 + lane * stride) * 2 + 1];
-  }
-  const float mmax = wave_max(ms);
-  const float w = (ms == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms - mmax);
-  const float lsum = wave_sum(w * ls);
-  float a0 = 0.f, a1 = 0.f;
-  for (int s0 = 0; s0 < n_splits; s0 += 16) {
-    float p0[16], p1[16], ws[16];
+  float M = -INFINITY, L = 0.f;
+  f32x4 a0 = f32x4{0.f, 0.f, 0.f, 0.f}, a1 = a0;
+  for (int s0 = 0; s0 < n_splits; s0 += SB) {
+    float2 ml[SB];
+    f32x4 p0[SB], p1[SB];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int sp = s0 + j;
-      ws[j] = __shfl(w, sp & 63, 64);
-      const int64_t base = (idx0 + (int64_t)min(sp, n_splits - 1) * stride) * 128;
-      p0[j] = o_part[base + lane];
-      p1[j] = o_part[base + 64 + lane];
+    for (int j = 0; j < SB; ++j) {  // every load of the batch before the first use
+      const int64_t at = idx0 + (int64_t)min(s0 + j, n_splits - 1) * stride;
+      ml[j] = *(const float2*)(ml_part + at * 2);
+      p0[j] = *(const f32x4*)(o_part + at * 128 + 8 * ch);
+      p1[j] = *(const f32x4*)(o_part + at * 128 + 8 * ch + 4);
     }
+    float mb = M;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      if (s0 + j < n_splits) {
-        a0 += ws[j] * p0[j];
-        a1 += ws[j] * p1[j];
+    for (int j = 0; j < SB; ++j)
+      if (s0 + j < n_splits) mb = fmaxf(mb, ml[j].x);
+    const float sc = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - mb);
+    a0 *= sc;
+    a1 *= sc;
+    L *= sc;
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      if (s0 + j < n_splits && ml[j].x != -INFINITY) {
+        const float w = __builtin_amdgcn_exp2f(ml[j].x - mb);
+        a0 += w * p0[j];
+        a1 += w * p1[j];
+        L += w * ml[j].y;
       }
     }
+    M = mb;
   }
-  const float inv = 1.f / lsum;
-  const float v0 = a0 * inv, v1 = a1 * inv;
+  const float inv = 1.f / L;
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] = a0[e] * inv;
+    v[e + 4] = a1[e] * inv;
+  }
   const int D = Hq * 128;
-  const int c0 = head * 128 + lane, c1 = c0 + 64;
+  const int c0 = head * 128 + 8 * ch;  // first column of this thread's chunk
   if (out_fmt == 0) {  // ACT_F16P: hi plane, lo plane at + n_rows * D
-    _Float16* o = (_Float16*)out + (int64_t)row * D;
-    _Float16* ol = o + (int64_t)n_rows * D;
-    const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
-    const _Float16 l0 = f16_lo(v0, h0), l1 = f16_lo(v1, h1);
-    o[f16p_index(c0)] = h0;
-    o[f16p_index(c1)] = h1;
-    ol[f16p_index(c0)] = l0;
-    ol[f16p_index(c1)] = l1;
-    if (__ballot(f16_overflows(v0) || f16_overflows(v1)) && lane == 0 && err)
-      atomicOr(err, DRT_ERR_F16_RANGE);
-    const float s0 = wave_sum((float)h0 + (float)l0), s1 = wave_sum((float)h1 + (float)l1);
-    if (lane == 0) {
-      xsum[(int64_t)row * (D >> 6) + (c0 >> 6)] = s0;
-      xsum[(int64_t)row * (D >> 6) + (c0 >> 6) + 1] = s1;
+    _Float16 h[8], lo[8];
+    float gs = 0.f;
+    bool over = false;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const _Float16 he = (_Float16)v[e], le = f16_lo(v[e], he);
+      h[f16p_index(e)] = he;
+      lo[f16p_index(e)] = le;
+      gs += (float)he + (float)le;
+      over = over || f16_overflows(v[e]);
     }
+    _Float16* o = (_Float16*)out + (int64_t)row * D + c0;
+    *(u32x4*)o = __builtin_bit_cast(u32x4, h);
+    *(u32x4*)(o + (int64_t)n_rows * D) = __builtin_bit_cast(u32x4, lo);
+    if (over && err) atomicOr(err, DRT_ERR_F16_RANGE);
+    // the 64-column group sums: eight threads of aligned lanes per group
+    gs += __shfl_xor(gs, 1, 64);
+    gs += __shfl_xor(gs, 2, 64);
+    gs += __shfl_xor(gs, 4, 64);
+    if ((ch & 7) == 0) xsum[(int64_t)row * (D >> 6) + (c0 >> 6)] = gs;
   } else if (out_fmt == 1 || out_fmt == 3) {
-    uint16_t* o = (uint16_t*)out + (int64_t)row * D;
-    o[c0] = float_to_bf16_bits(v0);
-    o[c1] = float_to_bf16_bits(v1);
+    uint16_t hb[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) hb[e] = float_to_bf16_bits(v[e]);
+    *(u32x4*)((uint16_t*)out + (int64_t)row * D + c0) = __builtin_bit_cast(u32x4, hb);
   } else {
-    float* o = (float*)out + (int64_t)row * D;
-    o[c0] = v0;
-    o[c1] = v1;
+    float* o = (float*)out + (int64_t)row * D + c0;
+    *(f32x4*)o = f32x4{v[0], v[1], v[2], v[3]};
+    *(f32x4*)(o + 4) = f32x4{v[4], v[5], v[6], v[7]};
   }
 }
 
@@ -989,8 +1006,8 @@ void attention(bool bf16, const void* q, const void* kv_layer, int64_t kv_head_s
   }
 #undef DRT_ATTN
   DRT_HIP(hipGetLastError());
-  const int64_t waves = (int64_t)n_rows * Hq;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s,
+  const int64_t threads = (int64_t)n_rows * Hq * 16;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
                      o_part, ml_part, plan.splits, n_rows, Hq, Hkv, out, xsum, out_fmt, err);
   DRT_HIP(hipGetLastError());
 }
