@@ -218,16 +218,21 @@ __global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int K
     if (gb + 1 < n_g) step(gb + 1, Slot<1>{});
   }
   if (EPI == EPI_SWIGLU && tail_idx >= 0) {  // (the split last round is used for gate|up)
-    // a K slice of a remaining tile: store it, lane-major (value i of thread t
-    // at i * 256 + t), and let the last slice to arrive add them all in order
-    float* pt = tail.part + (size_t)tail_idx * tail.kt * (BG_WM * BG_WN);
-    float* mine = pt + (size_t)ks * (BG_WM * BG_WN) + threadIdx.x;
+    // a K slice of a remaining tile: store it as 16-byte chunks (chunk c = four
+    // consecutive accumulators of thread t at (c * 256 + t) * 4), and let the
+    // last slice to arrive add them all in slice order, two chunks of every
+    // slice in flight at a time
+    constexpr int TILE = BG_WM * BG_WN;
+    float* pt = tail.part + (size_t)tail_idx * tail.kt * TILE;
+    f32x4* mine = (f32x4*)(pt + (size_t)ks * TILE) + threadIdx.x;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mine[((i * 2 + j) * 16 + r) * 256] = acc[i][j][r];
+        for (int q = 0; q < 4; ++q)
+          mine[((i * 2 + j) * 4 + q) * 256] =
+              f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
     __shared__ int last_flag;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();  // every store of the work-group is in this XCD's L2
@@ -236,23 +241,28 @@ __global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int K
                                          __HIP_MEMORY_SCOPE_WORKGROUP) == tail.kt - 1;
     __syncthreads();
     if (!last_flag) return;
+    const f32x4* pv = (const f32x4*)pt + threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int c0 = 0; c0 < 32; c0 += 2) {
+      f32x4 v[2][BG_TAIL_KT_MAX];
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int at = ((i * 2 + j) * 16 + r) * 256 + threadIdx.x;
-          float v[BG_TAIL_KT_MAX];
+        for (int k = 0; k < BG_TAIL_KT_MAX; ++k)  // every slice's chunk loaded first
+          v[cc][k] = pv[(size_t)min(k, tail.kt - 1) * (TILE / 4) + (c0 + cc) * 256];
 #pragma unroll
-          for (int k = 0; k < BG_TAIL_KT_MAX; ++k)  // every slice's value loaded first
-            v[k] = pt[(size_t)min(k, tail.kt - 1) * (BG_WM * BG_WN) + at];
+      for (int cc = 0; cc < 2; ++cc) {
+        const int c = c0 + cc, i = c >> 3, j = (c >> 2) & 1, q = c & 3;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
           float sum = 0.f;
 #pragma unroll
           for (int k = 0; k < BG_TAIL_KT_MAX; ++k)
-            if (k < tail.kt) sum += k == ks ? acc[i][j][r] : v[k];
-          acc[i][j][r] = sum;
+            if (k < tail.kt) sum += k == ks ? acc[i][j][4 * q + e] : v[cc][k][e];
+          acc[i][j][4 * q + e] = sum;
         }
+      }
+    }
     if (threadIdx.x == 0) tail.count[tail_idx] = 0;
   }
   __syncthreads();  // every wave's last fragment reads are done: the epilogue reuses the LDS
