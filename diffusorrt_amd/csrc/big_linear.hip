@@ -71,11 +71,30 @@ DRT_DEV f16x8 dequant_q4_step(uint32_t wt, uint32_t sbv) {
   return __builtin_bit_cast(f16x8, o);
 }
 
+// dequant_q4_step with the group's scale and bias already in fp16 pairs and
+// the nibble mask in a register (one v_and_or_b32 per nibble pair)
+DRT_DEV f16x8 dequant_q4_step_sz(uint32_t wt, h2v s2, h2v z2, uint32_t mask) {
+  const h2v k2 = {(_Float16)-1024.f, (_Float16)-1024.f};
+  u32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const h2v h = __builtin_bit_cast(h2v, ((wt >> (4 * e)) & mask) | 0x64006400u);
+    o[e] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(h + k2, s2, z2));
+  }
+  return __builtin_bit_cast(f16x8, o);
+}
+
 // LDS fragment read the compiler does not see: a plain read after a
 // direct-to-LDS load makes it wait for every global load in flight first
 // (it cannot tell the group being read from the one being filled).
 DRT_DEV void lds_read16(f16x8& v, uint32_t addr) {
   asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+}
+// ... at a constant byte offset from addr (the instruction's offset field)
+template <int OFF>
+DRT_DEV void lds_read16o(f16x8& v, uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds_read offset field");
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
 }
 
 }  // namespace
@@ -90,7 +109,8 @@ constexpr int BG_TAIL_KT_MAX = 8;
 
 template <int EPI>
 __global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int KS, const BgTail tail) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: LDS bases in SGPRs
   const int M = a.M, N = a.N, K = a.K, G = K >> 6;
   // Tiles t = y + MT (x + NX z) (row tile y fastest), dealt to the XCDs in
   // contiguous runs: work-group b runs on XCD b % 8 and takes tile
@@ -150,21 +170,30 @@ __global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int K
   uint32_t wsb[2][2];
   // A of group g into buffer buf: plane pl, 8-row block blk = wave + 4i is one
   // wave instruction (lane l: row blk*8 + (l >> 3), LDS position l & 7, which
-  // holds the row's chunk (l & 7) ^ (row & 7)); rows past M re-read row M - 1,
-  // whose copies feed only outputs that are never stored.
+  // holds the row's chunk (l & 7) ^ (l >> 3)); rows past M re-read row M - 1,
+  // whose copies feed only outputs that are never stored. Addresses are a
+  // uniform base per group plus 32-bit lane offsets (activation < 4 GiB),
+  // recomputed at each issue (24-bit multiplies, from lane values made opaque
+  // there) instead of staying live across the loop.
+  const int row_l = m0 + wave * 8 + (lane >> 3);
+  const uint32_t col_l = (uint32_t)(((lane & 7) ^ (lane >> 3)) * 16);
+  const uint32_t K2 = (uint32_t)K * 2u;
+  const char* act_b = (const char*)act;
   auto issue = [&](int g, int buf, auto slot) {
     constexpr int S = decltype(slot)::value;
-    const int r_in = lane >> 3, c = (lane & 7) ^ (r_in & 7);
+    const char* ag = act_b + (size_t)g * 128;
+    int rl = row_l;
+    uint32_t cl = col_l;
+    asm volatile("" : "+v"(rl), "+v"(cl));
 #pragma unroll
     for (int pl = 0; pl < 2; ++pl)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int blk = wave + 4 * i;
-        const int m = min(m0 + blk * 8 + r_in, M - 1);
-        const _Float16* src = act + ((int64_t)pl * M + m) * K + g * 64 + c * 8;
-        char* dst = smem + buf * BG_BUF_BYTES + pl * BG_PLANE_BYTES + blk * 1024;
-        __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)src,
-                                         (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+        const uint32_t m = (uint32_t)(min(rl + 32 * i, M - 1) + pl * M);
+        char* dst = smem + buf * BG_BUF_BYTES + pl * BG_PLANE_BYTES + (wave + 4 * i) * 1024;
+        __builtin_amdgcn_global_load_lds(
+            (__attribute__((address_space(1))) void*)(ag + (__umul24(m, K2) + cl)),
+            (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
       }
     wq[S][0] = *q4_tile_words(a.qw, nt0, G, g, lane);
     wq[S][1] = *q4_tile_words(a.qw, nt1, G, g, lane);
@@ -176,46 +205,101 @@ __global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int K
 #pragma unroll
   for (int i = 0; i < 4; ++i) acc[i][0] = acc[i][1] = f32x16{};
 
-  if (n_g > 0) issue(g_lo, 0, Slot<0>{});
   // this lane's fragment row within each 32-row m-tile is lane & 31; its k
   // chunk at step t is 4 * (lane >> 5) + t, stored at position chunk ^ (row & 7)
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem + (lane & 31) * 128;
-
-  auto step = [&](int gi, auto slot) {
+  // one k step's operands (A hi and lo fragments, the two dequantised B
+  // fragments); steps alternate between two sets, the next step's read and
+  // dequantised while the current step's MFMAs run
+  struct Ops {
+    f16x8 h[4], l[4], b[2];
+  };
+  uint32_t nib_mask = 0x000F000Fu;
+  asm volatile("" : "+v"(nib_mask));  // in a register: v_and_or_b32 takes one constant
+  h2v gs2[2], gz2[2];                // the current group's scale and bias pairs
+  auto group_scales = [&](auto slot) {
     constexpr int S = decltype(slot)::value;
-    // group gi's loads (issued one step ago) are complete in every lane, and
-    // every wave is done reading the buffer that group gi + 1 overwrites
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __syncthreads();
-    if (gi + 1 < n_g) issue(g_lo + gi + 1, (gi + 1) & 1, Slot<(S + 1) % 2>{});
-    const uint32_t ab = lds0 + (gi & 1) * BG_BUF_BYTES;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const uint32_t pos = (uint32_t)(((4 * (lane >> 5) + t) ^ (lane & 7)) * 16);
-      f16x8 ah[4], al[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        lds_read16(ah[i], ab + i * 32 * 128 + pos);
-        lds_read16(al[i], ab + BG_PLANE_BYTES + i * 32 * 128 + pos);
-      }
-      const f16x8 b0 = dequant_q4_step(wq[S][0][t], wsb[S][0]);
-      const f16x8 b1 = dequant_q4_step(wq[S][1][t], wsb[S][1]);
-      asm volatile("s_waitcnt lgkmcnt(0)"
-                   : "+v"(ah[0]), "+v"(ah[1]), "+v"(ah[2]), "+v"(ah[3]), "+v"(al[0]),
-                     "+v"(al[1]), "+v"(al[2]), "+v"(al[3]));
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[i][0] = mfma_f16(ah[i], b0, acc[i][0]);
-        acc[i][1] = mfma_f16(ah[i], b1, acc[i][1]);
-        acc[i][0] = mfma_f16(al[i], b0, acc[i][0]);
-        acc[i][1] = mfma_f16(al[i], b1, acc[i][1]);
-      }
+    for (int j = 0; j < 2; ++j) {
+      const _Float16 sc = (_Float16)bf16_bits_to_float(wsb[S][j] & 0xffffu);
+      const _Float16 zb = (_Float16)bf16_bits_to_float(wsb[S][j] >> 16);
+      gs2[j] = h2v{sc, sc};
+      gz2[j] = h2v{zb, zb};
     }
   };
+  auto load_ops = [&](Ops& o, int buf, int t, auto slot) {
+    constexpr int S = decltype(slot)::value;
+    // m-tile i of the hi plane at + 4096 i, of the lo plane at + BG_PLANE_BYTES + 4096 i
+    const uint32_t ab =
+        lds0 + buf * BG_BUF_BYTES + (uint32_t)(((4 * (lane >> 5) + t) ^ (lane & 7)) * 16);
+    lds_read16o<0>(o.h[0], ab);
+    lds_read16o<BG_PLANE_BYTES>(o.l[0], ab);
+    lds_read16o<4096>(o.h[1], ab);
+    lds_read16o<BG_PLANE_BYTES + 4096>(o.l[1], ab);
+    lds_read16o<8192>(o.h[2], ab);
+    lds_read16o<BG_PLANE_BYTES + 8192>(o.l[2], ab);
+    lds_read16o<12288>(o.h[3], ab);
+    lds_read16o<BG_PLANE_BYTES + 12288>(o.l[3], ab);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) o.b[j] = dequant_q4_step_sz(wq[S][j][t], gs2[j], gz2[j], nib_mask);
+  };
+  auto lds_wait = [](Ops& o) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(o.h[0]), "+v"(o.h[1]), "+v"(o.h[2]), "+v"(o.h[3]), "+v"(o.l[0]),
+                   "+v"(o.l[1]), "+v"(o.l[2]), "+v"(o.l[3]));
+  };
+  Ops X, Y;
+  if (n_g > 0) {
+    issue(g_lo, 0, Slot<0>{});
+    if (n_g > 1) issue(g_lo + 1, 1, Slot<1>{});
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();                     // group g_lo is in LDS in every wave
+    group_scales(Slot<0>{});
+    load_ops(X, 0, 0, Slot<0>{});
+    lds_wait(X);
+  }
+  // k step t of group gi (buffer and B slot S = gi & 1) on `cur`, the next
+  // step's operands into `nxt`; at the last step, once group gi + 1 is in LDS
+  // in every wave (and every wave is done with buffer S), group gi + 2 is
+  // issued into buffer and slot S
+  auto kstep = [&](Ops& cur, Ops& nxt, int gi, int t, auto slot) {
+    constexpr int S = decltype(slot)::value;
+    bool more = true;
+    if (t < 3) {
+      load_ops(nxt, S, t + 1, Slot<S>{});
+    } else if (gi + 1 < n_g) {
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      __syncthreads();
+      if (gi + 2 < n_g) issue(g_lo + gi + 2, S, Slot<S>{});
+      group_scales(Slot<S ^ 1>{});
+      load_ops(nxt, S ^ 1, 0, Slot<S ^ 1>{});
+    } else {
+      more = false;
+    }
+    // the hi products of the step, then the lo ones (a tile's two MFMAs eight apart)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[i][0] = mfma_f16(cur.h[i], cur.b[0], acc[i][0]);
+      acc[i][1] = mfma_f16(cur.h[i], cur.b[1], acc[i][1]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[i][0] = mfma_f16(cur.l[i], cur.b[0], acc[i][0]);
+      acc[i][1] = mfma_f16(cur.l[i], cur.b[1], acc[i][1]);
+    }
+    if (more) lds_wait(nxt);
+  };
+  auto group = [&](int gi, auto slot) {
+    kstep(X, Y, gi, 0, slot);
+    kstep(Y, X, gi, 1, slot);
+    kstep(X, Y, gi, 2, slot);
+    kstep(Y, X, gi, 3, slot);
+  };
   for (int gb = 0; gb < n_g; gb += 2) {
-    step(gb, Slot<0>{});
-    if (gb + 1 < n_g) step(gb + 1, Slot<1>{});
+    group(gb, Slot<0>{});
+    if (gb + 1 < n_g) group(gb + 1, Slot<1>{});
   }
   if (EPI == EPI_SWIGLU && tail_idx >= 0) {  // (the split last round is used for gate|up)
     // a K slice of a remaining tile: store it as 16-byte chunks (chunk c = four
