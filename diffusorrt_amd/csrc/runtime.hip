@@ -1679,21 +1679,23 @@ int32_t drt_session_bd3_decode(uint64_t session, int32_t prompt_len, int32_t max
         L.base = (int)frontier.size() / L.spb;
         L.rem = (int)frontier.size() % L.spb;
       }
-      // A whole aligned block at its first step: its forwards run back to back,
-      // each step's choice made on the device (the steps with a quota; a step
-      // without one forwards nothing, as below).
-      if (step % L.spb == 0 && lo == grid && hi == grid + B && !frontier.empty() &&
-          s->block_on_device()) {
+      // A whole aligned block, from this step to its last one or to the call's
+      // forward limit: the forwards run back to back, each step's choice made on
+      // the device (the steps with a quota; a step without one forwards nothing,
+      // as below). A block entered mid-way (an earlier call stopped inside it)
+      // continues the same way.
+      if (lo == grid && hi == grid + B && !frontier.empty() && s->block_on_device()) {
         std::vector<int> quotas;
-        for (int j = 0; j < L.spb; ++j) {
+        int j = step % L.spb;
+        for (; j < L.spb && (int)quotas.size() < max_forwards - forwards; ++j) {
           const int q = L.base + (j < L.rem ? 1 : 0);
           if (q > 0) quotas.push_back(q);
         }
-        if ((int)quotas.size() <= max_forwards - forwards &&
+        if (!quotas.empty() &&
             (int)quotas.size() <= Runtime::UPLOAD_SLOTS - Runtime::EAGER_SLOT0) {
           forwards += s->run_block(grid, quotas);
           for (int q : quotas) committed += q;
-          L.step = step + L.spb;
+          L.step = step + (j - step % L.spb);  // the steps run, quota-less ones included
           continue;
         }
       }
