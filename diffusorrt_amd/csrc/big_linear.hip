@@ -12,8 +12,11 @@
 //     64-k group straight into LDS (global_load_lds, no registers held),
 //     double buffered: 2 planes x 128 rows x 128 B per group. Rows are stored
 //     unpadded with the 16-byte chunks of row r permuted (chunk c at position
-//     c ^ (r & 7)), so the MFMA fragment reads of 8 consecutive rows hit 8
-//     different bank groups. Each MFMA step multiplies hi and lo by the same B.
+//     c ^ (r & 7) ^ ((r >> 3) & 1)), so the MFMA fragment reads of 8 consecutive
+//     rows hit 8 different 16-byte bank groups of a 128-byte row, and those of
+//     16 consecutive rows 16 different ones of two rows (256 bytes): no bank
+//     conflict whether the LDS serves 8 or 16 lanes of a 16-byte read per
+//     cycle. Each MFMA step multiplies hi and lo by the same B.
 //   B (q4 tile layout: per 32-column n-tile and 64-k group, 1 KiB of words and
 //     32 scale|bias pairs) goes straight from global memory to registers and is
 //     dequantized there, one k step at a time: 2 n-tiles per wave per group.
@@ -170,13 +173,14 @@ __global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int K
   uint32_t wsb[2][2];
   // A of group g into buffer buf: plane pl, 8-row block blk = wave + 4i is one
   // wave instruction (lane l: row blk*8 + (l >> 3), LDS position l & 7, which
-  // holds the row's chunk (l & 7) ^ (l >> 3)); rows past M re-read row M - 1,
+  // holds the row's chunk (l & 7) ^ (l >> 3) ^ (blk & 1), blk & 1 being
+  // wave & 1); rows past M re-read row M - 1,
   // whose copies feed only outputs that are never stored. Addresses are a
   // uniform base per group plus 32-bit lane offsets (activation < 4 GiB),
   // recomputed at each issue (24-bit multiplies, from lane values made opaque
   // there) instead of staying live across the loop.
   const int row_l = m0 + wave * 8 + (lane >> 3);
-  const uint32_t col_l = (uint32_t)(((lane & 7) ^ (lane >> 3)) * 16);
+  const uint32_t col_l = (uint32_t)(((lane & 7) ^ (lane >> 3) ^ (wave & 1)) * 16);
   const uint32_t K2 = (uint32_t)K * 2u;
   const char* act_b = (const char*)act;
   auto issue = [&](int g, int buf, auto slot) {
@@ -206,7 +210,8 @@ __global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int K
   for (int i = 0; i < 4; ++i) acc[i][0] = acc[i][1] = f32x16{};
 
   // this lane's fragment row within each 32-row m-tile is lane & 31; its k
-  // chunk at step t is 4 * (lane >> 5) + t, stored at position chunk ^ (row & 7)
+  // chunk at step t is 4 * (lane >> 5) + t, stored at position
+  // chunk ^ (row & 7) ^ ((row >> 3) & 1) (row & 15 == lane & 15)
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem + (lane & 31) * 128;
   // one k step's operands (A hi and lo fragments, the two dequantised B
   // fragments); steps alternate between two sets, the next step's read and
@@ -231,7 +236,8 @@ __global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int K
     constexpr int S = decltype(slot)::value;
     // m-tile i of the hi plane at + 4096 i, of the lo plane at + BG_PLANE_BYTES + 4096 i
     const uint32_t ab =
-        lds0 + buf * BG_BUF_BYTES + (uint32_t)(((4 * (lane >> 5) + t) ^ (lane & 7)) * 16);
+        lds0 + buf * BG_BUF_BYTES +
+        (uint32_t)(((4 * (lane >> 5) + t) ^ (lane & 7) ^ ((lane >> 3) & 1)) * 16);
     lds_read16o<0>(o.h[0], ab);
     lds_read16o<BG_PLANE_BYTES>(o.l[0], ab);
     lds_read16o<4096>(o.h[1], ab);
