@@ -77,8 +77,15 @@ __global__ __launch_bounds__(64 * WAVES) void lmhead_kernel(
   const int G = K >> 6, KC = K >> 4;
   const int NTILES = N >> 5, NB = N >> 6;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int m0 = blockIdx.z * 32;
-  const int wblk = blockIdx.x * WAVES + wave;  // 64-column block of this wave
+  // work-group b of the one-dimensional grid takes (column group x, row tile z)
+  // = (t / Z, t % Z) with t dealt to the XCDs in contiguous runs (work-group b
+  // runs on XCD b % 8; t = (b % 8) * T8 / 8 + b / 8, the last T - T8 as they
+  // come): the row tiles of a column group run on one XCD together, so its
+  // weights come from HBM once and from that XCD's L2 for the other row tiles
+  const int Z = (M + 31) / 32, T = (int)gridDim.x, T8 = T & ~7, b = (int)blockIdx.x;
+  const int t = b < T8 ? (b & 7) * (T8 >> 3) + (b >> 3) : b;
+  const int m0 = (t % Z) * 32;
+  const int wblk = (t / Z) * WAVES + wave;  // 64-column block of this wave
   const bool active = wblk < NB;
   const int nt0 = active ? wblk * NT : 0;
 
@@ -759,7 +766,7 @@ void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* 
   } else {
   const size_t lds = (size_t)(w.q4 ? 2 : 1) * 32 * (chunk_k + 8) * 2 +
                      (size_t)32 * (chunk_k / 64) * 4 + (size_t)WAVES * 32 * 65 * 4;
-  const dim3 grid((NB + WAVES - 1) / WAVES, 1, (M + 31) / 32);
+  const dim3 grid((unsigned)(((NB + WAVES - 1) / WAVES) * ((M + 31) / 32)));  // (column group, row tile) pairs
   if (w.q4) {
     auto fn = lmhead_kernel<0, WAVES, 4>;
     static size_t granted = 0;
