@@ -348,15 +348,16 @@ def test_dream_real_shapes_window():
     rt.close()
 
 
-@pytest.mark.parametrize("hidden", [256, 512, 1024])
-def test_dream_block_threshold_exact_kv(hidden):
+@pytest.mark.parametrize("hidden,BS", [(256, 8), (512, 8), (1024, 8), (1024, 24)])
+def test_dream_block_threshold_exact_kv(hidden, BS):
     """Dream's block-threshold policy on the device session: prompt-relative
-    8-row blocks over the exact K/V of the prompt and the frozen blocks, the
+    8-row (or 24-row) blocks over the exact K/V of the prompt and the frozen blocks, the
     logits shift's feeder row, the MASK column left out of the scoring. The LM
     head's MASK row is set to 4x the row of the first frontier row's top token,
     so MASK would win that row if it were scored. (Hidden size 1024 takes the
     persistent q4 LM head, 256 the chunked one; 512 and 1024 take the whole-K
-    gate|up kernel at K = 512 and 1024.)"""
+    gate|up kernel at K = 512 and 1024, whose second 16-row half is partly
+    filled with 24-row blocks.)"""
     from diffusorrt_amd import decode
     from diffusorrt_amd import synthetic as syn
     from diffusorrt_amd.runtime import Runtime, block_threshold_session_config
@@ -365,7 +366,7 @@ def test_dream_block_threshold_exact_kv(hidden):
     geom = tiny_dream_geometry(hidden_size=hidden)
     model = syn.build_model(geom, "q4", 13)
     W, cfg = _oracle(model)
-    P_LEN, GEN, BS = 45, 24, 8
+    P_LEN, GEN = 45, 24
     prompt = np.random.default_rng(5).integers(0, 900, P_LEN).tolist()
     x = prompt + [geom.mask_token_id] * GEN
 
