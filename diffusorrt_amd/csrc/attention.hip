@@ -958,7 +958,11 @@ AttnPlan plan_attention(int n_rows, int Hq, int Hkv, int n_keys, size_t part_bud
   p.qw = qtiles <= 2 ? 2 : 4;
   p.qgroups = (qtiles + p.qw - 1) / p.qw;
   const int n_tiles = std::max(1, (n_keys + 31) / 32);
-  const int target_wgs = 512;
+  // two work-groups per CU for long key ranges; one for short ones (<= 2048 keys),
+  // where a split's fixed costs (Q staging, partial stores, the combine's reads)
+  // outweigh the extra parallelism (Dream's 512-key canvas: 18.7 + 8.4 ->
+  // 18.2 + 7.0 us per layer with two splits instead of four)
+  const int target_wgs = n_tiles <= 64 ? 256 : 512;
   int splits = std::max(1, target_wgs / (Hkv * p.qgroups));
   splits = std::min({splits, n_tiles, 64});  // the combine reads <= 64 splits
   // keep the fp32 partials within budget
