@@ -177,3 +177,6 @@ struct StepDesc {
   // token (highest scores first, equal scores lower row first; 0: none)
   int32_t quota;
 };
+// Entries of a device block's quota table (indexed by step modulo this; a block
+// runs fewer steps).
+constexpr int QUOTA_TAB = 64;

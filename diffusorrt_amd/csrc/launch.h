@@ -229,9 +229,11 @@ void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* 
             double* scores_d = nullptr, int32_t* tokens_d = nullptr);
 // The device-side fixed-quota commit of a block step (desc->quota of the
 // desc->n_lm LM rows at `positions`, from the LM head's device scores / tokens)
-// into the device canvas.
+// into the device canvas. advance (optional): the descriptor of the next step,
+// whose step becomes desc->step + 1 and quota quota_tab[that step % QUOTA_TAB].
 void block_commit(const double* scores_d, const int32_t* tokens_d, const int32_t* positions,
-                  int32_t* canvas, int mask_id, const StepDesc* desc, hipStream_t s);
+                  int32_t* canvas, int mask_id, const StepDesc* desc, hipStream_t s,
+                  StepDesc* advance = nullptr, const int32_t* quota_tab = nullptr);
 
 // y = round_bf16(y) (+ bias after rounding); x fp32 -> bf16 bits.
 void round_bf16_inplace(float* y, int64_t n, const uint16_t* bias, int N, hipStream_t s);

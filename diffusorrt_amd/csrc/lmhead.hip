@@ -687,13 +687,13 @@ extern "C" __global__ void lmhead_finalize_kernel(const LmStat* __restrict__ sta
 // host loop's stable order does. One wave, n_lm <= 64; rows are distinct
 // positions, and every canvas read happens before any write. A NaN score ranks
 // below every number.
-extern "C" __global__ void block_commit_kernel(const double* __restrict__ scores,
-                                               const int32_t* __restrict__ tokens,
-                                               const int32_t* __restrict__ positions,
-                                               int32_t* __restrict__ canvas, int mask_id,
-                                               const StepDesc* __restrict__ desc) {
-  const int quota = desc->quota, n = min(desc->n_lm, 64);
-  if (quota <= 0) return;
+// The fixed-quota choice of one step: `quota` of the n LM rows whose canvas
+// token is still the mask take their proposed token, highest scores first.
+__device__ __forceinline__ void commit_quota(const double* __restrict__ scores,
+                                             const int32_t* __restrict__ tokens,
+                                             const int32_t* __restrict__ positions,
+                                             int32_t* __restrict__ canvas, int mask_id,
+                                             int quota, int n) {
   const int r = threadIdx.x;
   const bool row = r < n;
   const int pos = row ? positions[r] : 0;
@@ -709,6 +709,24 @@ extern "C" __global__ void block_commit_kernel(const double* __restrict__ scores
     rank += (mj && (sj > sc || (sj == sc && j < r))) ? 1 : 0;
   }
   if (masked && rank < quota) canvas[pos] = tokens[r];
+}
+
+// One wave. `advance` (may be desc itself, so neither is restrict) receives the
+// next step's sampling index and quota, from quota_tab indexed by step modulo
+// QUOTA_TAB: a device block's later steps replay one graph on one descriptor.
+extern "C" __global__ void block_commit_kernel(const double* __restrict__ scores,
+                                               const int32_t* __restrict__ tokens,
+                                               const int32_t* __restrict__ positions,
+                                               int32_t* __restrict__ canvas, int mask_id,
+                                               const StepDesc* desc, StepDesc* advance,
+                                               const int32_t* __restrict__ quota_tab) {
+  const int quota = desc->quota, n = min(desc->n_lm, 64), step = desc->step;
+  if (quota > 0) commit_quota(scores, tokens, positions, canvas, mask_id, quota, n);
+  // every lane's loads of desc completed before its values were used above
+  if (advance && threadIdx.x == 0) {
+    advance->step = step + 1;
+    advance->quota = quota_tab[(step + 1) & (QUOTA_TAB - 1)];
+  }
 }
 
 template __global__ void lmhead_kernel<0, 4, 4>(const uint32_t*, const uint32_t*, const uint16_t*,
@@ -797,11 +815,13 @@ void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* 
 }
 
 void block_commit(const double* scores_d, const int32_t* tokens_d, const int32_t* positions,
-                  int32_t* canvas, int mask_id, const StepDesc* desc, hipStream_t s) {
+                  int32_t* canvas, int mask_id, const StepDesc* desc, hipStream_t s,
+                  StepDesc* advance, const int32_t* quota_tab) {
   require(desc && scores_d && tokens_d && positions && canvas,
           "block_commit needs the step descriptor, device scores, tokens, positions and canvas");
+  require(!advance || quota_tab, "block_commit: a descriptor advance needs the quota table");
   hipLaunchKernelGGL(block_commit_kernel, dim3(1), dim3(64), 0, s, scores_d, tokens_d, positions,
-                     canvas, mask_id, desc);
+                     canvas, mask_id, desc, advance, quota_tab);
   DRT_HIP(hipGetLastError());
 }
 

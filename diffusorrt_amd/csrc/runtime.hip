@@ -170,6 +170,7 @@ struct Runtime {
     int32_t lm_rows[32];
     int32_t lm_pos[32];
     int32_t tokens[64];
+    int32_t quotas[QUOTA_TAB];  // a device block's quotas by step (block_commit's advance)
   };
   static constexpr int UPLOAD_SLOTS = 64;
   static constexpr int EAGER_SLOT0 = 3;
@@ -542,6 +543,8 @@ struct ForwardArgs {
   // [0, row0 + seg_rows) (a block committed with the next block's step; 0: none)
   int seg_rows = 0;
   int quota = 0;  // device-side block commit of this many proposals (0: none)
+  // a device block's quotas indexed by step % QUOTA_TAB (host, QUOTA_TAB entries; null: zeros)
+  const int32_t* quota_tab = nullptr;
 };
 
 // Rows [row0, row0 + n_rows) sit in one mask segment and see every key in
@@ -588,6 +591,9 @@ struct ForwardPtrs {
   const int32_t* lm_pos = nullptr;
   int n_lm_launch = 0;  // LM rows launched (graph mode pads to 32)
   int ranges = 0;       // decode-attention ranges (0: from n_keys)
+  // the block commit writes the next step's index and quota here (from quota_tab)
+  StepDesc* advance = nullptr;
+  const int32_t* quota_tab = nullptr;
 };
 
 // Upload the forward's descriptor and LM rows with one async copy from a pinned
@@ -595,10 +601,13 @@ struct ForwardPtrs {
 // the device canvas at desc->row0; the slot's copy of the canvas rows is copied
 // there first unless upload_tokens is false (the canvas rows were written on the
 // device, by a block commit). dev_slot (>= 0) receives the slot's contents
-// instead of the slot's own device copy (a graph's fixed descriptor).
+// instead of the slot's own device copy (a graph's fixed descriptor). copy_slot
+// false: the device slot holds (or will hold) these inputs; only the pointers
+// are returned and the host slot is left alone (a device block's later steps,
+// advanced by the block commit; a capture ahead of the slot's upload).
 ForwardPtrs stage_forward(Runtime& rt, const ForwardArgs& a, int slot, bool graph_mode,
                           const int32_t* tokens_host, bool upload_tokens = true,
-                          int dev_slot = -1) {
+                          int dev_slot = -1, bool copy_slot = true) {
   hipStream_t s = rt.stream;
   if (slot < 0) {
     if (rt.up_next >= Runtime::UPLOAD_SLOTS) {  // every slot in flight: drain first
@@ -609,6 +618,10 @@ ForwardPtrs stage_forward(Runtime& rt, const ForwardArgs& a, int slot, bool grap
   }
   Runtime::StepUpload* u = rt.up_host + slot;
   Runtime::StepUpload* d = rt.up_dev.as<Runtime::StepUpload>() + (dev_slot >= 0 ? dev_slot : slot);
+  require(copy_slot || (graph_mode && !upload_tokens && a.n_lm <= 32),
+          "only graph forwards of <= 32 LM rows reuse a device slot's inputs");
+  Runtime::StepUpload scratch_slot;  // the writes below land here when the slot is not copied
+  if (!copy_slot) u = &scratch_slot;
   StepDesc& hd = u->desc;
   hd = StepDesc{};
   hd.row0 = a.row0;
@@ -624,8 +637,10 @@ ForwardPtrs stage_forward(Runtime& rt, const ForwardArgs& a, int slot, bool grap
   hd.exclude_col = a.exclude_col;
   hd.seg_rows = a.seg_rows;
   hd.quota = a.quota;
+  for (int i = 0; i < QUOTA_TAB; ++i) u->quotas[i] = a.quota_tab ? a.quota_tab[i] : 0;
   ForwardPtrs p;
   p.desc = &d->desc;
+  p.quota_tab = d->quotas;
   if (a.n_lm <= 32) {
     const int n = graph_mode && a.n_lm > 0 ? 32 : a.n_lm;
     for (int i = 0; i < n; ++i) {
@@ -644,7 +659,8 @@ ForwardPtrs stage_forward(Runtime& rt, const ForwardArgs& a, int slot, bool grap
     p.lm_pos = rt.lm_pos.as<int32_t>();
     p.n_lm_launch = a.n_lm;
   }
-  DRT_HIP(hipMemcpyAsync(d, u, sizeof(Runtime::StepUpload), hipMemcpyHostToDevice, s));
+  if (copy_slot)
+    DRT_HIP(hipMemcpyAsync(d, u, sizeof(Runtime::StepUpload), hipMemcpyHostToDevice, s));
   if (graph_mode) {
     require(a.n_rows <= 64 && tokens_host && a.tokens_dev, "graph forwards take at most 64 rows");
     if (upload_tokens) {
@@ -914,7 +930,7 @@ void launch_forward(Runtime& rt, void* kv, int64_t head_stride, int64_t layer_st
            rt.lm_scores_d.as<double>(), rt.lm_tokens_d.as<int32_t>());
     if (p.canvas && desc)
       block_commit(rt.lm_scores_d.as<double>(), rt.lm_tokens_d.as<int32_t>(), p.lm_pos, p.canvas,
-                   p.mask_id, desc, s);
+                   p.mask_id, desc, s, p.advance, p.quota_tab);
   }
 }
 
@@ -985,9 +1001,15 @@ struct Session {
   // HIP graphs of the fixed-shape forwards of a block-diffusion decode: the
   // commit of one finished block, the denoise step of the active block, and the
   // two together (a block's first step after the block before it finished).
-  enum GraphKind { G_COMMIT = 0, G_STEP = 1, G_PAIR = 2, G_KINDS = 3 };
-  hipGraphExec_t g_exec[G_KINDS] = {nullptr, nullptr, nullptr};
-  bool g_warm[G_KINDS] = {false, false, false};
+  // G_BLOCK: a whole block of the native loop, the merged commit + step forward
+  // then g_block_n - 1 step forwards on the step slot (each advanced on the
+  // device by the step before), replayed with one launch per block.
+  enum GraphKind { G_COMMIT = 0, G_STEP = 1, G_PAIR = 2, G_BLOCK = 3, G_KINDS = 4 };
+  hipGraphExec_t g_exec[G_KINDS] = {nullptr, nullptr, nullptr, nullptr};
+  bool g_warm[G_KINDS] = {false, false, false, false};
+  int g_block_n = 0;
+  // forwards with a quota in a whole block of the native loop (0: unknown)
+  int full_block_steps = 0;
   int g_ranges = 0;
   bool use_graphs = getenv("DRT_DISABLE_GRAPHS") == nullptr;
   // DRT_SEPARATE_COMMIT=1 keeps the commit forward of a finished block apart
@@ -1012,18 +1034,15 @@ struct Session {
   // commit (a no-op unless the descriptor carries a quota). host_slot >= 0: the
   // inputs are staged in that pinned slot (a block's steps queued without a
   // synchronisation keep one slot each) and copied to the graph's own.
+  // upload false: the graph's slot already holds this step's inputs (a device
+  // block's step after another step forward, whose block commit advanced the
+  // slot's step and quota).
   void graph_forward(GraphKind kind, const ForwardArgs& a, int host_slot = -1,
-                     bool upload_tokens = true) {
+                     bool upload_tokens = true, bool upload = true) {
     Runtime& r = *rt;
     hipGraphExec_t& exec = g_exec[kind];
     bool& warm = g_warm[kind];
-    ForwardPtrs p = stage_forward(r, a, host_slot >= 0 ? host_slot : (int)kind, true,
-                                  canvas.data(), upload_tokens, host_slot >= 0 ? (int)kind : -1);
-    if (kind != G_COMMIT) {
-      p.canvas = tokens_dev.as<int32_t>();
-      p.mask_id = mask_id;
-    }
-    p.ranges = g_ranges;
+    const ForwardPtrs p = graph_ptrs(kind, a, host_slot, upload_tokens, upload);
     if (!warm) {
       launch_forward(r, kv.p, head_stride, layer_stride, a, p);
       warm = true;
@@ -1033,13 +1052,60 @@ struct Session {
     DRT_HIP(hipGraphLaunch(exec, r.stream));
   }
 
+  // Stage a graph forward's inputs in the slot of its kind (see graph_forward)
+  // and return its device pointers.
+  ForwardPtrs graph_ptrs(GraphKind kind, const ForwardArgs& a, int host_slot, bool upload_tokens,
+                         bool upload) {
+    ForwardPtrs p = stage_forward(*rt, a, host_slot >= 0 ? host_slot : (int)kind, true,
+                                  canvas.data(), upload_tokens, host_slot >= 0 ? (int)kind : -1,
+                                  upload);
+    if (kind != G_COMMIT) {
+      p.canvas = tokens_dev.as<int32_t>();
+      p.mask_id = mask_id;
+    }
+    // a step forward's block commit sets up its own slot for the step after it
+    if (kind == G_STEP) p.advance = const_cast<StepDesc*>(p.desc);
+    p.ranges = g_ranges;
+    return p;
+  }
+
+  // The inputs of step j of the native loop's block [fp, fp + block): the first
+  // step of a paired block also commits the block before it.
+  ForwardArgs block_step(int fp, int j, bool pair, int quota, const int32_t* quota_tab) const {
+    ForwardArgs a;
+    a.tokens_dev = tokens_dev.as<int32_t>();
+    a.temperature = (float)temperature;
+    a.seed = seed;
+    a.step = proposals + j;
+    a.row0 = j == 0 && pair ? fp - block : fp;
+    a.n_rows = fp + block - a.row0;
+    a.n_keys = fp + block;
+    a.mask_kind = 1;
+    a.mask_prompt_len = origin;
+    a.mask_block = block;
+    a.seg_rows = a.row0 < fp ? block : 0;
+    a.quota = quota;
+    a.quota_tab = quota_tab;
+    for (int p = fp; p < fp + block; ++p) {
+      a.lm_rows.push_back(p - a.row0);
+      a.lm_pos.push_back(p);
+    }
+    a.n_lm = block;
+    return a;
+  }
+
   // Record the kernels of one forward into an instantiated graph (nothing runs).
   void capture_into(hipGraphExec_t& exec, const ForwardArgs& a, const ForwardPtrs& p) {
+    capture_with(exec, [&] { launch_forward(*rt, kv.p, head_stride, layer_stride, a, p); });
+  }
+
+  // Record what `record` launches on the session stream into an instantiated graph.
+  template <class F> void capture_with(hipGraphExec_t& exec, F&& record) {
     Runtime& r = *rt;
     hipGraph_t g = nullptr;
     DRT_HIP(hipStreamBeginCapture(r.stream, hipStreamCaptureModeThreadLocal));
     try {
-      launch_forward(r, kv.p, head_stride, layer_stride, a, p);
+      record();
     } catch (...) {
       (void)hipStreamEndCapture(r.stream, &g);
       if (g) (void)hipGraphDestroy(g);
@@ -1094,6 +1160,34 @@ struct Session {
     } catch (const std::exception&) {
       (void)hipGetLastError();
       g_exec[G_PAIR] = nullptr;
+    }
+  }
+
+  // A whole paired block of n steps as one graph (G_BLOCK), captured ahead of
+  // its first use like the merged step above, once the pair and step forwards
+  // have each run (their kernels' attributes granted). Its slots (the pair's and
+  // the step's) are uploaded before each replay; nothing is staged here.
+  void precapture_block(int next_fp, int n) {
+    Runtime& r = *rt;
+    const int hi = next_fp + block;
+    if (!use_graphs || prof.on || !pairable() || !graphable(block) || g_exec[G_BLOCK] ||
+        !g_warm[G_PAIR] || !g_warm[G_STEP] || n < 2 ||
+        n > Runtime::UPLOAD_SLOTS - Runtime::EAGER_SLOT0 || next_fp < block ||
+        hi > (int)canvas.size() || hi > r.rope_positions)
+      return;
+    const ForwardArgs a0 = block_step(next_fp, 0, true, 0, nullptr);
+    const ForwardArgs a1 = block_step(next_fp, 1, true, 0, nullptr);
+    const ForwardPtrs p0 = graph_ptrs(G_PAIR, a0, -1, false, false);
+    const ForwardPtrs p1 = graph_ptrs(G_STEP, a1, -1, false, false);
+    try {  // an optimisation only, as above: on failure the blocks replay step by step
+      capture_with(g_exec[G_BLOCK], [&] {
+        launch_forward(r, kv.p, head_stride, layer_stride, a0, p0);
+        for (int j = 1; j < n; ++j) launch_forward(r, kv.p, head_stride, layer_stride, a1, p1);
+      });
+      g_block_n = n;
+    } catch (const std::exception&) {
+      (void)hipGetLastError();
+      g_exec[G_BLOCK] = nullptr;
     }
   }
 
@@ -1155,28 +1249,28 @@ struct Session {
     }
     const int row_first = pair ? fp - block : fp;
     upload_tokens(row_first, hi);  // the device canvas is the forwards' from here on
-    for (int j = 0; j < S; ++j) {
-      ForwardArgs a;
-      a.tokens_dev = tokens_dev.as<int32_t>();
-      a.temperature = (float)temperature;
-      a.seed = seed;
-      a.step = proposals + j;
-      a.row0 = j == 0 ? row_first : fp;
-      a.n_rows = hi - a.row0;
-      a.n_keys = hi;
-      a.mask_kind = 1;
-      a.mask_prompt_len = origin;
-      a.mask_block = block;
-      a.seg_rows = a.row0 < fp ? block : 0;
-      a.quota = quotas[j];
-      for (int p = fp; p < hi; ++p) {
-        a.lm_rows.push_back(p - a.row0);
-        a.lm_pos.push_back(p);
+    // the quotas by step: the first step forward's upload carries them, and each
+    // step's block commit writes the next step's index and quota into the slot
+    int32_t quota_tab[QUOTA_TAB] = {};
+    for (int j = 0; j < S; ++j) quota_tab[(proposals + j) & (QUOTA_TAB - 1)] = quotas[j];
+    if (pair && S == g_block_n && g_exec[G_BLOCK]) {
+      // the whole block in one launch: the pair's slot and the first step
+      // forward's slot, then the captured block
+      const ForwardArgs a0 = block_step(fp, 0, true, quotas[0], quota_tab);
+      const ForwardArgs a1 = block_step(fp, 1, true, quotas[1], quota_tab);
+      (void)graph_ptrs(G_PAIR, a0, Runtime::EAGER_SLOT0, false, true);
+      (void)graph_ptrs(G_STEP, a1, Runtime::EAGER_SLOT0 + 1, false, true);
+      DRT_HIP(hipGraphLaunch(g_exec[G_BLOCK], r.stream));
+    } else {
+      for (int j = 0; j < S; ++j) {
+        const ForwardArgs a = block_step(fp, j, pair, quotas[j], quota_tab);
+        const GraphKind kind = a.seg_rows > 0 ? G_PAIR : G_STEP;
+        const bool after_step = j > 0 && kind == G_STEP && (j > 1 || !pair);
+        graph_forward(kind, a, Runtime::EAGER_SLOT0 + j, false, !after_step);
       }
-      a.n_lm = block;
-      graph_forward(a.seg_rows > 0 ? G_PAIR : G_STEP, a, Runtime::EAGER_SLOT0 + j, false);
     }
     precapture_pair(hi);  // the next block's first step, while these run
+    if (full_block_steps > 0) precapture_block(hi, full_block_steps);
     if (pair) {
       m.commit_rows += block;
       cache_len = fp;
@@ -1693,6 +1787,8 @@ int32_t drt_session_bd3_decode(uint64_t session, int32_t prompt_len, int32_t max
         }
         if (!quotas.empty() &&
             (int)quotas.size() <= Runtime::UPLOAD_SLOTS - Runtime::EAGER_SLOT0) {
+          // a fresh block's forwards with a quota (every row masked)
+          s->full_block_steps = std::min(L.spb, B);
           forwards += s->run_block(grid, quotas);
           for (int q : quotas) committed += q;
           L.step = step + (j - step % L.spb);  // the steps run, quota-less ones included

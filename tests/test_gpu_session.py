@@ -514,6 +514,46 @@ def test_bd3_native_loop_matches_host_loop(kind):
     rt.close()
 
 
+def test_bd3_native_loop_sampled_uneven_quotas():
+    """At temperature > 0 a step's sampled tokens depend on its forward index,
+    which the native loop's later steps of a block read from a descriptor that
+    the step before advanced on the device (index and quota); 21 steps over
+    three blocks give each block the uneven quotas 5, 5, 5, 5, 4, 4, 4, and a
+    decode split by max_forwards enters blocks part-way. Native and host loops
+    agree token for token."""
+    from diffusorrt_amd import decode
+    from diffusorrt_amd.runtime import bd3_session_config
+
+    _say("bd3 native loop vs host loop, temperature 0.8, uneven quotas")
+    geom = tiny_geometry()
+    _, rt = _build(geom, "q4", seed=17)
+    prompt = np.random.default_rng(12).integers(0, 900, 64).tolist()
+    cfg = bd3_session_config(32, 21, 64 + 96)
+
+    def run(native, seed):
+        with rt.session(cfg) as s:
+            return decode.generate_device_tokens(
+                s, prompt, max_tokens=96, mask_token_id=geom.mask_token_id, eos_token_id=-1,
+                steps=21, block_size=32, temperature=0.8, seed=seed, native=native)
+
+    host, nat = run(False, 5), run(True, 5)
+    assert host.forward_count == 21 and host.committed_token_count == 96
+    assert nat.full_token_ids == host.full_token_ids
+    assert nat.forward_count == host.forward_count
+    assert run(True, 6).full_token_ids != host.full_token_ids  # the seed reaches the tokens
+    with rt.session(cfg) as s:
+        s.start_device(prompt + [geom.mask_token_id] * 96, prompt_len=0, block_size=32,
+                       mask_token_id=geom.mask_token_id, exact_kv=False, steps=21,
+                       temperature=0.8, seed=5)
+        total, done = 0, False
+        while not done:
+            f, _, done = s.bd3_decode(prompt_len=64, max_tokens=96, steps=21, eos_token_id=-1,
+                                      max_forwards=4)
+            total += f
+        assert total == 21 and s.canvas() == host.full_token_ids
+    rt.close()
+
+
 def test_bd3_native_loop_long_prompt_warm_session():
     """A prompt longer than four blocks is committed by eager forwards before the
     first device block, and those forwards' descriptors sit in the staging slots
