@@ -601,13 +601,16 @@ struct ForwardPtrs {
 // the device canvas at desc->row0; the slot's copy of the canvas rows is copied
 // there first unless upload_tokens is false (the canvas rows were written on the
 // device, by a block commit). dev_slot (>= 0) receives the slot's contents
-// instead of the slot's own device copy (a graph's fixed descriptor). copy_slot
-// false: the device slot holds (or will hold) these inputs; only the pointers
-// are returned and the host slot is left alone (a device block's later steps,
-// advanced by the block commit; a capture ahead of the slot's upload).
+// instead of the slot's own device copy (a graph's fixed descriptor). stage:
+// STAGE_COPY writes the host slot and copies it; STAGE_HOST only writes it (the
+// caller copies several adjacent slots at once); STAGE_PTRS leaves the host slot
+// alone and only returns the pointers (the device slot holds or will hold these
+// inputs: a device block's later steps, advanced by the block commit; a capture
+// ahead of the slot's upload).
+enum { STAGE_COPY = 0, STAGE_HOST = 1, STAGE_PTRS = 2 };
 ForwardPtrs stage_forward(Runtime& rt, const ForwardArgs& a, int slot, bool graph_mode,
                           const int32_t* tokens_host, bool upload_tokens = true,
-                          int dev_slot = -1, bool copy_slot = true) {
+                          int dev_slot = -1, int stage = STAGE_COPY) {
   hipStream_t s = rt.stream;
   if (slot < 0) {
     if (rt.up_next >= Runtime::UPLOAD_SLOTS) {  // every slot in flight: drain first
@@ -618,10 +621,10 @@ ForwardPtrs stage_forward(Runtime& rt, const ForwardArgs& a, int slot, bool grap
   }
   Runtime::StepUpload* u = rt.up_host + slot;
   Runtime::StepUpload* d = rt.up_dev.as<Runtime::StepUpload>() + (dev_slot >= 0 ? dev_slot : slot);
-  require(copy_slot || (graph_mode && !upload_tokens && a.n_lm <= 32),
-          "only graph forwards of <= 32 LM rows reuse a device slot's inputs");
-  Runtime::StepUpload scratch_slot;  // the writes below land here when the slot is not copied
-  if (!copy_slot) u = &scratch_slot;
+  require(stage == STAGE_COPY || (graph_mode && !upload_tokens && a.n_lm <= 32),
+          "only graph forwards of <= 32 LM rows stage a slot without copying it");
+  Runtime::StepUpload scratch_slot;  // the writes below land here when the host slot is left alone
+  if (stage == STAGE_PTRS) u = &scratch_slot;
   StepDesc& hd = u->desc;
   hd = StepDesc{};
   hd.row0 = a.row0;
@@ -659,7 +662,7 @@ ForwardPtrs stage_forward(Runtime& rt, const ForwardArgs& a, int slot, bool grap
     p.lm_pos = rt.lm_pos.as<int32_t>();
     p.n_lm_launch = a.n_lm;
   }
-  if (copy_slot)
+  if (stage == STAGE_COPY)
     DRT_HIP(hipMemcpyAsync(d, u, sizeof(Runtime::StepUpload), hipMemcpyHostToDevice, s));
   if (graph_mode) {
     require(a.n_rows <= 64 && tokens_host && a.tokens_dev, "graph forwards take at most 64 rows");
@@ -1026,6 +1029,12 @@ struct Session {
   ~Session() {
     if (rt && rt->stream) (void)hipStreamSynchronize(rt->stream);
     drop_graphs();
+    for (QueuedBlock& q : qblk) {
+      if (q.t0) (void)hipEventDestroy(q.t0);
+      if (q.t1) (void)hipEventDestroy(q.t1);
+      if (q.done) (void)hipEventDestroy(q.done);
+      if (q.tokens) (void)hipHostFree(q.tokens);
+    }
   }
 
   // Run a <= 64-row forward whose inputs live in a fixed upload slot: eager the
@@ -1042,7 +1051,8 @@ struct Session {
     Runtime& r = *rt;
     hipGraphExec_t& exec = g_exec[kind];
     bool& warm = g_warm[kind];
-    const ForwardPtrs p = graph_ptrs(kind, a, host_slot, upload_tokens, upload);
+    const ForwardPtrs p =
+        graph_ptrs(kind, a, host_slot, upload_tokens, upload ? STAGE_COPY : STAGE_PTRS);
     if (!warm) {
       launch_forward(r, kv.p, head_stride, layer_stride, a, p);
       warm = true;
@@ -1055,10 +1065,10 @@ struct Session {
   // Stage a graph forward's inputs in the slot of its kind (see graph_forward)
   // and return its device pointers.
   ForwardPtrs graph_ptrs(GraphKind kind, const ForwardArgs& a, int host_slot, bool upload_tokens,
-                         bool upload) {
+                         int stage) {
     ForwardPtrs p = stage_forward(*rt, a, host_slot >= 0 ? host_slot : (int)kind, true,
                                   canvas.data(), upload_tokens, host_slot >= 0 ? (int)kind : -1,
-                                  upload);
+                                  stage);
     if (kind != G_COMMIT) {
       p.canvas = tokens_dev.as<int32_t>();
       p.mask_id = mask_id;
@@ -1177,8 +1187,8 @@ struct Session {
       return;
     const ForwardArgs a0 = block_step(next_fp, 0, true, 0, nullptr);
     const ForwardArgs a1 = block_step(next_fp, 1, true, 0, nullptr);
-    const ForwardPtrs p0 = graph_ptrs(G_PAIR, a0, -1, false, false);
-    const ForwardPtrs p1 = graph_ptrs(G_STEP, a1, -1, false, false);
+    const ForwardPtrs p0 = graph_ptrs(G_PAIR, a0, -1, false, STAGE_PTRS);
+    const ForwardPtrs p1 = graph_ptrs(G_STEP, a1, -1, false, STAGE_PTRS);
     try {  // an optimisation only, as above: on failure the blocks replay step by step
       capture_with(g_exec[G_BLOCK], [&] {
         launch_forward(r, kv.p, head_stride, layer_stride, a0, p0);
@@ -1226,18 +1236,53 @@ struct Session {
   // synchronisation between its steps: the commit of what precedes it (merged
   // into the first step when pairable), then one graph-replayed step forward per
   // quota, each ending in the device-side choice and commit of its quota into the
-  // device canvas; the stream is drained once, at the end, and the block's
-  // tokens are read back into the host canvas. Every LM row of the block is
-  // scored (graph forwards score 32 rows either way); the rows already committed
-  // are left out of the choice. Returns the forwards run.
-  int run_block(int fp, const std::vector<int>& quotas) {
+  // device canvas (a whole paired block replays as one graph). Every LM row of
+  // the block is scored (graph forwards score 32 rows either way); the rows
+  // already committed are left out of the choice. queue_block enqueues the block
+  // and the readback of its tokens (into pinned staging); finish_block waits for
+  // them and accounts the block, so that the loop can queue the next block ahead
+  // while this one runs; discard_block drops a block queued ahead that the loop
+  // does not run after all (an end token or a full canvas stops the decode at
+  // the boundary before it).
+  struct QueuedBlock {
+    bool on = false, pair = false;
+    int fp = 0, S = 0;
+    std::vector<int> quotas;
+    int cache_len_before = 0;
+    int64_t commit_rows_before = 0;
+    hipEvent_t t0 = nullptr, t1 = nullptr, done = nullptr;
+    int32_t* tokens = nullptr;  // pinned, block entries
+  };
+  QueuedBlock qblk[2];
+  int qblk_next = 0;  // the QueuedBlock (and half of the eager slots) the next queue takes
+  // eager upload slots per queued block: two blocks in flight take disjoint halves
+  static constexpr int QB_SLOTS = (Runtime::UPLOAD_SLOTS - Runtime::EAGER_SLOT0) / 2;
+
+  QueuedBlock& queue_block(int fp, const std::vector<int>& quotas, bool upload_canvas) {
     Runtime& r = *rt;
     const int hi = fp + block, S = (int)quotas.size();
+    QueuedBlock& q = qblk[qblk_next];
+    require(!q.on, "internal: a queued block's record is still in use");
     require(S >= 1 && Runtime::EAGER_SLOT0 + S <= Runtime::UPLOAD_SLOTS,
             "a device block takes 1..61 steps");
-    DRT_HIP(hipEventRecord(r.ev0, r.stream));
-    const bool pair = pairable() && cache_len + block == fp && cache_len % block == 0;
-    if (!pair) {
+    // a block of more steps than half the slots takes them all (nothing else queued)
+    require(S <= QB_SLOTS || !other_queued(q), "internal: a long block queued behind another");
+    const int slot0 = Runtime::EAGER_SLOT0 + (S <= QB_SLOTS ? qblk_next * QB_SLOTS : 0);
+    if (!q.done) {
+      DRT_HIP(hipEventCreate(&q.t0));
+      DRT_HIP(hipEventCreate(&q.t1));
+      DRT_HIP(hipEventCreate(&q.done));
+      DRT_HIP(hipHostMalloc((void**)&q.tokens, (size_t)block * 4, hipHostMallocDefault));
+    }
+    q.fp = fp;
+    q.S = S;
+    q.quotas = quotas;
+    q.cache_len_before = cache_len;
+    q.commit_rows_before = m.commit_rows;
+    DRT_HIP(hipEventRecord(q.t0, r.stream));
+    q.pair = pairable() && cache_len + block == fp && cache_len % block == 0;
+    if (!q.pair) {
+      require(!other_queued(q), "internal: an unpaired block queued behind another");
       commit_to(fp);
       // commit forwards run eagerly (a prefix longer than four blocks) staged their
       // descriptors in the eager slots that the steps below rewrite: their copies
@@ -1247,47 +1292,108 @@ struct Session {
         r.up_next = Runtime::EAGER_SLOT0;
       }
     }
-    const int row_first = pair ? fp - block : fp;
-    upload_tokens(row_first, hi);  // the device canvas is the forwards' from here on
+    // the device canvas is the forwards' from here on (a block queued behind
+    // another finds its rows there: the earlier block's written on the device,
+    // its own still masked on both sides)
+    if (upload_canvas) upload_tokens(q.pair ? fp - block : fp, hi);
     // the quotas by step: the first step forward's upload carries them, and each
     // step's block commit writes the next step's index and quota into the slot
     int32_t quota_tab[QUOTA_TAB] = {};
     for (int j = 0; j < S; ++j) quota_tab[(proposals + j) & (QUOTA_TAB - 1)] = quotas[j];
-    if (pair && S == g_block_n && g_exec[G_BLOCK]) {
-      // the whole block in one launch: the pair's slot and the first step
-      // forward's slot, then the captured block
+    if (q.pair && S == g_block_n && g_exec[G_BLOCK]) {
+      // the whole block in one launch: the step slot (the first step forward
+      // after the pair) and the pair's slot, adjacent on both sides, in one copy
+      static_assert(G_PAIR == G_STEP + 1, "the step and pair slots are adjacent");
       const ForwardArgs a0 = block_step(fp, 0, true, quotas[0], quota_tab);
       const ForwardArgs a1 = block_step(fp, 1, true, quotas[1], quota_tab);
-      (void)graph_ptrs(G_PAIR, a0, Runtime::EAGER_SLOT0, false, true);
-      (void)graph_ptrs(G_STEP, a1, Runtime::EAGER_SLOT0 + 1, false, true);
+      (void)graph_ptrs(G_STEP, a1, slot0, false, STAGE_HOST);
+      (void)graph_ptrs(G_PAIR, a0, slot0 + 1, false, STAGE_HOST);
+      DRT_HIP(hipMemcpyAsync(r.up_dev.as<Runtime::StepUpload>() + G_STEP, r.up_host + slot0,
+                             2 * sizeof(Runtime::StepUpload), hipMemcpyHostToDevice, r.stream));
       DRT_HIP(hipGraphLaunch(g_exec[G_BLOCK], r.stream));
     } else {
       for (int j = 0; j < S; ++j) {
-        const ForwardArgs a = block_step(fp, j, pair, quotas[j], quota_tab);
+        const ForwardArgs a = block_step(fp, j, q.pair, quotas[j], quota_tab);
         const GraphKind kind = a.seg_rows > 0 ? G_PAIR : G_STEP;
-        const bool after_step = j > 0 && kind == G_STEP && (j > 1 || !pair);
-        graph_forward(kind, a, Runtime::EAGER_SLOT0 + j, false, !after_step);
+        const bool after_step = j > 0 && kind == G_STEP && (j > 1 || !q.pair);
+        graph_forward(kind, a, slot0 + j, false, !after_step);
       }
     }
-    precapture_pair(hi);  // the next block's first step, while these run
-    if (full_block_steps > 0) precapture_block(hi, full_block_steps);
-    if (pair) {
+    if (!other_queued(q)) {  // (with a block in flight the graphs exist already)
+      precapture_pair(hi);  // the next block's first step, while these run
+      if (full_block_steps > 0) precapture_block(hi, full_block_steps);
+    }
+    if (q.pair) {
       m.commit_rows += block;
       cache_len = fp;
     }
-    DRT_HIP(hipEventRecord(r.ev1, r.stream));
-    DRT_HIP(hipMemcpyAsync(canvas.data() + fp, tokens_dev.as<int32_t>() + fp, (size_t)block * 4,
+    DRT_HIP(hipEventRecord(q.t1, r.stream));
+    DRT_HIP(hipMemcpyAsync(q.tokens, tokens_dev.as<int32_t>() + fp, (size_t)block * 4,
                            hipMemcpyDeviceToHost, r.stream));
-    DRT_HIP(hipStreamSynchronize(r.stream));
-    r.up_next = Runtime::EAGER_SLOT0;
+    DRT_HIP(hipEventRecord(q.done, r.stream));
+    proposals += S;  // a block queued behind this one continues the sampling index
+    q.on = true;
+    qblk_next ^= 1;
+    return q;
+  }
+
+  bool other_queued(const QueuedBlock& q) const { return qblk[&q == &qblk[0] ? 1 : 0].on; }
+
+  // A block may be queued behind another: every graph it replays is captured
+  // (whole paired blocks), and nothing else is queued ahead.
+  bool queue_ahead_ready() const {
+    return use_graphs && !prof.on && pairable() && graphable(block) && g_exec[G_PAIR] &&
+           g_exec[G_STEP] && g_exec[G_BLOCK] && !qblk[0].on != !qblk[1].on;
+  }
+
+  // The block queued ahead at fp, or null.
+  QueuedBlock* queued_at(int fp) {
+    for (QueuedBlock& q : qblk)
+      if (q.on && q.fp == fp) return &q;
+    return nullptr;
+  }
+
+  // Wait for a queued block's tokens and account it. Returns its forwards.
+  int finish_block(QueuedBlock& q) {
+    Runtime& r = *rt;
+    DRT_HIP(hipEventSynchronize(q.done));
+    std::memcpy(canvas.data() + q.fp, q.tokens, (size_t)block * 4);
+    q.on = false;
+    if (!other_queued(q)) r.up_next = Runtime::EAGER_SLOT0;
     check_placement(r);
-    finish_timing();
-    proposals += S;
-    m.forward_count += S;
-    m.active_rows += (int64_t)S * block;
-    m.lm_rows += (int64_t)S * block;
+    float ms = 0.f;
+    DRT_HIP(hipEventElapsedTime(&ms, q.t0, q.t1));
+    m.last_forward_ms = ms;
+    m.total_forward_ms += ms;
+    m.forward_count += q.S;
+    m.active_rows += (int64_t)q.S * block;
+    m.lm_rows += (int64_t)q.S * block;
     m.kv_cache_len = cache_len;
-    return S;
+    return q.S;
+  }
+
+  // Drop a block queued ahead: drain the stream, put its rows of the device
+  // canvas back to the host's (still masked) and undo its accounting. The
+  // commit its first step made (the block before it) stays on the device, not
+  // counted: those K/V rows are exact, and a later commit rewrites them.
+  void discard_block(QueuedBlock& q) {
+    Runtime& r = *rt;
+    DRT_HIP(hipStreamSynchronize(r.stream));
+    q.on = false;
+    upload_tokens(q.fp, q.fp + block);
+    DRT_HIP(hipStreamSynchronize(r.stream));
+    proposals -= q.S;
+    cache_len = q.cache_len_before;
+    m.commit_rows = q.commit_rows_before;
+    m.kv_cache_len = cache_len;
+    if (!other_queued(q)) r.up_next = Runtime::EAGER_SLOT0;
+    check_placement(r);
+  }
+
+  // Drop whatever is queued ahead (the loop stops, or runs something else next).
+  void discard_queued() {
+    for (QueuedBlock& q : qblk)
+      if (q.on) discard_block(q);
   }
 
   // Graph forwards apply to block-sized rows of a session whose decode
@@ -1747,6 +1853,16 @@ int32_t drt_session_bd3_decode(uint64_t session, int32_t prompt_len, int32_t max
       L.limit = L.count * L.spb;
     }
     int forwards = 0, committed = 0, done = 0;
+    // a block queued ahead that the loop does not reach is dropped on the way out
+    struct DropQueued {
+      Session* s;
+      ~DropQueued() {
+        try {
+          s->discard_queued();
+        } catch (...) {
+        }
+      }
+    } drop_queued{&*s};
     std::vector<int32_t> frontier, pos, tok;
     std::vector<double> sc;
     std::vector<int32_t> tk, order;
@@ -1789,12 +1905,42 @@ int32_t drt_session_bd3_decode(uint64_t session, int32_t prompt_len, int32_t max
             (int)quotas.size() <= Runtime::UPLOAD_SLOTS - Runtime::EAGER_SLOT0) {
           // a fresh block's forwards with a quota (every row masked)
           s->full_block_steps = std::min(L.spb, B);
-          forwards += s->run_block(grid, quotas);
+          // this block, unless it was queued ahead (with the same quotas)
+          Session::QueuedBlock* qb = s->queued_at(grid);
+          if (qb && qb->quotas != quotas) {
+            s->discard_block(*qb);
+            qb = nullptr;
+          }
+          if (!qb) {
+            s->discard_queued();
+            qb = &s->queue_block(grid, quotas, true);
+          }
+          // Queue the next block behind it while it runs, when the loop will run
+          // that block next in this call unless the decode stops at the boundary
+          // (then it is dropped): a whole block from its first step, fresh (every
+          // row masked), within the step and forward budgets, on the captured graphs.
+          const int ngrid = grid + B;
+          if (j == L.spb && s->queue_ahead_ready() && block_id + 1 < L.count &&
+              ngrid + B <= prompt_len + max_tokens && !s->queued_at(ngrid)) {
+            bool fresh = true;
+            for (int p = ngrid; p < ngrid + B && fresh; ++p) fresh = s->canvas[p] == s->mask_id;
+            std::vector<int> nq;
+            for (int k = 0; k < L.spb; ++k) {
+              const int q = B / L.spb + (k < B % L.spb ? 1 : 0);
+              if (q > 0) nq.push_back(q);
+            }
+            if (fresh && (int)nq.size() == s->g_block_n && qb->S <= Session::QB_SLOTS &&
+                (int)nq.size() <= Session::QB_SLOTS &&
+                forwards + qb->S + (int)nq.size() <= max_forwards)
+              s->queue_block(ngrid, nq, false);
+          }
+          forwards += s->finish_block(*qb);
           for (int q : quotas) committed += q;
           L.step = step + (j - step % L.spb);  // the steps run, quota-less ones included
           continue;
         }
       }
+      s->discard_queued();  // (a block queued ahead is always the loop's next block)
       const int quota = L.base + (step % L.spb < L.rem ? 1 : 0);
       if (frontier.empty() || quota == 0) {
         L.step = step + 1;
