@@ -36,11 +36,14 @@
 //   EPI_STORE : y (+ bias on slice 0)
 //   EPI_SWIGLU: [gate 64 | up 64] column blocks -> silu(g) * u -> ACT_F16P
 //   EPI_QKV   : (+ bias), q/k RMSNorm, RoPE, Q out / K,V into the tiled cache
+//   EPI_LMSTAT: the LM head's softmax statistics per (row, 64-column block),
+//               the logits themselves only on request
 #include "fused.h"
 #include "gemm_core.h"
 #include "launch.h"
 
 #include "linear_dev.h"
+#include "lmstat.h"
 
 namespace {
 
@@ -413,6 +416,43 @@ __global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int K
         }
       }
       if (over) raise_range(a);
+    } else if (EPI == EPI_LMSTAT) {
+      // lane: row lane & 31 of the piece, the 32 columns half of its wave's 64
+      // (the rows of 8 consecutive lanes sit in 8 different 16-byte bank groups)
+      const int r = lane & 31, half = lane >> 5;
+      const int col0 = n0 + wave * 64 + half * 32, row = mp + r;
+      const bool valid = row < M && n0 + wave * 64 < N;  // (N % 64 == 0)
+      const float temperature = a.desc ? a.desc->temperature : a.lm_temp;
+      const uint64_t seed = a.desc ? a.desc->seed : a.lm_seed;
+      const int step = a.desc ? a.desc->step : a.lm_step;
+      const int excl = a.desc ? a.desc->exclude_col : a.lm_excl;
+      float v[32];
+      const float* src = e + r * BG_EROW + wave * 64 + half * 32;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const f32x4 t4 = *(const f32x4*)(src + 4 * q);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[4 * q + k] = t4[k];
+      }
+      if (a.lm_logits && valid) {
+        f32x4* lp = (f32x4*)(a.lm_logits + (int64_t)row * N + col0);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) lp[q] = f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+      }
+#pragma unroll
+      for (int c = 0; c < 32; ++c) v[c] = col0 + c == excl ? -INFINITY : v[c];
+      const bool samp = temperature > 0.f && row < M;
+      const uint64_t rk = samp ? sampling_row_key(seed, step, a.lm_pos[row]) : 0ull;
+      const LmRun32 mine = lm_run32(v, col0, samp, temperature, rk);
+      LmRun32 other;
+      other.mx = __shfl_xor(mine.mx, 32, 64);
+      other.arg = __shfl_xor(mine.arg, 32, 64);
+      other.se = __shfl_xor(mine.se, 32, 64);
+      other.skey = __shfl_xor(mine.skey, 32, 64);
+      other.sarg = __shfl_xor(mine.sarg, 32, 64);
+      other.sl = __shfl_xor(mine.sl, 32, 64);
+      if (half == 0 && valid)
+        ((LmStat*)a.lm_stats)[(int64_t)row * (N >> 6) + (n0 >> 6) + wave] = lm_join64(mine, other);
     } else if (EPI == EPI_QKV) {
       const int rows = min(32, M - mp);
 #pragma unroll
@@ -433,6 +473,7 @@ __global__ __launch_bounds__(256, 2) void big_q4_kernel(const FusedArgs a, int K
 template __global__ void big_q4_kernel<EPI_STORE>(const FusedArgs, int, const BgTail);
 template __global__ void big_q4_kernel<EPI_SWIGLU>(const FusedArgs, int, const BgTail);
 template __global__ void big_q4_kernel<EPI_QKV>(const FusedArgs, int, const BgTail);
+template __global__ void big_q4_kernel<EPI_LMSTAT>(const FusedArgs, int, const BgTail);
 
 // The QKV epilogue of a split-K q|k|v projection: work-group (head, 32-row
 // block) sums the KS fp32 partial slices of its head's 128 columns (bias
@@ -516,6 +557,7 @@ bool big_linear_supported(const FusedArgs& a, int kind) {
   if (!a.qw || !a.sb || a.M <= 32 || a.N % 32 != 0 || a.K % 64 != 0) return false;
   if ((kind == FL_QKV || kind == FL_SWIGLU) && a.N % 128 != 0) return false;
   if (kind == FL_SWIGLU && a.act_fmt != ACT_F16P) return false;
+  if (kind == FL_LMSTAT) return a.N % 64 == 0 && a.lm_stats != nullptr;
   return kind == FL_QKV || kind == FL_SWIGLU || kind == FL_STORE;
 }
 
@@ -561,6 +603,7 @@ void big_linear(const FusedArgs& a, int kind, int KS, hipStream_t s, float* tail
   }
   if (kind == FL_QKV) DRT_BG(EPI_QKV)
   else if (kind == FL_SWIGLU) DRT_BG(EPI_SWIGLU)
+  else if (kind == FL_LMSTAT) DRT_BG(EPI_LMSTAT)
   else DRT_BG(EPI_STORE)
 #undef DRT_BG
   DRT_HIP(hipGetLastError());

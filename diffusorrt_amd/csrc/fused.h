@@ -4,9 +4,9 @@
 
 enum { W_Q4 = 0, W_BF16 = 1 };
 enum { PRO_ACT = 0, PRO_NORM = 1 };
-enum { EPI_STORE = 0, EPI_QKV = 1, EPI_RESID = 2, EPI_SWIGLU = 3 };
+enum { EPI_STORE = 0, EPI_QKV = 1, EPI_RESID = 2, EPI_SWIGLU = 3, EPI_LMSTAT = 4 };
 // launch kinds (prologue + epilogue pairs used by the runtime)
-enum { FL_QKV = 0, FL_RESID = 1, FL_SWIGLU = 2, FL_STORE = 3 };
+enum { FL_QKV = 0, FL_RESID = 1, FL_SWIGLU = 2, FL_STORE = 3, FL_LMSTAT = 4 };
 
 struct FusedArgs {
   // weights: q4 tile32-g64 (qw, sb) or bf16 tiles (wb); optional bf16 bias [N]
@@ -83,6 +83,17 @@ struct FusedArgs {
   // producer (from this kernel's norm factors).
   const float* pre_sc_in = nullptr;
   float* pre_sc_out = nullptr;
+  // EPI_LMSTAT (the large-M LM head): one LmStat per (row, 64-column block) at
+  // lm_stats[row * (N / 64) + block], the logits themselves only when lm_logits
+  // is set; sampling controls (temperature, seed, forward, excluded column) from
+  // desc when it is set, else from these fields
+  void* lm_stats = nullptr;
+  float* lm_logits = nullptr;
+  const int32_t* lm_pos = nullptr;  // canvas position of each row (sampling keys)
+  float lm_temp = 0.f;
+  uint64_t lm_seed = 0;
+  int lm_step = 0;
+  int lm_excl = -1;
 };
 
 // Row tiles of the runtime's split-K workspaces: forwards of up to 64 rows (a

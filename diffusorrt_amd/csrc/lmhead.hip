@@ -14,45 +14,13 @@
 // sum of exp(l - block max) in fp32, sampling candidate), so the logits only
 // leave the chip when the caller asks for them. lmhead_finalize_kernel joins
 // the blocks of a row in float64.
+#include "fused.h"
 #include "gemm_core.h"
 #include "launch.h"
+#include "lmstat.h"
 
 #include <cstdlib>
 #include <type_traits>
-
-struct LmStat {
-  float m;       // block max logit
-  float s;       // sum exp(l - m) over the block (fp32)
-  int arg;       // first column attaining m
-  int sarg;      // sampling: column of the best key
-  double skey;   // sampling: best l + T * g
-  float sl;      // sampling: logit at sarg
-  float pad;
-};
-
-namespace {
-
-constexpr uint64_t GOLDEN = 0x9E3779B97F4A7C15ull;
-
-DRT_DEV uint64_t mix64(uint64_t z) {
-  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-  return z ^ (z >> 31);
-}
-
-DRT_DEV uint64_t sampling_row_key(uint64_t seed, int step, int position) {
-  uint64_t key = mix64(seed + GOLDEN);
-  key = mix64(key + (uint64_t)(int64_t)(step + 1) * GOLDEN);
-  return mix64(key + (uint64_t)(int64_t)(position + 1) * GOLDEN);
-}
-
-DRT_DEV float gumbel(uint64_t row_key, int token) {
-  const uint64_t bits = mix64(row_key + (uint64_t)(token + 1) * GOLDEN);
-  const float u = ((float)(uint32_t)(bits >> 41) + 0.5f) * 0x1p-23f;
-  return -logf(-logf(u));
-}
-
-}  // namespace
 
 // WK = 0: q4 tile32-g64 weights + ACT_F16P activation (hi and lo planes of M
 // rows, group sums of hi + lo); WK = 1: bf16 tile weights
@@ -755,7 +723,8 @@ void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* 
   require(w.K % chunk_k == 0 || w.K % 64 == 0, "lm head K must be a multiple of 64");
   int NB = w.N / 64;
   constexpr int WAVES = 4;
-  // K = 1024 heads (q4 or bf16) run on the persistent kernel, other K on the chunked one
+  // K = 1024 heads (q4 or bf16) run on the persistent kernel, other K on the
+  // large-M GEMM (q4, more than 64 rows) or the chunked kernel
   if (w.K == LMP_G * 64) {
     int dev = 0, n_cu = 0;
     DRT_HIP(hipGetDevice(&dev));
@@ -781,6 +750,29 @@ void lmhead(const LinearW& w, const void* act, const float* xsum, int M, float* 
                  (const uint16_t*)act, xsum, M, w.N, logits_out, (LmStat*)stats, temperature,
                  seed, step, positions, desc, exclude_col);
     }
+  } else if (w.q4 && M > 64) {
+    // more than two 32-row tiles of a q4 head of another K (Dream's canvas rows):
+    // the large-M GEMM, whose 128 x 256 tiles dequantize the weights once per
+    // 128 rows, with the statistics epilogue (the same records, N / 64 per row).
+    // Dream's head (N = 152064, K = 3584): 272 us for 65-128 rows, 462 us for
+    // 129-256, against about 120 us per 32-row tile on the chunked kernel.
+    FusedArgs f;
+    f.qw = w.qw.as<uint32_t>();
+    f.sb = w.sb.as<uint32_t>();
+    f.M = M;
+    f.N = w.N;
+    f.K = w.K;
+    f.act = act;
+    f.act_fmt = ACT_F16P;
+    f.desc = desc;
+    f.lm_stats = stats;
+    f.lm_logits = logits_out;
+    f.lm_pos = positions;
+    f.lm_temp = temperature;
+    f.lm_seed = seed;
+    f.lm_step = step;
+    f.lm_excl = exclude_col;
+    big_linear(f, FL_LMSTAT, 1, s);
   } else {
   const size_t lds = (size_t)(w.q4 ? 2 : 1) * 32 * (chunk_k + 8) * 2 +
                      (size_t)32 * (chunk_k / 64) * 4 + (size_t)WAVES * 32 * 65 * 4;

@@ -335,15 +335,16 @@ def _q4_dequant64_cuda(w_q, scales, biases):
     return (q * scales.double().unsqueeze(-1) + biases.double().unsqueeze(-1)).reshape(n, -1)
 
 
-@pytest.mark.parametrize("kind,rows", [("q4", 256), ("bf16", 64)])
+@pytest.mark.parametrize("kind,rows", [("q4", 256), ("q4", 64), ("bf16", 64)])
 def test_lm_head_full_vocab_chunked_k3584(kind, rows):
-    """Dream's LM head at its real size (vocabulary 152064, K = 3584: the
-    chunked kernel, every K other than 1024): 256 rows (8 row tiles) for q4,
-    64 for bf16. Logits against float64 truth computed in column chunks (the
-    chunk dequantisation pinned to the oracle's on the first chunk), greedy
-    scores and tokens equal to the float64 scoring of the device's own logits,
-    and, for q4, the T > 0 sampling rule against the oracle on 24 rows spread
-    over the 8 row tiles."""
+    """Dream's LM head at its real size (vocabulary 152064, K = 3584, every K
+    other than 1024): q4 over 256 rows (the large-M GEMM with its statistics
+    epilogue, two 128-row tiles) and 64 rows (the chunked kernel, two 32-row
+    tiles), bf16 over 64 rows (chunked). Logits against float64 truth computed
+    in column chunks (the chunk dequantisation pinned to the oracle's on the
+    first chunk), greedy scores and tokens equal to the float64 scoring of the
+    device's own logits, and, for q4, the T > 0 sampling rule against the oracle
+    on three rows of every 32-row tile."""
     from diffusorrt_amd import _lib, kernels
     from diffusorrt_amd import synthetic as syn
     import ctypes as C
@@ -396,8 +397,9 @@ def test_lm_head_full_vocab_chunked_k3584(kind, rows):
         torch.cuda.synchronize()
         err = ((logits.double() - ref).abs().amax(dim=1) / ref.abs().amax(dim=1)).max().item()
         _say(f"  T={T} logits rel err max over rows={err:.2e}")
-        # q4: fp32 sums of the exact-nibble products (hi + lo activation);
-        # bf16: compared at the bf16 resolution of the reference's logits
+        # q4: fp32 sums over the hi + lo activation (exact-nibble products on
+        # the chunked kernel, one fp16 rounding of s * q + b per weight on the
+        # GEMM); bf16: compared at the bf16 resolution of the reference's logits
         assert err < (1e-4 if kind == "q4" else 1e-2)
         got = logits.cpu().numpy()
         if T == 0.0:
