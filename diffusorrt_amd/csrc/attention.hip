@@ -372,6 +372,12 @@ DRT_DEV void attend_tile_rq(const typename MfmaT<T>::vec (&kc)[1][8],
 // Tile slots of the ring: as many as the LDS left by the Q planes holds (160
 // KiB per work-group): 8 for 32 query vectors, 7 for 64, 5 for 128.
 template <int QT> constexpr int decr_slots() { return QT == 1 ? 8 : (QT == 2 ? 7 : 5); }
+// Consumer waves: 4, or 8 for four query tiles, whose 128 query vectors would
+// otherwise give each consumer wave every tile of the range (the kernel then ran
+// on the consumers' MFMA and softmax work, not on the stream). With 8 consumers
+// three waves share a SIMD, so their Q fragments are read from LDS per tile
+// instead of being held in registers for the whole range.
+template <int QT> constexpr int decr_ncw() { return QT == 4 ? 8 : 4; }
 constexpr int DECR_SPIN = 1 << 22;
 // s_waitcnt immediates (gfx9: vmcnt bits 3:0 + 15:14, expcnt 6:4, lgkmcnt 11:8)
 constexpr int DECR_VM48 = 0xCF70, DECR_VM32 = 0x8F70, DECR_VM16 = 0x4F70, DECR_VM0 = 0x0F70;
@@ -417,7 +423,7 @@ DRT_DEV bool decr_wait(const int* flag, int want, int* err) {
 }
 
 template <typename T, int QT>
-__global__ __launch_bounds__(320) void attn_decode_kernel(
+__global__ __launch_bounds__(64 * (decr_ncw<QT>() + 1)) void attn_decode_kernel(
     const T* __restrict__ q, const T* __restrict__ q_lo, const T* __restrict__ kv,
     int64_t kv_head_stride, int n_rows,
     int Hq, int Hkv, int n_keys_arg, const StepDesc* __restrict__ desc,
@@ -469,8 +475,9 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
     decr_lds_write(&ready[t % DECR_SLOTS], t + 1);  // every lane writes the same value
   };
 
-  constexpr int QCH = QT * 2;  // Q chunks per consumer thread
-  if (wave == 4) {
+  constexpr int NCW = decr_ncw<QT>(), CT = 64 * NCW;  // consumer waves and threads
+  constexpr int QCH = QT * 512 / CT;                   // Q chunks per consumer thread
+  if (wave == NCW) {
     const int n0 = min(n, 2);
     for (int t = 0; t < n0; ++t) dma_tile(t);
   } else {
@@ -478,7 +485,7 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
     u32x4 qraw[QCH], qrawl[QCH];
 #pragma unroll
     for (int i = 0; i < QCH; ++i) {
-      const int ch = threadIdx.x + 256 * i;
+      const int ch = threadIdx.x + CT * i;
       const int qvc = min(ch >> 4, n_qv - 1);
       const int row = qvc / G, head = kvh * G + (qvc - row * G);
       const int64_t off = ((int64_t)row * Hq + head) * 128 + (ch & 15) * 8;
@@ -488,7 +495,7 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
     if (threadIdx.x < 2 * DECR_SLOTS) ready[threadIdx.x] = 0;  // ready and freed
 #pragma unroll
     for (int i = 0; i < QCH; ++i) {
-      const int ch = threadIdx.x + 256 * i;
+      const int ch = threadIdx.x + CT * i;
       const bool ok = (ch >> 4) < n_qv;
       T* d = qs + (ch >> 4) * DEC_QROW + (ch & 15) * 8;
       *(u32x4*)d = ok ? qraw[i] : u32x4{0u, 0u, 0u, 0u};
@@ -503,10 +510,10 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
   asm volatile("" ::: "memory");
 
   // Consumer waves split each tile by query tile: wave w takes query tile
-  // w % QT of tiles w / QT, w / QT + 4 / QT, ..., so a tile's work is spread over
-  // QT waves (a shorter dependency chain per tile) and the merge adds 4 / QT
-  // partials per query tile.
-  constexpr int TSTRIDE = 4 / QT;
+  // w % QT of tiles w / QT, w / QT + NCW / QT, ..., so a tile's work is spread
+  // over QT waves (a shorter dependency chain per tile) and the merge adds
+  // NCW / QT partials per query tile.
+  constexpr int TSTRIDE = NCW / QT;
   constexpr int SLOT1 = 4096 + 64 * 2;  // one wave's merge slot: O of one query tile + (m, l)
   const int my_qt = wave % QT, phase = wave / QT;
   // a first mask segment (desc->seg_rows rows, a whole number of query tiles)
@@ -517,7 +524,7 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
   f32x16 o[1][4];
 #pragma unroll
   for (int hb = 0; hb < 4; ++hb) o[0][hb] = f32x16{};
-  if (wave == 4) {
+  if (wave == NCW) {
     // Tiles 0 and 1 were issued before the barrier. The first two tiles are
     // proven with two newer tiles in flight (vmcnt(32) after issuing tiles 2, 3),
     // so the consumers start as soon as tile 0 lands; tile 4 then goes out
@@ -548,24 +555,9 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
     decr_waitcnt<DECR_VM0>();
     while (next < n) signal(next++);
   } else {
-    // the query tile's Q fragments, read from LDS once for the whole range
-    typename MfmaT<T>::vec qh[8], ql[8];
     const T* qrow = qs + (my_qt * 32 + (lane & 31)) * DEC_QROW + 8 * (lane >> 5);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      qh[i] = *(const vec*)(qrow + 16 * i);
-      ql[i] = *(const vec*)(qrow + QLO + 16 * i);
-    }
-    for (int t = phase; t < n; t += TSTRIDE) {
-      decr_wait(&ready[t % DECR_SLOTS], t + 1, err);
-      const vec* tp = (const vec*)(tiles + (t % DECR_SLOTS) * 16384);
-      vec kc[1][8], vc[1][8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        kc[0][i] = tp[i * 64 + lane];
-        vc[0][i] = tp[512 + i * 64 + lane];
-      }
-      if (t + DECR_SLOTS < n) {  // the producer reuses the slot for tile t + DECR_SLOTS
+    auto release = [&](int t) {  // the producer reuses the slot for tile t + DECR_SLOTS
+      if (t + DECR_SLOTS < n) {
         decr_waitcnt<DECR_LGKM0>();  // the slot's reads are complete
         if (lane == 0)
           asm volatile("ds_add_u32 %0, %1"
@@ -573,7 +565,49 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
                        : "v"((uint32_t)(uintptr_t)&freed[t % DECR_SLOTS]), "v"(1)
                        : "memory");
       }
-      attend_tile_rq<T>(kc, vc, qh, ql, (t_begin + t) * 32, nk_mine, c, lane, m_run, l_run, o);
+    };
+    if (NCW == 4) {
+      // the query tile's Q fragments, read from LDS once for the whole range
+      typename MfmaT<T>::vec qh[8], ql[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        qh[i] = *(const vec*)(qrow + 16 * i);
+        ql[i] = *(const vec*)(qrow + QLO + 16 * i);
+      }
+      for (int t = phase; t < n; t += TSTRIDE) {
+        decr_wait(&ready[t % DECR_SLOTS], t + 1, err);
+        const vec* tp = (const vec*)(tiles + (t % DECR_SLOTS) * 16384);
+        vec kc[1][8], vc[1][8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          kc[0][i] = tp[i * 64 + lane];
+          vc[0][i] = tp[512 + i * 64 + lane];
+        }
+        release(t);
+        attend_tile_rq<T>(kc, vc, qh, ql, (t_begin + t) * 32, nk_mine, c, lane, m_run, l_run, o);
+      }
+    } else {
+      // three waves share a SIMD: K, then the score chain with the Q fragments
+      // read from LDS a k step at a time, then V (the slot is released after V)
+      for (int t = phase; t < n; t += TSTRIDE) {
+        decr_wait(&ready[t % DECR_SLOTS], t + 1, err);
+        const vec* tp = (const vec*)(tiles + (t % DECR_SLOTS) * 16384);
+        vec kc[8], vc[1][8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) kc[i] = tp[i * 64 + lane];
+        f32x16 sc[1][1] = {{f32x16{}}};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const vec qh = *(const vec*)(qrow + 16 * i), ql = *(const vec*)(qrow + QLO + 16 * i);
+          sc[0][0] = MfmaT<T>::mma(kc[i], qh, sc[0][0]);
+          sc[0][0] = MfmaT<T>::mma(kc[i], ql, sc[0][0]);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) vc[0][i] = tp[512 + i * 64 + lane];
+        release(t);
+        const int k0[1] = {(t_begin + t) * 32}, nk1[1] = {nk_mine};
+        softmax_pv<T, 1, 1>(sc, vc, k0, nk1, c, lane, m_run, l_run, o);
+      }
     }
     l_run[0] += __shfl_xor(l_run[0], 32, 64);
   }
@@ -582,7 +616,7 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
   // in phase order and stores the range partial itself.
   __syncthreads();  // every tile consumed: Q and the slots become the merge area
   const int lane_f4 = lane;  // f32x4 (hb * 4 + r4) * 64 + lane of a slot
-  if (wave < 4 && phase > 0) {
+  if (wave < NCW && phase > 0) {
     float* mine = mrg + wave * SLOT1;
 #pragma unroll
     for (int hb = 0; hb < 4; ++hb)
@@ -594,7 +628,7 @@ __global__ __launch_bounds__(320) void attn_decode_kernel(
     mine[4096 + lane * 2 + 1] = l_run[0];
   }
   __syncthreads();  // the phase-0 waves wait for the others' slots
-  if (wave >= 4 || phase > 0) return;
+  if (wave >= NCW || phase > 0) return;
   float mw[TSTRIDE], lw[TSTRIDE], wgt[TSTRIDE];
   mw[0] = m_run[0];
   lw[0] = l_run[0];
@@ -1052,7 +1086,8 @@ void attention_decode(bool bf16, const void* q, const void* kv_layer, int64_t kv
     auto fn = attn_decode_kernel<T, QT>;                                                   \
     static size_t granted = 0;                                                              \
     grant_lds((const void*)fn, ldsr, granted);                                              \
-    DRT_LAUNCH(Profiler::ATTN, bytes, fn, grid, dim3(320), ldsr, s, (const T*)q,            \
+    DRT_LAUNCH(Profiler::ATTN, bytes, fn, grid, dim3(64 * (decr_ncw<QT>() + 1)), ldsr, s,   \
+               (const T*)q,                                                                 \
                q_has_lo ? (const T*)q + (int64_t)n_rows * Hq * 128 : (const T*)nullptr,     \
                (const T*)kv_layer, kv_head_stride, n_rows, Hq, Hkv, n_keys, desc, o_part,   \
                ml_part, scale, err);                                                        \

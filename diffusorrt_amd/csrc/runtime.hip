@@ -2438,7 +2438,7 @@ int32_t drt_op_attention(const void* q, const void* cache, int64_t head_stride, 
     const size_t q_bytes = (size_t)rows * hq * 128 * 2;
     float* o_part = (float*)((char*)workspace + (2 * q_bytes + 255) / 256 * 256);
     const int ofmt = out_dtype == DRT_F32 ? 2 : 3;
-    if (rows * (hq / hkv) <= 64 && one_segment(fa)) {
+    if (rows * (hq / hkv) <= 128 && one_segment(fa)) {
       const int ranges = attention_decode_ranges(n_keys, hkv);
       attention_decode(kv_dtype == DRT_BF16, q, cache, head_stride, rows, hq, hkv, n_keys,
                        nullptr, ranges, o_part, out, nullptr, ofmt, as_stream(stream), nullptr,
